@@ -1,0 +1,795 @@
+// Flash-attention forward for gfx950 (CDNA4): bf16 / fp16 / OCP e4m3 inputs, GQA/MQA,
+// packed varlen, causal or full masks, and the per-sequence half selections the zig-zag
+// ring schedule needs.  Replaces the FA4 `_flash_attn_fwd` call of
+// fa4_ring/fa4_backend.py:106-120; the three ring step patterns of
+// fa4_ring/ring_attention.py:108-166 map to
+//   step 0        causal=1, q_sel=ALL,       k_sel=ALL
+//   step s<=rank  causal=0, q_sel=ALL,       k_sel=FRONT_HALF  (no K/V gather)
+//   step s>rank   causal=0, q_sel=BACK_HALF, k_sel=ALL         (no Q gather, no padding)
+//
+// Work decomposition
+//   A workgroup is 4 wavefronts.  It owns HP query heads that share one kv head and RB
+//   blocks of 32 query rows (HP * RB = 4); wavefront w computes head w % HP for rows
+//   block w / HP.  K/V tiles of BN keys are staged once in LDS and read by all four
+//   wavefronts, so a tile feeds 128 query rows.
+//
+// Per-wavefront math (32 queries x BN keys per tile), written transposed:
+//   S^T = K Q^T   with v_mfma_f32_32x32x16_{bf16,f16} (or 32x32x64_f8f6f4 for e4m3);
+//                 A = K rows from LDS, B = Q^T held in registers for the whole loop.
+//   In the 32x32 accumulator layout lane l holds column l % 32 (one query) and 16 rows
+//   (keys), so the running max / sum of a query live in one lane pair (l, l ^ 32): the
+//   row max costs one v_permlane32_swap per tile and the row sum none until the end.
+//   O^T += V^T P^T  with B = P^T taken straight from the S^T accumulator registers.
+//   The MFMA pairs A k-slot 8*(l/32)+j with B k-slot 8*(l/32)+j; in the accumulator the
+//   lane's keys of a 16-key group are {4h..4h+3, 8+4h..8+4h+3} (h = l / 32), so V^T is
+//   stored in LDS with the keys of every 16-key group permuted to match (pos = 8h + j),
+//   and each A fragment is one 16-byte LDS read.
+//
+// LDS layouts (per buffer, double buffered; one barrier per tile)
+//   K   [BN][D]  16-byte chunks XOR-swizzled by (key & 7): conflict-free fragment reads.
+//   V^T [D][BN]  keys permuted as above, 16-byte chunks XOR-swizzled by (d ^ d >> 3).
+//   BN = 8192 / D (16 KB of K and 16 KB of V per tile for every head dim).
+//
+// Softmax runs in the exp2 domain with scale * log2(e) (times the q/k descales) folded
+// into one FMA per score; the LSE written is natural-log, as fa4_ring/merge.py expects.
+#include <cfloat>
+
+#include "common.h"
+
+namespace fa4cp {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+
+struct AttnParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  float* lse;
+  int64_t q_rs, q_hs, k_rs, k_hs, v_rs, v_hs, o_rs, o_hs, lse_rs;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  int nseq, total_q, total_k;
+  int h_kv, group;
+  int causal, q_sel, k_sel;
+  float scale;  // softmax scale (natural units)
+  const float* qd;
+  const float* kd;
+  const float* vd;
+  int n_rt;  // row tiles per sequence (of 32 * RB rows)
+  int n_hg;  // head groups: h_kv * group / HP
+  int n_blocks;
+};
+
+// Query / key row range [start, start + len) of sequence j after the half selection.
+__device__ __forceinline__ void seq_range(const int32_t* cu, int j, int total, int sel,
+                                          int& start, int& len) {
+  int s = 0, e = total;
+  if (cu != nullptr) {
+    s = cu[j];
+    e = cu[j + 1];
+  }
+  const int mid = (s + e) >> 1;
+  if (sel == FA4CP_SEL_FRONT_HALF) e = mid;
+  if (sel == FA4CP_SEL_BACK_HALF) s = mid;
+  start = s;
+  len = e - s;
+}
+
+// Pair reduction across lanes l and l ^ 32 (v_permlane32_swap: lanes 0-31 receive the
+// upper half's value in the second result, lanes 32-63 the lower half's in the first).
+__device__ __forceinline__ float pair_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Position of key kk (0..15) of a 16-key group inside the permuted V^T row.
+__host__ __device__ constexpr int vperm16(int kk) {
+  return 8 * ((kk >> 2) & 1) + 4 * (kk >> 3) + (kk & 3);
+}
+
+template <typename T>
+struct MfmaOps;
+
+template <>
+struct MfmaOps<__bf16> {
+  typedef bf16x8 frag;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct MfmaOps<_Float16> {
+  typedef f16x8 frag;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Decodes the workgroup id into (head group, sequence, row tile).  Row tiles are handed
+// out longest-first (the causal diagonal makes late row tiles the most expensive), and
+// head groups are laid out so that each XCD works on few kv heads (shared L2).
+__device__ __forceinline__ void decode_block(const AttnParams& p, int& hg, int& seq, int& rt) {
+  const int b = xcd_remap((int)blockIdx.x, p.n_blocks);
+  const int per_hg = p.nseq * p.n_rt;
+  hg = b / per_hg;
+  const int r = b - hg * per_hg;
+  seq = r / p.n_rt;
+  rt = p.n_rt - 1 - (r - seq * p.n_rt);
+}
+
+//--------------------------------------------------------------------------------------
+// bf16 / fp16 kernel
+//--------------------------------------------------------------------------------------
+template <typename T, int D, int HP>
+__global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(AttnParams p) {
+  using Ops = MfmaOps<T>;
+  using frag = typename Ops::frag;
+  constexpr int BN = 8192 / D;          // keys per tile
+  constexpr int RB = kWaves / HP;       // 32-row blocks per workgroup
+  constexpr int KCH = D / 8;            // 16-byte chunks per K row
+  constexpr int VCH = BN / 8;           // 16-byte chunks per V^T row
+  constexpr int KU = BN * KCH / kThreads;  // K 16-byte units per thread per tile
+  constexpr int NMT = BN / 32;          // S^T accumulator tiles
+  constexpr int NDT = D / 32;           // O^T accumulator tiles
+  constexpr int NKS = D / 16;           // k-steps of S^T (over d)
+  constexpr int NPS = BN / 16;          // k-steps of O^T (over keys)
+  static_assert(KU * kThreads == BN * KCH, "K tile must split evenly");
+  static_assert((BN / 4) * KCH == kThreads, "one V^T task per thread");
+
+  __shared__ __attribute__((aligned(16))) T smem[2][2][BN * D];  // [buf][K|V^T][...]
+
+  int hg, seq, rt;
+  decode_block(p, hg, seq, rt);
+  int qs, Lq, ks, Lk;
+  seq_range(p.cu_q, seq, p.total_q, p.q_sel, qs, Lq);
+  seq_range(p.cu_k, seq, p.total_k, p.k_sel, ks, Lk);
+  const int row_tile0 = rt * RB * 32;
+  if (row_tile0 >= Lq) return;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int lq = lane & 31;  // query column owned by this lane
+  const int lh = lane >> 5;  // k-slot half
+  const int groups_per_kv = p.group / HP;
+  const int kvh = hg / groups_per_kv;
+  const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
+  const int r0 = row_tile0 + (wave / HP) * 32;  // first row of this wavefront (selection-local)
+  const int off = Lk - Lq;                       // bottom-right causal alignment
+
+  // number of key tiles this workgroup visits
+  int n_tiles = (Lk + BN - 1) / BN;
+  if (p.causal) {
+    const int last_row = min(row_tile0 + RB * 32, Lq) - 1;
+    const int kmax = last_row + off;  // largest visible key
+    n_tiles = kmax < 0 ? 0 : min(n_tiles, kmax / BN + 1);
+  }
+
+  const T* __restrict__ qg = reinterpret_cast<const T*>(p.q);
+  const T* __restrict__ kg = reinterpret_cast<const T*>(p.k);
+  const T* __restrict__ vg = reinterpret_cast<const T*>(p.v);
+
+  // Q^T fragments: lane (lq, lh) holds q[row r0+lq][16t + 8lh .. +7] for every k-step t.
+  frag qf[NKS];
+  {
+    const int row = r0 + lq;
+    const bool ok = row < Lq;
+    const T* src = qg + (int64_t)(qs + (ok ? row : 0)) * p.q_rs + (int64_t)head * p.q_hs + 8 * lh;
+#pragma unroll
+    for (int t = 0; t < NKS; ++t) {
+      frag x = *reinterpret_cast<const frag*>(src + 16 * t);
+      qf[t] = ok ? x : frag{};
+    }
+  }
+
+  // Global -> register staging of one K/V tile.
+  const T* kbase = kg + (int64_t)ks * p.k_rs + (int64_t)kvh * p.k_hs;
+  const T* vbase = vg + (int64_t)ks * p.v_rs + (int64_t)kvh * p.v_hs;
+  frag kreg[KU];
+  frag vreg[4];
+  const int v_dc = tid % KCH;  // V task: d chunk
+  const int v_kq = tid / KCH;  // V task: key quad
+  auto load_tile = [&](int tile) {
+    const int kb = tile * BN;
+#pragma unroll
+    for (int i = 0; i < KU; ++i) {
+      const int u = tid + i * kThreads;
+      const int key = u / KCH, c = u % KCH;
+      const bool ok = kb + key < Lk;
+      frag x = *reinterpret_cast<const frag*>(kbase + (int64_t)(ok ? kb + key : 0) * p.k_rs + 8 * c);
+      kreg[i] = ok ? x : frag{};
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = kb + 4 * v_kq + i;
+      const bool ok = key < Lk;
+      frag x = *reinterpret_cast<const frag*>(vbase + (int64_t)(ok ? key : 0) * p.v_rs + 8 * v_dc);
+      vreg[i] = ok ? x : frag{};
+    }
+  };
+  auto store_tile = [&](int buf) {
+    T* ks_ = smem[buf][0];
+    T* vs_ = smem[buf][1];
+#pragma unroll
+    for (int i = 0; i < KU; ++i) {
+      const int u = tid + i * kThreads;
+      const int key = u / KCH, c = u % KCH;
+      *reinterpret_cast<frag*>(ks_ + key * D + 8 * (c ^ (key & 7))) = kreg[i];
+    }
+    // transpose 4 keys x 8 d into 8 rows of V^T, 4 keys (8 bytes) each
+    const int grp = v_kq >> 2;          // 16-key group
+    const int kk0 = 4 * (v_kq & 3);     // first key inside the group
+    const int pos = 16 * grp + vperm16(kk0);
+    const int chunk = pos >> 3, within = pos & 7;
+#pragma unroll
+    for (int dd = 0; dd < 8; ++dd) {
+      const int d = 8 * v_dc + dd;
+      const int sw = (d ^ (d >> 3)) & (VCH - 1);
+      typedef T t4 __attribute__((ext_vector_type(4)));
+      t4 w = {vreg[0][dd], vreg[1][dd], vreg[2][dd], vreg[3][dd]};
+      *reinterpret_cast<t4*>(vs_ + d * BN + 8 * (chunk ^ sw) + within) = w;
+    }
+  };
+
+  float c_log2 = p.scale * kLog2e;
+  f32x16 o[NDT];
+#pragma unroll
+  for (int i = 0; i < NDT; ++i) o[i] = f32x16{};
+  float m = -INFINITY;
+  float lsum = 0.f;
+
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int it = 0; it < n_tiles; ++it) {
+    const int buf = it & 1;
+    const bool more = it + 1 < n_tiles;
+    if (more) load_tile(it + 1);
+    const T* ks_ = smem[buf][0];
+    const T* vs_ = smem[buf][1];
+
+    // S^T = K Q^T
+    f32x16 s[NMT];
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt) {
+      s[mt] = f32x16{};
+      const int key = 32 * mt + lq;
+#pragma unroll
+      for (int t = 0; t < NKS; ++t) {
+        frag a = *reinterpret_cast<const frag*>(ks_ + key * D + 8 * ((2 * t + lh) ^ (key & 7)));
+        s[mt] = Ops::mma(a, qf[t], s[mt]);
+      }
+    }
+
+    // masking: keys past the selection, and the causal diagonal
+    const int kb = it * BN;
+    const bool tail = kb + BN > Lk;
+    const bool diag = p.causal && (kb + BN - 1 > r0 + off);
+    if (tail || diag) {
+      const int qq = r0 + lq + off;
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kk = kb + 32 * mt + (i >> 2) * 8 + 4 * lh + (i & 3);
+          const bool dead = kk >= Lk || (p.causal && kk > qq);
+          s[mt][i] = dead ? -INFINITY : s[mt][i];
+        }
+    }
+
+    // online softmax (exp2 domain)
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[mt][i]);
+    tmax = pair_max(tmax);
+    const float m_new = fmaxf(m, tmax);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float mc = m_use * c_log2;
+    const float alpha = fast_exp2(m * c_log2 - mc);
+    float rs = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float e = fast_exp2(fmaf(s[mt][i], c_log2, -mc));
+        s[mt][i] = e;
+        rs += e;
+      }
+    lsum = fmaf(lsum, alpha, rs);
+    m = m_new;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+
+    // P^T fragments: k-step t takes accumulator registers 8*(t%2) .. +7 of tile t/2
+    frag pf[NPS];
+#pragma unroll
+    for (int t = 0; t < NPS; ++t)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pf[t][j] = (T)s[t >> 1][8 * (t & 1) + j];
+
+    // O^T += V^T P^T
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const int d = 32 * dt + lq;
+      const int sw = (d ^ (d >> 3)) & (VCH - 1);
+#pragma unroll
+      for (int t = 0; t < NPS; ++t) {
+        frag a = *reinterpret_cast<const frag*>(vs_ + d * BN + 8 * ((2 * t + lh) ^ sw));
+        o[dt] = Ops::mma(a, pf[t], o[dt]);
+      }
+    }
+
+    if (more) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: combine the lane pair's partial sums, normalise, write out and LSE
+  const float ltot = pair_sum(lsum);
+  const float inv = ltot > 0.f ? 1.0f / ltot : 0.f;
+  const int row = r0 + lq;
+  if (row < Lq) {
+    T* og = reinterpret_cast<T*>(p.out) + (int64_t)(qs + row) * p.o_rs + (int64_t)head * p.o_hs;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        typedef T t4 __attribute__((ext_vector_type(4)));
+        t4 w = {(T)(o[dt][4 * g + 0] * inv), (T)(o[dt][4 * g + 1] * inv),
+                (T)(o[dt][4 * g + 2] * inv), (T)(o[dt][4 * g + 3] * inv)};
+        *reinterpret_cast<t4*>(og + 32 * dt + 8 * g + 4 * lh) = w;
+      }
+    if (lh == 0) {
+      const float lse = ltot > 0.f ? m * p.scale + logf(ltot) : -INFINITY;
+      p.lse[(int64_t)(qs + row) * p.lse_rs + head] = lse;
+    }
+  }
+}
+
+//--------------------------------------------------------------------------------------
+// OCP e4m3 kernel
+//
+// QK^T and PV run on v_mfma_f32_32x32x64_f8f6f4 (fp8 x fp8, 64-deep).  The MFMA pairs
+// A slot (h, j) with B slot (h, j) (h = lane / 32, j = byte 0..31 of the lane's operand);
+// the kernel only relies on that symmetry.  For QK^T slot (h, j) of k-step t is
+// d = 64t + 32h + j on both sides.  For PV slot (h, j) of a 64-key group is accumulator
+// register j % 16 of S^T tile j / 16, i.e. key 32(j/16) + 8((j%16)/4) + 4h + j%4, and V^T
+// is stored in LDS with the keys of each 64-key group permuted so that the lane's 32
+// slots are contiguous bytes.
+//
+// P is rounded to e4m3 for the fast PV product.  Queries with few visible keys (the
+// first rows of a causal sequence) would see that rounding undamped, so tiles on the
+// causal diagonal and all tiles of the first kPreciseRows rows of a causal launch use a
+// bf16 PV product instead: P in bf16 against V widened exactly from e4m3 to bf16.
+//--------------------------------------------------------------------------------------
+constexpr int kPreciseRows = 512;
+
+__host__ __device__ constexpr int vperm64(int kk) {
+  // key kk (0..63) of a 64-key group -> byte position in the permuted V^T row
+  return 32 * ((kk >> 2) & 1) + 16 * (kk >> 5) + 4 * ((kk & 31) >> 3) + (kk & 3);
+}
+
+__device__ __forceinline__ f32x16 mma_fp8(i32x8 a, i32x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// Widens 8 e4m3 bytes (two dwords) to 8 bf16 (exact).
+__device__ __forceinline__ bf16x8 e4m3x8_to_bf16(u32x2 x) {
+  bf16x8 r;
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[w], false);
+    f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[w], true);
+    r[4 * w + 0] = (__bf16)lo[0];
+    r[4 * w + 1] = (__bf16)lo[1];
+    r[4 * w + 2] = (__bf16)hi[0];
+    r[4 * w + 3] = (__bf16)hi[1];
+  }
+  return r;
+}
+
+template <int D, int HP>
+__global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_e4m3(AttnParams p) {
+  constexpr int BN = 64;               // keys per tile (one PV k-step)
+  constexpr int RB = kWaves / HP;
+  constexpr int KCH = D / 16;          // 16-byte chunks per K row
+  constexpr int KU = BN * KCH / kThreads;
+  constexpr int NKS = D / 64;          // S^T k-steps
+  constexpr int NDT = D / 32;
+  constexpr int VROW = BN;             // bytes per V^T row
+  constexpr int DQ = D / 8;            // V tasks: 8-byte d chunks per key quad
+  constexpr int VT = (BN / 4) * DQ / kThreads;  // V tasks per thread
+  static_assert(KU >= 1 && KU * kThreads == BN * KCH, "K tile split");
+  static_assert(VT >= 1 && VT * kThreads == (BN / 4) * DQ, "V tile split");
+  static_assert(KCH >= 8 || D == 64, "swizzle assumes >= 8 chunks per K row");
+
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2][2][BN * D];
+
+  int hg, seq, rt;
+  decode_block(p, hg, seq, rt);
+  int qs, Lq, ks, Lk;
+  seq_range(p.cu_q, seq, p.total_q, p.q_sel, qs, Lq);
+  seq_range(p.cu_k, seq, p.total_k, p.k_sel, ks, Lk);
+  const int row_tile0 = rt * RB * 32;
+  if (row_tile0 >= Lq) return;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int lq = lane & 31;
+  const int lh = lane >> 5;
+  const int groups_per_kv = p.group / HP;
+  const int kvh = hg / groups_per_kv;
+  const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
+  const int r0 = row_tile0 + (wave / HP) * 32;
+  const int off = Lk - Lq;
+
+  int n_tiles = (Lk + BN - 1) / BN;
+  if (p.causal) {
+    const int last_row = min(row_tile0 + RB * 32, Lq) - 1;
+    const int kmax = last_row + off;
+    n_tiles = kmax < 0 ? 0 : min(n_tiles, kmax / BN + 1);
+  }
+
+  const uint8_t* __restrict__ qg = reinterpret_cast<const uint8_t*>(p.q);
+  const uint8_t* __restrict__ kg = reinterpret_cast<const uint8_t*>(p.k);
+  const uint8_t* __restrict__ vg = reinterpret_cast<const uint8_t*>(p.v);
+
+  i32x8 qf[NKS];
+  {
+    const int row = r0 + lq;
+    const bool ok = row < Lq;
+    const uint8_t* src = qg + (int64_t)(qs + (ok ? row : 0)) * p.q_rs + (int64_t)head * p.q_hs + 32 * lh;
+#pragma unroll
+    for (int t = 0; t < NKS; ++t) {
+      i32x4 a = *reinterpret_cast<const i32x4*>(src + 64 * t);
+      i32x4 b = *reinterpret_cast<const i32x4*>(src + 64 * t + 16);
+      i32x8 x = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+      qf[t] = ok ? x : i32x8{};
+    }
+  }
+
+  const uint8_t* kbase = kg + (int64_t)ks * p.k_rs + (int64_t)kvh * p.k_hs;
+  const uint8_t* vbase = vg + (int64_t)ks * p.v_rs + (int64_t)kvh * p.v_hs;
+  i32x4 kreg[KU];
+  u32x2 vreg[VT][4];
+  auto load_tile = [&](int tile) {
+    const int kb = tile * BN;
+#pragma unroll
+    for (int i = 0; i < KU; ++i) {
+      const int u = tid + i * kThreads;
+      const int key = u / KCH, c = u % KCH;
+      const bool ok = kb + key < Lk;
+      i32x4 x = *reinterpret_cast<const i32x4*>(kbase + (int64_t)(ok ? kb + key : 0) * p.k_rs + 16 * c);
+      kreg[i] = ok ? x : i32x4{};
+    }
+#pragma unroll
+    for (int tk = 0; tk < VT; ++tk) {
+      const int task = tid + tk * kThreads;
+      const int dq = task % DQ, kq = task / DQ;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = kb + 4 * kq + i;
+        const bool ok = key < Lk;
+        u32x2 x = *reinterpret_cast<const u32x2*>(vbase + (int64_t)(ok ? key : 0) * p.v_rs + 8 * dq);
+        vreg[tk][i] = ok ? x : u32x2{};
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+    uint8_t* ks_ = smem[buf][0];
+    uint8_t* vs_ = smem[buf][1];
+#pragma unroll
+    for (int i = 0; i < KU; ++i) {
+      const int u = tid + i * kThreads;
+      const int key = u / KCH, c = u % KCH;
+      *reinterpret_cast<i32x4*>(ks_ + key * D + 16 * (c ^ (key & 7 & (KCH - 1)))) = kreg[i];
+    }
+#pragma unroll
+    for (int tk = 0; tk < VT; ++tk) {
+      const int task = tid + tk * kThreads;
+      const int dq = task % DQ, kq = task / DQ;
+      const int pos = vperm64(4 * kq);  // 4 consecutive keys stay contiguous
+      // 4 keys x 8 d bytes -> 8 d rows x 4 key bytes (byte transpose with v_perm)
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        const unsigned a0 = vreg[tk][0][w], a1 = vreg[tk][1][w], a2 = vreg[tk][2][w], a3 = vreg[tk][3][w];
+        // t01 = interleave bytes of a0,a1 ; t23 = of a2,a3
+        const unsigned t01_lo = __builtin_amdgcn_perm(a1, a0, 0x05010400u);  // a0b0 a1b0 a0b1 a1b1
+        const unsigned t01_hi = __builtin_amdgcn_perm(a1, a0, 0x07030602u);  // a0b2 a1b2 a0b3 a1b3
+        const unsigned t23_lo = __builtin_amdgcn_perm(a3, a2, 0x05010400u);
+        const unsigned t23_hi = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
+        unsigned col[4];
+        col[0] = __builtin_amdgcn_perm(t23_lo, t01_lo, 0x05040100u);  // d=0: a0 a1 a2 a3
+        col[1] = __builtin_amdgcn_perm(t23_lo, t01_lo, 0x07060302u);  // d=1
+        col[2] = __builtin_amdgcn_perm(t23_hi, t01_hi, 0x05040100u);  // d=2
+        col[3] = __builtin_amdgcn_perm(t23_hi, t01_hi, 0x07060302u);  // d=3
+#pragma unroll
+        for (int dd = 0; dd < 4; ++dd) {
+          const int d = 8 * dq + 4 * w + dd;
+          const int sw = (d >> 2) & 3;  // 64-byte rows: spread rows d, d+4, d+8, d+12
+          const int chunk = (pos >> 4) ^ sw;
+          *reinterpret_cast<unsigned*>(vs_ + d * VROW + 16 * chunk + (pos & 15)) = col[dd];
+        }
+      }
+    }
+  };
+
+  const int qd_idx = kvh;
+  const float qd = p.qd ? p.qd[qd_idx] : 1.f;
+  const float kd = p.kd ? p.kd[qd_idx] : 1.f;
+  const float vd = p.vd ? p.vd[qd_idx] : 1.f;
+  const float c_log2 = p.scale * qd * kd * kLog2e;
+  const float c_nat = p.scale * qd * kd;
+
+  f32x16 o[NDT];
+#pragma unroll
+  for (int i = 0; i < NDT; ++i) o[i] = f32x16{};
+  float m = -INFINITY;
+  float lsum = 0.f;
+
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int it = 0; it < n_tiles; ++it) {
+    const int buf = it & 1;
+    const bool more = it + 1 < n_tiles;
+    if (more) load_tile(it + 1);
+    const uint8_t* ks_ = smem[buf][0];
+    const uint8_t* vs_ = smem[buf][1];
+
+    f32x16 s[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      s[mt] = f32x16{};
+      const int key = 32 * mt + lq;
+#pragma unroll
+      for (int t = 0; t < NKS; ++t) {
+        const int c0 = 4 * t + 2 * lh;
+        i32x4 a0 = *reinterpret_cast<const i32x4*>(ks_ + key * D + 16 * ((c0) ^ (key & 7 & (KCH - 1))));
+        i32x4 a1 = *reinterpret_cast<const i32x4*>(ks_ + key * D + 16 * ((c0 + 1) ^ (key & 7 & (KCH - 1))));
+        i32x8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        s[mt] = mma_fp8(a, qf[t], s[mt]);
+      }
+    }
+
+    const int kb = it * BN;
+    const bool tail = kb + BN > Lk;
+    const bool diag = p.causal && (kb + BN - 1 > r0 + off);
+    if (tail || diag) {
+      const int qq = r0 + lq + off;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kk = kb + 32 * mt + (i >> 2) * 8 + 4 * lh + (i & 3);
+          const bool dead = kk >= Lk || (p.causal && kk > qq);
+          s[mt][i] = dead ? -INFINITY : s[mt][i];
+        }
+    }
+
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[mt][i]);
+    tmax = pair_max(tmax);
+    const float m_new = fmaxf(m, tmax);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float mc = m_use * c_log2;
+    const float alpha = fast_exp2(m * c_log2 - mc);
+    float rs = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float e = fast_exp2(fmaf(s[mt][i], c_log2, -mc));
+        s[mt][i] = e;
+        rs += e;
+      }
+    lsum = fmaf(lsum, alpha, rs);
+    m = m_new;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+
+    const bool precise = p.causal && (diag || r0 < kPreciseRows);
+    if (!precise) {
+      // P^T as e4m3: slot j <- s[j / 16][j % 16]
+      i32x8 pf;
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        const int j = 4 * w;
+        int x = __builtin_amdgcn_cvt_pk_fp8_f32(s[j >> 4][(j & 15) + 0], s[j >> 4][(j & 15) + 1], 0, false);
+        x = __builtin_amdgcn_cvt_pk_fp8_f32(s[j >> 4][(j & 15) + 2], s[j >> 4][(j & 15) + 3], x, true);
+        pf[w] = x;
+      }
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const int d = 32 * dt + lq;
+        const int sw = (d >> 2) & 3;
+        i32x4 a0 = *reinterpret_cast<const i32x4*>(vs_ + d * VROW + 16 * ((2 * lh) ^ sw));
+        i32x4 a1 = *reinterpret_cast<const i32x4*>(vs_ + d * VROW + 16 * ((2 * lh + 1) ^ sw));
+        i32x8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        o[dt] = mma_fp8(a, pf, o[dt]);
+      }
+    } else {
+      // bf16 PV: k-step t (16 keys) uses registers 8*(t%2)..+7 of tile t/2 and the V^T
+      // bytes at position 32h + 8t .. +7 of the permuted row
+      bf16x8 pb[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pb[t][j] = (__bf16)s[t >> 1][8 * (t & 1) + j];
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const int d = 32 * dt + lq;
+        const int sw = (d >> 2) & 3;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int pos = 32 * lh + 8 * t;
+          u32x2 raw = *reinterpret_cast<const u32x2*>(vs_ + d * VROW + 16 * ((pos >> 4) ^ sw) + (pos & 15));
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(e4m3x8_to_bf16(raw), pb[t], o[dt], 0, 0, 0);
+        }
+      }
+    }
+
+    if (more) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  const float ltot = pair_sum(lsum);
+  const float inv = ltot > 0.f ? vd / ltot : 0.f;
+  const int row = r0 + lq;
+  if (row < Lq) {
+    __bf16* og = reinterpret_cast<__bf16*>(p.out) + (int64_t)(qs + row) * p.o_rs + (int64_t)head * p.o_hs;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        bf16x4 w = {(__bf16)(o[dt][4 * g + 0] * inv), (__bf16)(o[dt][4 * g + 1] * inv),
+                    (__bf16)(o[dt][4 * g + 2] * inv), (__bf16)(o[dt][4 * g + 3] * inv)};
+        *reinterpret_cast<bf16x4*>(og + 32 * dt + 8 * g + 4 * lh) = w;
+      }
+    if (lh == 0) {
+      const float lse = ltot > 0.f ? m * c_nat + logf(ltot) : -INFINITY;
+      p.lse[(int64_t)(qs + row) * p.lse_rs + head] = lse;
+    }
+  }
+}
+
+//--------------------------------------------------------------------------------------
+// host dispatch
+//--------------------------------------------------------------------------------------
+int heads_per_wg(int group) {
+  if (group % 4 == 0) return 4;
+  if (group % 2 == 0) return 2;
+  return 1;
+}
+
+typedef void (*KernelFn)(AttnParams);
+
+template <typename T>
+KernelFn pick16(int d, int hp) {
+#define FA4CP_PICK(DD)                          \
+  if (d == DD) {                                \
+    if (hp == 4) return attn_fwd_16bit<T, DD, 4>; \
+    if (hp == 2) return attn_fwd_16bit<T, DD, 2>; \
+    return attn_fwd_16bit<T, DD, 1>;            \
+  }
+  FA4CP_PICK(64)
+  FA4CP_PICK(128)
+  FA4CP_PICK(256)
+#undef FA4CP_PICK
+  return nullptr;
+}
+
+KernelFn pick8(int d, int hp) {
+#define FA4CP_PICK(DD)                        \
+  if (d == DD) {                              \
+    if (hp == 4) return attn_fwd_e4m3<DD, 4>; \
+    if (hp == 2) return attn_fwd_e4m3<DD, 2>; \
+    return attn_fwd_e4m3<DD, 1>;              \
+  }
+  FA4CP_PICK(128)
+  FA4CP_PICK(256)
+#undef FA4CP_PICK
+  return nullptr;
+}
+
+}  // namespace
+}  // namespace fa4cp
+
+using namespace fa4cp;
+
+extern "C" int fa4cp_attn_fwd(const fa4cp_attn_args* a, void* stream) {
+  clear_error();
+  if (a == nullptr) return set_error(FA4CP_EINVAL, "attn_fwd: null args");
+  if (!a->q || !a->k || !a->v || !a->out || !a->lse)
+    return set_error(FA4CP_EINVAL, "attn_fwd: null tensor pointer");
+  if (a->h_q <= 0 || a->h_kv <= 0 || a->h_q % a->h_kv != 0)
+    return set_error(FA4CP_EINVAL, "attn_fwd: h_q=%d must be a positive multiple of h_kv=%d",
+                     a->h_q, a->h_kv);
+  if (a->total_q < 0 || a->total_k < 0) return set_error(FA4CP_EINVAL, "attn_fwd: negative rows");
+  if ((a->cu_q == nullptr) != (a->cu_k == nullptr))
+    return set_error(FA4CP_EINVAL, "attn_fwd: cu_q and cu_k must both be given or both be NULL");
+  const int nseq = a->cu_q ? a->nseq : 1;
+  if (nseq < 1) return set_error(FA4CP_EINVAL, "attn_fwd: nseq must be >= 1");
+  if (a->q_sel != FA4CP_SEL_ALL && a->q_sel != FA4CP_SEL_BACK_HALF &&
+      a->q_sel != FA4CP_SEL_FRONT_HALF)
+    return set_error(FA4CP_EINVAL, "attn_fwd: bad q_sel %d", a->q_sel);
+  if (a->k_sel != FA4CP_SEL_ALL && a->k_sel != FA4CP_SEL_BACK_HALF &&
+      a->k_sel != FA4CP_SEL_FRONT_HALF)
+    return set_error(FA4CP_EINVAL, "attn_fwd: bad k_sel %d", a->k_sel);
+  const int max_q_full = a->cu_q ? a->max_seqlen_q : a->total_q;
+  if (max_q_full < 0) return set_error(FA4CP_EINVAL, "attn_fwd: bad max_seqlen_q");
+  const int max_q = (a->q_sel == FA4CP_SEL_ALL) ? max_q_full : (max_q_full + 1) / 2;
+  const int group = a->h_q / a->h_kv;
+  const int hp = heads_per_wg(group);
+  const int rb = kWaves / hp;
+  const int d = a->d;
+
+  KernelFn fn = nullptr;
+  switch (a->dtype) {
+    case FA4CP_BF16: fn = pick16<__bf16>(d, hp); break;
+    case FA4CP_FP16: fn = pick16<_Float16>(d, hp); break;
+    case FA4CP_E4M3: fn = pick8(d, hp); break;
+    default: return set_error(FA4CP_EUNSUPPORTED, "attn_fwd: unsupported dtype %d", a->dtype);
+  }
+  if (fn == nullptr)
+    return set_error(FA4CP_EUNSUPPORTED, "attn_fwd: head dim %d not implemented for dtype %d "
+                     "(bf16/fp16: 64, 128, 256; e4m3: 128, 256)", d, a->dtype);
+  // Fragment loads are 16 bytes wide (8 bytes for e4m3 V) and outputs are written 4
+  // elements at a time, so every row / head start must keep that alignment.
+  {
+    const bool fp8 = a->dtype == FA4CP_E4M3;
+    const int64_t qa = fp8 ? 16 : 8, ka = fp8 ? 16 : 8, va = 8;  // elements
+    auto ok = [](const void* ptr, int64_t rs, int64_t hs, int64_t al, int esz) {
+      return rs > 0 && hs > 0 && rs % al == 0 && hs % al == 0 &&
+             ((uintptr_t)ptr % (uintptr_t)(al * esz)) == 0;
+    };
+    const int esz = fp8 ? 1 : 2;
+    if (!ok(a->q, a->q_row_stride, a->q_head_stride, qa, esz) ||
+        !ok(a->k, a->k_row_stride, a->k_head_stride, ka, esz) ||
+        !ok(a->v, a->v_row_stride, a->v_head_stride, va, esz) ||
+        !ok(a->out, a->o_row_stride, a->o_head_stride, 4, 2) || a->lse_row_stride < a->h_q)
+      return set_error(FA4CP_EINVAL, "attn_fwd: misaligned pointer or stride (q/k rows and heads "
+                       "need 16-byte alignment, v 8-byte for e4m3, out 8-byte; lse_row_stride >= h_q)");
+  }
+  AttnParams p;
+  p.q = a->q; p.k = a->k; p.v = a->v; p.out = a->out; p.lse = a->lse;
+  p.q_rs = a->q_row_stride; p.q_hs = a->q_head_stride;
+  p.k_rs = a->k_row_stride; p.k_hs = a->k_head_stride;
+  p.v_rs = a->v_row_stride; p.v_hs = a->v_head_stride;
+  p.o_rs = a->o_row_stride; p.o_hs = a->o_head_stride;
+  p.lse_rs = a->lse_row_stride;
+  p.cu_q = a->cu_q; p.cu_k = a->cu_k;
+  p.nseq = nseq; p.total_q = a->total_q; p.total_k = a->total_k;
+  p.h_kv = a->h_kv; p.group = group;
+  p.causal = a->causal ? 1 : 0; p.q_sel = a->q_sel; p.k_sel = a->k_sel;
+  p.scale = a->softmax_scale;
+  p.qd = a->q_descale; p.kd = a->k_descale; p.vd = a->v_descale;
+  p.n_rt = (max_q + 32 * rb - 1) / (32 * rb);
+  p.n_hg = a->h_kv * (group / hp);
+  const int64_t blocks = (int64_t)p.n_hg * nseq * p.n_rt;
+  if (blocks == 0) return FA4CP_OK;
+  if (blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "attn_fwd: grid too large");
+  p.n_blocks = (int)blocks;
+  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kThreads), 0, (hipStream_t)stream, p);
+  return check_launch("attn_fwd");
+}

@@ -1,0 +1,103 @@
+// Shared definitions for the gfx950 kernels and the C ABI glue.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/fa4cp.h"
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+namespace fa4cp {
+
+// Records a failure message for fa4cp_last_error() and returns `code`.
+int set_error(int code, const char* fmt, ...);
+void clear_error();
+
+// Converts a pending launch error (if any) into a status code.
+int check_launch(const char* what);
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float bf16_to_f32(__bf16 x) { return (float)x; }
+
+// Loads 8 elements of dtype T starting at p and widens them to fp32.
+template <typename T>
+__device__ __forceinline__ void load8_f32(const T* p, float (&out)[8]);
+
+template <>
+__device__ __forceinline__ void load8_f32<float>(const float* p, float (&out)[8]) {
+  f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+  out[0] = a[0]; out[1] = a[1]; out[2] = a[2]; out[3] = a[3];
+  out[4] = b[0]; out[5] = b[1]; out[6] = b[2]; out[7] = b[3];
+}
+template <>
+__device__ __forceinline__ void load8_f32<__bf16>(const __bf16* p, float (&out)[8]) {
+  bf16x8 a = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = (float)a[i];
+}
+template <>
+__device__ __forceinline__ void load8_f32<_Float16>(const _Float16* p, float (&out)[8]) {
+  f16x8 a = *reinterpret_cast<const f16x8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = (float)a[i];
+}
+
+template <typename T>
+__device__ __forceinline__ void store8_f32(T* p, const float (&in)[8]);
+
+template <>
+__device__ __forceinline__ void store8_f32<float>(float* p, const float (&in)[8]) {
+  f32x4 a = {in[0], in[1], in[2], in[3]};
+  f32x4 b = {in[4], in[5], in[6], in[7]};
+  *reinterpret_cast<f32x4*>(p) = a;
+  *reinterpret_cast<f32x4*>(p + 4) = b;
+}
+template <>
+__device__ __forceinline__ void store8_f32<__bf16>(__bf16* p, const float (&in)[8]) {
+  bf16x8 a;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = (__bf16)in[i];
+  *reinterpret_cast<bf16x8*>(p) = a;
+}
+template <>
+__device__ __forceinline__ void store8_f32<_Float16>(_Float16* p, const float (&in)[8]) {
+  f16x8 a;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = (_Float16)in[i];
+  *reinterpret_cast<f16x8*>(p) = a;
+}
+
+// Index of the packed sequence that contains `row`: the largest j with cu[j] <= row
+// (binary search over cu[0..nseq]).
+__device__ __forceinline__ int find_seq(const int32_t* __restrict__ cu, int nseq, int64_t row) {
+  int lo = 0, hi = nseq - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if ((int64_t)cu[mid] <= row) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Remaps a linear workgroup id so that ids the hardware dispatches round-robin to the
+// eight XCDs of an MI355X see contiguous ranges of logical work: logical tile
+// (b % 8) * (n / 8) + b / 8 runs on XCD b % 8.  Identity when n is not a multiple of 8.
+__device__ __forceinline__ int xcd_remap(int b, int n) {
+  if ((n & 7) != 0) return b;
+  return (b & 7) * (n >> 3) + (b >> 3);
+}
+
+}  // namespace fa4cp

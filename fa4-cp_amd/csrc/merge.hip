@@ -1,0 +1,209 @@
+// LSE online-softmax merge kernels (HBM-bound).
+//
+// Replaces flashinfer.cascade.merge_state_in_place / merge_states as called from
+// fa4_ring/merge.py:31-42.  The arithmetic is the natural-log merge of
+// tests/test_algorithm_cpu.py:51-59 (max-shifted weights, logaddexp of the LSEs), done in
+// fp32 whatever the storage type of v.
+//
+// Layout: one (row, head) pair is handled by a group of 16 consecutive lanes, each lane
+// owning 16-byte vectors (8 elements) of the head dim; groups never straddle a
+// wavefront, so the lanes of a group all read the old LSE before the group's first lane
+// overwrites it (in-place merge).
+#include "common.h"
+
+namespace fa4cp {
+namespace {
+
+constexpr int kGroup = 16;   // lanes per (row, head)
+constexpr int kBlock = 256;  // lanes per workgroup
+
+// Maps the index of a selected row to its row in the packed tensor.  With row_sel != ALL
+// each sequence contributes half of its (even) length, so selected rows of sequence j
+// start at cu[j] / 2.
+__device__ __forceinline__ int64_t selected_row(const int32_t* __restrict__ cu, int nseq,
+                                                int row_sel, int64_t i) {
+  int lo = 0, hi = nseq - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if ((int64_t)(cu[mid] >> 1) <= i) lo = mid; else hi = mid - 1;
+  }
+  const int64_t start = cu[lo];
+  const int64_t end = cu[lo + 1];
+  const int64_t half_start = (row_sel == FA4CP_SEL_BACK_HALF) ? (start + end) / 2 : start;
+  return half_start + (i - (start >> 1));
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void merge_inplace_kernel(
+    T* __restrict__ v, float* __restrict__ s, const T* __restrict__ vo,
+    const float* __restrict__ so, int64_t n_groups, int h, int d, const int32_t* __restrict__ cu,
+    int nseq, int row_sel, int64_t single_rows) {
+  const int64_t g = (int64_t)blockIdx.x * (kBlock / kGroup) + (threadIdx.x / kGroup);
+  const int lane = threadIdx.x % kGroup;
+  if (g >= n_groups) return;
+  const int64_t sel = g / h;
+  const int head = (int)(g - sel * h);
+  int64_t row;
+  if (row_sel == FA4CP_SEL_ALL) {
+    row = sel;
+  } else if (cu == nullptr) {
+    // one sequence of single_rows rows: halves are [0, n/2) and [n/2, n)
+    row = (row_sel == FA4CP_SEL_BACK_HALF) ? single_rows / 2 + sel : sel;
+  } else {
+    row = selected_row(cu, nseq, row_sel, sel);
+  }
+  const int64_t sidx = row * h + head;
+  const float sa = s[sidx];
+  const float sb = so[sidx];
+  if (sb == -INFINITY) return;  // other side contributes nothing; row unchanged
+  T* va = v + sidx * (int64_t)d;
+  const T* vb = vo + sidx * (int64_t)d;
+  if (sa == -INFINITY) {
+    // accumulator side is empty: take the other state verbatim
+    for (int c = lane * 8; c < d; c += kGroup * 8) {
+      float x[8];
+      load8_f32<T>(vb + c, x);
+      store8_f32<T>(va + c, x);
+    }
+    if (lane == 0) s[sidx] = sb;
+    return;
+  }
+  const float m = fmaxf(sa, sb);
+  const float wa = expf(sa - m);
+  const float wb = expf(sb - m);
+  const float inv = 1.0f / (wa + wb);
+  const float ca = wa * inv, cb = wb * inv;
+  for (int c = lane * 8; c < d; c += kGroup * 8) {
+    float x[8], y[8];
+    load8_f32<T>(va + c, x);
+    load8_f32<T>(vb + c, y);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = x[i] * ca + y[i] * cb;
+    store8_f32<T>(va + c, x);
+  }
+  if (lane == 0) s[sidx] = m + logf(wa + wb);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void merge_states_kernel(
+    const T* __restrict__ v, const float* __restrict__ s, T* __restrict__ vout,
+    float* __restrict__ sout, int64_t n_groups, int num_states, int h, int d) {
+  const int64_t g = (int64_t)blockIdx.x * (kBlock / kGroup) + (threadIdx.x / kGroup);
+  const int lane = threadIdx.x % kGroup;
+  if (g >= n_groups) return;
+  const int64_t row = g / h;
+  const int head = (int)(g - row * h);
+  const float* srow = s + row * (int64_t)num_states * h + head;
+  float m = -INFINITY;
+  for (int st = 0; st < num_states; ++st) m = fmaxf(m, srow[(int64_t)st * h]);
+  T* vo = vout + (row * h + head) * (int64_t)d;
+  if (m == -INFINITY) {
+    float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int c = lane * 8; c < d; c += kGroup * 8) store8_f32<T>(vo + c, z);
+    if (lane == 0 && sout != nullptr) sout[row * h + head] = -INFINITY;
+    return;
+  }
+  float wsum = 0.f;
+  for (int st = 0; st < num_states; ++st) {
+    const float ss = srow[(int64_t)st * h];
+    if (ss != -INFINITY) wsum += expf(ss - m);
+  }
+  const float inv = 1.0f / wsum;
+  for (int c = lane * 8; c < d; c += kGroup * 8) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int st = 0; st < num_states; ++st) {
+      const float ss = srow[(int64_t)st * h];
+      if (ss == -INFINITY) continue;
+      const float w = expf(ss - m) * inv;
+      float x[8];
+      load8_f32<T>(v + ((row * num_states + st) * h + head) * (int64_t)d + c, x);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += w * x[i];
+    }
+    store8_f32<T>(vo + c, acc);
+  }
+  if (lane == 0 && sout != nullptr) sout[row * h + head] = m + logf(wsum);
+}
+
+}  // namespace
+}  // namespace fa4cp
+
+using namespace fa4cp;
+
+extern "C" int fa4cp_merge_state_inplace(void* v, float* s, const void* v_other,
+                                         const float* s_other, int64_t rows, int32_t h,
+                                         int32_t d, int32_t dtype, const int32_t* cu,
+                                         int32_t nseq, int32_t row_sel, void* stream) {
+  clear_error();
+  if (!v || !s || !v_other || !s_other)
+    return set_error(FA4CP_EINVAL, "merge_state_inplace: null pointer");
+  if (rows < 0 || h <= 0 || d <= 0 || (d % 8) != 0)
+    return set_error(FA4CP_EINVAL, "merge_state_inplace: bad shape rows=%lld h=%d d=%d "
+                     "(d must be a positive multiple of 8)", (long long)rows, h, d);
+  if (row_sel != FA4CP_SEL_ALL && row_sel != FA4CP_SEL_FRONT_HALF &&
+      row_sel != FA4CP_SEL_BACK_HALF)
+    return set_error(FA4CP_EINVAL, "merge_state_inplace: bad row_sel %d", row_sel);
+  if (cu != nullptr && nseq <= 0)
+    return set_error(FA4CP_EINVAL, "merge_state_inplace: nseq must be >= 1 with cu");
+  if (row_sel != FA4CP_SEL_ALL && cu == nullptr && (rows % 2) != 0)
+    return set_error(FA4CP_EINVAL, "merge_state_inplace: half selection needs even rows");
+  const int64_t sel_rows = (row_sel == FA4CP_SEL_ALL) ? rows : rows / 2;
+  const int64_t n_groups = sel_rows * h;
+  if (n_groups == 0) return FA4CP_OK;
+  const int64_t blocks = (n_groups + (kBlock / kGroup) - 1) / (kBlock / kGroup);
+  if (blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "merge_state_inplace: too many rows");
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case FA4CP_BF16:
+      hipLaunchKernelGGL(merge_inplace_kernel<__bf16>, dim3((unsigned)blocks), dim3(kBlock), 0, st,
+                         (__bf16*)v, s, (const __bf16*)v_other, s_other, n_groups, h, d, cu, nseq,
+                         row_sel, rows);
+      break;
+    case FA4CP_FP16:
+      hipLaunchKernelGGL(merge_inplace_kernel<_Float16>, dim3((unsigned)blocks), dim3(kBlock), 0,
+                         st, (_Float16*)v, s, (const _Float16*)v_other, s_other, n_groups, h, d,
+                         cu, nseq, row_sel, rows);
+      break;
+    case FA4CP_FP32:
+      hipLaunchKernelGGL(merge_inplace_kernel<float>, dim3((unsigned)blocks), dim3(kBlock), 0, st,
+                         (float*)v, s, (const float*)v_other, s_other, n_groups, h, d, cu, nseq,
+                         row_sel, rows);
+      break;
+    default:
+      return set_error(FA4CP_EUNSUPPORTED, "merge_state_inplace: unsupported dtype %d", dtype);
+  }
+  return check_launch("merge_state_inplace");
+}
+
+extern "C" int fa4cp_merge_states(const void* v, const float* s, void* v_out, float* s_out,
+                                  int64_t rows, int32_t num_states, int32_t h, int32_t d,
+                                  int32_t dtype, void* stream) {
+  clear_error();
+  if (!v || !s || !v_out) return set_error(FA4CP_EINVAL, "merge_states: null pointer");
+  if (rows < 0 || num_states <= 0 || h <= 0 || d <= 0 || (d % 8) != 0)
+    return set_error(FA4CP_EINVAL, "merge_states: bad shape rows=%lld states=%d h=%d d=%d",
+                     (long long)rows, num_states, h, d);
+  const int64_t n_groups = rows * h;
+  if (n_groups == 0) return FA4CP_OK;
+  const int64_t blocks = (n_groups + (kBlock / kGroup) - 1) / (kBlock / kGroup);
+  if (blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "merge_states: too many rows");
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case FA4CP_BF16:
+      hipLaunchKernelGGL(merge_states_kernel<__bf16>, dim3((unsigned)blocks), dim3(kBlock), 0, st,
+                         (const __bf16*)v, s, (__bf16*)v_out, s_out, n_groups, num_states, h, d);
+      break;
+    case FA4CP_FP16:
+      hipLaunchKernelGGL(merge_states_kernel<_Float16>, dim3((unsigned)blocks), dim3(kBlock), 0,
+                         st, (const _Float16*)v, s, (_Float16*)v_out, s_out, n_groups, num_states,
+                         h, d);
+      break;
+    case FA4CP_FP32:
+      hipLaunchKernelGGL(merge_states_kernel<float>, dim3((unsigned)blocks), dim3(kBlock), 0, st,
+                         (const float*)v, s, (float*)v_out, s_out, n_groups, num_states, h, d);
+      break;
+    default:
+      return set_error(FA4CP_EUNSUPPORTED, "merge_states: unsupported dtype %d", dtype);
+  }
+  return check_launch("merge_states");
+}

@@ -1,0 +1,28 @@
+"""fa4_ring on MI355X: one rank's causal zig-zag ring attention on gfx950 HIP kernels.
+
+Public API (the reference package's names):
+    RingConfig          configuration (cp_size, cp_rank, merge_mode, ...)
+    ring_flash_attn     causal ring attention over a zig-zag local shard
+    Descales            FP8 per-tensor descales (k / v indexed by source rank)
+    zigzag_shard / zigzag_unshard   shard a full sequence / stitch shards back
+    IncrementalMerger / BatchedMerger / make_merger   online-softmax mergers
+and, for the single-GPU ring:
+    LocalKVRing         every source rank's KV shard resident in HBM
+"""
+
+from .config import RingConfig
+from .merge import BatchedMerger, IncrementalMerger, make_merger
+from .ring_attention import Descales, LocalKVRing, ring_flash_attn
+from .zigzag import zigzag_shard, zigzag_unshard
+
+__all__ = [
+    "RingConfig",
+    "ring_flash_attn",
+    "Descales",
+    "LocalKVRing",
+    "zigzag_shard",
+    "zigzag_unshard",
+    "IncrementalMerger",
+    "BatchedMerger",
+    "make_merger",
+]

@@ -1,0 +1,177 @@
+"""Per-chunk attention forward on the gfx950 HIP kernel (operator level of the ring).
+
+Keeps the interface of fa4_ring/fa4_backend.py:58-123 (``fa4_attn`` returning out and a
+natural-log LSE laid out [T_q, H]) so the module drops in where the reference called
+FlashAttention-4's ``_flash_attn_fwd``; the computation is ``fa4cp_attn_fwd`` of
+libfa4cp.so, launched on torch's current stream without any host synchronisation.
+
+Beyond the reference signature, ``q_sel`` / ``k_sel`` select the back half of every
+query sequence or the front half of every key sequence inside the kernel (the two
+non-local zig-zag step patterns, fa4_ring/ring_attention.py:139-165, without the
+index_select gathers), and ``out`` / ``lse`` accept preallocated (possibly strided)
+destinations, such as one slot of a batched-merge buffer.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF
+
+SUPPORTED_HEAD_DIMS = {torch.bfloat16: (64, 128, 256), torch.float16: (64, 128, 256),
+                       torch.float8_e4m3fn: (128, 256)}
+
+
+def has_fa4() -> bool:
+    """True when the HIP attention library is built and loadable (the reference's
+    ``has_fa4`` probes the FlashAttention-4 import, fa4_backend.py:41-42)."""
+    return _lib.available()
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise AssertionError(msg)
+
+
+def _norm_descale(d: Optional[torch.Tensor], h_kv: int, device) -> Optional[torch.Tensor]:
+    """Descale -> float32 contiguous [h_kv] on `device` (a scalar broadcasts to every kv
+    head, [h_kv] and (1, h_kv) are taken as is; fa4_backend.py:45-55)."""
+    if d is None:
+        return None
+    if not torch.is_tensor(d):
+        d = torch.tensor(float(d))
+    d = d.to(device=device, dtype=torch.float32)
+    if d.dim() == 0:
+        d = d.reshape(1).expand(h_kv)
+    elif d.dim() == 2:
+        _require(d.shape[0] == 1, f"descale batch dimension must be 1, got {tuple(d.shape)}")
+        d = d[0]
+    _require(d.dim() == 1 and d.shape[0] == h_kv,
+             f"descale must be a scalar, [H_kv] or (1, H_kv) with H_kv={h_kv}, got {tuple(d.shape)}")
+    return d.contiguous()
+
+
+def _cu_ok(cu: torch.Tensor, device, name: str) -> None:
+    _require(cu.dtype == torch.int32, f"{name} must be int32, got {cu.dtype}")
+    _require(cu.device == device, f"{name} must live on {device}, got {cu.device}")
+    _require(cu.dim() == 1 and cu.shape[0] >= 2, f"{name} must be [num_seq + 1]")
+    _require(cu.is_contiguous(), f"{name} must be contiguous")
+
+
+def out_dtype_for(dt: torch.dtype) -> torch.dtype:
+    """FP8 inputs produce a bf16 output, other inputs their own type."""
+    return torch.bfloat16 if dt == torch.float8_e4m3fn else dt
+
+
+def fa4_attn(
+    q: torch.Tensor,  # [T_q, H, D]
+    k: torch.Tensor,  # [T_k, H_kv, D]
+    v: torch.Tensor,  # [T_k, H_kv, D]
+    *,
+    causal: bool,
+    softmax_scale: Optional[float] = None,
+    cu_seqlens_q: Optional[torch.Tensor] = None,
+    cu_seqlens_k: Optional[torch.Tensor] = None,
+    max_seqlen_q: Optional[int] = None,
+    max_seqlen_k: Optional[int] = None,
+    q_descale: Optional[torch.Tensor] = None,
+    k_descale: Optional[torch.Tensor] = None,
+    v_descale: Optional[torch.Tensor] = None,
+    q_sel: int = SEL_ALL,
+    k_sel: int = SEL_ALL,
+    out: Optional[torch.Tensor] = None,
+    lse: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Varlen flash-attention forward.
+
+    Returns ``out [T_q, H, D]`` (bf16 for e4m3 inputs, else the input type) and
+    ``lse [T_q, H]`` float32 natural log.  ``cu_seqlens_q/k`` (int32 [num_seq+1], on the
+    device) with ``max_seqlen_q/k`` describe packed sequences; omitted, each side is one
+    sequence.  Causal masking is bottom-right aligned per sequence.  With
+    ``q_sel=SEL_BACK_HALF`` only the back half of each query sequence is computed and
+    written (at its own rows of ``out`` / ``lse``); with ``k_sel=SEL_FRONT_HALF`` only
+    the front half of each key sequence is attended."""
+    lib = _lib.load()
+    _require(q.dim() == 3 and k.dim() == 3 and v.dim() == 3, "q, k, v must be [T, H, D]")
+    _require(q.is_cuda, "fa4_attn runs on the GPU: q must be a device tensor")
+    dev = q.device
+    _require(k.device == dev and v.device == dev, "q, k, v must share a device")
+    _require(q.dtype == k.dtype == v.dtype, f"q/k/v dtypes differ: {q.dtype} {k.dtype} {v.dtype}")
+    dt = q.dtype
+    _require(dt in SUPPORTED_HEAD_DIMS, f"unsupported dtype {dt}")
+    t_q, h_q, d = q.shape
+    t_k, h_kv, dk = k.shape
+    _require(v.shape == k.shape, f"k {tuple(k.shape)} and v {tuple(v.shape)} must match")
+    _require(dk == d, f"q head dim {d} != k head dim {dk}")
+    _require(d in SUPPORTED_HEAD_DIMS[dt], f"head dim {d} not supported for {dt} "
+             f"(supported: {SUPPORTED_HEAD_DIMS[dt]})")
+    _require(h_q % h_kv == 0, f"H_q={h_q} not a multiple of H_kv={h_kv}")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _require(t.stride(2) == 1, f"{name} must be contiguous in the head dim")
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(d)
+
+    if (cu_seqlens_q is None) != (cu_seqlens_k is None):
+        # one side packed, the other a single sequence: describe the latter explicitly
+        if cu_seqlens_q is None:
+            cu_seqlens_q = torch.tensor([0, t_q], dtype=torch.int32, device=dev)
+            max_seqlen_q = t_q
+        else:
+            cu_seqlens_k = torch.tensor([0, t_k], dtype=torch.int32, device=dev)
+            max_seqlen_k = t_k
+    nseq = 1
+    if cu_seqlens_q is not None:
+        _cu_ok(cu_seqlens_q, dev, "cu_seqlens_q")
+        _cu_ok(cu_seqlens_k, dev, "cu_seqlens_k")
+        _require(cu_seqlens_q.shape == cu_seqlens_k.shape,
+                 "cu_seqlens_q and cu_seqlens_k must describe the same number of sequences")
+        _require(max_seqlen_q is not None and max_seqlen_k is not None,
+                 "max_seqlen_q/k required when cu_seqlens are given")
+        nseq = cu_seqlens_q.shape[0] - 1
+    else:
+        max_seqlen_q, max_seqlen_k = t_q, t_k
+
+    odt = out_dtype_for(dt)
+    if out is None:
+        out = torch.empty((t_q, h_q, d), dtype=odt, device=dev)
+    if lse is None:
+        lse = torch.empty((t_q, h_q), dtype=torch.float32, device=dev)
+    _require(out.shape == (t_q, h_q, d) and out.dtype == odt and out.device == dev,
+             f"out must be [{t_q}, {h_q}, {d}] {odt}")
+    _require(out.stride(2) == 1, "out must be contiguous in the head dim")
+    _require(lse.shape == (t_q, h_q) and lse.dtype == torch.float32 and lse.stride(1) == 1,
+             "lse must be [T_q, H] float32 with unit head stride")
+
+    qd = _norm_descale(q_descale, h_kv, dev)
+    kd = _norm_descale(k_descale, h_kv, dev)
+    vd = _norm_descale(v_descale, h_kv, dev)
+
+    a = _lib.AttnArgs()
+    a.q, a.k, a.v, a.out, a.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr()
+    a.q_row_stride, a.q_head_stride = q.stride(0), q.stride(1)
+    a.k_row_stride, a.k_head_stride = k.stride(0), k.stride(1)
+    a.v_row_stride, a.v_head_stride = v.stride(0), v.stride(1)
+    a.o_row_stride, a.o_head_stride = out.stride(0), out.stride(1)
+    a.lse_row_stride = lse.stride(0)
+    a.cu_q = _lib.ptr(cu_seqlens_q)
+    a.cu_k = _lib.ptr(cu_seqlens_k)
+    a.nseq = nseq
+    a.max_seqlen_q, a.max_seqlen_k = int(max_seqlen_q), int(max_seqlen_k)
+    a.total_q, a.total_k = t_q, t_k
+    a.h_q, a.h_kv, a.d = h_q, h_kv, d
+    a.dtype = _lib.dtype_code(dt)
+    a.causal = 1 if causal else 0
+    a.q_sel, a.k_sel = int(q_sel), int(k_sel)
+    a.softmax_scale = float(softmax_scale)
+    a.q_descale, a.k_descale, a.v_descale = _lib.ptr(qd), _lib.ptr(kd), _lib.ptr(vd)
+    rc = lib.fa4cp_attn_fwd(ctypes.byref(a), _lib.stream_handle(dev))
+    _lib.check(rc, "fa4cp_attn_fwd")
+    return out, lse
+
+
+__all__ = ["fa4_attn", "has_fa4", "out_dtype_for", "SEL_ALL", "SEL_BACK_HALF", "SEL_FRONT_HALF"]

@@ -1,0 +1,165 @@
+"""Causal zig-zag ring attention for one rank (interface of fa4_ring/ring_attention.py:43-174).
+
+A rank holds its local zig-zag shard ``[first_half (early) | second_half (late)]`` of Q, K
+and V and walks ``cp_size`` steps; at step ``s`` it attends to the KV of source rank
+``src = (rank - s) % cp_size``:
+
+  * step 0 (src == rank):  causal attention over the local 2h tokens;
+  * step s <= rank:        the source's KV is earlier, so all local Q attend only the
+                           source's front (early) half;
+  * step s > rank:         the source's KV is later, so only the local back (late) half of
+                           Q attends, to all of it.
+
+Each step's (out, LSE) partial is merged with the online-softmax merge, incrementally or
+all at once at the end.
+
+On MI355X the multi-GPU KV rotation (NCCL point-to-point in the reference) is replaced by
+``LocalKVRing``: one GPU holds every source rank's KV shard in HBM and the sweep indexes
+them by source rank.  Step ``s`` uses source ``(rank - s) % cp_size`` with that source's
+descales, as the reference's CPU algorithm does (tests/test_algorithm_cpu.py:75-88).
+
+No host synchronisation happens inside the sweep: the half selections are done inside the
+attention kernel (no index_select gathers, no zero / -inf padding of the late-Q partial),
+and every launch goes to torch's current stream.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import List, Optional, Sequence, Tuple
+
+import torch
+
+from .config import RingConfig
+from .fa4_backend import SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, fa4_attn, out_dtype_for
+from .merge import merge_state_in_place, merge_states
+from .zigzag import zigzag_shard, zigzag_shard_varlen
+
+
+@dataclass
+class Descales:
+    """FP8 descales.  ``k`` / ``v`` are indexed by the SOURCE rank whose KV is attended;
+    each entry is a float32 scalar, [H_kv] or (1, H_kv) tensor."""
+
+    q: Optional[torch.Tensor] = None
+    k: Optional[List[torch.Tensor]] = None
+    v: Optional[List[torch.Tensor]] = None
+
+
+class LocalKVRing:
+    """The ring's KV source on one GPU: the (k, v) zig-zag shard of every source rank,
+    resident in HBM and indexed by rank.  Pass it as ``group=`` to ring_flash_attn."""
+
+    def __init__(self, k_shards: Sequence[torch.Tensor], v_shards: Sequence[torch.Tensor]):
+        assert len(k_shards) == len(v_shards) and len(k_shards) >= 1
+        for k, v in zip(k_shards, v_shards):
+            assert k.shape == v.shape == k_shards[0].shape, "every shard must have one shape"
+            assert k.dtype == v.dtype == k_shards[0].dtype
+        self.k = list(k_shards)
+        self.v = list(v_shards)
+
+    @property
+    def cp_size(self) -> int:
+        return len(self.k)
+
+    def kv(self, src: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        return self.k[src], self.v[src]
+
+    @classmethod
+    def from_full(cls, k: torch.Tensor, v: torch.Tensor, cp_size: int, full_cu_seqlens=None):
+        """Shards full-sequence K and V for every rank with the zig-zag gather kernel."""
+        if full_cu_seqlens is None:
+            ks = [zigzag_shard(k, r, cp_size) for r in range(cp_size)]
+            vs = [zigzag_shard(v, r, cp_size) for r in range(cp_size)]
+        else:
+            ks = [zigzag_shard_varlen(k, full_cu_seqlens, r, cp_size)[0] for r in range(cp_size)]
+            vs = [zigzag_shard_varlen(v, full_cu_seqlens, r, cp_size)[0] for r in range(cp_size)]
+        return cls(ks, vs)
+
+
+def ring_flash_attn(
+    local_q: torch.Tensor,  # [T, H, D] zig-zag local shard (T = sum of 2*h_j)
+    local_k: torch.Tensor,  # [T, H_kv, D]
+    local_v: torch.Tensor,  # [T, H_kv, D]
+    cfg: RingConfig,
+    *,
+    group: Optional[LocalKVRing] = None,
+    descales: Optional[Descales] = None,
+    cu_seqlens: Optional[torch.Tensor] = None,  # local int32 [num_seq+1]; None -> one sequence
+    max_seqlen: Optional[int] = None,
+) -> torch.Tensor:
+    """This rank's local causal ring-attention output ``[T, H, D]``.
+
+    One sequence per rank: leave ``cu_seqlens=None``.  Packed sequences: pass the LOCAL
+    ``cu_seqlens`` (each entry a zig-zag ``2*h_j`` shard length) on the device and
+    ``max_seqlen``.  For cp_size > 1 ``group`` must be a LocalKVRing holding every source
+    rank's KV shard (this build does not move KV between GPUs)."""
+    S = cfg.cp_size
+    rank = cfg.cp_rank
+    scale = cfg.softmax_scale
+    total = local_q.shape[0]
+    if cu_seqlens is not None:
+        assert max_seqlen is not None, "max_seqlen required when cu_seqlens is given"
+    else:
+        max_seqlen = total
+    if S > 1:
+        if not isinstance(group, LocalKVRing):
+            raise RuntimeError(
+                "ring_flash_attn: cp_size > 1 needs group=LocalKVRing(k_shards, v_shards); "
+                "KV rotation between GPUs is not part of this single-GPU build")
+        assert group.cp_size == S, f"LocalKVRing holds {group.cp_size} shards, cp_size is {S}"
+
+    qd = descales.q if descales else None
+
+    def kd(src):
+        return descales.k[src] if (descales and descales.k) else None
+
+    def vd(src):
+        return descales.v[src] if (descales and descales.v) else None
+
+    h_q, d = local_q.shape[1], local_q.shape[2]
+    odt = out_dtype_for(local_q.dtype)
+    dev = local_q.device
+    common = dict(softmax_scale=scale, cu_seqlens_q=cu_seqlens, cu_seqlens_k=cu_seqlens,
+                  max_seqlen_q=max_seqlen, max_seqlen_k=max_seqlen, q_descale=qd)
+
+    if cfg.merge_mode == "batched" and S > 1:
+        # every step writes its partial straight into slot `step` of the merge buffer
+        vbuf = torch.empty((total, S, h_q, d), dtype=odt, device=dev)
+        sbuf = torch.empty((total, S, h_q), dtype=torch.float32, device=dev)
+        fa4_attn(local_q, local_k, local_v, causal=True, k_descale=kd(rank), v_descale=vd(rank),
+                 out=vbuf[:, 0], lse=sbuf[:, 0], **common)
+        for step in range(1, S):
+            src = (rank - step) % S
+            k, v = group.kv(src)
+            if step <= rank:
+                fa4_attn(local_q, k, v, causal=False, k_sel=SEL_FRONT_HALF, k_descale=kd(src),
+                         v_descale=vd(src), out=vbuf[:, step], lse=sbuf[:, step], **common)
+            else:
+                # front rows of this slot stay empty: -inf LSE makes them the identity
+                sbuf[:, step].fill_(float("-inf"))
+                fa4_attn(local_q, k, v, causal=False, q_sel=SEL_BACK_HALF, k_descale=kd(src),
+                         v_descale=vd(src), out=vbuf[:, step], lse=sbuf[:, step], **common)
+        out, _ = merge_states(vbuf, sbuf)
+        return out
+
+    # incremental (and cp_size == 1): step 0 seeds the accumulator with every row finite
+    acc, acc_lse = fa4_attn(local_q, local_k, local_v, causal=True, k_descale=kd(rank),
+                            v_descale=vd(rank), **common)
+    if S == 1:
+        return acc
+    part = torch.empty_like(acc)
+    part_lse = torch.empty_like(acc_lse)
+    for step in range(1, S):
+        src = (rank - step) % S
+        k, v = group.kv(src)
+        if step <= rank:
+            fa4_attn(local_q, k, v, causal=False, k_sel=SEL_FRONT_HALF, k_descale=kd(src),
+                     v_descale=vd(src), out=part, lse=part_lse, **common)
+            merge_state_in_place(acc, acc_lse, part, part_lse)
+        else:
+            fa4_attn(local_q, k, v, causal=False, q_sel=SEL_BACK_HALF, k_descale=kd(src),
+                     v_descale=vd(src), out=part, lse=part_lse, **common)
+            merge_state_in_place(acc, acc_lse, part, part_lse, cu_seqlens=cu_seqlens,
+                                 row_sel=SEL_BACK_HALF)
+    return acc

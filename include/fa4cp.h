@@ -1,0 +1,156 @@
+/*
+ * fa4cp.h -- C ABI of the MI355X (gfx950) per-rank zig-zag ring-attention compute path.
+ *
+ * One shared library (libfa4cp.so) exports these entry points.  Conventions shared by all:
+ *   - every pointer argument is a DEVICE pointer owned by the caller, unless the comment
+ *     says "host";
+ *   - nothing here allocates device memory, and nothing synchronises the host: every
+ *     kernel is launched on the hipStream_t passed as `stream` (NULL = legacy default
+ *     stream) and the call returns as soon as the launch is queued;
+ *   - the return value is 0 on success and a negative FA4CP_E* code otherwise; the
+ *     message for the last failure on the calling thread is in fa4cp_last_error();
+ *   - the library keeps no state besides that thread-local message, so every entry point
+ *     is reentrant.  Two calls that write the same memory on different streams race.
+ *
+ * Reference interfaces replaced (paths are in hxy0118/fa4-cp):
+ *   fa4cp_attn_fwd              <- fa4_ring/fa4_backend.py:58-123 (fa4_attn -> FA4 _flash_attn_fwd)
+ *   fa4cp_merge_state_inplace   <- fa4_ring/merge.py:31-36 (flashinfer.cascade.merge_state_in_place)
+ *   fa4cp_merge_states          <- fa4_ring/merge.py:39-42 (flashinfer.cascade.merge_states)
+ *   fa4cp_zigzag_shard          <- fa4_ring/zigzag.py:31-39 and :82-97 (zigzag_shard, zigzag_shard_varlen)
+ *   fa4cp_zigzag_unshard        <- fa4_ring/zigzag.py:42-50 (zigzag_unshard)
+ */
+#ifndef FA4CP_H_
+#define FA4CP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA4CP_ABI_VERSION 1
+
+/* status codes */
+#define FA4CP_OK 0
+#define FA4CP_EINVAL -1      /* bad argument (null pointer, bad size, inconsistent shape) */
+#define FA4CP_EUNSUPPORTED -2 /* valid but not implemented (head dim, dtype combination) */
+#define FA4CP_ELAUNCH -3     /* the HIP runtime refused the launch */
+
+/* element types */
+#define FA4CP_BF16 0
+#define FA4CP_FP16 1
+#define FA4CP_E4M3 2 /* OCP float8_e4m3fn */
+#define FA4CP_FP32 3
+
+/* per-sequence row selection: which rows of each packed sequence a kernel touches.
+ * Each sequence j occupies rows [cu[j], cu[j+1]) and has even length; its midpoint is
+ * (cu[j] + cu[j+1]) / 2 (fa4_ring/zigzag.py:65-79). */
+#define FA4CP_SEL_ALL 0
+#define FA4CP_SEL_FRONT_HALF 1 /* rows [cu[j], mid_j): the early zig-zag chunk          */
+#define FA4CP_SEL_BACK_HALF 2  /* rows [mid_j, cu[j+1]): the late zig-zag chunk         */
+
+/*
+ * Flash-attention forward over packed variable-length sequences:
+ *     out[i, h, :] = softmax(scale * qd * kd * q[i,h,:] . k[j,g(h),:]^T  (+ mask)) @ v[j,g(h),:] * vd
+ *     lse[i, h]    = natural-log logsumexp of the same scaled scores
+ * with g(h) = h / (h_q / h_kv) (GQA / MQA; fa4_ring/reference.py:20-27).
+ *
+ * Sequence j's queries are the q rows selected by q_sel inside [cu_q[j], cu_q[j+1]) and
+ * its keys are the k/v rows selected by k_sel inside [cu_k[j], cu_k[j+1]).  With
+ * cu_q == NULL (resp. cu_k) there is one sequence of total_q (resp. total_k) rows.
+ * causal != 0 masks key position kk against query position qq (both counted from the
+ * start of the selection) unless kk <= qq + (Lk - Lq), i.e. bottom-right aligned as in
+ * FlashAttention; the ring schedule only uses it with Lq == Lk.  A query with no key left
+ * gets out = 0 and lse = -inf.
+ *
+ * Output rows are addressed like q rows: the result for q row i goes to out row i and
+ * lse row i, so with q_sel = BACK_HALF only the back rows of `out`/`lse` are written.
+ *
+ * dtype is the type of q, k and v: BF16, FP16 or E4M3.  out is bf16 for E4M3 inputs and
+ * the input type otherwise; lse is float32.  Descales (float32 [h_kv], NULL = 1.0) are
+ * the dequantisation multipliers of fa4_ring/fa4_backend.py:45-55, indexed by kv head.
+ * Head dims 64, 128 and 256 are implemented.
+ */
+typedef struct fa4cp_attn_args {
+  const void* q; /* [total_q rows] x h_q heads x d, strides below, in elements */
+  const void* k; /* [total_k rows] x h_kv heads x d */
+  const void* v; /* [total_k rows] x h_kv heads x d */
+  void* out;     /* [total_q rows] x h_q heads x d */
+  float* lse;    /* lse[row * lse_row_stride + head] */
+  int64_t q_row_stride, q_head_stride;
+  int64_t k_row_stride, k_head_stride;
+  int64_t v_row_stride, v_head_stride;
+  int64_t o_row_stride, o_head_stride;
+  int64_t lse_row_stride;
+  const int32_t* cu_q; /* [nseq + 1] or NULL */
+  const int32_t* cu_k; /* [nseq + 1] or NULL */
+  int32_t nseq;
+  int32_t max_seqlen_q; /* upper bound of cu_q[j+1]-cu_q[j] (before q_sel halves it) */
+  int32_t max_seqlen_k;
+  int32_t total_q, total_k;
+  int32_t h_q, h_kv, d;
+  int32_t dtype;
+  int32_t causal;
+  int32_t q_sel, k_sel; /* FA4CP_SEL_ALL, or BACK_HALF for q / FRONT_HALF for k */
+  float softmax_scale;
+  const float* q_descale; /* [h_kv] or NULL */
+  const float* k_descale; /* [h_kv] or NULL */
+  const float* v_descale; /* [h_kv] or NULL */
+} fa4cp_attn_args;
+
+int fa4cp_attn_fwd(const fa4cp_attn_args* args, void* stream);
+
+/*
+ * In-place online-softmax merge (flashinfer.cascade.merge_state_in_place semantics, natural
+ * log LSE):
+ *     m = max(s, s_o);  w = e^(s-m);  w_o = e^(s_o-m)
+ *     v <- (v*w + v_o*w_o) / (w + w_o);   s <- m + log(w + w_o)
+ * A side whose s is -inf contributes nothing (its v is not read).  v, v_other: [rows, h, d]
+ * contiguous in dtype (BF16, FP16 or FP32); s, s_other: [rows, h] float32.  Math is fp32.
+ * row_sel = SEL_ALL merges every row; BACK_HALF / FRONT_HALF merge only those rows of each
+ * sequence of cu[0..nseq] (cu == NULL: one sequence of `rows` rows).
+ */
+int fa4cp_merge_state_inplace(void* v, float* s, const void* v_other, const float* s_other,
+                              int64_t rows, int32_t h, int32_t d, int32_t dtype,
+                              const int32_t* cu, int32_t nseq, int32_t row_sel, void* stream);
+
+/*
+ * Batched merge of num_states partial states (flashinfer.cascade.merge_states semantics):
+ * v [rows, num_states, h, d] (dtype), s [rows, num_states, h] float32 ->
+ * v_out [rows, h, d] (dtype), s_out [rows, h] float32 (s_out may be NULL).
+ * States with s = -inf are skipped; a row where every state is -inf gets v = 0, s = -inf.
+ */
+int fa4cp_merge_states(const void* v, const float* s, void* v_out, float* s_out, int64_t rows,
+                       int32_t num_states, int32_t h, int32_t d, int32_t dtype, void* stream);
+
+/*
+ * Zig-zag shard for one rank: sequence j of the full packed tensor (rows
+ * [full_cu[j], full_cu[j+1]), length N_j divisible by 2*cp_size, h_j = N_j / (2*cp_size))
+ * contributes chunk cp_rank followed by chunk 2*cp_size-1-cp_rank to the local tensor,
+ * which holds 2*h_j rows per sequence starting at local row full_cu[j] / cp_size.
+ * full_cu == NULL: one sequence of total_full rows.  Rows are row_bytes bytes, copied
+ * bit-exactly.  dst holds total_full / cp_size rows.
+ */
+int fa4cp_zigzag_shard(const void* src_full, void* dst_local, int64_t row_bytes,
+                       const int32_t* full_cu, int32_t nseq, int64_t total_full,
+                       int32_t cp_rank, int32_t cp_size, void* stream);
+
+/*
+ * Inverse of fa4cp_zigzag_shard over all ranks: shard_ptrs is a HOST array of cp_size
+ * device pointers (rank r's local tensor); dst_full receives total_full rows.
+ */
+int fa4cp_zigzag_unshard(const void* const* shard_ptrs, void* dst_full, int64_t row_bytes,
+                         const int32_t* full_cu, int32_t nseq, int64_t total_full,
+                         int32_t cp_size, void* stream);
+
+/* Message describing the last failure on this thread ("" if none). */
+const char* fa4cp_last_error(void);
+
+/* FA4CP_ABI_VERSION of the library. */
+int fa4cp_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA4CP_H_ */

@@ -1,0 +1,260 @@
+"""GPU parity of the individual HIP kernels against the CPU oracle, through the C ABI
+(zig-zag gather/scatter bit-exact, merges within 1e-5 in fp32, attention per step pattern)."""
+
+import math
+
+import pytest
+import torch
+
+import fa4_ring
+from fa4_ring import zigzag as Z
+from fa4_ring.fa4_backend import SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, fa4_attn
+from fa4_ring.merge import merge_state_in_place, merge_states
+from gpu_helpers import (DEV, TOL_BF16_OUT, TOL_FP8_OUT, TOL_LSE, TOL_MERGE_FP32, lse_err, max_err,
+                         oracle_attn, rounded, say, scale_for)
+from oracle import ring_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+# ------------------------------------------------------------------------- zig-zag
+
+@pytest.mark.parametrize("shape,dtype", [((96, 3, 8), torch.bfloat16), ((64, 5), torch.uint8),
+                                         ((128, 8, 128), torch.float16), ((48, 7), torch.float32),
+                                         ((256, 2, 64), torch.float8_e4m3fn)])
+@pytest.mark.parametrize("cp", [1, 2, 4, 8])
+def test_zigzag_shard_unshard_bit_exact(shape, dtype, cp):
+    n = shape[0]
+    if n % (2 * cp):
+        pytest.skip("length not shardable")
+    say(f"zigzag shape={shape} dtype={dtype} cp={cp}")
+    g = torch.Generator().manual_seed(cp)
+    x = torch.randint(0, 255, shape, generator=g, dtype=torch.uint8)
+    if dtype != torch.uint8:
+        x = torch.randn(shape, generator=g).to(dtype)
+    xd = x.to(DEV)
+    shards = []
+    for r in range(cp):
+        s = Z.zigzag_shard(xd, r, cp)
+        exp = x[torch.from_numpy(O.zigzag_rows(n, r, cp))]
+        assert torch.equal(s.cpu().view(torch.uint8), exp.contiguous().view(torch.uint8))
+        shards.append(s)
+    back = Z.zigzag_unshard(shards, cp)
+    assert torch.equal(back.cpu().view(torch.uint8), x.view(torch.uint8))
+
+
+@pytest.mark.parametrize("lens,cp", [([16, 32], 2), ([32, 16, 48], 4), ([64, 64], 8),
+                                     ([4856, 9720, 8592, 4864, 1832, 15456, 2784, 1576], 4)])
+def test_zigzag_varlen_bit_exact(lens, cp):
+    say(f"zigzag varlen lens={lens} cp={cp}")
+    full_cu = [0]
+    for n in lens:
+        full_cu.append(full_cu[-1] + n)
+    x = torch.randn(full_cu[-1], 2, 64).to(torch.bfloat16)
+    xd = x.to(DEV)
+    shards = []
+    for r in range(cp):
+        loc, lcu = Z.zigzag_shard_varlen(xd, full_cu, r, cp)
+        exp, ecu = O.zigzag_shard_varlen(x.float(), full_cu, r, cp)
+        assert lcu.cpu().tolist() == ecu
+        assert lcu.dtype == torch.int32
+        assert torch.equal(loc.cpu().float(), exp)
+        shards.append(loc)
+    back = Z.zigzag_unshard_varlen(shards, full_cu, cp)
+    assert torch.equal(back.cpu(), x)
+
+
+# ------------------------------------------------------------------------- merges
+
+_HALF_ULP = {torch.float32: 0.0, torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}
+
+
+def assert_rounded_close(got, exp, dtype, mask=None):
+    """fp32 math within 1e-5, plus one rounding of the result to the storage type."""
+    g, e = got.float().cpu(), exp.float()
+    bound = TOL_MERGE_FP32 + _HALF_ULP[dtype] * e.abs()
+    bad = (g - e).abs() > bound
+    if mask is not None:
+        bad &= mask
+    assert not bad.any(), f"{int(bad.sum())} elements off, max err {max_err(g, e, mask)}"
+
+def _states(t, h, d, seed, dtype, inf_frac=0.0):
+    g = torch.Generator().manual_seed(seed)
+    v = torch.randn(t, h, d, generator=g)
+    s = torch.randn(t, h, generator=g) * 4
+    if inf_frac:
+        s[torch.rand(t, h, generator=g) < inf_frac] = float("-inf")
+    return rounded(v, dtype), s
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("t,h,d", [(37, 3, 64), (256, 8, 128), (100, 2, 256), (8, 1, 8)])
+def test_merge_state_in_place(dtype, t, h, d):
+    say(f"merge_state_in_place dtype={dtype} t={t} h={h} d={d}")
+    va, sa = _states(t, h, d, 1, dtype, inf_frac=0.1)
+    vb, sb = _states(t, h, d, 2, dtype, inf_frac=0.1)
+    both = torch.isinf(sa) & torch.isinf(sb)
+    vd, sd = va.to(dtype).to(DEV), sa.to(DEV)
+    merge_state_in_place(vd, sd, vb.to(dtype).to(DEV), sb.to(DEV))
+    eo, el = O.merge(va, sa, vb, sb)
+    ok = ~both
+    assert_rounded_close(vd, eo, dtype, ok.unsqueeze(-1).expand_as(eo))
+    assert lse_err(sd.cpu()[ok], el[ok]) <= TOL_MERGE_FP32
+    # rows where both sides are empty keep the accumulator untouched (documented; the
+    # reference's merge would produce NaN there)
+    assert torch.equal(sd.cpu()[both], sa[both])
+
+
+@pytest.mark.parametrize("cu", [None, [0, 8, 20, 64]])
+@pytest.mark.parametrize("sel", [SEL_BACK_HALF, SEL_FRONT_HALF])
+def test_merge_state_in_place_half_rows(cu, sel):
+    say(f"merge half rows cu={cu} sel={sel}")
+    t, h, d = 64, 4, 128
+    va, sa = _states(t, h, d, 3, torch.float32)
+    vb, sb = _states(t, h, d, 4, torch.float32)
+    vd, sd = va.to(DEV), sa.to(DEV)
+    cud = None if cu is None else torch.tensor(cu, dtype=torch.int32, device=DEV)
+    merge_state_in_place(vd, sd, vb.to(DEV), sb.to(DEV), cu_seqlens=cud, row_sel=sel)
+    rows = O.get_half_index(cu if cu is not None else [0, t], front=(sel == SEL_FRONT_HALF))
+    eo, el = va.clone(), sa.clone()
+    mo, ml = O.merge(va[rows], sa[rows], vb[rows], sb[rows])
+    eo[rows], el[rows] = mo, ml
+    assert max_err(vd, eo) <= TOL_MERGE_FP32
+    assert lse_err(sd, el) <= TOL_MERGE_FP32
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("t,ns,h,d", [(50, 8, 4, 128), (17, 3, 2, 64), (64, 1, 1, 256)])
+def test_merge_states(dtype, t, ns, h, d):
+    say(f"merge_states dtype={dtype} t={t} S={ns} h={h} d={d}")
+    g = torch.Generator().manual_seed(ns)
+    v = rounded(torch.randn(t, ns, h, d, generator=g), dtype)
+    s = torch.randn(t, ns, h, generator=g) * 3
+    s[torch.rand(t, ns, h, generator=g) < 0.2] = float("-inf")
+    s[0] = float("-inf")  # one row with every state empty
+    vd = v.clone()
+    vd[torch.isinf(s)] = float("nan")  # never read when its LSE is -inf
+    out, so = merge_states(vd.to(dtype).to(DEV), s.to(DEV))
+    eo, el = O.merge_states(v, s)
+    assert_rounded_close(out, eo, dtype)
+    assert lse_err(so, el) <= TOL_MERGE_FP32
+
+
+# ------------------------------------------------------------------------- attention
+
+def _qkv(tq, tk, h, hkv, d, seed, dtype):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(tq, h, d, generator=g)
+    k = torch.randn(tk, hkv, d, generator=g)
+    v = torch.randn(tk, hkv, d, generator=g)
+    return rounded(q, dtype), rounded(k, dtype), rounded(v, dtype)
+
+
+ATTN_CASES = [
+    # tq, tk, h, hkv, d, causal, q_sel, k_sel, cu
+    (256, 256, 4, 1, 128, True, SEL_ALL, SEL_ALL, None),
+    (200, 200, 8, 2, 128, True, SEL_ALL, SEL_ALL, None),         # tail rows/keys
+    (512, 256, 8, 8, 128, False, SEL_ALL, SEL_ALL, None),        # plain non-causal
+    (512, 512, 8, 2, 128, False, SEL_ALL, SEL_FRONT_HALF, None),  # step s <= rank
+    (512, 512, 8, 2, 128, False, SEL_BACK_HALF, SEL_ALL, None),   # step s > rank
+    (300, 300, 6, 3, 64, True, SEL_ALL, SEL_ALL, None),
+    (130, 130, 2, 2, 256, True, SEL_ALL, SEL_ALL, None),
+    (160, 160, 16, 2, 256, False, SEL_BACK_HALF, SEL_ALL, None),
+    (192, 192, 8, 1, 64, False, SEL_ALL, SEL_FRONT_HALF, None),
+    (None, None, 8, 2, 128, True, SEL_ALL, SEL_ALL, [0, 64, 200, 202, 460]),
+    (None, None, 8, 2, 128, False, SEL_ALL, SEL_FRONT_HALF, [0, 64, 200, 202, 460]),
+    (None, None, 4, 4, 128, False, SEL_BACK_HALF, SEL_ALL, [0, 96, 100, 612]),
+    (64, 96, 4, 2, 128, True, SEL_ALL, SEL_ALL, None),            # bottom-right causal
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", ATTN_CASES)
+def test_attention_16bit(dtype, case):
+    tq, tk, h, hkv, d, causal, q_sel, k_sel, cu = case
+    if cu is not None:
+        tq = tk = cu[-1]
+    say(f"attn {dtype} tq={tq} tk={tk} h={h}/{hkv} d={d} causal={causal} sel={q_sel},{k_sel} cu={cu}")
+    q, k, v = _qkv(tq, tk, h, hkv, d, 7, dtype)
+    scale = scale_for(d)
+    cud = None if cu is None else torch.tensor(cu, dtype=torch.int32, device=DEV)
+    mx = None if cu is None else max(b - a for a, b in zip(cu[:-1], cu[1:]))
+    out = torch.full((tq, h, d), float("nan"), dtype=dtype, device=DEV)
+    lse = torch.full((tq, h), float("nan"), device=DEV)
+    fa4_attn(q.to(dtype).to(DEV), k.to(dtype).to(DEV), v.to(dtype).to(DEV), causal=causal,
+             softmax_scale=scale, cu_seqlens_q=cud, cu_seqlens_k=cud, max_seqlen_q=mx,
+             max_seqlen_k=mx, q_sel=q_sel, k_sel=k_sel, out=out, lse=lse)
+    eo, el = oracle_attn(q, k, v, causal, scale, cu, cu, q_sel, k_sel)
+    sel = ~torch.isnan(el)
+    # rows outside the selection are left untouched
+    assert torch.isnan(out.cpu().float()[~sel]).all() and torch.isnan(lse.cpu()[~sel]).all()
+    assert max_err(out, eo, sel.unsqueeze(-1).expand_as(eo)) <= TOL_BF16_OUT
+    assert lse_err(lse.cpu()[sel], el[sel]) <= TOL_LSE
+
+
+def test_attention_default_layout_and_gqa_strided_views():
+    """Reference calling convention: no cu_seqlens, default scale, fresh outputs; q given
+    as a strided view of a larger buffer."""
+    say("attn strided views")
+    q, k, v = _qkv(256, 256, 8, 2, 128, 9, torch.bfloat16)
+    big = torch.zeros(256, 12, 128, dtype=torch.bfloat16)
+    big[:, 2:10] = q.to(torch.bfloat16)
+    qd = big.to(DEV)[:, 2:10]
+    out, lse = fa4_attn(qd, k.to(torch.bfloat16).to(DEV), v.to(torch.bfloat16).to(DEV), causal=True)
+    eo, el = O.cpu_attn(q, k, v, True, 1 / math.sqrt(128))
+    assert out.shape == (256, 8, 128) and lse.shape == (256, 8) and lse.dtype == torch.float32
+    assert max_err(out, eo) <= TOL_BF16_OUT and lse_err(lse, el) <= TOL_LSE
+
+
+FP8_CASES = [
+    (512, 512, 8, 2, 128, True, SEL_ALL, SEL_ALL, None),
+    (600, 600, 8, 2, 128, True, SEL_ALL, SEL_ALL, None),
+    (512, 512, 8, 2, 128, False, SEL_ALL, SEL_FRONT_HALF, None),
+    (512, 512, 8, 2, 128, False, SEL_BACK_HALF, SEL_ALL, None),
+    (384, 384, 16, 2, 256, True, SEL_ALL, SEL_ALL, None),
+    (384, 384, 16, 2, 256, False, SEL_BACK_HALF, SEL_ALL, None),
+    (None, None, 8, 8, 128, True, SEL_ALL, SEL_ALL, [0, 128, 136, 520]),
+]
+
+
+@pytest.mark.parametrize("case", FP8_CASES)
+def test_attention_e4m3(case):
+    tq, tk, h, hkv, d, causal, q_sel, k_sel, cu = case
+    if cu is not None:
+        tq = tk = cu[-1]
+    say(f"attn e4m3 tq={tq} h={h}/{hkv} d={d} causal={causal} sel={q_sel},{k_sel} cu={cu}")
+    g = torch.Generator().manual_seed(21)
+    qf = torch.randn(tq, h, d, generator=g)
+    kf = torch.randn(tk, hkv, d, generator=g)
+    vf = torch.randn(tk, hkv, d, generator=g)
+    sq, sk, sv = O.amax_scale(qf), O.amax_scale(kf), O.amax_scale(vf)
+    q8, k8, v8 = O.quantize_e4m3(qf, sq), O.quantize_e4m3(kf, sk), O.quantize_e4m3(vf, sv)
+    scale = scale_for(d)
+    cud = None if cu is None else torch.tensor(cu, dtype=torch.int32, device=DEV)
+    mx = None if cu is None else max(b - a for a, b in zip(cu[:-1], cu[1:]))
+    out = torch.full((tq, h, d), float("nan"), dtype=torch.bfloat16, device=DEV)
+    lse = torch.full((tq, h), float("nan"), device=DEV)
+    fa4_attn(q8.to(DEV), k8.to(DEV), v8.to(DEV), causal=causal, softmax_scale=scale,
+             cu_seqlens_q=cud, cu_seqlens_k=cud, max_seqlen_q=mx, max_seqlen_k=mx,
+             q_descale=torch.tensor(sq, device=DEV), k_descale=torch.tensor([sk] * hkv, device=DEV),
+             v_descale=torch.tensor(sv, device=DEV).reshape(1, 1).expand(1, hkv),
+             q_sel=q_sel, k_sel=k_sel, out=out, lse=lse)
+    eo, el = oracle_attn(O.dequantize_e4m3(q8, sq), O.dequantize_e4m3(k8, sk),
+                         O.dequantize_e4m3(v8, sv), causal, scale, cu, cu, q_sel, k_sel)
+    sel = ~torch.isnan(el)
+    assert max_err(out, eo, sel.unsqueeze(-1).expand_as(eo)) <= TOL_FP8_OUT
+    assert lse_err(lse.cpu()[sel], el[sel]) <= TOL_LSE
+
+
+def test_attention_rejects_unsupported():
+    say("attn rejects")
+    x = torch.zeros(64, 2, 96, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(AssertionError, match="head dim"):
+        fa4_attn(x, x, x, causal=True)
+    y = torch.zeros(64, 2, 64, dtype=torch.float8_e4m3fn, device=DEV)
+    with pytest.raises(AssertionError, match="head dim"):
+        fa4_attn(y, y, y, causal=True)
+    z = torch.zeros(64, 3, 128, dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros(64, 2, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(AssertionError, match="multiple"):
+        fa4_attn(z, w, w, causal=True)

@@ -1,0 +1,261 @@
+"""GPU parity of the whole per-rank ring sweep (ring_flash_attn on the HIP kernels).
+
+Small shapes: every rank against the oracle's ring (same rounded inputs) and the stitched
+output against dense causal attention.  Benchmark sizes: one rank's sweep checked on
+sampled rows against exact dense causal attention (a row's ring output must equal plain
+causal attention over every key before it), plus run-to-run bit reproducibility.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from fa4_ring import Descales, LocalKVRing, RingConfig, ring_flash_attn, zigzag_shard
+from fa4_ring.zigzag import zigzag_shard_varlen
+from gpu_helpers import DEV, TOL_BF16_OUT, TOL_FP8_OUT, max_err, rounded, say, scale_for
+from oracle import ring_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+SMALL_CASES = [  # (N, H, H_kv, D, cp): the reference's CPU cases' structure at GPU head dims
+    (256, 4, 4, 64, 2), (512, 8, 2, 128, 4), (1024, 8, 8, 64, 4), (1024, 4, 1, 128, 8),
+    (2048, 8, 2, 128, 8), (768, 6, 3, 64, 2), (1536, 8, 8, 128, 4),
+    (2048, 8, 2, 128, 4),  # the CPU benchmark configuration's shape
+]
+
+
+def _device_ring(q, k, v, cp, dtype):
+    qd, kd, vd = (t.to(dtype).to(DEV) for t in (q, k, v))
+    return qd, LocalKVRing.from_full(kd, vd, cp)
+
+
+@pytest.mark.parametrize("mode", ["incremental", "batched"])
+@pytest.mark.parametrize("n,h,hkv,d,cp", SMALL_CASES)
+def test_ring_all_ranks_small(n, h, hkv, d, cp, mode):
+    say(f"ring bf16 n={n} h={h}/{hkv} d={d} cp={cp} mode={mode}")
+    q, k, v = O.random_qkv(n, h, hkv, d, seed=0)
+    q, k, v = (rounded(t, torch.bfloat16) for t in (q, k, v))
+    scale = scale_for(d)
+    qd, ring = _device_ring(q, k, v, cp, torch.bfloat16)
+    ks = [O.zigzag_shard(k, r, cp) for r in range(cp)]
+    vs = [O.zigzag_shard(v, r, cp) for r in range(cp)]
+    outs = []
+    for rank in range(cp):
+        cfg = RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode)
+        out = ring_flash_attn(zigzag_shard(qd, rank, cp), ring.k[rank], ring.v[rank], cfg, group=ring)
+        assert out.dtype == torch.bfloat16 and out.shape == (n // cp, h, d)
+        ref, _ = O.ring_rank(O.zigzag_shard(q, rank, cp), ks, vs, rank, cp, scale, merge_mode=mode)
+        assert max_err(out, ref) <= TOL_BF16_OUT, f"rank {rank}"
+        outs.append(out.float().cpu())
+    dense = O.dense_causal(q, k, v, scale)
+    assert max_err(O.zigzag_unshard(outs, cp), dense) <= TOL_BF16_OUT
+
+
+def test_ring_cp1_is_causal_attention():
+    say("ring cp=1")
+    q, k, v = O.random_qkv(512, 8, 2, 128, seed=2)
+    q, k, v = (rounded(t, torch.bfloat16) for t in (q, k, v))
+    out = ring_flash_attn(q.to(torch.bfloat16).to(DEV), k.to(torch.bfloat16).to(DEV),
+                          v.to(torch.bfloat16).to(DEV), RingConfig(cp_size=1, cp_rank=0))
+    assert max_err(out, O.dense_causal(q, k, v, scale_for(128))) <= TOL_BF16_OUT
+
+
+@pytest.mark.parametrize("mode", ["incremental", "batched"])
+def test_ring_varlen_all_ranks(mode):
+    lens = [608, 1216, 1072, 608, 232, 1928, 344, 200]  # the packed benchmark lengths / 8
+    cp, h, hkv, d = 4, 8, 2, 128
+    say(f"ring varlen lens={lens} cp={cp} mode={mode}")
+    full_cu = [0]
+    for n in lens:
+        full_cu.append(full_cu[-1] + n)
+    q, k, v = O.random_qkv(full_cu[-1], h, hkv, d, seed=3)
+    q, k, v = (rounded(t, torch.bfloat16) for t in (q, k, v))
+    scale = scale_for(d)
+    qd, kd, vd = (t.to(torch.bfloat16).to(DEV) for t in (q, k, v))
+    ring = LocalKVRing.from_full(kd, vd, cp, full_cu)
+    ks = [O.zigzag_shard_varlen(k, full_cu, r, cp)[0] for r in range(cp)]
+    vs = [O.zigzag_shard_varlen(v, full_cu, r, cp)[0] for r in range(cp)]
+    outs = []
+    for rank in range(cp):
+        lq, local_cu = zigzag_shard_varlen(qd, full_cu, rank, cp)
+        max_local = int((local_cu[1:] - local_cu[:-1]).max())
+        cfg = RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode)
+        out = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring,
+                              cu_seqlens=local_cu, max_seqlen=max_local)
+        oq, ocu = O.zigzag_shard_varlen(q, full_cu, rank, cp)
+        ref, _ = O.ring_rank(oq, ks, vs, rank, cp, scale, cu=ocu, merge_mode=mode)
+        assert max_err(out, ref) <= TOL_BF16_OUT, f"rank {rank}"
+        outs.append(out.float().cpu())
+    lcu = O.local_cu_from_full(full_cu, cp)
+    for j in range(len(lens)):
+        seq = O.zigzag_unshard([outs[r][lcu[j]:lcu[j + 1]] for r in range(cp)], cp)
+        s, e = full_cu[j], full_cu[j + 1]
+        assert max_err(seq, O.dense_causal(q[s:e], k[s:e], v[s:e], scale)) <= TOL_BF16_OUT
+
+
+def _fp8_ring_inputs(q, k, v, cp, rank, full_cu=None):
+    """Per-tensor q scale (local shard amax / 448), per-source-rank k / v scales."""
+    if full_cu is None:
+        lq = O.zigzag_shard(q, rank, cp)
+        ks = [O.zigzag_shard(k, r, cp) for r in range(cp)]
+        vs = [O.zigzag_shard(v, r, cp) for r in range(cp)]
+    else:
+        lq = O.zigzag_shard_varlen(q, full_cu, rank, cp)[0]
+        ks = [O.zigzag_shard_varlen(k, full_cu, r, cp)[0] for r in range(cp)]
+        vs = [O.zigzag_shard_varlen(v, full_cu, r, cp)[0] for r in range(cp)]
+    sq = O.amax_scale(lq)
+    sk = [O.amax_scale(x) for x in ks]
+    sv = [O.amax_scale(x) for x in vs]
+    q8 = O.quantize_e4m3(lq, sq)
+    k8 = [O.quantize_e4m3(x, s) for x, s in zip(ks, sk)]
+    v8 = [O.quantize_e4m3(x, s) for x, s in zip(vs, sv)]
+    deq = (O.dequantize_e4m3(q8, sq), [O.dequantize_e4m3(x, s) for x, s in zip(k8, sk)],
+           [O.dequantize_e4m3(x, s) for x, s in zip(v8, sv)])
+    return (q8, k8, v8, sq, sk, sv), deq
+
+
+@pytest.mark.parametrize("mode", ["incremental", "batched"])
+@pytest.mark.parametrize("n,h,hkv,d,cp", [(2048, 8, 2, 128, 8), (1024, 16, 2, 256, 4),
+                                          (1024, 8, 8, 128, 2)])
+def test_ring_fp8_all_ranks(n, h, hkv, d, cp, mode):
+    say(f"ring e4m3 n={n} h={h}/{hkv} d={d} cp={cp} mode={mode}")
+    q, k, v = O.random_qkv(n, h, hkv, d, seed=4)
+    scale = scale_for(d)
+    for rank in range(cp):
+        (q8, k8, v8, sq, sk, sv), (dq, dk, dv) = _fp8_ring_inputs(q, k, v, cp, rank)
+        ring = LocalKVRing([x.to(DEV) for x in k8], [x.to(DEV) for x in v8])
+        desc = Descales(q=torch.tensor(sq, device=DEV),
+                        k=[torch.tensor(s, device=DEV) for s in sk],
+                        v=[torch.tensor([s] * hkv, device=DEV) for s in sv])
+        cfg = RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode)
+        out = ring_flash_attn(q8.to(DEV), ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc)
+        assert out.dtype == torch.bfloat16
+        ref, _ = O.ring_rank(dq, dk, dv, rank, cp, scale, merge_mode=mode)
+        assert max_err(out, ref) <= TOL_FP8_OUT, f"rank {rank}"
+
+
+# ----------------------------------------------------------------- benchmark sizes
+
+def _sample_local_rows(t, n_random, seed):
+    h = t // 2
+    fixed = [0, 1, 31, 32, 63, 64, h - 1, h, h + 1, h + 63, h + 64, t - 1]
+    rng = np.random.default_rng(seed)
+    return sorted(set(fixed + rng.integers(0, t, n_random).tolist()))
+
+
+def _check_sampled(out_local, rank, cp, n, qfull_f, kfull_f, vfull_f, scale, tol, seed):
+    """Compares sampled rows of one rank's output with exact dense causal attention."""
+    t, h, _ = out_local.shape
+    rows = _sample_local_rows(t, 24, seed)
+    grow = O.zigzag_rows(n, rank, cp)
+    rng = np.random.default_rng(seed + 1)
+    heads = rng.integers(0, h, len(rows)).tolist()
+    exp, _ = O.dense_causal_rows(qfull_f, kfull_f, vfull_f, [int(grow[i]) for i in rows], heads, scale)
+    got = out_local[rows, heads].float().cpu()
+    err = float((got - exp).abs().max())
+    assert err <= tol, f"rank {rank}: sampled max err {err}"
+    return err
+
+
+@pytest.mark.parametrize("rank", [3, 7])
+def test_ring_c2_bf16_full_size(rank):
+    n, cp, hq, hkv, d = 131072, 8, 32, 8, 128
+    say(f"ring C2 bf16 n={n} rank={rank}")
+    gen = torch.Generator(device=DEV).manual_seed(0)
+    q = torch.randn(n, hq, d, device=DEV, generator=gen, dtype=torch.bfloat16)
+    k = torch.randn(n, hkv, d, device=DEV, generator=gen, dtype=torch.bfloat16)
+    v = torch.randn(n, hkv, d, device=DEV, generator=gen, dtype=torch.bfloat16)
+    ring = LocalKVRing.from_full(k, v, cp)
+    lq = zigzag_shard(q, rank, cp)
+    outs = {}
+    for mode in ("incremental", "batched"):
+        cfg = RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode)
+        outs[mode] = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring)
+    again = ring_flash_attn(lq, ring.k[rank], ring.v[rank], RingConfig(cp_size=cp, cp_rank=rank),
+                            group=ring)
+    assert torch.equal(again, outs["incremental"]), "sweep is not bit-reproducible"
+    kc, vc = k.float().cpu(), v.float().cpu()
+    grow = O.zigzag_rows(n, rank, cp)
+    qc = torch.zeros(n, hq, d)
+    qc[torch.from_numpy(grow)] = lq.float().cpu()
+    for mode, out in outs.items():
+        _check_sampled(out, rank, cp, n, qc, kc, vc, scale_for(d), TOL_BF16_OUT, seed=rank)
+
+
+def _fp8_full_size(n, cp, hq, hkv, d, rank, modes, seed):
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    q = torch.randn(n, hq, d, device=DEV, generator=gen)
+    k = torch.randn(n, hkv, d, device=DEV, generator=gen)
+    v = torch.randn(n, hkv, d, device=DEV, generator=gen)
+    lq = zigzag_shard(q, rank, cp)
+    sq = float(lq.abs().max()) / 448.0
+    q8 = (lq / sq).clamp(-448, 448).to(torch.float8_e4m3fn)
+    ks = [zigzag_shard(k, r, cp) for r in range(cp)]
+    vs = [zigzag_shard(v, r, cp) for r in range(cp)]
+    sk = [float(x.abs().max()) / 448.0 for x in ks]
+    sv = [float(x.abs().max()) / 448.0 for x in vs]
+    k8 = [(x / s).clamp(-448, 448).to(torch.float8_e4m3fn) for x, s in zip(ks, sk)]
+    v8 = [(x / s).clamp(-448, 448).to(torch.float8_e4m3fn) for x, s in zip(vs, sv)]
+    del q, k, v, ks, vs
+    ring = LocalKVRing(k8, v8)
+    desc = Descales(q=torch.tensor(sq, device=DEV), k=[torch.tensor(s, device=DEV) for s in sk],
+                    v=[torch.tensor(s, device=DEV) for s in sv])
+    outs = {}
+    for mode in modes:
+        cfg = RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode)
+        outs[mode] = ring_flash_attn(q8, ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc)
+    # dense reference on the dequantised tensors
+    kf = O.zigzag_unshard([x.float().cpu() * s for x, s in zip(k8, sk)], cp)
+    vf = O.zigzag_unshard([x.float().cpu() * s for x, s in zip(v8, sv)], cp)
+    qf = torch.zeros(n, hq, d)
+    qf[torch.from_numpy(O.zigzag_rows(n, rank, cp))] = q8.float().cpu() * sq
+    for mode, out in outs.items():
+        _check_sampled(out, rank, cp, n, qf, kf, vf, scale_for(d), TOL_FP8_OUT, seed=rank + 10)
+
+
+@pytest.mark.parametrize("rank", [0, 3, 7])
+def test_ring_c3_fp8_full_size(rank):
+    say(f"ring C3 e4m3 n=131072 rank={rank}")
+    _fp8_full_size(131072, 8, 32, 8, 128, rank, ("incremental",), seed=1)
+
+
+def test_ring_c5_fp8_d256_full_size():
+    say("ring C5 e4m3 d=256 n=262144 rank=3")
+    _fp8_full_size(262144, 8, 16, 2, 256, 3, ("batched", "incremental"), seed=2)
+
+
+@pytest.mark.parametrize("rank", [0, 3])
+def test_ring_c4_varlen_full_size(rank):
+    lens = [4856, 9720, 8592, 4864, 1832, 15456, 2784, 1576]
+    cp, hq, hkv, d = 4, 32, 8, 128
+    say(f"ring C4 varlen rank={rank}")
+    full_cu = [0]
+    for n in lens:
+        full_cu.append(full_cu[-1] + n)
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    q = torch.randn(full_cu[-1], hq, d, device=DEV, generator=gen, dtype=torch.bfloat16)
+    k = torch.randn(full_cu[-1], hkv, d, device=DEV, generator=gen, dtype=torch.bfloat16)
+    v = torch.randn(full_cu[-1], hkv, d, device=DEV, generator=gen, dtype=torch.bfloat16)
+    ring = LocalKVRing.from_full(k, v, cp, full_cu)
+    lq, local_cu = zigzag_shard_varlen(q, full_cu, rank, cp)
+    max_local = int((local_cu[1:] - local_cu[:-1]).max())
+    qc, kc, vc = q.float().cpu(), k.float().cpu(), v.float().cpu()
+    grow = O.zigzag_rows_varlen(full_cu, rank, cp)
+    rng = np.random.default_rng(rank)
+    rows = sorted(set(rng.integers(0, lq.shape[0], 40).tolist() + [0, lq.shape[0] - 1]))
+    heads = rng.integers(0, hq, len(rows)).tolist()
+    for mode in ("incremental", "batched"):
+        cfg = RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode)
+        out = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring,
+                              cu_seqlens=local_cu, max_seqlen=max_local)
+        got = out[rows, heads].float().cpu()
+        exp = []
+        for i, hh in zip(rows, heads):
+            g = int(grow[i])
+            j = int(np.searchsorted(full_cu, g, side="right") - 1)
+            o, _ = O.dense_causal_rows(qc, kc, vc, [g], [hh], scale_for(d), seq_start=full_cu[j])
+            exp.append(o[0])
+        err = float((got - torch.stack(exp)).abs().max())
+        assert err <= TOL_BF16_OUT, f"{mode}: {err}"

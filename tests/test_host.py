@@ -1,0 +1,150 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports every declared
+entry point, the ctypes struct mirror matches the C layout, and the Python interface keeps
+the reference's argument checking and error behaviour."""
+
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+import torch
+
+import fa4_ring
+from fa4_ring import _lib
+from fa4_ring.config import RingConfig
+from fa4_ring.fa4_backend import _norm_descale, fa4_attn
+from fa4_ring.merge import BatchedMerger, IncrementalMerger, make_merger
+from fa4_ring.ring_attention import LocalKVRing, ring_flash_attn
+from fa4_ring.zigzag import get_half_index, half_indices, local_seqlen
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fa4cp.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(fa4cp_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    syms = _declared_symbols()
+    assert len(syms) >= 7
+    for s in syms:
+        assert hasattr(lib, s), f"{s} declared in include/fa4cp.h but not exported"
+    assert set(syms) <= set(_lib.SIGNATURES), "every declared entry point has a ctypes signature"
+    assert lib.fa4cp_abi_version() == _lib.ABI_VERSION
+
+
+def test_error_path_reports_message_without_gpu():
+    lib = _lib.load()
+    # invalid arguments are rejected before any HIP call
+    rc = lib.fa4cp_merge_states(None, None, None, None, 1, 1, 1, 8, 0, None)
+    assert rc == -1
+    assert b"null pointer" in lib.fa4cp_last_error()
+    rc = lib.fa4cp_zigzag_shard(1, 1, 16, None, 1, 10, 0, 4, None)
+    assert rc == -1 and b"divisible" in lib.fa4cp_last_error()
+    a = _lib.AttnArgs()
+    rc = lib.fa4cp_attn_fwd(ctypes.byref(a), None)
+    assert rc == -1 and b"null tensor" in lib.fa4cp_last_error()
+    with pytest.raises(RuntimeError, match="null tensor"):
+        _lib.check(rc, "fa4cp_attn_fwd")
+
+
+def test_attn_args_layout_matches_c_header():
+    fields = [f for f, _ in _lib.AttnArgs._fields_]
+    prog = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",
+            'printf("%zu\\n", sizeof(fa4cp_attn_args));']
+    prog += [f'printf("%zu\\n", offsetof(fa4cp_attn_args, {f}));' for f in fields]
+    prog.append("return 0;}")
+    with tempfile.TemporaryDirectory() as td:
+        src, exe = os.path.join(td, "l.c"), os.path.join(td, "l")
+        open(src, "w").write("\n".join(prog))
+        subprocess.run(["gcc", "-o", exe, src], check=True)
+        vals = [int(x) for x in subprocess.run([exe], check=True, capture_output=True,
+                                               text=True).stdout.split()]
+    assert vals[0] == ctypes.sizeof(_lib.AttnArgs)
+    for f, off in zip(fields, vals[1:]):
+        assert getattr(_lib.AttnArgs, f).offset == off, f
+
+
+def test_ring_config_checks():
+    RingConfig(cp_size=8, cp_rank=7)
+    with pytest.raises(AssertionError):
+        RingConfig(cp_size=4, cp_rank=4)
+    with pytest.raises(AssertionError):
+        RingConfig(cp_size=0, cp_rank=0)
+    with pytest.raises(AssertionError):
+        RingConfig(cp_size=2, cp_rank=0, causal=False)
+    with pytest.raises(AssertionError):
+        RingConfig(cp_size=2, cp_rank=0, merge_mode="tree")
+
+
+def test_make_merger():
+    assert isinstance(make_merger("incremental"), IncrementalMerger)
+    assert isinstance(make_merger("batched"), BatchedMerger)
+    with pytest.raises(ValueError):
+        make_merger("nope")
+    with pytest.raises(AssertionError):
+        IncrementalMerger().result()
+    with pytest.raises(AssertionError):
+        BatchedMerger().result()
+    # one partial is returned as is
+    b = BatchedMerger()
+    t = torch.zeros(2, 1, 8)
+    b.add(t, torch.zeros(2, 1))
+    assert b.result() is t
+
+
+def test_norm_descale_shapes():
+    assert _norm_descale(None, 4, "cpu") is None
+    assert _norm_descale(torch.tensor(0.5), 4, "cpu").tolist() == [0.5] * 4
+    assert _norm_descale(torch.arange(4.0), 4, "cpu").tolist() == [0, 1, 2, 3]
+    assert _norm_descale(torch.arange(4.0).reshape(1, 4), 4, "cpu").tolist() == [0, 1, 2, 3]
+    assert _norm_descale(torch.tensor(2, dtype=torch.float64), 2, "cpu").dtype == torch.float32
+    with pytest.raises(AssertionError):
+        _norm_descale(torch.ones(3), 4, "cpu")
+
+
+def test_index_helpers_kat():
+    f, s = half_indices(8, torch.device("cpu"))
+    assert f.tolist() == [0, 1, 2, 3] and s.tolist() == [4, 5, 6, 7]
+    cu = torch.tensor([0, 4, 12], dtype=torch.int32)
+    assert get_half_index(cu, front=True).tolist() == [0, 1, 4, 5, 6, 7]
+    assert get_half_index(cu, front=False).tolist() == [2, 3, 8, 9, 10, 11]
+    assert local_seqlen(64, 4) == 16
+    with pytest.raises(AssertionError):
+        local_seqlen(30, 4)
+
+
+def test_device_entry_points_reject_host_tensors():
+    q = torch.zeros(16, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="device tensor"):
+        fa4_attn(q, q, q, causal=True)
+    with pytest.raises(AssertionError, match="device tensor"):
+        fa4_ring.zigzag_shard(q, 0, 2)
+
+
+def test_ring_without_local_kv_source_raises():
+    q = torch.zeros(16, 2, 128, dtype=torch.bfloat16)
+    cfg = RingConfig(cp_size=2, cp_rank=0)
+    with pytest.raises(RuntimeError, match="LocalKVRing"):
+        ring_flash_attn(q, q, q, cfg)
+    with pytest.raises(AssertionError):
+        ring_flash_attn(q, q, q, cfg, cu_seqlens=torch.tensor([0, 16], dtype=torch.int32))
+    ring = LocalKVRing([q, q, q], [q, q, q])
+    with pytest.raises(AssertionError, match="3 shards"):
+        ring_flash_attn(q, q, q, cfg, group=ring)
+
+
+def test_public_api_names():
+    for name in ["RingConfig", "ring_flash_attn", "Descales", "zigzag_shard", "zigzag_unshard",
+                 "IncrementalMerger", "BatchedMerger", "make_merger", "LocalKVRing"]:
+        assert hasattr(fa4_ring, name)
+    from fa4_ring.zigzag import zigzag_shard_varlen  # noqa: F401
+    from fa4_ring.reference import full_causal_reference  # noqa: F401
+    from fa4_ring.fa4_backend import has_fa4
+
+    assert has_fa4() is True
