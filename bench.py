@@ -1,0 +1,328 @@
+"""Benchmark of one rank's causal zig-zag ring sweep on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--rank 3] [--no-cpu-baseline]
+
+A step is one rank's full ring sweep (cp_size attention launches plus cp_size - 1
+incremental LSE merges) over inputs already resident in HBM, at the bf16 benchmark
+configuration: N = 131072 tokens, cp_size = 8 (local Q, K, V of 16384 tokens each),
+H_q = 32, H_kv = 8, D = 128, causal, rank 3 (all source ranks' KV shards in HBM).
+
+Prints one JSON line.  `value` is causal-adjusted attention TFLOP/s of the sweep:
+F = sum over steps of 4 * Tq * Tk * D * H_q (halved for the causal step) = 17.592 TFLOP per
+sweep, divided by the measured sweep time.  Also reported: the same sweep in OCP e4m3
+with per-source-rank descales, the incremental and batched merge kernels and the zig-zag
+gather in GB/s against the 8 TB/s HBM peak, and the CPU oracle timed on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "fa4-cp_amd"), ROOT):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "ring-sweep attn TFLOP/s + % MFMA peak (bf16/fp8); merge GB/s, 1×MI355X"
+PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU
+PEAK_FP8_TFLOPS = 5033.2
+PEAK_HBM_GBS = 8000.0
+
+N, CP, HQ, HKV, D = 131072, 8, 32, 8, 128
+
+
+def sweep_flops(t_local: int, cp: int, hq: int, d: int) -> float:
+    """Causal-adjusted FLOPs of one rank's sweep: every step is 4 * (T*T/2) * D * H_q
+    (causal T x T, front-half T x T/2, back-half T/2 x T), i.e. cp * 8 * h^2 * D * H_q."""
+    h = t_local // 2
+    return cp * 8.0 * h * h * d * hq
+
+
+class KernelClock:
+    """Records torch.cuda events around every attention / merge launch of the sweep (the
+    launches go to torch's current stream, where the events are recorded too)."""
+
+    def __init__(self):
+        self.events = {}
+
+    def wrap(self, name, fn):
+        import torch
+
+        def inner(*a, **k):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            r = fn(*a, **k)
+            e.record()
+            self.events.setdefault(name, []).append((s, e))
+            return r
+
+        return inner
+
+    def mean_ms(self, name):
+        ev = self.events.get(name, [])
+        return sum(s.elapsed_time(e) for s, e in ev) / len(ev) if ev else float("nan")
+
+    def count(self, name):
+        return len(self.events.get(name, []))
+
+
+def make_bf16_inputs(rank: int, seed: int = 0):
+    import torch
+
+    from fa4_ring import LocalKVRing, zigzag_shard
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q = torch.randn(N, HQ, D, device=dev, generator=g, dtype=torch.bfloat16)
+    k = torch.randn(N, HKV, D, device=dev, generator=g, dtype=torch.bfloat16)
+    v = torch.randn(N, HKV, D, device=dev, generator=g, dtype=torch.bfloat16)
+    ring = LocalKVRing.from_full(k, v, CP)
+    lq = zigzag_shard(q, rank, CP)
+    return q, lq, ring
+
+
+def make_fp8_inputs(rank: int, seed: int = 1):
+    """q scale = amax(local q) / 448; k / v scales per source rank = amax(shard) / 448."""
+    import torch
+
+    from fa4_ring import Descales, LocalKVRing, zigzag_shard
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q = torch.randn(N, HQ, D, device=dev, generator=g)
+    k = torch.randn(N, HKV, D, device=dev, generator=g)
+    v = torch.randn(N, HKV, D, device=dev, generator=g)
+    lq = zigzag_shard(q, rank, CP)
+    del q
+
+    def quant(x):
+        s = x.abs().amax() / 448.0
+        return (x / s).clamp(-448, 448).to(torch.float8_e4m3fn), s.float().reshape(())
+
+    q8, sq = quant(lq)
+    ks, vs, sk, sv = [], [], [], []
+    for r in range(CP):
+        a, sa = quant(zigzag_shard(k, r, CP))
+        b, sb = quant(zigzag_shard(v, r, CP))
+        ks.append(a)
+        vs.append(b)
+        sk.append(sa)
+        sv.append(sb)
+    return q8, LocalKVRing(ks, vs), Descales(q=sq, k=sk, v=sv)
+
+
+def timed_sweeps(fn, steps: int, warmup: int, clock: KernelClock = None):
+    import torch
+
+    from fa4_ring import ring_attention as RA
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    saved = (RA.fa4_attn, RA.merge_state_in_place, RA.merge_states)
+    if clock is not None:
+        RA.fa4_attn = clock.wrap("attn", saved[0])
+        RA.merge_state_in_place = clock.wrap("merge_inplace", saved[1])
+        RA.merge_states = clock.wrap("merge_states", saved[2])
+    try:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+    finally:
+        RA.fa4_attn, RA.merge_state_in_place, RA.merge_states = saved
+    return dt
+
+
+def merge_bytes_inplace(rows: int, h: int, d: int, bv: int) -> float:
+    """Read v, v_other, s, s_other; write v, s."""
+    return rows * h * (3 * d * bv + 3 * 4)
+
+
+def merge_bytes_batched(rows: int, s: int, h: int, d: int, bv: int) -> float:
+    return rows * h * (s * (d * bv + 4) + d * bv + 4)
+
+
+def cpu_baseline(rank: int, rows: int) -> dict:
+    """The CPU oracle (fp32 torch on the host cores) on a bounded sample of the same
+    workload: step 1 of the rank's sweep (all local Q x front half of source rank-1's KV)
+    restricted to the first `rows` local query rows, all heads."""
+    import torch
+
+    from oracle import ring_oracle as O
+
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = min(threads, int(os.environ.get("OMP_NUM_THREADS", threads)))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    t = N // CP
+    q = torch.randn(rows, HQ, D, generator=g).to(torch.bfloat16).float()
+    k = torch.randn(t // 2, HKV, D, generator=g).to(torch.bfloat16).float()
+    v = torch.randn(t // 2, HKV, D, generator=g).to(torch.bfloat16).float()
+    O.cpu_attn(q[:64], k, v, False, 1 / math.sqrt(D))  # warm the BLAS
+    t0 = time.perf_counter()
+    O.cpu_attn(q, k, v, False, 1 / math.sqrt(D))
+    dt = time.perf_counter() - t0
+    flops = 4.0 * rows * (t // 2) * D * HQ
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle cpu_attn fp32, ring step {1} of rank {rank} (all Q x front half of "
+                       f"source {rank - 1}'s KV) on the first {rows} of {t} local query rows, "
+                       f"{HQ} heads, Tk={t // 2}, D={D}: {flops / 1e12:.3f} TFLOP in {dt:.2f} s on {cpu}"),
+            "full_sweep_s_extrapolated": round(sweep_flops(t, CP, HQ, D) / (flops / dt), 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--rank", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=16384)
+    ap.add_argument("--skip-extra", action="store_true", help="only the headline bf16 sweep")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (one rank's sweep with every source "
+              f"rank's KV resident in HBM); --gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from fa4_ring import RingConfig, ring_flash_attn
+    from fa4_ring.merge import merge_states
+    from fa4_ring.zigzag import zigzag_shard
+
+    rank = args.rank
+    t_local = N // CP
+    flops = sweep_flops(t_local, CP, HQ, D)
+    per_launch = flops / CP
+
+    # ---------------- headline: bf16 incremental sweep
+    q_full, lq, ring = make_bf16_inputs(rank)
+    cfg = RingConfig(cp_size=CP, cp_rank=rank, merge_mode="incremental")
+
+    def sweep():
+        return ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring)
+
+    clock = KernelClock()
+    sec = timed_sweeps(sweep, args.steps, args.warmup, clock)
+    attn_ms = clock.mean_ms("attn")
+    merge_ms = clock.mean_ms("merge_inplace")
+    value = flops / sec / 1e12
+    attn_tflops = per_launch / (attn_ms * 1e-3) / 1e12
+    # merge bytes: steps 1..rank merge every row, steps rank+1.. only the back half
+    n_full = min(rank, CP - 1)
+    n_back = CP - 1 - n_full
+    mbytes = (n_full * merge_bytes_inplace(t_local, HQ, D, 2) +
+              n_back * merge_bytes_inplace(t_local // 2, HQ, D, 2)) / (CP - 1)
+    merge_gbs = mbytes / (merge_ms * 1e-3) / 1e9
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (q/k/v ~ N(0,1) bf16, seeded on the GPU)",
+        "config": {"workload": "bf16 causal zig-zag ring sweep, one rank's share of cp_size=8 over "
+                               "N=131072 (local Q/K/V 16384 tokens), H_q=32, H_kv=8, D=128, "
+                               f"rank {rank}, incremental merge, all 8 source KV shards in HBM",
+                   "global_batch": 1, "seq_len": N, "cp_size": CP, "cp_rank": rank,
+                   "h_q": HQ, "h_kv": HKV, "head_dim": D, "parallelism": "cp8 (one rank's share on 1 GPU)"},
+        "frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
+        "roofline": {"bound": "mfma", "kernel": "attn_fwd_16bit<bf16,128,4>",
+                     "achieved": round(attn_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "algorithmic_per_launch": f"{per_launch / 1e12:.4f} TFLOP "
+                                               "(4*Tq*Tk*D*H_q, halved for the causal step)",
+                     "avg_launch_ms": round(attn_ms, 4), "launches": clock.count("attn")},
+        "merge": {"kernel": "merge_inplace_kernel<bf16>", "avg_launch_ms": round(merge_ms, 4),
+                  "algorithmic_bytes_per_launch": round(mbytes),
+                  "achieved_GBs": round(merge_gbs, 1), "peak_GBs": PEAK_HBM_GBS,
+                  "frac": round(merge_gbs / PEAK_HBM_GBS, 4), "launches": clock.count("merge_inplace")},
+    }
+
+    if not args.skip_extra:
+        # rank 7 (only front-half steps)
+        lq7 = zigzag_shard(q_full, 7, CP)
+        cfg7 = RingConfig(cp_size=CP, cp_rank=7)
+        sec7 = timed_sweeps(lambda: ring_flash_attn(lq7, ring.k[7], ring.v[7], cfg7, group=ring),
+                            max(3, args.steps // 2), 2)
+        result["rank7_bf16"] = {"ms_per_step": round(sec7 * 1e3, 3), "TFLOP/s": round(flops / sec7 / 1e12, 2)}
+        # batched merge mode and one merge_states launch at S = 8
+        cfgb = RingConfig(cp_size=CP, cp_rank=rank, merge_mode="batched")
+        clockb = KernelClock()
+        secb = timed_sweeps(lambda: ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfgb, group=ring),
+                            max(3, args.steps // 2), 2, clockb)
+        ms_ms = clockb.mean_ms("merge_states")
+        bb = merge_bytes_batched(t_local, CP, HQ, D, 2)
+        result["batched_bf16"] = {"ms_per_step": round(secb * 1e3, 3), "TFLOP/s": round(flops / secb / 1e12, 2),
+                                  "merge_states_ms": round(ms_ms, 4), "merge_states_bytes": round(bb),
+                                  "merge_states_GBs": round(bb / (ms_ms * 1e-3) / 1e9, 1)}
+        # zig-zag gather of the full q (bf16, 1 GiB -> 128 MiB)
+        zz = []
+        for _ in range(3):
+            zigzag_shard(q_full, rank, CP)
+        for _ in range(10):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            zigzag_shard(q_full, rank, CP)
+            e.record()
+            zz.append((s, e))
+        torch.cuda.synchronize()
+        zms = sum(s.elapsed_time(e) for s, e in zz) / len(zz)
+        zbytes = 2.0 * t_local * HQ * D * 2
+        result["zigzag"] = {"kernel": "shard_kernel<u32x4>", "avg_launch_ms": round(zms, 4),
+                            "bytes": round(zbytes), "achieved_GBs": round(zbytes / (zms * 1e-3) / 1e9, 1),
+                            "frac": round(zbytes / (zms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        del q_full, lq7
+        # fp8 sweep
+        q8, ring8, desc = make_fp8_inputs(rank)
+        cfg8 = RingConfig(cp_size=CP, cp_rank=rank)
+        clock8 = KernelClock()
+        sec8 = timed_sweeps(lambda: ring_flash_attn(q8, ring8.k[rank], ring8.v[rank], cfg8, group=ring8,
+                                                    descales=desc), args.steps, args.warmup, clock8)
+        a8 = clock8.mean_ms("attn")
+        result["fp8"] = {"workload": "same shape, OCP e4m3 q/k/v, per-source-rank k/v descales, bf16 out",
+                         "ms_per_step": round(sec8 * 1e3, 3), "TFLOP/s": round(flops / sec8 / 1e12, 2),
+                         "frac_of_fp8_peak": round(flops / sec8 / 1e12 / PEAK_FP8_TFLOPS, 4),
+                         "attn_avg_launch_ms": round(a8, 4),
+                         "attn_TFLOP/s": round(per_launch / (a8 * 1e-3) / 1e12, 2),
+                         "attn_frac": round(per_launch / (a8 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)}
+        del q8, ring8
+    del ring, lq
+    torch.cuda.synchronize()
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(rank, args.cpu_rows)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
