@@ -91,6 +91,64 @@ __device__ __forceinline__ float pair_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Raw buffer resource over `bytes` bytes at `base`: loads past the end return zero in
+// hardware, which is how rows beyond a sequence's end are read without a branch or a
+// select (and without making the compiler wait for the data at the load).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int n = bytes <= 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : (int)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bload128(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ u32x2 bload64(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+}
+
+// True when any lane of the wavefront has `p` set (wave-uniform result).
+__device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
+
+// Rescaling of the running output is deferred until the row max has grown by more than
+// 2^kLazyLog2 (in exp2 units): until then probabilities are taken relative to the older,
+// smaller reference max and may reach 2^kLazyLog2, which bf16 / e4m3 and the fp32
+// accumulators hold without loss.
+constexpr float kLazyLog2 = 8.0f;
+
+// Online-softmax update for one tile of raw scores s (masked entries -inf): converts s in
+// place to probabilities exp2((s - m) * c_log2) relative to the lane's reference max m,
+// adds their sum to lsum, and rescales o / lsum when the reference max moves.  Max and sum
+// are reduced as four independent chains to keep the dependency depth short.
+template <int NMT, int NDT>
+__device__ __forceinline__ void softmax_tile(f32x16 (&s)[NMT], f32x16 (&o)[NDT], float& m,
+                                             float& lsum, float c_log2) {
+  float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+  for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mx[i & 3] = fmaxf(mx[i & 3], s[mt][i]);
+  const float tmax = pair_max(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])));
+  const bool grow = tmax > m && (m == -INFINITY || (tmax - m) * c_log2 > kLazyLog2);
+  if (wave_any(grow)) {
+    const float m_new = fmaxf(m, tmax);
+    const float alpha = fast_exp2(m == -INFINITY ? -INFINITY : (m - m_new) * c_log2);
+    m = m_new;
+    lsum *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+  }
+  const float mc = (m == -INFINITY) ? 0.f : m * c_log2;
+  float rs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float e = fast_exp2(fmaf(s[mt][i], c_log2, -mc));
+      s[mt][i] = e;
+      rs[i & 3] += e;
+    }
+  lsum += (rs[0] + rs[1]) + (rs[2] + rs[3]);
+}
+
 // Position of key kk (0..15) of a 16-key group inside the permuted V^T row.
 __host__ __device__ constexpr int vperm16(int kk) {
   return 8 * ((kk >> 2) & 1) + 4 * (kk >> 3) + (kk & 3);
@@ -156,7 +214,7 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
   if (row_tile0 >= Lq) return;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int lane = tid & 63;
   const int lq = lane & 31;  // query column owned by this lane
   const int lh = lane >> 5;  // k-slot half
@@ -181,14 +239,12 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
   // Q^T fragments: lane (lq, lh) holds q[row r0+lq][16t + 8lh .. +7] for every k-step t.
   frag qf[NKS];
   {
-    const int row = r0 + lq;
-    const bool ok = row < Lq;
-    const T* src = qg + (int64_t)(qs + (ok ? row : 0)) * p.q_rs + (int64_t)head * p.q_hs + 8 * lh;
+    const int64_t rsb = p.q_rs * (int64_t)sizeof(T);
+    const auto rq = make_rsrc(qg + (int64_t)(qs + r0) * p.q_rs + (int64_t)head * p.q_hs,
+                              (int64_t)min(Lq - r0, 32) * rsb);
 #pragma unroll
-    for (int t = 0; t < NKS; ++t) {
-      frag x = *reinterpret_cast<const frag*>(src + 16 * t);
-      qf[t] = ok ? x : frag{};
-    }
+    for (int t = 0; t < NKS; ++t)
+      qf[t] = __builtin_bit_cast(frag, bload128(rq, lq * (int)rsb + (int)sizeof(T) * (16 * t + 8 * lh)));
   }
 
   // Global -> register staging of one K/V tile.
@@ -198,23 +254,22 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
   frag vreg[4];
   const int v_dc = tid % KCH;  // V task: d chunk
   const int v_kq = tid / KCH;  // V task: key quad
+  const int k_rsb = (int)(p.k_rs * (int64_t)sizeof(T));
+  const int v_rsb = (int)(p.v_rs * (int64_t)sizeof(T));
   auto load_tile = [&](int tile) {
     const int kb = tile * BN;
+    const int rows = min(Lk - kb, BN);
+    const auto rk = make_rsrc(kbase + (int64_t)kb * p.k_rs, (int64_t)rows * k_rsb);
+    const auto rv = make_rsrc(vbase + (int64_t)kb * p.v_rs, (int64_t)rows * v_rsb);
 #pragma unroll
     for (int i = 0; i < KU; ++i) {
       const int u = tid + i * kThreads;
       const int key = u / KCH, c = u % KCH;
-      const bool ok = kb + key < Lk;
-      frag x = *reinterpret_cast<const frag*>(kbase + (int64_t)(ok ? kb + key : 0) * p.k_rs + 8 * c);
-      kreg[i] = ok ? x : frag{};
+      kreg[i] = __builtin_bit_cast(frag, bload128(rk, key * k_rsb + 16 * c));
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = kb + 4 * v_kq + i;
-      const bool ok = key < Lk;
-      frag x = *reinterpret_cast<const frag*>(vbase + (int64_t)(ok ? key : 0) * p.v_rs + 8 * v_dc);
-      vreg[i] = ok ? x : frag{};
-    }
+    for (int i = 0; i < 4; ++i)
+      vreg[i] = __builtin_bit_cast(frag, bload128(rv, (4 * v_kq + i) * v_rsb + 16 * v_dc));
   };
   auto store_tile = [&](int buf) {
     T* ks_ = smem[buf][0];
@@ -251,6 +306,9 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
     load_tile(0);
     store_tile(0);
   }
+  // Q and the first tile are in place: drain every counter once here so that the loop's
+  // only outstanding global loads are its own prefetches.
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   for (int it = 0; it < n_tiles; ++it) {
@@ -290,29 +348,7 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
     }
 
     // online softmax (exp2 domain)
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int mt = 0; mt < NMT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[mt][i]);
-    tmax = pair_max(tmax);
-    const float m_new = fmaxf(m, tmax);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float mc = m_use * c_log2;
-    const float alpha = fast_exp2(m * c_log2 - mc);
-    float rs = 0.f;
-#pragma unroll
-    for (int mt = 0; mt < NMT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float e = fast_exp2(fmaf(s[mt][i], c_log2, -mc));
-        s[mt][i] = e;
-        rs += e;
-      }
-    lsum = fmaf(lsum, alpha, rs);
-    m = m_new;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+    softmax_tile<NMT, NDT>(s, o, m, lsum, c_log2);
 
     // P^T fragments: k-step t takes accumulator registers 8*(t%2) .. +7 of tile t/2
     frag pf[NPS];
@@ -427,7 +463,7 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_e4m3(At
   if (row_tile0 >= Lq) return;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int lane = tid & 63;
   const int lq = lane & 31;
   const int lh = lane >> 5;
@@ -450,15 +486,14 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_e4m3(At
 
   i32x8 qf[NKS];
   {
-    const int row = r0 + lq;
-    const bool ok = row < Lq;
-    const uint8_t* src = qg + (int64_t)(qs + (ok ? row : 0)) * p.q_rs + (int64_t)head * p.q_hs + 32 * lh;
+    const int rsb = (int)p.q_rs;
+    const auto rq = make_rsrc(qg + (int64_t)(qs + r0) * p.q_rs + (int64_t)head * p.q_hs,
+                              (int64_t)min(Lq - r0, 32) * rsb);
 #pragma unroll
     for (int t = 0; t < NKS; ++t) {
-      i32x4 a = *reinterpret_cast<const i32x4*>(src + 64 * t);
-      i32x4 b = *reinterpret_cast<const i32x4*>(src + 64 * t + 16);
-      i32x8 x = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-      qf[t] = ok ? x : i32x8{};
+      const u32x4 a = bload128(rq, lq * rsb + 64 * t + 32 * lh);
+      const u32x4 b = bload128(rq, lq * rsb + 64 * t + 32 * lh + 16);
+      qf[t] = i32x8{(int)a[0], (int)a[1], (int)a[2], (int)a[3], (int)b[0], (int)b[1], (int)b[2], (int)b[3]};
     }
   }
 
@@ -466,27 +501,25 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_e4m3(At
   const uint8_t* vbase = vg + (int64_t)ks * p.v_rs + (int64_t)kvh * p.v_hs;
   i32x4 kreg[KU];
   u32x2 vreg[VT][4];
+  const int k_rsb = (int)p.k_rs;
+  const int v_rsb = (int)p.v_rs;
   auto load_tile = [&](int tile) {
     const int kb = tile * BN;
+    const int rows = min(Lk - kb, BN);
+    const auto rk = make_rsrc(kbase + (int64_t)kb * p.k_rs, (int64_t)rows * k_rsb);
+    const auto rv = make_rsrc(vbase + (int64_t)kb * p.v_rs, (int64_t)rows * v_rsb);
 #pragma unroll
     for (int i = 0; i < KU; ++i) {
       const int u = tid + i * kThreads;
       const int key = u / KCH, c = u % KCH;
-      const bool ok = kb + key < Lk;
-      i32x4 x = *reinterpret_cast<const i32x4*>(kbase + (int64_t)(ok ? kb + key : 0) * p.k_rs + 16 * c);
-      kreg[i] = ok ? x : i32x4{};
+      kreg[i] = __builtin_bit_cast(i32x4, bload128(rk, key * k_rsb + 16 * c));
     }
 #pragma unroll
     for (int tk = 0; tk < VT; ++tk) {
       const int task = tid + tk * kThreads;
       const int dq = task % DQ, kq = task / DQ;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = kb + 4 * kq + i;
-        const bool ok = key < Lk;
-        u32x2 x = *reinterpret_cast<const u32x2*>(vbase + (int64_t)(ok ? key : 0) * p.v_rs + 8 * dq);
-        vreg[tk][i] = ok ? x : u32x2{};
-      }
+      for (int i = 0; i < 4; ++i) vreg[tk][i] = bload64(rv, (4 * kq + i) * v_rsb + 8 * dq);
     }
   };
   auto store_tile = [&](int buf) {
@@ -545,6 +578,9 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_e4m3(At
     load_tile(0);
     store_tile(0);
   }
+  // Q and the first tile are in place: drain every counter once here so that the loop's
+  // only outstanding global loads are its own prefetches.
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   for (int it = 0; it < n_tiles; ++it) {
@@ -584,29 +620,7 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_e4m3(At
         }
     }
 
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[mt][i]);
-    tmax = pair_max(tmax);
-    const float m_new = fmaxf(m, tmax);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float mc = m_use * c_log2;
-    const float alpha = fast_exp2(m * c_log2 - mc);
-    float rs = 0.f;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float e = fast_exp2(fmaf(s[mt][i], c_log2, -mc));
-        s[mt][i] = e;
-        rs += e;
-      }
-    lsum = fmaf(lsum, alpha, rs);
-    m = m_new;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+    softmax_tile<2, NDT>(s, o, m, lsum, c_log2);
 
     const bool precise = p.causal && (diag || r0 < kPreciseRows);
     if (!precise) {
