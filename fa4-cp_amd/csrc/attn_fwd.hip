@@ -10,29 +10,32 @@
 // Work decomposition
 //   A workgroup is 4 wavefronts.  It owns HP query heads that share one kv head and RB
 //   blocks of 32 query rows (HP * RB = 4); wavefront w computes head w % HP for rows
-//   block w / HP.  K/V tiles of BN keys are staged once in LDS and read by all four
-//   wavefronts, so a tile feeds 128 query rows.
+//   block w / HP.  K/V tiles of 64 keys are staged once in LDS and read by all four
+//   wavefronts, so a tile feeds 128 query rows.  Two workgroups share a CU, so each SIMD
+//   interleaves the MFMA work of one wavefront with the softmax of the other.
 //
-// Per-wavefront math (32 queries x BN keys per tile), written transposed:
-//   S^T = K Q^T   with v_mfma_f32_32x32x16_{bf16,f16} (or 32x32x64_f8f6f4 for e4m3);
+// Per-wavefront math (32 queries x 64 keys per tile), written transposed:
+//   S^T = K Q^T   with v_mfma_f32_32x32x16_{bf16,f16} (32x32x64_f8f6f4 for e4m3);
 //                 A = K rows from LDS, B = Q^T held in registers for the whole loop.
 //   In the 32x32 accumulator layout lane l holds column l % 32 (one query) and 16 rows
 //   (keys), so the running max / sum of a query live in one lane pair (l, l ^ 32): the
 //   row max costs one v_permlane32_swap per tile and the row sum none until the end.
-//   O^T += V^T P^T  with B = P^T taken straight from the S^T accumulator registers.
-//   The MFMA pairs A k-slot 8*(l/32)+j with B k-slot 8*(l/32)+j; in the accumulator the
-//   lane's keys of a 16-key group are {4h..4h+3, 8+4h..8+4h+3} (h = l / 32), so V^T is
-//   stored in LDS with the keys of every 16-key group permuted to match (pos = 8h + j),
-//   and each A fragment is one 16-byte LDS read.
+//   O^T += V^T P^T  with B = P^T taken straight from the S^T accumulator registers.  The
+//   lane's keys in one 16-key group are {4h..4h+3, 8+4h..8+4h+3} (h = l / 32); the V^T
+//   A fragment with exactly those keys comes from two ds_read_b64_tr_b16 transposing LDS
+//   reads of the row-major V tile (each returns 4 consecutive keys of one column).
 //
-// LDS layouts (per buffer, double buffered; one barrier per tile)
-//   K   [BN][D]  16-byte chunks XOR-swizzled by (key & 7): conflict-free fragment reads.
-//   V^T [D][BN]  keys permuted as above, 16-byte chunks XOR-swizzled by (d ^ d >> 3).
-//   BN = 8192 / D (16 KB of K and 16 KB of V per tile for every head dim).
+// LDS (double buffered, one barrier per tile): K and V tiles row-major exactly as in
+// HBM, copied with 16-byte loads and stores; rows are padded (K by 16 bytes, V by 64)
+// so the fragment reads are bank-conflict free and every fragment address is a per-lane
+// base plus a compile-time offset.  Tiles that need no mask (all but the causal diagonal
+// and a partial last tile) run a loop without any masking code.
 //
 // Softmax runs in the exp2 domain with scale * log2(e) (times the q/k descales) folded
-// into one FMA per score; the LSE written is natural-log, as fa4_ring/merge.py expects.
+// into one FMA per score, and rescales the output only when the running max grows by
+// more than 2^8; the LSE written is natural-log, as fa4_ring/merge.py expects.
 #include <cfloat>
+#include <type_traits>
 
 #include "common.h"
 
@@ -41,6 +44,7 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
+constexpr int kBN = 64;  // keys per tile
 
 struct AttnParams {
   const void* q;
@@ -62,6 +66,10 @@ struct AttnParams {
   int n_hg;  // head groups: h_kv * group / HP
   int n_blocks;
 };
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 
 // Query / key row range [start, start + len) of sequence j after the half selection.
 __device__ __forceinline__ void seq_range(const int32_t* cu, int j, int total, int sel,
@@ -101,8 +109,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
 __device__ __forceinline__ u32x4 bload128(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
-__device__ __forceinline__ u32x2 bload64(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+
+// Transposing LDS reads (gfx950).  Within each group of 16 lanes, with M[j] the 8 bytes at
+// lane j's address: ds_read_b64_tr_b16 gives lane i the 16-bit elements
+// M[4m + i/4][i % 4] for m = 0..3, and ds_read_b64_tr_b8 the bytes M[2m + i/8][i % 8] for
+// m = 0..7.  Pointing lane j at row (base + j/4), column (c0 + 4 (j%4)) of a row-major
+// 16-bit tile therefore hands lane i rows base..base+3 of column c0 + i.
+__device__ __forceinline__ s16x4 lds_tr16(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+}
+__device__ __forceinline__ i32x2 lds_tr8(const void* p) {
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)p);
 }
 
 // True when any lane of the wavefront has `p` set (wave-uniform result).
@@ -149,9 +166,19 @@ __device__ __forceinline__ void softmax_tile(f32x16 (&s)[NMT], f32x16 (&o)[NDT],
   lsum += (rs[0] + rs[1]) + (rs[2] + rs[3]);
 }
 
-// Position of key kk (0..15) of a 16-key group inside the permuted V^T row.
-__host__ __device__ constexpr int vperm16(int kk) {
-  return 8 * ((kk >> 2) & 1) + 4 * (kk >> 3) + (kk & 3);
+// Sets to -inf the scores of keys past the selection and, for causal, keys after the
+// query (bottom-right aligned: key kk is visible to query qq iff kk <= qq + off).
+template <int NMT>
+__device__ __forceinline__ void mask_tile(f32x16 (&s)[NMT], int kb, int Lk, int qq, bool causal,
+                                          int lh) {
+#pragma unroll
+  for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kk = kb + 32 * mt + (i >> 2) * 8 + 4 * lh + (i & 3);
+      const bool dead = kk >= Lk || (causal && kk > qq);
+      s[mt][i] = dead ? -INFINITY : s[mt][i];
+    }
 }
 
 template <typename T>
@@ -184,6 +211,17 @@ __device__ __forceinline__ void decode_block(const AttnParams& p, int& hg, int& 
   rt = p.n_rt - 1 - (r - seq * p.n_rt);
 }
 
+// Number of leading key tiles that need no mask for any row of the workgroup.
+__device__ __forceinline__ int mask_free_tiles(int n_tiles, int Lk, bool causal, int row_tile0,
+                                               int off) {
+  int n = Lk / kBN;
+  if (causal) {
+    const int lim = row_tile0 + off + 1;  // keys < lim are visible to every row
+    n = min(n, lim > 0 ? lim / kBN : 0);
+  }
+  return min(n, n_tiles);
+}
+
 //--------------------------------------------------------------------------------------
 // bf16 / fp16 kernel
 //--------------------------------------------------------------------------------------
@@ -191,19 +229,20 @@ template <typename T, int D, int HP>
 __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(AttnParams p) {
   using Ops = MfmaOps<T>;
   using frag = typename Ops::frag;
-  constexpr int BN = 8192 / D;          // keys per tile
+  constexpr int BN = kBN;
   constexpr int RB = kWaves / HP;       // 32-row blocks per workgroup
-  constexpr int KCH = D / 8;            // 16-byte chunks per K row
-  constexpr int VCH = BN / 8;           // 16-byte chunks per V^T row
-  constexpr int KU = BN * KCH / kThreads;  // K 16-byte units per thread per tile
+  constexpr int KCH = D / 8;            // 16-byte chunks per row
+  constexpr int NU = BN * KCH / kThreads;  // 16-byte units per thread per tile (K and V each)
+  constexpr int KS = D + 8;             // K row stride in LDS (elements)
+  constexpr int VS = D + 32;            // V row stride in LDS (elements)
+  constexpr int BUF = BN * (KS + VS);   // elements per buffer
   constexpr int NMT = BN / 32;          // S^T accumulator tiles
   constexpr int NDT = D / 32;           // O^T accumulator tiles
   constexpr int NKS = D / 16;           // k-steps of S^T (over d)
   constexpr int NPS = BN / 16;          // k-steps of O^T (over keys)
-  static_assert(KU * kThreads == BN * KCH, "K tile must split evenly");
-  static_assert((BN / 4) * KCH == kThreads, "one V^T task per thread");
+  static_assert(NU * kThreads == BN * KCH, "tile must split evenly");
 
-  __shared__ __attribute__((aligned(16))) T smem[2][2][BN * D];  // [buf][K|V^T][...]
+  __shared__ __attribute__((aligned(16))) T smem[2 * BUF];
 
   int hg, seq, rt;
   decode_block(p, hg, seq, rt);
@@ -224,13 +263,13 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
   const int r0 = row_tile0 + (wave / HP) * 32;  // first row of this wavefront (selection-local)
   const int off = Lk - Lq;                       // bottom-right causal alignment
 
-  // number of key tiles this workgroup visits
   int n_tiles = (Lk + BN - 1) / BN;
   if (p.causal) {
     const int last_row = min(row_tile0 + RB * 32, Lq) - 1;
     const int kmax = last_row + off;  // largest visible key
     n_tiles = kmax < 0 ? 0 : min(n_tiles, kmax / BN + 1);
   }
+  const int n_free = mask_free_tiles(n_tiles, Lk, p.causal, row_tile0, off);
 
   const T* __restrict__ qg = reinterpret_cast<const T*>(p.q);
   const T* __restrict__ kg = reinterpret_cast<const T*>(p.k);
@@ -247,55 +286,45 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
       qf[t] = __builtin_bit_cast(frag, bload128(rq, lq * (int)rsb + (int)sizeof(T) * (16 * t + 8 * lh)));
   }
 
-  // Global -> register staging of one K/V tile.
+  // Global -> register -> LDS staging of one K/V tile (row-major, 16-byte units).
   const T* kbase = kg + (int64_t)ks * p.k_rs + (int64_t)kvh * p.k_hs;
   const T* vbase = vg + (int64_t)ks * p.v_rs + (int64_t)kvh * p.v_hs;
-  frag kreg[KU];
-  frag vreg[4];
-  const int v_dc = tid % KCH;  // V task: d chunk
-  const int v_kq = tid / KCH;  // V task: key quad
   const int k_rsb = (int)(p.k_rs * (int64_t)sizeof(T));
   const int v_rsb = (int)(p.v_rs * (int64_t)sizeof(T));
+  u32x4 kreg[NU], vreg[NU];
   auto load_tile = [&](int tile) {
     const int kb = tile * BN;
     const int rows = min(Lk - kb, BN);
     const auto rk = make_rsrc(kbase + (int64_t)kb * p.k_rs, (int64_t)rows * k_rsb);
     const auto rv = make_rsrc(vbase + (int64_t)kb * p.v_rs, (int64_t)rows * v_rsb);
 #pragma unroll
-    for (int i = 0; i < KU; ++i) {
+    for (int i = 0; i < NU; ++i) {
       const int u = tid + i * kThreads;
-      const int key = u / KCH, c = u % KCH;
-      kreg[i] = __builtin_bit_cast(frag, bload128(rk, key * k_rsb + 16 * c));
+      kreg[i] = bload128(rk, (u / KCH) * k_rsb + 16 * (u % KCH));
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      vreg[i] = __builtin_bit_cast(frag, bload128(rv, (4 * v_kq + i) * v_rsb + 16 * v_dc));
+    for (int i = 0; i < NU; ++i) {
+      const int u = tid + i * kThreads;
+      vreg[i] = bload128(rv, (u / KCH) * v_rsb + 16 * (u % KCH));
+    }
   };
   auto store_tile = [&](int buf) {
-    T* ks_ = smem[buf][0];
-    T* vs_ = smem[buf][1];
+    T* ks_ = smem + buf * BUF;
+    T* vs_ = ks_ + BN * KS;
 #pragma unroll
-    for (int i = 0; i < KU; ++i) {
+    for (int i = 0; i < NU; ++i) {
       const int u = tid + i * kThreads;
-      const int key = u / KCH, c = u % KCH;
-      *reinterpret_cast<frag*>(ks_ + key * D + 8 * (c ^ (key & 7))) = kreg[i];
-    }
-    // transpose 4 keys x 8 d into 8 rows of V^T, 4 keys (8 bytes) each
-    const int grp = v_kq >> 2;          // 16-key group
-    const int kk0 = 4 * (v_kq & 3);     // first key inside the group
-    const int pos = 16 * grp + vperm16(kk0);
-    const int chunk = pos >> 3, within = pos & 7;
-#pragma unroll
-    for (int dd = 0; dd < 8; ++dd) {
-      const int d = 8 * v_dc + dd;
-      const int sw = (d ^ (d >> 3)) & (VCH - 1);
-      typedef T t4 __attribute__((ext_vector_type(4)));
-      t4 w = {vreg[0][dd], vreg[1][dd], vreg[2][dd], vreg[3][dd]};
-      *reinterpret_cast<t4*>(vs_ + d * BN + 8 * (chunk ^ sw) + within) = w;
+      *reinterpret_cast<u32x4*>(ks_ + (u / KCH) * KS + 8 * (u % KCH)) = kreg[i];
+      *reinterpret_cast<u32x4*>(vs_ + (u / KCH) * VS + 8 * (u % KCH)) = vreg[i];
     }
   };
 
-  float c_log2 = p.scale * kLog2e;
+  // per-lane fragment bases (elements); everything else is a compile-time offset
+  const int k_lane = lq * KS + 8 * lh;
+  const int j16 = lane & 15;
+  const int v_lane = (4 * lh + (j16 >> 2)) * VS + 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+
+  const float c_log2 = p.scale * kLog2e;
   f32x16 o[NDT];
 #pragma unroll
   for (int i = 0; i < NDT; ++i) o[i] = f32x16{};
@@ -311,43 +340,26 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  for (int it = 0; it < n_tiles; ++it) {
+  auto tile_step = [&](int it, auto masked) {
     const int buf = it & 1;
     const bool more = it + 1 < n_tiles;
     if (more) load_tile(it + 1);
-    const T* ks_ = smem[buf][0];
-    const T* vs_ = smem[buf][1];
+    const T* ks_ = smem + buf * BUF;
+    const T* vs_ = ks_ + BN * KS;
 
     // S^T = K Q^T
     f32x16 s[NMT];
 #pragma unroll
     for (int mt = 0; mt < NMT; ++mt) {
       s[mt] = f32x16{};
-      const int key = 32 * mt + lq;
 #pragma unroll
       for (int t = 0; t < NKS; ++t) {
-        frag a = *reinterpret_cast<const frag*>(ks_ + key * D + 8 * ((2 * t + lh) ^ (key & 7)));
+        const frag a = *reinterpret_cast<const frag*>(ks_ + k_lane + 32 * mt * KS + 16 * t);
         s[mt] = Ops::mma(a, qf[t], s[mt]);
       }
     }
+    if constexpr (decltype(masked)::value) mask_tile<NMT>(s, it * BN, Lk, r0 + lq + off, p.causal, lh);
 
-    // masking: keys past the selection, and the causal diagonal
-    const int kb = it * BN;
-    const bool tail = kb + BN > Lk;
-    const bool diag = p.causal && (kb + BN - 1 > r0 + off);
-    if (tail || diag) {
-      const int qq = r0 + lq + off;
-#pragma unroll
-      for (int mt = 0; mt < NMT; ++mt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int kk = kb + 32 * mt + (i >> 2) * 8 + 4 * lh + (i & 3);
-          const bool dead = kk >= Lk || (p.causal && kk > qq);
-          s[mt][i] = dead ? -INFINITY : s[mt][i];
-        }
-    }
-
-    // online softmax (exp2 domain)
     softmax_tile<NMT, NDT>(s, o, m, lsum, c_log2);
 
     // P^T fragments: k-step t takes accumulator registers 8*(t%2) .. +7 of tile t/2
@@ -357,21 +369,24 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
 #pragma unroll
       for (int j = 0; j < 8; ++j) pf[t][j] = (T)s[t >> 1][8 * (t & 1) + j];
 
-    // O^T += V^T P^T
+    // O^T += V^T P^T; the A fragment of k-step t is rows 16t + 4h .. +3 and
+    // 16t + 8 + 4h .. +3 of column d, read transposed from the row-major V tile
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const int d = 32 * dt + lq;
-      const int sw = (d ^ (d >> 3)) & (VCH - 1);
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int t = 0; t < NPS; ++t) {
-        frag a = *reinterpret_cast<const frag*>(vs_ + d * BN + 8 * ((2 * t + lh) ^ sw));
+        const s16x4 lo = lds_tr16(vs_ + v_lane + 16 * t * VS + 32 * dt);
+        const s16x4 hi = lds_tr16(vs_ + v_lane + (16 * t + 8) * VS + 32 * dt);
+        const frag a = __builtin_bit_cast(frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         o[dt] = Ops::mma(a, pf[t], o[dt]);
       }
-    }
 
     if (more) store_tile(buf ^ 1);
     __syncthreads();
-  }
+  };
+  int it = 0;
+  for (; it < n_free; ++it) tile_step(it, std::false_type{});
+  for (; it < n_tiles; ++it) tile_step(it, std::true_type{});
 
   // epilogue: combine the lane pair's partial sums, normalise, write out and LSE
   const float ltot = pair_sum(lsum);
@@ -401,10 +416,10 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
 // QK^T and PV run on v_mfma_f32_32x32x64_f8f6f4 (fp8 x fp8, 64-deep).  The MFMA pairs
 // A slot (h, j) with B slot (h, j) (h = lane / 32, j = byte 0..31 of the lane's operand);
 // the kernel only relies on that symmetry.  For QK^T slot (h, j) of k-step t is
-// d = 64t + 32h + j on both sides.  For PV slot (h, j) of a 64-key group is accumulator
-// register j % 16 of S^T tile j / 16, i.e. key 32(j/16) + 8((j%16)/4) + 4h + j%4, and V^T
-// is stored in LDS with the keys of each 64-key group permuted so that the lane's 32
-// slots are contiguous bytes.
+// d = 64t + 32h + j on both sides.  For PV, slot j of lane half h is accumulator register
+// j % 16 of S^T tile j / 16, i.e. key 16(j/8) + 8((j%8)/4) + 4h + j%4; the V tile is
+// stored with its rows permuted (vrow8) so that the eight keys of slots 8g..8g+7 are
+// consecutive LDS rows, and one ds_read_b64_tr_b8 per 8 slots yields the A fragment.
 //
 // P is rounded to e4m3 for the fast PV product.  Queries with few visible keys (the
 // first rows of a causal sequence) would see that rounding undamped, so tiles on the
@@ -413,9 +428,9 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
 //--------------------------------------------------------------------------------------
 constexpr int kPreciseRows = 512;
 
-__host__ __device__ constexpr int vperm64(int kk) {
-  // key kk (0..63) of a 64-key group -> byte position in the permuted V^T row
-  return 32 * ((kk >> 2) & 1) + 16 * (kk >> 5) + 4 * ((kk & 31) >> 3) + (kk & 3);
+// LDS row of key kk (0..63) in the permuted e4m3 V tile.
+__host__ __device__ constexpr int vrow8(int kk) {
+  return 32 * ((kk >> 2) & 1) + 8 * (kk >> 4) + 4 * ((kk >> 3) & 1) + (kk & 3);
 }
 
 __device__ __forceinline__ f32x16 mma_fp8(i32x8 a, i32x8 b, f32x16 c) {
@@ -423,12 +438,12 @@ __device__ __forceinline__ f32x16 mma_fp8(i32x8 a, i32x8 b, f32x16 c) {
 }
 
 // Widens 8 e4m3 bytes (two dwords) to 8 bf16 (exact).
-__device__ __forceinline__ bf16x8 e4m3x8_to_bf16(u32x2 x) {
+__device__ __forceinline__ bf16x8 e4m3x8_to_bf16(i32x2 x) {
   bf16x8 r;
 #pragma unroll
   for (int w = 0; w < 2; ++w) {
-    f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[w], false);
-    f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[w], true);
+    f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(x[w], false);
+    f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(x[w], true);
     r[4 * w + 0] = (__bf16)lo[0];
     r[4 * w + 1] = (__bf16)lo[1];
     r[4 * w + 2] = (__bf16)hi[0];
@@ -439,20 +454,17 @@ __device__ __forceinline__ bf16x8 e4m3x8_to_bf16(u32x2 x) {
 
 template <int D, int HP>
 __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_e4m3(AttnParams p) {
-  constexpr int BN = 64;               // keys per tile (one PV k-step)
+  constexpr int BN = kBN;
   constexpr int RB = kWaves / HP;
-  constexpr int KCH = D / 16;          // 16-byte chunks per K row
-  constexpr int KU = BN * KCH / kThreads;
+  constexpr int KCH = D / 16;          // 16-byte chunks per row
+  constexpr int NU = BN * KCH / kThreads;
+  constexpr int RS = D + 16;           // K and V row stride in LDS (bytes)
+  constexpr int BUF = 2 * BN * RS;     // bytes per buffer
   constexpr int NKS = D / 64;          // S^T k-steps
   constexpr int NDT = D / 32;
-  constexpr int VROW = BN;             // bytes per V^T row
-  constexpr int DQ = D / 8;            // V tasks: 8-byte d chunks per key quad
-  constexpr int VT = (BN / 4) * DQ / kThreads;  // V tasks per thread
-  static_assert(KU >= 1 && KU * kThreads == BN * KCH, "K tile split");
-  static_assert(VT >= 1 && VT * kThreads == (BN / 4) * DQ, "V tile split");
-  static_assert(KCH >= 8 || D == 64, "swizzle assumes >= 8 chunks per K row");
+  static_assert(NU >= 1 && NU * kThreads == BN * KCH, "tile split");
 
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][2][BN * D];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * BUF];
 
   int hg, seq, rt;
   decode_block(p, hg, seq, rt);
@@ -479,6 +491,7 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_e4m3(At
     const int kmax = last_row + off;
     n_tiles = kmax < 0 ? 0 : min(n_tiles, kmax / BN + 1);
   }
+  const int n_free = mask_free_tiles(n_tiles, Lk, p.causal, row_tile0, off);
 
   const uint8_t* __restrict__ qg = reinterpret_cast<const uint8_t*>(p.q);
   const uint8_t* __restrict__ kg = reinterpret_cast<const uint8_t*>(p.k);
@@ -499,72 +512,40 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_e4m3(At
 
   const uint8_t* kbase = kg + (int64_t)ks * p.k_rs + (int64_t)kvh * p.k_hs;
   const uint8_t* vbase = vg + (int64_t)ks * p.v_rs + (int64_t)kvh * p.v_hs;
-  i32x4 kreg[KU];
-  u32x2 vreg[VT][4];
   const int k_rsb = (int)p.k_rs;
   const int v_rsb = (int)p.v_rs;
+  u32x4 kreg[NU], vreg[NU];
   auto load_tile = [&](int tile) {
     const int kb = tile * BN;
     const int rows = min(Lk - kb, BN);
     const auto rk = make_rsrc(kbase + (int64_t)kb * p.k_rs, (int64_t)rows * k_rsb);
     const auto rv = make_rsrc(vbase + (int64_t)kb * p.v_rs, (int64_t)rows * v_rsb);
 #pragma unroll
-    for (int i = 0; i < KU; ++i) {
+    for (int i = 0; i < NU; ++i) {
       const int u = tid + i * kThreads;
-      const int key = u / KCH, c = u % KCH;
-      kreg[i] = __builtin_bit_cast(i32x4, bload128(rk, key * k_rsb + 16 * c));
-    }
-#pragma unroll
-    for (int tk = 0; tk < VT; ++tk) {
-      const int task = tid + tk * kThreads;
-      const int dq = task % DQ, kq = task / DQ;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) vreg[tk][i] = bload64(rv, (4 * kq + i) * v_rsb + 8 * dq);
+      kreg[i] = bload128(rk, (u / KCH) * k_rsb + 16 * (u % KCH));
+      vreg[i] = bload128(rv, (u / KCH) * v_rsb + 16 * (u % KCH));
     }
   };
   auto store_tile = [&](int buf) {
-    uint8_t* ks_ = smem[buf][0];
-    uint8_t* vs_ = smem[buf][1];
+    uint8_t* ks_ = smem + buf * BUF;
+    uint8_t* vs_ = ks_ + BN * RS;
 #pragma unroll
-    for (int i = 0; i < KU; ++i) {
+    for (int i = 0; i < NU; ++i) {
       const int u = tid + i * kThreads;
       const int key = u / KCH, c = u % KCH;
-      *reinterpret_cast<i32x4*>(ks_ + key * D + 16 * (c ^ (key & 7 & (KCH - 1)))) = kreg[i];
-    }
-#pragma unroll
-    for (int tk = 0; tk < VT; ++tk) {
-      const int task = tid + tk * kThreads;
-      const int dq = task % DQ, kq = task / DQ;
-      const int pos = vperm64(4 * kq);  // 4 consecutive keys stay contiguous
-      // 4 keys x 8 d bytes -> 8 d rows x 4 key bytes (byte transpose with v_perm)
-#pragma unroll
-      for (int w = 0; w < 2; ++w) {
-        const unsigned a0 = vreg[tk][0][w], a1 = vreg[tk][1][w], a2 = vreg[tk][2][w], a3 = vreg[tk][3][w];
-        // t01 = interleave bytes of a0,a1 ; t23 = of a2,a3
-        const unsigned t01_lo = __builtin_amdgcn_perm(a1, a0, 0x05010400u);  // a0b0 a1b0 a0b1 a1b1
-        const unsigned t01_hi = __builtin_amdgcn_perm(a1, a0, 0x07030602u);  // a0b2 a1b2 a0b3 a1b3
-        const unsigned t23_lo = __builtin_amdgcn_perm(a3, a2, 0x05010400u);
-        const unsigned t23_hi = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
-        unsigned col[4];
-        col[0] = __builtin_amdgcn_perm(t23_lo, t01_lo, 0x05040100u);  // d=0: a0 a1 a2 a3
-        col[1] = __builtin_amdgcn_perm(t23_lo, t01_lo, 0x07060302u);  // d=1
-        col[2] = __builtin_amdgcn_perm(t23_hi, t01_hi, 0x05040100u);  // d=2
-        col[3] = __builtin_amdgcn_perm(t23_hi, t01_hi, 0x07060302u);  // d=3
-#pragma unroll
-        for (int dd = 0; dd < 4; ++dd) {
-          const int d = 8 * dq + 4 * w + dd;
-          const int sw = (d >> 2) & 3;  // 64-byte rows: spread rows d, d+4, d+8, d+12
-          const int chunk = (pos >> 4) ^ sw;
-          *reinterpret_cast<unsigned*>(vs_ + d * VROW + 16 * chunk + (pos & 15)) = col[dd];
-        }
-      }
+      *reinterpret_cast<u32x4*>(ks_ + key * RS + 16 * c) = kreg[i];
+      *reinterpret_cast<u32x4*>(vs_ + vrow8(key) * RS + 16 * c) = vreg[i];
     }
   };
 
-  const int qd_idx = kvh;
-  const float qd = p.qd ? p.qd[qd_idx] : 1.f;
-  const float kd = p.kd ? p.kd[qd_idx] : 1.f;
-  const float vd = p.vd ? p.vd[qd_idx] : 1.f;
+  const int k_lane = lq * RS + 32 * lh;
+  const int j16 = lane & 15;
+  const int v_lane = (32 * lh + (j16 >> 1)) * RS + 16 * ((lane >> 4) & 1) + 8 * (j16 & 1);
+
+  const float qd = p.qd ? p.qd[kvh] : 1.f;
+  const float kd = p.kd ? p.kd[kvh] : 1.f;
+  const float vd = p.vd ? p.vd[kvh] : 1.f;
   const float c_log2 = p.scale * qd * kd * kLog2e;
   const float c_nat = p.scale * qd * kd;
 
@@ -578,51 +559,34 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_e4m3(At
     load_tile(0);
     store_tile(0);
   }
-  // Q and the first tile are in place: drain every counter once here so that the loop's
-  // only outstanding global loads are its own prefetches.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  for (int it = 0; it < n_tiles; ++it) {
+  auto tile_step = [&](int it, auto masked) {
     const int buf = it & 1;
     const bool more = it + 1 < n_tiles;
     if (more) load_tile(it + 1);
-    const uint8_t* ks_ = smem[buf][0];
-    const uint8_t* vs_ = smem[buf][1];
+    const uint8_t* ks_ = smem + buf * BUF;
+    const uint8_t* vs_ = ks_ + BN * RS;
 
     f32x16 s[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       s[mt] = f32x16{};
-      const int key = 32 * mt + lq;
 #pragma unroll
       for (int t = 0; t < NKS; ++t) {
-        const int c0 = 4 * t + 2 * lh;
-        i32x4 a0 = *reinterpret_cast<const i32x4*>(ks_ + key * D + 16 * ((c0) ^ (key & 7 & (KCH - 1))));
-        i32x4 a1 = *reinterpret_cast<const i32x4*>(ks_ + key * D + 16 * ((c0 + 1) ^ (key & 7 & (KCH - 1))));
-        i32x8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-        s[mt] = mma_fp8(a, qf[t], s[mt]);
+        const uint8_t* src = ks_ + k_lane + 32 * mt * RS + 64 * t;
+        const i32x4 a0 = *reinterpret_cast<const i32x4*>(src);
+        const i32x4 a1 = *reinterpret_cast<const i32x4*>(src + 16);
+        s[mt] = mma_fp8(__builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7), qf[t], s[mt]);
       }
     }
-
     const int kb = it * BN;
-    const bool tail = kb + BN > Lk;
-    const bool diag = p.causal && (kb + BN - 1 > r0 + off);
-    if (tail || diag) {
-      const int qq = r0 + lq + off;
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int kk = kb + 32 * mt + (i >> 2) * 8 + 4 * lh + (i & 3);
-          const bool dead = kk >= Lk || (p.causal && kk > qq);
-          s[mt][i] = dead ? -INFINITY : s[mt][i];
-        }
-    }
+    if constexpr (decltype(masked)::value) mask_tile<2>(s, kb, Lk, r0 + lq + off, p.causal, lh);
 
     softmax_tile<2, NDT>(s, o, m, lsum, c_log2);
 
-    const bool precise = p.causal && (diag || r0 < kPreciseRows);
+    const bool precise = decltype(masked)::value ? p.causal != 0 : (p.causal && r0 < kPreciseRows);
     if (!precise) {
       // P^T as e4m3: slot j <- s[j / 16][j % 16]
       i32x8 pf;
@@ -635,37 +599,35 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_e4m3(At
       }
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
-        const int d = 32 * dt + lq;
-        const int sw = (d >> 2) & 3;
-        i32x4 a0 = *reinterpret_cast<const i32x4*>(vs_ + d * VROW + 16 * ((2 * lh) ^ sw));
-        i32x4 a1 = *reinterpret_cast<const i32x4*>(vs_ + d * VROW + 16 * ((2 * lh + 1) ^ sw));
-        i32x8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        i32x2 g[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) g[q] = lds_tr8(vs_ + v_lane + 8 * q * RS + 32 * dt);
+        const i32x8 a = {g[0][0], g[0][1], g[1][0], g[1][1], g[2][0], g[2][1], g[3][0], g[3][1]};
         o[dt] = mma_fp8(a, pf, o[dt]);
       }
     } else {
-      // bf16 PV: k-step t (16 keys) uses registers 8*(t%2)..+7 of tile t/2 and the V^T
-      // bytes at position 32h + 8t .. +7 of the permuted row
+      // bf16 PV: k-step t (16 keys) uses registers 8*(t%2)..+7 of tile t/2, and its V^T
+      // fragment is the t-th eight-row group of the permuted tile, widened to bf16
       bf16x8 pb[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int j = 0; j < 8; ++j) pb[t][j] = (__bf16)s[t >> 1][8 * (t & 1) + j];
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        const int d = 32 * dt + lq;
-        const int sw = (d >> 2) & 3;
+      for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const int pos = 32 * lh + 8 * t;
-          u32x2 raw = *reinterpret_cast<const u32x2*>(vs_ + d * VROW + 16 * ((pos >> 4) ^ sw) + (pos & 15));
+          const i32x2 raw = lds_tr8(vs_ + v_lane + 8 * t * RS + 32 * dt);
           o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(e4m3x8_to_bf16(raw), pb[t], o[dt], 0, 0, 0);
         }
-      }
     }
 
     if (more) store_tile(buf ^ 1);
     __syncthreads();
-  }
+  };
+  int it = 0;
+  for (; it < n_free; ++it) tile_step(it, std::false_type{});
+  for (; it < n_tiles; ++it) tile_step(it, std::true_type{});
 
   const float ltot = pair_sum(lsum);
   const float inv = ltot > 0.f ? vd / ltot : 0.f;
