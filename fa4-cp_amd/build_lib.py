@@ -47,6 +47,16 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
+def check_resolved(path: str) -> None:
+    """Fails the build when the library references one of its own symbols it does not
+    define (clang can drop a kernel's host stub without a diagnostic)."""
+    out = subprocess.run(["nm", "-D", "--undefined-only", path], stdout=subprocess.PIPE,
+                         stderr=subprocess.STDOUT, text=True).stdout
+    missing = [l.split()[-1] for l in out.splitlines() if "fa4cp" in l]
+    if missing:
+        raise RuntimeError(f"{path}: unresolved internal symbols: {missing[:4]}")
+
+
 def build_library(verbose: bool = False, jobs: int = 8) -> str:
     """Compiles every csrc/*.hip for gfx950 and links libfa4cp.so; returns its path."""
     cc = hipcc()
@@ -62,6 +72,7 @@ def build_library(verbose: bool = False, jobs: int = 8) -> str:
                     print(out)
     tmp = LIB + ".tmp"
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
+    check_resolved(tmp)
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")

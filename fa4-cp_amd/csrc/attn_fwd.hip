@@ -122,6 +122,13 @@ __device__ __forceinline__ i32x2 lds_tr8(const void* p) {
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)p);
 }
 
+// 16-byte LDS-DMA load: lane L's 16 bytes from `r` at byte offset voff land at lds + 16 L
+// (lanes past the end of `r` write zeros).  `lds` must be wave-uniform.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff,
+                                           0, 0, 0);
+}
+
 // True when any lane of the wavefront has `p` set (wave-uniform result).
 __device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 
@@ -153,6 +160,45 @@ __device__ __forceinline__ void softmax_tile(f32x16 (&s)[NMT], f32x16 (&o)[NDT],
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
   }
+  const float mc = (m == -INFINITY) ? 0.f : m * c_log2;
+  float rs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float e = fast_exp2(fmaf(s[mt][i], c_log2, -mc));
+      s[mt][i] = e;
+      rs[i & 3] += e;
+    }
+  lsum += (rs[0] + rs[1]) + (rs[2] + rs[3]);
+}
+
+// The online-softmax update split in two halves, so that each can be interleaved with
+// independent MFMA work: tile_max_rescale computes the tile's row max and moves the
+// reference max (rescaling o and lsum) when it grew by more than 2^kLazyLog2;
+// tile_exp turns the scores into probabilities relative to the reference max and adds
+// their sum to lsum.
+template <int NMT, int NDT>
+__device__ __forceinline__ void tile_max_rescale(const f32x16 (&s)[NMT], f32x16 (&o)[NDT], float& m,
+                                                 float& lsum, float c_log2) {
+  float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+  for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mx[i & 3] = fmaxf(mx[i & 3], s[mt][i]);
+  const float tmax = pair_max(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])));
+  const bool grow = tmax > m && (m == -INFINITY || (tmax - m) * c_log2 > kLazyLog2);
+  if (wave_any(grow)) {
+    const float m_new = fmaxf(m, tmax);
+    const float alpha = fast_exp2(m == -INFINITY ? -INFINITY : (m - m_new) * c_log2);
+    m = m_new;
+    lsum *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+  }
+}
+template <int NMT>
+__device__ __forceinline__ void tile_exp(f32x16 (&s)[NMT], float m, float& lsum, float c_log2) {
   const float mc = (m == -INFINITY) ? 0.f : m * c_log2;
   float rs[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -231,18 +277,21 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
   using frag = typename Ops::frag;
   constexpr int BN = kBN;
   constexpr int RB = kWaves / HP;       // 32-row blocks per workgroup
-  constexpr int KCH = D / 8;            // 16-byte chunks per row
-  constexpr int NU = BN * KCH / kThreads;  // 16-byte units per thread per tile (K and V each)
-  constexpr int KS = D + 8;             // K row stride in LDS (elements)
-  constexpr int VS = D + 32;            // V row stride in LDS (elements)
-  constexpr int BUF = BN * (KS + VS);   // elements per buffer
+  constexpr int CH = D / 8;             // 16-byte chunks per K / V row
+  constexpr int NLD = BN * CH / 64;     // wave-wide 1 KB LDS-DMA loads per tile (K or V)
   constexpr int NMT = BN / 32;          // S^T accumulator tiles
   constexpr int NDT = D / 32;           // O^T accumulator tiles
   constexpr int NKS = D / 16;           // k-steps of S^T (over d)
   constexpr int NPS = BN / 16;          // k-steps of O^T (over keys)
-  static_assert(NU * kThreads == BN * KCH, "tile must split evenly");
+  constexpr int KX = (CH >= 16 ? 16 : CH) - 1;  // K swizzle: chunk ^= row & KX
+  static_assert(NLD % kWaves == 0, "tile loads must split over the wavefronts");
 
-  __shared__ __attribute__((aligned(16))) T smem[2 * BUF];
+  // K tile t lives in kl[t % 2] and V tile t in vl[t % 2] (see the loop below).  Both are
+  // row-major [BN][D] with the 16-byte chunks of each row XOR-swizzled: K chunk c of row r
+  // sits at c ^ (r & KX), V chunk c at c ^ (4 (r & 3)), which makes the K fragment reads
+  // and the transposing V reads free of bank conflicts.
+  __shared__ __attribute__((aligned(1024))) T kl[2][BN * D];
+  __shared__ __attribute__((aligned(1024))) T vl[2][BN * D];
 
   int hg, seq, rt;
   decode_block(p, hg, seq, rt);
@@ -286,43 +335,48 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
       qf[t] = __builtin_bit_cast(frag, bload128(rq, lq * (int)rsb + (int)sizeof(T) * (16 * t + 8 * lh)));
   }
 
-  // Global -> register -> LDS staging of one K/V tile (row-major, 16-byte units).
+  // HBM -> LDS tile loads (LDS DMA, no registers): load n of this wavefront fills LDS
+  // chunks [64 (wave + 4n), +64) of the tile; lane L takes chunk P = 64 (wave + 4n) + L,
+  // i.e. row P / CH, stored position P % CH, which holds logical chunk (P % CH) ^ swizzle.
   const T* kbase = kg + (int64_t)ks * p.k_rs + (int64_t)kvh * p.k_hs;
   const T* vbase = vg + (int64_t)ks * p.v_rs + (int64_t)kvh * p.v_hs;
   const int k_rsb = (int)(p.k_rs * (int64_t)sizeof(T));
   const int v_rsb = (int)(p.v_rs * (int64_t)sizeof(T));
-  u32x4 kreg[NU], vreg[NU];
-  auto load_tile = [&](int tile) {
+  auto dma_k = [&](int tile, T* dst) {
     const int kb = tile * BN;
-    const int rows = min(Lk - kb, BN);
-    const auto rk = make_rsrc(kbase + (int64_t)kb * p.k_rs, (int64_t)rows * k_rsb);
-    const auto rv = make_rsrc(vbase + (int64_t)kb * p.v_rs, (int64_t)rows * v_rsb);
+    const auto rk = make_rsrc(kbase + (int64_t)kb * p.k_rs, (int64_t)min(Lk - kb, BN) * k_rsb);
 #pragma unroll
-    for (int i = 0; i < NU; ++i) {
-      const int u = tid + i * kThreads;
-      kreg[i] = bload128(rk, (u / KCH) * k_rsb + 16 * (u % KCH));
-    }
-#pragma unroll
-    for (int i = 0; i < NU; ++i) {
-      const int u = tid + i * kThreads;
-      vreg[i] = bload128(rv, (u / KCH) * v_rsb + 16 * (u % KCH));
+    for (int n = 0; n < NLD / kWaves; ++n) {
+      const int P = 64 * (wave + kWaves * n) + lane;
+      const int row = P / CH, c = (P % CH) ^ (row & KX);
+      dma16(rk, dst + 512 * (wave + kWaves * n), row * k_rsb + 16 * c);
     }
   };
-  auto store_tile = [&](int buf) {
-    T* ks_ = smem + buf * BUF;
-    T* vs_ = ks_ + BN * KS;
+  auto dma_v = [&](int tile, T* dst) {
+    const int kb = tile * BN;
+    const auto rv = make_rsrc(vbase + (int64_t)kb * p.v_rs, (int64_t)min(Lk - kb, BN) * v_rsb);
 #pragma unroll
-    for (int i = 0; i < NU; ++i) {
-      const int u = tid + i * kThreads;
-      *reinterpret_cast<u32x4*>(ks_ + (u / KCH) * KS + 8 * (u % KCH)) = kreg[i];
-      *reinterpret_cast<u32x4*>(vs_ + (u / KCH) * VS + 8 * (u % KCH)) = vreg[i];
+    for (int n = 0; n < NLD / kWaves; ++n) {
+      const int P = 64 * (wave + kWaves * n) + lane;
+      const int row = P / CH, c = (P % CH) ^ ((4 * (row & 3)) & (CH - 1));
+      dma16(rv, dst + 512 * (wave + kWaves * n), row * v_rsb + 16 * c);
     }
   };
 
-  // per-lane fragment bases (elements); everything else is a compile-time offset
-  const int k_lane = lq * KS + 8 * lh;
+  // Per-lane fragment offsets (elements); tile row offsets are compile-time immediates.
+  // K fragment of k-step t: row 32 mt + lq, logical chunk 2t + lh.
+  int k_off[NKS];
+#pragma unroll
+  for (int t = 0; t < NKS; ++t) k_off[t] = lq * D + 8 * ((2 * t + lh) ^ (lq & KX));
+  // V^T half-fragment: lane j of each 16-lane group reads row (16t + 8r) + 4h + j/4,
+  // columns 32 dt + 16 ((lane / 16) % 2) + 4 (j % 4) .. +3 (logical chunk and 8-byte half).
   const int j16 = lane & 15;
-  const int v_lane = (4 * lh + (j16 >> 2)) * VS + 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+  int v_off[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+    const int c = 4 * dt + 2 * ((lane >> 4) & 1) + ((j16 & 3) >> 1);
+    v_off[dt] = (4 * lh + (j16 >> 2)) * D + 8 * (c ^ ((4 * (j16 >> 2)) & (CH - 1))) + 4 * (j16 & 1);
+  }
 
   const float c_log2 = p.scale * kLog2e;
   f32x16 o[NDT];
@@ -331,62 +385,88 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
   float m = -INFINITY;
   float lsum = 0.f;
 
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  // Q and the first tile are in place: drain every counter once here so that the loop's
-  // only outstanding global loads are its own prefetches.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  auto tile_step = [&](int it, auto masked) {
-    const int buf = it & 1;
-    const bool more = it + 1 < n_tiles;
-    if (more) load_tile(it + 1);
-    const T* ks_ = smem + buf * BUF;
-    const T* vs_ = ks_ + BN * KS;
-
-    // S^T = K Q^T
-    f32x16 s[NMT];
+  // S^T = K Q^T for the K tile at ksrc
+  auto qk = [&](f32x16 (&s)[NMT], const T* ksrc) {
 #pragma unroll
     for (int mt = 0; mt < NMT; ++mt) {
       s[mt] = f32x16{};
 #pragma unroll
       for (int t = 0; t < NKS; ++t) {
-        const frag a = *reinterpret_cast<const frag*>(ks_ + k_lane + 32 * mt * KS + 16 * t);
+        const frag a = *reinterpret_cast<const frag*>(ksrc + k_off[t] + 32 * mt * D);
         s[mt] = Ops::mma(a, qf[t], s[mt]);
       }
     }
-    if constexpr (decltype(masked)::value) mask_tile<NMT>(s, it * BN, Lk, r0 + lq + off, p.causal, lh);
-
-    softmax_tile<NMT, NDT>(s, o, m, lsum, c_log2);
-
-    // P^T fragments: k-step t takes accumulator registers 8*(t%2) .. +7 of tile t/2
-    frag pf[NPS];
-#pragma unroll
-    for (int t = 0; t < NPS; ++t)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) pf[t][j] = (T)s[t >> 1][8 * (t & 1) + j];
-
-    // O^T += V^T P^T; the A fragment of k-step t is rows 16t + 4h .. +3 and
-    // 16t + 8 + 4h .. +3 of column d, read transposed from the row-major V tile
+  };
+  // O^T += V^T P^T for the V tile at vsrc; the A fragment of k-step t is rows 16t + 4h .. +3
+  // and 16t + 8 + 4h .. +3 of column d, read transposed from the row-major V tile
+  auto pv = [&](const frag (&pf)[NPS], const T* vsrc) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int t = 0; t < NPS; ++t) {
-        const s16x4 lo = lds_tr16(vs_ + v_lane + 16 * t * VS + 32 * dt);
-        const s16x4 hi = lds_tr16(vs_ + v_lane + (16 * t + 8) * VS + 32 * dt);
+        const s16x4 lo = lds_tr16(vsrc + v_off[dt] + 16 * t * D);
+        const s16x4 hi = lds_tr16(vsrc + v_off[dt] + (16 * t + 8) * D);
         const frag a = __builtin_bit_cast(frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         o[dt] = Ops::mma(a, pf[t], o[dt]);
       }
-
-    if (more) store_tile(buf ^ 1);
-    __syncthreads();
   };
-  int it = 0;
-  for (; it < n_free; ++it) tile_step(it, std::false_type{});
-  for (; it < n_tiles; ++it) tile_step(it, std::true_type{});
+  // P^T fragments: k-step t takes accumulator registers 8*(t%2) .. +7 of tile t/2
+  auto to_frags = [&](const f32x16 (&s)[NMT], frag (&pf)[NPS]) {
+#pragma unroll
+    for (int t = 0; t < NPS; ++t)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pf[t][j] = (T)s[t >> 1][8 * (t & 1) + j];
+  };
+
+  // Software pipeline over key tiles.  Iteration j holds the scores S_j of tile j and
+  // the probabilities P_{j-1} of the previous tile; it runs
+  //   A: O += V_{j-1} P_{j-1} (MFMA)     beside   row max of S_j and the rescale (VALU)
+  //   B: S_{j+1} = K_{j+1} Q^T (MFMA)    beside   P_j = exp2(S_j - max), row sums (VALU)
+  // so every MFMA burst has independent VALU work next to it.  K runs two tiles ahead
+  // of the scores and V one tile behind: iteration j starts the LDS-DMA of K_{j+2} into
+  // kl[j % 2] (last read as K_j in iteration j - 1) and of V_j into vl[j % 2] (last read
+  // as V_{j-2} in iteration j - 1), and ends by waiting for them and the barrier.
+  f32x16 s_cur[NMT], s_nxt[NMT];
+  frag pf[NPS];
+  if (n_tiles > 0) {
+    dma_k(0, kl[0]);
+    dma_k(1, kl[1]);
+  }
+  // Q and the first K tiles are in place: drain every counter once here so that the
+  // loop's only outstanding global loads are its own prefetches.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (n_tiles > 0) qk(s_cur, kl[0]);
+  __syncthreads();  // kl[0] is refilled by the first iteration
+
+  auto step = [&](int j, auto masked, auto has_prev, auto has_next) {
+    dma_k(j + 2, kl[j & 1]);
+    dma_v(j, vl[j & 1]);
+    if constexpr (decltype(masked)::value) mask_tile<NMT>(s_cur, j * BN, Lk, r0 + lq + off, p.causal, lh);
+    if constexpr (decltype(has_prev)::value) pv(pf, vl[(j - 1) & 1]);
+    tile_max_rescale<NMT, NDT>(s_cur, o, m, lsum, c_log2);
+    if constexpr (decltype(has_next)::value) qk(s_nxt, kl[(j + 1) & 1]);
+    tile_exp<NMT>(s_cur, m, lsum, c_log2);
+    to_frags(s_cur, pf);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if constexpr (decltype(has_next)::value) {
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt) s_cur[mt] = s_nxt[mt];
+    }
+  };
+  using F = std::false_type;
+  using Tr = std::true_type;
+  if (n_tiles == 1) {
+    if (n_free >= 1) step(0, F{}, F{}, F{}); else step(0, Tr{}, F{}, F{});
+  } else if (n_tiles > 1) {
+    if (n_free >= 1) step(0, F{}, F{}, Tr{}); else step(0, Tr{}, F{}, Tr{});
+    int j = 1;
+    for (; j < min(n_free, n_tiles - 1); ++j) step(j, F{}, Tr{}, Tr{});
+    for (; j < n_tiles - 1; ++j) step(j, Tr{}, Tr{}, Tr{});
+    if (n_tiles - 1 < n_free) step(n_tiles - 1, F{}, Tr{}, F{}); else step(n_tiles - 1, Tr{}, Tr{}, F{});
+  }
+  if (n_tiles > 0) pv(pf, vl[(n_tiles - 1) & 1]);
 
   // epilogue: combine the lane pair's partial sums, normalise, write out and LSE
   const float ltot = pair_sum(lsum);
