@@ -129,6 +129,25 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, int v
                                            0, 0, 0);
 }
 
+// Instruction-scheduling groups for __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedValu = 0x002 | 0x400;  // VALU including transcendentals
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
+
+// Orders the current scheduling region as: `pre` LDS reads, then `n` times
+// {1 MFMA, `rd` LDS reads, `va` VALU ops}.  Keeps fragment reads a few MFMAs ahead of
+// their use and puts independent VALU work behind every MFMA so both pipes stay busy.
+template <int n, int pre, int rd, int va>
+__device__ __forceinline__ void sched_interleave() {
+  __builtin_amdgcn_sched_group_barrier(kSchedDsRead, pre, 0);
+#pragma unroll
+  for (int i = 0; i < n; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, rd, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedValu, va, 0);
+  }
+}
+
 // True when any lane of the wavefront has `p` set (wave-uniform result).
 __device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 
@@ -442,12 +461,20 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
   auto step = [&](int j, auto masked, auto has_prev, auto has_next) {
     dma_k(j + 2, kl[j & 1]);
     dma_v(j, vl[j & 1]);
+    __builtin_amdgcn_sched_barrier(0);
+    // phase A: PV of the previous tile beside the row max of this one
     if constexpr (decltype(masked)::value) mask_tile<NMT>(s_cur, j * BN, Lk, r0 + lq + off, p.causal, lh);
-    if constexpr (decltype(has_prev)::value) pv(pf, vl[(j - 1) & 1]);
+    if constexpr (decltype(has_prev)::value) {
+      pv(pf, vl[(j - 1) & 1]);
+      sched_interleave<NDT * NPS, 4, 2, 2>();
+    }
     tile_max_rescale<NMT, NDT>(s_cur, o, m, lsum, c_log2);
+    // phase B: QK of the next tile beside the exponentials of this one
     if constexpr (decltype(has_next)::value) qk(s_nxt, kl[(j + 1) & 1]);
     tile_exp<NMT>(s_cur, m, lsum, c_log2);
     to_frags(s_cur, pf);
+    if constexpr (decltype(has_next)::value) sched_interleave<NMT * NKS, 3, 1, 8>();
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if constexpr (decltype(has_next)::value) {
@@ -469,6 +496,224 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
   if (n_tiles > 0) pv(pf, vl[(n_tiles - 1) & 1]);
 
   // epilogue: combine the lane pair's partial sums, normalise, write out and LSE
+  const float ltot = pair_sum(lsum);
+  const float inv = ltot > 0.f ? 1.0f / ltot : 0.f;
+  const int row = r0 + lq;
+  if (row < Lq) {
+    T* og = reinterpret_cast<T*>(p.out) + (int64_t)(qs + row) * p.o_rs + (int64_t)head * p.o_hs;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        typedef T t4 __attribute__((ext_vector_type(4)));
+        t4 w = {(T)(o[dt][4 * g + 0] * inv), (T)(o[dt][4 * g + 1] * inv),
+                (T)(o[dt][4 * g + 2] * inv), (T)(o[dt][4 * g + 3] * inv)};
+        *reinterpret_cast<t4*>(og + 32 * dt + 8 * g + 4 * lh) = w;
+      }
+    if (lh == 0) {
+      const float lse = ltot > 0.f ? m * p.scale + logf(ltot) : -INFINITY;
+      p.lse[(int64_t)(qs + row) * p.lse_rs + head] = lse;
+    }
+  }
+}
+
+//--------------------------------------------------------------------------------------
+// bf16 / fp16 kernel, head dim <= 128: eight-wavefront ping-pong
+//
+// A workgroup is 8 wavefronts, two per SIMD: group 0 (wavefronts 0-3) and group 1 (4-7),
+// each wavefront owning 32 query rows of one head; the K/V tiles in LDS are shared by all
+// eight, so one tile feeds 256 query rows.  Every wavefront alternates
+//   MFMA phase j:  S_j = K_j Q^T  and  O += V_{j-1} P_{j-1}      (32 MFMAs)
+//   VALU phase j:  P_j = softmax(S_j) with the rescale of O       (~150 VALU ops)
+// with a workgroup barrier after each phase.  Group 1 starts one phase late, so on every
+// SIMD one wavefront is always in its MFMA phase (raised issue priority) while the other
+// runs its softmax: the MFMA pipe never waits for the exponentials.
+//
+// Tiles are triple-buffered (tile t in slot t % 3).  Counting phases from 0 (group 0's
+// first MFMA phase), K_t is read in phases 2t (group 0) and 2t+1 (group 1), V_t in phases
+// 2t+2 and 2t+3.  Group 1 loads K_{j+3} during its VALU phase j (phase 2j+2, after the
+// last read of K_j, its slot) and group 0 loads V_{j+1} during its VALU phase j (phase
+// 2j+1, after the last read of V_{j-2}, its slot); each wavefront waits for its own
+// LDS-DMA at the end of its next phase, so the data is published by that phase's
+// barrier, at least one phase before it is read.
+//--------------------------------------------------------------------------------------
+constexpr int kPPWaves = 8;
+constexpr int kPPThreads = kPPWaves * 64;
+
+template <typename T, int D, int HP>
+__global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_pp(AttnParams p) {
+  using Ops = MfmaOps<T>;
+  using frag = typename Ops::frag;
+  constexpr int BN = kBN;
+  constexpr int RB = kPPWaves / HP;     // 32-row blocks per workgroup
+  constexpr int CH = D / 8;             // 16-byte chunks per K / V row
+  constexpr int NLD = BN * CH / 64;     // wave-wide 1 KB LDS-DMA loads per tile (K or V)
+  constexpr int NMT = BN / 32;
+  constexpr int NDT = D / 32;
+  constexpr int NKS = D / 16;
+  constexpr int NPS = BN / 16;
+  constexpr int KX = (CH >= 16 ? 16 : CH) - 1;
+  static_assert(D <= 128, "ping-pong kernel holds one 32 x D output tile per wavefront");
+  static_assert(NLD % 4 == 0 && NLD % kPPWaves == 0, "tile loads must split over the wavefronts");
+
+  // Row-major [BN][D] tiles with XOR-swizzled 16-byte chunks (as in attn_fwd_16bit).
+  __shared__ __attribute__((aligned(1024))) T kl[3][BN * D];
+  __shared__ __attribute__((aligned(1024))) T vl[3][BN * D];
+
+  int hg, seq, rt;
+  decode_block(p, hg, seq, rt);
+  int qs, Lq, ks, Lk;
+  seq_range(p.cu_q, seq, p.total_q, p.q_sel, qs, Lq);
+  seq_range(p.cu_k, seq, p.total_k, p.k_sel, ks, Lk);
+  const int row_tile0 = rt * RB * 32;
+  if (row_tile0 >= Lq) return;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int grp = wave >> 2;     // ping-pong group
+  const int wi = wave & 3;       // index inside the group
+  const int lane = tid & 63;
+  const int lq = lane & 31;
+  const int lh = lane >> 5;
+  const int groups_per_kv = p.group / HP;
+  const int kvh = hg / groups_per_kv;
+  const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
+  const int r0 = row_tile0 + (wave / HP) * 32;
+  const int off = Lk - Lq;
+
+  int n_tiles = (Lk + BN - 1) / BN;
+  if (p.causal) {
+    const int last_row = min(row_tile0 + RB * 32, Lq) - 1;
+    const int kmax = last_row + off;
+    n_tiles = kmax < 0 ? 0 : min(n_tiles, kmax / BN + 1);
+  }
+  const int n_free = mask_free_tiles(n_tiles, Lk, p.causal, row_tile0, off);
+
+  const T* __restrict__ qg = reinterpret_cast<const T*>(p.q);
+  const T* __restrict__ kg = reinterpret_cast<const T*>(p.k);
+  const T* __restrict__ vg = reinterpret_cast<const T*>(p.v);
+
+  frag qf[NKS];
+  {
+    const int64_t rsb = p.q_rs * (int64_t)sizeof(T);
+    const auto rq = make_rsrc(qg + (int64_t)(qs + r0) * p.q_rs + (int64_t)head * p.q_hs,
+                              (int64_t)min(Lq - r0, 32) * rsb);
+#pragma unroll
+    for (int t = 0; t < NKS; ++t)
+      qf[t] = __builtin_bit_cast(frag, bload128(rq, lq * (int)rsb + (int)sizeof(T) * (16 * t + 8 * lh)));
+  }
+
+  const T* kbase = kg + (int64_t)ks * p.k_rs + (int64_t)kvh * p.k_hs;
+  const T* vbase = vg + (int64_t)ks * p.v_rs + (int64_t)kvh * p.v_hs;
+  const int k_rsb = (int)(p.k_rs * (int64_t)sizeof(T));
+  const int v_rsb = (int)(p.v_rs * (int64_t)sizeof(T));
+  // LDS-DMA of one K / V tile by `nw` wavefronts (this one is number `w`): its load n fills
+  // LDS chunks [64 (w + nw n), +64) of the tile (see attn_fwd_16bit).
+  auto dma_k = [&](int tile, T* dst, int w, auto nw) {
+    const int kb = tile * BN;
+    const auto rk = make_rsrc(kbase + (int64_t)kb * p.k_rs, (int64_t)min(Lk - kb, BN) * k_rsb);
+#pragma unroll
+    for (int n = 0; n < NLD / decltype(nw)::value; ++n) {
+      const int P = 64 * (w + decltype(nw)::value * n) + lane;
+      const int row = P / CH, c = (P % CH) ^ (row & KX);
+      dma16(rk, dst + 512 * (w + decltype(nw)::value * n), row * k_rsb + 16 * c);
+    }
+  };
+  auto dma_v = [&](int tile, T* dst, int w, auto nw) {
+    const int kb = tile * BN;
+    const auto rv = make_rsrc(vbase + (int64_t)kb * p.v_rs, (int64_t)min(Lk - kb, BN) * v_rsb);
+#pragma unroll
+    for (int n = 0; n < NLD / decltype(nw)::value; ++n) {
+      const int P = 64 * (w + decltype(nw)::value * n) + lane;
+      const int row = P / CH, c = (P % CH) ^ ((4 * (row & 3)) & (CH - 1));
+      dma16(rv, dst + 512 * (w + decltype(nw)::value * n), row * v_rsb + 16 * c);
+    }
+  };
+
+  int k_off[NKS];
+#pragma unroll
+  for (int t = 0; t < NKS; ++t) k_off[t] = lq * D + 8 * ((2 * t + lh) ^ (lq & KX));
+  const int j16 = lane & 15;
+  int v_off[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+    const int c = 4 * dt + 2 * ((lane >> 4) & 1) + ((j16 & 3) >> 1);
+    v_off[dt] = (4 * lh + (j16 >> 2)) * D + 8 * (c ^ ((4 * (j16 >> 2)) & (CH - 1))) + 4 * (j16 & 1);
+  }
+
+  const float c_log2 = p.scale * kLog2e;
+  f32x16 o[NDT];
+#pragma unroll
+  for (int i = 0; i < NDT; ++i) o[i] = f32x16{};
+  float m = -INFINITY;
+  float lsum = 0.f;
+  f32x16 s[NMT];
+  frag pf[NPS];
+
+  auto qk = [&](const T* ksrc) {
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt) {
+      s[mt] = f32x16{};
+#pragma unroll
+      for (int t = 0; t < NKS; ++t) {
+        const frag a = *reinterpret_cast<const frag*>(ksrc + k_off[t] + 32 * mt * D);
+        s[mt] = Ops::mma(a, qf[t], s[mt]);
+      }
+    }
+  };
+  auto pv = [&](const T* vsrc) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int t = 0; t < NPS; ++t) {
+        const s16x4 lo = lds_tr16(vsrc + v_off[dt] + 16 * t * D);
+        const s16x4 hi = lds_tr16(vsrc + v_off[dt] + (16 * t + 8) * D);
+        const frag a = __builtin_bit_cast(frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[dt] = Ops::mma(a, pf[t], o[dt]);
+      }
+  };
+
+  std::integral_constant<int, kPPWaves> all8;
+  std::integral_constant<int, 4> four;
+  if (n_tiles > 0) {
+    dma_k(0, kl[0], wave, all8);
+    dma_k(1, kl[1], wave, all8);
+    dma_k(2, kl[2], wave, all8);
+    dma_v(0, vl[0], wave, all8);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (grp == 1) __syncthreads();  // group 1 runs one phase behind group 0
+
+  for (int j = 0; j < n_tiles; ++j) {
+    // MFMA phase
+    __builtin_amdgcn_s_setprio(1);
+    qk(kl[j % 3]);
+    if (j > 0) pv(vl[(j - 1) % 3]);
+    __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's LDS-DMA from its previous VALU phase
+    __syncthreads();
+    // VALU phase
+    if (grp == 1) dma_k(j + 3, kl[j % 3], wi, four);
+    else dma_v(j + 1, vl[(j + 1) % 3], wi, four);
+    if (j >= n_free) mask_tile<NMT>(s, j * BN, Lk, r0 + lq + off, p.causal, lh);
+    tile_max_rescale<NMT, NDT>(s, o, m, lsum, c_log2);
+    tile_exp<NMT>(s, m, lsum, c_log2);
+#pragma unroll
+    for (int t = 0; t < NPS; ++t)
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) pf[t][jj] = (T)s[t >> 1][8 * (t & 1) + jj];
+    __syncthreads();
+  }
+  if (n_tiles > 0) {
+    __builtin_amdgcn_s_setprio(1);
+    pv(vl[(n_tiles - 1) % 3]);
+    __builtin_amdgcn_s_setprio(0);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (grp == 0) __syncthreads();  // both groups pass the same number of barriers
+
   const float ltot = pair_sum(lsum);
   const float inv = ltot > 0.f ? 1.0f / ltot : 0.f;
   const int row = r0 + lq;
@@ -740,32 +985,51 @@ int heads_per_wg(int group) {
 
 typedef void (*KernelFn)(AttnParams);
 
+struct KernelChoice {
+  KernelFn fn = nullptr;
+  int threads = 0;   // workgroup size
+  int rows = 0;      // query rows per workgroup (per head)
+};
+
 template <typename T>
-KernelFn pick16(int d, int hp) {
-#define FA4CP_PICK(DD)                          \
-  if (d == DD) {                                \
-    if (hp == 4) return attn_fwd_16bit<T, DD, 4>; \
-    if (hp == 2) return attn_fwd_16bit<T, DD, 2>; \
-    return attn_fwd_16bit<T, DD, 1>;            \
+KernelChoice pick16(int d, int hp) {
+  KernelChoice k;
+  if (d == 64 || d == 128) {
+    k.threads = kPPThreads;
+    k.rows = 32 * kPPWaves / hp;
+#define FA4CP_PICK(DD)                                  \
+  if (d == DD) {                                        \
+    if (hp == 4) k.fn = attn_fwd_16bit_pp<T, DD, 4>;    \
+    else if (hp == 2) k.fn = attn_fwd_16bit_pp<T, DD, 2>; \
+    else k.fn = attn_fwd_16bit_pp<T, DD, 1>;            \
   }
-  FA4CP_PICK(64)
-  FA4CP_PICK(128)
-  FA4CP_PICK(256)
+    FA4CP_PICK(64)
+    FA4CP_PICK(128)
 #undef FA4CP_PICK
-  return nullptr;
+  } else if (d == 256) {
+    k.threads = kThreads;
+    k.rows = 32 * kWaves / hp;
+    if (hp == 4) k.fn = attn_fwd_16bit<T, 256, 4>;
+    else if (hp == 2) k.fn = attn_fwd_16bit<T, 256, 2>;
+    else k.fn = attn_fwd_16bit<T, 256, 1>;
+  }
+  return k;
 }
 
-KernelFn pick8(int d, int hp) {
-#define FA4CP_PICK(DD)                        \
-  if (d == DD) {                              \
-    if (hp == 4) return attn_fwd_e4m3<DD, 4>; \
-    if (hp == 2) return attn_fwd_e4m3<DD, 2>; \
-    return attn_fwd_e4m3<DD, 1>;              \
+KernelChoice pick8(int d, int hp) {
+  KernelChoice k;
+  k.threads = kThreads;
+  k.rows = 32 * kWaves / hp;
+#define FA4CP_PICK(DD)                                \
+  if (d == DD) {                                      \
+    if (hp == 4) k.fn = attn_fwd_e4m3<DD, 4>;         \
+    else if (hp == 2) k.fn = attn_fwd_e4m3<DD, 2>;    \
+    else k.fn = attn_fwd_e4m3<DD, 1>;                 \
   }
   FA4CP_PICK(128)
   FA4CP_PICK(256)
 #undef FA4CP_PICK
-  return nullptr;
+  return k;
 }
 
 }  // namespace
@@ -797,17 +1061,16 @@ extern "C" int fa4cp_attn_fwd(const fa4cp_attn_args* a, void* stream) {
   const int max_q = (a->q_sel == FA4CP_SEL_ALL) ? max_q_full : (max_q_full + 1) / 2;
   const int group = a->h_q / a->h_kv;
   const int hp = heads_per_wg(group);
-  const int rb = kWaves / hp;
   const int d = a->d;
 
-  KernelFn fn = nullptr;
+  KernelChoice kc;
   switch (a->dtype) {
-    case FA4CP_BF16: fn = pick16<__bf16>(d, hp); break;
-    case FA4CP_FP16: fn = pick16<_Float16>(d, hp); break;
-    case FA4CP_E4M3: fn = pick8(d, hp); break;
+    case FA4CP_BF16: kc = pick16<__bf16>(d, hp); break;
+    case FA4CP_FP16: kc = pick16<_Float16>(d, hp); break;
+    case FA4CP_E4M3: kc = pick8(d, hp); break;
     default: return set_error(FA4CP_EUNSUPPORTED, "attn_fwd: unsupported dtype %d", a->dtype);
   }
-  if (fn == nullptr)
+  if (kc.fn == nullptr)
     return set_error(FA4CP_EUNSUPPORTED, "attn_fwd: head dim %d not implemented for dtype %d "
                      "(bf16/fp16: 64, 128, 256; e4m3: 128, 256)", d, a->dtype);
   // Fragment loads are 16 bytes wide (8 bytes for e4m3 V) and outputs are written 4
@@ -840,12 +1103,12 @@ extern "C" int fa4cp_attn_fwd(const fa4cp_attn_args* a, void* stream) {
   p.causal = a->causal ? 1 : 0; p.q_sel = a->q_sel; p.k_sel = a->k_sel;
   p.scale = a->softmax_scale;
   p.qd = a->q_descale; p.kd = a->k_descale; p.vd = a->v_descale;
-  p.n_rt = (max_q + 32 * rb - 1) / (32 * rb);
+  p.n_rt = (max_q + kc.rows - 1) / kc.rows;
   p.n_hg = a->h_kv * (group / hp);
   const int64_t blocks = (int64_t)p.n_hg * nseq * p.n_rt;
   if (blocks == 0) return FA4CP_OK;
   if (blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "attn_fwd: grid too large");
   p.n_blocks = (int)blocks;
-  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kThreads), 0, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(kc.fn, dim3((unsigned)blocks), dim3(kc.threads), 0, (hipStream_t)stream, p);
   return check_launch("attn_fwd");
 }
