@@ -253,7 +253,7 @@ def main():
                    "global_batch": 1, "seq_len": N, "cp_size": CP, "cp_rank": rank,
                    "h_q": HQ, "h_kv": HKV, "head_dim": D, "parallelism": "cp8 (one rank's share on 1 GPU)"},
         "frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
-        "roofline": {"bound": "mfma", "kernel": "attn_fwd_16bit<bf16,128,4>",
+        "roofline": {"bound": "mfma", "kernel": "attn_fwd_16bit_pp<bf16,128,4>",
                      "achieved": round(attn_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
                      "algorithmic_per_launch": f"{per_launch / 1e12:.4f} TFLOP "
@@ -265,6 +265,22 @@ def main():
                   "frac": round(merge_gbs / PEAK_HBM_GBS, 4), "launches": clock.count("merge_inplace")},
     }
 
+    # zig-zag gather of the full q (bf16, 1 GiB -> 128 MiB)
+    zz = []
+    for _ in range(3):
+        zigzag_shard(q_full, rank, CP)
+    for _ in range(10):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        zigzag_shard(q_full, rank, CP)
+        e.record()
+        zz.append((s, e))
+    torch.cuda.synchronize()
+    zms = sum(s.elapsed_time(e) for s, e in zz) / len(zz)
+    zbytes = 2.0 * t_local * HQ * D * 2
+    result["zigzag"] = {"kernel": "shard_kernel<u32x4>", "avg_launch_ms": round(zms, 4),
+                        "bytes": round(zbytes), "achieved_GBs": round(zbytes / (zms * 1e-3) / 1e9, 1),
+                        "frac": round(zbytes / (zms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
     if not args.skip_extra:
         # rank 7 (only front-half steps)
         lq7 = zigzag_shard(q_full, 7, CP)
@@ -282,23 +298,7 @@ def main():
         result["batched_bf16"] = {"ms_per_step": round(secb * 1e3, 3), "TFLOP/s": round(flops / secb / 1e12, 2),
                                   "merge_states_ms": round(ms_ms, 4), "merge_states_bytes": round(bb),
                                   "merge_states_GBs": round(bb / (ms_ms * 1e-3) / 1e9, 1)}
-        # zig-zag gather of the full q (bf16, 1 GiB -> 128 MiB)
-        zz = []
-        for _ in range(3):
-            zigzag_shard(q_full, rank, CP)
-        for _ in range(10):
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            zigzag_shard(q_full, rank, CP)
-            e.record()
-            zz.append((s, e))
-        torch.cuda.synchronize()
-        zms = sum(s.elapsed_time(e) for s, e in zz) / len(zz)
-        zbytes = 2.0 * t_local * HQ * D * 2
-        result["zigzag"] = {"kernel": "shard_kernel<u32x4>", "avg_launch_ms": round(zms, 4),
-                            "bytes": round(zbytes), "achieved_GBs": round(zbytes / (zms * 1e-3) / 1e9, 1),
-                            "frac": round(zbytes / (zms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
-        del q_full, lq7
+        del lq7
         # fp8 sweep
         q8, ring8, desc = make_fp8_inputs(rank)
         cfg8 = RingConfig(cp_size=CP, cp_rank=rank)
@@ -313,7 +313,7 @@ def main():
                          "attn_TFLOP/s": round(per_launch / (a8 * 1e-3) / 1e12, 2),
                          "attn_frac": round(per_launch / (a8 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)}
         del q8, ring8
-    del ring, lq
+    del ring, lq, q_full
     torch.cuda.synchronize()
 
     if not args.no_cpu_baseline:

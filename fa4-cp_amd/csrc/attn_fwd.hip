@@ -529,16 +529,19 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
 // SIMD one wavefront is always in its MFMA phase (raised issue priority) while the other
 // runs its softmax: the MFMA pipe never waits for the exponentials.
 //
-// Tiles are triple-buffered (tile t in slot t % 3).  Counting phases from 0 (group 0's
-// first MFMA phase), K_t is read in phases 2t (group 0) and 2t+1 (group 1), V_t in phases
-// 2t+2 and 2t+3.  Group 1 loads K_{j+3} during its VALU phase j (phase 2j+2, after the
-// last read of K_j, its slot) and group 0 loads V_{j+1} during its VALU phase j (phase
-// 2j+1, after the last read of V_{j-2}, its slot); each wavefront waits for its own
-// LDS-DMA at the end of its next phase, so the data is published by that phase's
-// barrier, at least one phase before it is read.
+// K tiles are triple-buffered (tile t in slot t % 3).  Counting phases from 0 (group 0's
+// first MFMA phase), K_t is read in phases 2t (group 0) and 2t+1 (group 1); group 1 loads
+// K_{j+3} during its VALU phase j (phase 2j+2, after the last read of K_j, its slot).
+// V_t arrives row-major (LDS-DMA by group 0 in phase 2t-1, published at the end of phase
+// 2t) and is transposed once, by group 0 in phase 2t+1, into a padded V^T tile that both
+// groups read with plain 16-byte loads in phases 2t+2 and 2t+3: the transposing LDS reads
+// are slow, and doing them once per workgroup instead of once per wavefront keeps them
+// off the MFMA phases.  Each wavefront waits for its own LDS-DMA at the end of its next
+// phase, so data is published by that phase's barrier, at least one phase before use.
 //--------------------------------------------------------------------------------------
 constexpr int kPPWaves = 8;
 constexpr int kPPThreads = kPPWaves * 64;
+constexpr int kPPReadAhead = 4;  // LDS fragment reads issued ahead of the MFMA chain
 
 template <typename T, int D, int HP>
 __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_pp(AttnParams p) {
@@ -556,9 +559,15 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_pp(AttnParams p)
   static_assert(D <= 128, "ping-pong kernel holds one 32 x D output tile per wavefront");
   static_assert(NLD % 4 == 0 && NLD % kPPWaves == 0, "tile loads must split over the wavefronts");
 
-  // Row-major [BN][D] tiles with XOR-swizzled 16-byte chunks (as in attn_fwd_16bit).
+  // K: row-major [BN][D] tiles with XOR-swizzled 16-byte chunks (as in attn_fwd_16bit),
+  // three slots.  V arrives row-major in vr (two slots) and is transposed once per tile into
+  // vt: [D][VTS] rows of keys, padded so that fragment reads are conflict free, with the
+  // keys of every 16-key group in the accumulator order {0-3, 8-11 | 4-7, 12-15}, so the
+  // PV A fragment of lane (d, h) for k-step t is the 16 bytes at vt[d][16t + 8h].
+  constexpr int VTS = BN + 8;
   __shared__ __attribute__((aligned(1024))) T kl[3][BN * D];
-  __shared__ __attribute__((aligned(1024))) T vl[3][BN * D];
+  __shared__ __attribute__((aligned(1024))) T vr[2][BN * D];
+  __shared__ __attribute__((aligned(1024))) T vt[2][D * VTS];
 
   int hg, seq, rt;
   decode_block(p, hg, seq, rt);
@@ -661,16 +670,30 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_pp(AttnParams p)
       }
     }
   };
+  const int vt_lane = lq * VTS + 8 * lh;
   auto pv = [&](const T* vsrc) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int t = 0; t < NPS; ++t) {
-        const s16x4 lo = lds_tr16(vsrc + v_off[dt] + 16 * t * D);
-        const s16x4 hi = lds_tr16(vsrc + v_off[dt] + (16 * t + 8) * D);
-        const frag a = __builtin_bit_cast(frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        const frag a = *reinterpret_cast<const frag*>(vsrc + vt_lane + 32 * dt * VTS + 16 * t);
         o[dt] = Ops::mma(a, pf[t], o[dt]);
       }
+  };
+  // Transposes the row-major V tile at vsrc into vt layout at vdst: this wavefront (one
+  // of the four of group 0) builds fragments (dt, t) with dt * NPS + t = wi, wi + 4, ...
+  // from two transposing reads each and stores them with one 16-byte write.
+  auto transpose_v = [&](const T* vsrc, T* vdst) {
+#pragma unroll
+    for (int f = 0; f < NDT * NPS / 4; ++f) {
+      const int fi = wi + 4 * f;
+      const int dt = fi / NPS, t = fi % NPS;
+      const s16x4 lo = lds_tr16(vsrc + v_off[dt] + 16 * t * D);
+      const s16x4 hi = lds_tr16(vsrc + v_off[dt] + (16 * t + 8) * D);
+      typedef short s16x8 __attribute__((ext_vector_type(8)));
+      *reinterpret_cast<s16x8*>(vdst + (32 * dt + lq) * VTS + 16 * t + 8 * lh) =
+          __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
   };
 
   std::integral_constant<int, kPPWaves> all8;
@@ -679,7 +702,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_pp(AttnParams p)
     dma_k(0, kl[0], wave, all8);
     dma_k(1, kl[1], wave, all8);
     dma_k(2, kl[2], wave, all8);
-    dma_v(0, vl[0], wave, all8);
+    dma_v(0, vr[0], wave, all8);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -689,13 +712,28 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_pp(AttnParams p)
     // MFMA phase
     __builtin_amdgcn_s_setprio(1);
     qk(kl[j % 3]);
-    if (j > 0) pv(vl[(j - 1) % 3]);
+    if (j > 0) {
+      pv(vt[(j - 1) & 1]);
+      // fragment reads run kPPReadAhead MFMAs ahead of their use, hiding LDS latency
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kPPReadAhead, 0);
+#pragma unroll
+      for (int i = 0; i < NMT * NKS + NDT * NPS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+    }
     __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_s_waitcnt(0);  // this wavefront's LDS-DMA from its previous VALU phase
     __syncthreads();
     // VALU phase
-    if (grp == 1) dma_k(j + 3, kl[j % 3], wi, four);
-    else dma_v(j + 1, vl[(j + 1) % 3], wi, four);
+    if (grp == 1) {
+      dma_k(j + 3, kl[j % 3], wi, four);
+    } else {
+      // V_j (published at the end of phase 2j) becomes vt[j % 2], last read as V_{j-2}
+      // in phase 2j - 1; V_{j+1} refills vr[(j + 1) % 2], transposed in phase 2j - 1.
+      transpose_v(vr[j & 1], vt[j & 1]);
+      dma_v(j + 1, vr[(j + 1) & 1], wi, four);
+    }
     if (j >= n_free) mask_tile<NMT>(s, j * BN, Lk, r0 + lq + off, p.causal, lh);
     tile_max_rescale<NMT, NDT>(s, o, m, lsum, c_log2);
     tile_exp<NMT>(s, m, lsum, c_log2);
@@ -707,7 +745,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_pp(AttnParams p)
   }
   if (n_tiles > 0) {
     __builtin_amdgcn_s_setprio(1);
-    pv(vl[(n_tiles - 1) % 3]);
+    pv(vt[(n_tiles - 1) & 1]);
     __builtin_amdgcn_s_setprio(0);
   }
   __builtin_amdgcn_s_waitcnt(0);

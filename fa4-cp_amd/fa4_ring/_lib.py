@@ -14,7 +14,8 @@ from typing import Optional
 import torch
 
 LIB_NAME = "libfa4cp.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# FA4CP_LIB selects another build of the library (the in-tree one by default)
+LIB_PATH = os.environ.get("FA4CP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 ABI_VERSION = 1
 
 # element types (FA4CP_*)
