@@ -36,6 +36,12 @@ PEAK_HBM_GBS = 8000.0
 
 N, CP, HQ, HKV, D = 131072, 8, 32, 8, 128
 
+# HBM bytes per attention launch of the rank-3 sweep (mean over its 8 launches), from two
+# rocprofv3 counter passes over this script: FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the
+# factors being what those counters read for the zig-zag gather (a plain copy of known size).
+# The summary with both commands is under profiles/.
+ATTN_TRAFFIC_BYTES_RANK3 = 466728 * 1024
+
 
 def sweep_flops(t_local: int, cp: int, hq: int, d: int) -> float:
     """Causal-adjusted FLOPs of one rank's sweep: every step is 4 * (T*T/2) * D * H_q
@@ -255,7 +261,8 @@ def main():
         "frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
         "roofline": {"bound": "mfma", "kernel": "attn_fwd_16bit_pp<bf16,128,4>",
                      "achieved": round(attn_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": ATTN_TRAFFIC_BYTES_RANK3 if rank == 3 else None,
                      "algorithmic_per_launch": f"{per_launch / 1e12:.4f} TFLOP "
                                                "(4*Tq*Tk*D*H_q, halved for the causal step)",
                      "avg_launch_ms": round(attn_ms, 4), "launches": clock.count("attn")},

@@ -8,11 +8,13 @@
 //   step s>rank   causal=0, q_sel=BACK_HALF, k_sel=ALL         (no Q gather, no padding)
 //
 // Work decomposition
-//   A workgroup is 4 wavefronts.  It owns HP query heads that share one kv head and RB
-//   blocks of 32 query rows (HP * RB = 4); wavefront w computes head w % HP for rows
-//   block w / HP.  K/V tiles of 64 keys are staged once in LDS and read by all four
-//   wavefronts, so a tile feeds 128 query rows.  Two workgroups share a CU, so each SIMD
-//   interleaves the MFMA work of one wavefront with the softmax of the other.
+//   Every wavefront owns 32 query rows of one query head.  A workgroup owns HP query heads
+//   that share one kv head, and its wavefronts split as HP heads x (waves / HP) row blocks,
+//   so one K/V tile staged in LDS feeds all of them.  Three kernels:
+//     attn_fwd_16bit_pp  bf16/fp16, D = 64 or 128: 8 wavefronts in two ping-pong groups
+//                        (256 query rows per tile), two workgroups per CU
+//     attn_fwd_16bit     bf16/fp16, D = 256: 4 wavefronts, software-pipelined tile loop
+//     attn_fwd_e4m3      OCP e4m3, D = 128 or 256: 4 wavefronts
 //
 // Per-wavefront math (32 queries x 64 keys per tile), written transposed:
 //   S^T = K Q^T   with v_mfma_f32_32x32x16_{bf16,f16} (32x32x64_f8f6f4 for e4m3);
@@ -25,11 +27,12 @@
 //   A fragment with exactly those keys comes from two ds_read_b64_tr_b16 transposing LDS
 //   reads of the row-major V tile (each returns 4 consecutive keys of one column).
 //
-// LDS (double buffered, one barrier per tile): K and V tiles row-major exactly as in
-// HBM, copied with 16-byte loads and stores; rows are padded (K by 16 bytes, V by 64)
-// so the fragment reads are bank-conflict free and every fragment address is a per-lane
-// base plus a compile-time offset.  Tiles that need no mask (all but the causal diagonal
-// and a partial last tile) run a loop without any masking code.
+// LDS: K and V tiles of 64 keys arrive by LDS-DMA (buffer loads straight into LDS, rows
+// past a sequence's end read as zeros) into row-major tiles whose 16-byte chunks are
+// XOR-swizzled per row, so fragment reads are bank-conflict free and every fragment
+// address is a per-lane base plus a compile-time offset (the e4m3 kernel stages through
+// registers into padded tiles instead).  Tiles that need no mask (all but the causal
+// diagonal and a partial last tile) run a loop without any masking code.
 //
 // Softmax runs in the exp2 domain with scale * log2(e) (times the q/k descales) folded
 // into one FMA per score, and rescales the output only when the running max grows by

@@ -105,7 +105,7 @@ def test_merge_state_in_place(dtype, t, h, d):
     assert torch.equal(sd.cpu()[both], sa[both])
 
 
-@pytest.mark.parametrize("cu", [None, [0, 8, 20, 64]])
+@pytest.mark.parametrize("cu", [None, [0, 8, 20, 64], [0, 8, 8, 20, 64, 64]])
 @pytest.mark.parametrize("sel", [SEL_BACK_HALF, SEL_FRONT_HALF])
 def test_merge_state_in_place_half_rows(cu, sel):
     say(f"merge half rows cu={cu} sel={sel}")
@@ -165,6 +165,9 @@ ATTN_CASES = [
     (None, None, 8, 2, 128, False, SEL_ALL, SEL_FRONT_HALF, [0, 64, 200, 202, 460]),
     (None, None, 4, 4, 128, False, SEL_BACK_HALF, SEL_ALL, [0, 96, 100, 612]),
     (64, 96, 4, 2, 128, True, SEL_ALL, SEL_ALL, None),            # bottom-right causal
+    (None, None, 8, 2, 128, True, SEL_ALL, SEL_ALL, [0, 64, 64, 200, 200]),         # empty seqs
+    (None, None, 8, 2, 64, False, SEL_BACK_HALF, SEL_ALL, [0, 0, 130, 131, 260]),   # 1-row seq
+    (None, None, 4, 1, 128, False, SEL_ALL, SEL_FRONT_HALF, [0, 1, 1, 67]),         # no keys
 ]
 
 
@@ -214,6 +217,7 @@ FP8_CASES = [
     (384, 384, 16, 2, 256, True, SEL_ALL, SEL_ALL, None),
     (384, 384, 16, 2, 256, False, SEL_BACK_HALF, SEL_ALL, None),
     (None, None, 8, 8, 128, True, SEL_ALL, SEL_ALL, [0, 128, 136, 520]),
+    (None, None, 8, 2, 128, False, SEL_BACK_HALF, SEL_ALL, [0, 0, 256, 256, 390]),
 ]
 
 
