@@ -102,17 +102,6 @@ __device__ __forceinline__ float pair_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Raw buffer resource over `bytes` bytes at `base`: loads past the end return zero in
-// hardware, which is how rows beyond a sequence's end are read without a branch or a
-// select (and without making the compiler wait for the data at the load).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  const int n = bytes <= 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : (int)bytes);
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
-}
-__device__ __forceinline__ u32x4 bload128(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-}
-
 // Transposing LDS reads (gfx950).  Within each group of 16 lanes, with M[j] the 8 bytes at
 // lane j's address: ds_read_b64_tr_b16 gives lane i the 16-bit elements
 // M[4m + i/4][i % 4] for m = 0..3, and ds_read_b64_tr_b8 the bytes M[2m + i/8][i % 8] for

@@ -81,6 +81,36 @@ __device__ __forceinline__ void store8_f32<_Float16>(_Float16* p, const float (&
   *reinterpret_cast<f16x8*>(p) = a;
 }
 
+// Raw buffer resource over `bytes` bytes at `base`: loads past the end return zero in
+// hardware, which is how rows beyond a sequence's end are read without a branch or a
+// select (and without making the compiler wait for the data at the load).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int n = bytes <= 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : (int)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bload128(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+// Eight elements at byte offset `off` of buffer `r`, widened to fp32 (zeros past the end).
+template <typename T>
+__device__ __forceinline__ void bload8_f32(__amdgpu_buffer_rsrc_t r, int off, float (&out)[8]) {
+  if constexpr (sizeof(T) == 4) {
+    const f32x4 a = __builtin_bit_cast(f32x4, bload128(r, off));
+    const f32x4 b = __builtin_bit_cast(f32x4, bload128(r, off + 16));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[i] = a[i];
+      out[4 + i] = b[i];
+    }
+  } else {
+    typedef T t8 __attribute__((ext_vector_type(8)));
+    const t8 a = __builtin_bit_cast(t8, bload128(r, off));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = (float)a[i];
+  }
+}
+
 // Index of the packed sequence that contains `row`: the largest j with cu[j] <= row
 // (binary search over cu[0..nseq]).
 __device__ __forceinline__ int find_seq(const int32_t* __restrict__ cu, int nseq, int64_t row) {

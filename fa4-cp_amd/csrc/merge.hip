@@ -84,45 +84,85 @@ __global__ __launch_bounds__(kBlock) void merge_inplace_kernel(
   if (lane == 0) s[sidx] = m + logf(wa + wb);
 }
 
+constexpr int kStateChunk = 4;  // states whose loads are in flight together
+
+// S-way merge of one (row, head): 16 lanes, 8 elements of v per lane per pass.  States go
+// in chunks: the chunk's LSEs are loaded together, and unless all are -inf its v slices are
+// loaded together through a buffer resource over the row's states; a state with LSE -inf
+// (whose v may never have been written) and a state past num_states read past the end,
+// which returns zeros without touching memory.  Each chunk is folded into a running
+// (max, weight sum, accumulator) with an online rescale.  Weights use the hardware exp2
+// (relative error a few ulp; the sum and the final log are in fp32).
 template <typename T>
 __global__ __launch_bounds__(kBlock) void merge_states_kernel(
     const T* __restrict__ v, const float* __restrict__ s, T* __restrict__ vout,
     float* __restrict__ sout, int64_t n_groups, int num_states, int h, int d) {
+  constexpr int NQ = sizeof(T) == 4 ? 2 : 1;  // 16-byte loads per 8 elements
+  constexpr float kLog2e = 1.4426950408889634f;
   const int64_t g = (int64_t)blockIdx.x * (kBlock / kGroup) + (threadIdx.x / kGroup);
   const int lane = threadIdx.x % kGroup;
   if (g >= n_groups) return;
   const int64_t row = g / h;
   const int head = (int)(g - row * h);
-  const float* srow = s + row * (int64_t)num_states * h + head;
-  float m = -INFINITY;
-  for (int st = 0; st < num_states; ++st) m = fmaxf(m, srow[(int64_t)st * h]);
+  const auto rs = make_rsrc(s + row * (int64_t)num_states * h, (int64_t)num_states * h * 4);
+  const int64_t row_bytes = (int64_t)num_states * h * d * (int64_t)sizeof(T);
+  const auto rv = make_rsrc(v + row * (int64_t)num_states * h * d, row_bytes);
+  const int past_end = (int)row_bytes;  // < 2^31, checked by the host
   T* vo = vout + (row * h + head) * (int64_t)d;
-  if (m == -INFINITY) {
-    float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int c = lane * 8; c < d; c += kGroup * 8) store8_f32<T>(vo + c, z);
-    if (lane == 0 && sout != nullptr) sout[row * h + head] = -INFINITY;
-    return;
-  }
-  float wsum = 0.f;
-  for (int st = 0; st < num_states; ++st) {
-    const float ss = srow[(int64_t)st * h];
-    if (ss != -INFINITY) wsum += expf(ss - m);
-  }
-  const float inv = 1.0f / wsum;
+  float m = -INFINITY, wsum = 0.f;
   for (int c = lane * 8; c < d; c += kGroup * 8) {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int st = 0; st < num_states; ++st) {
-      const float ss = srow[(int64_t)st * h];
-      if (ss == -INFINITY) continue;
-      const float w = expf(ss - m) * inv;
-      float x[8];
-      load8_f32<T>(v + ((row * num_states + st) * h + head) * (int64_t)d + c, x);
+    m = -INFINITY;
+    wsum = 0.f;
+    for (int st0 = 0; st0 < num_states; st0 += kStateChunk) {
+      float sv[kStateChunk];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += w * x[i];
+      for (int i = 0; i < kStateChunk; ++i) {
+        const int st = st0 + i;
+        sv[i] = st < num_states
+                    ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, 4 * (st * h + head), 0, 0))
+                    : -INFINITY;
+      }
+      float cm = sv[0];
+#pragma unroll
+      for (int i = 1; i < kStateChunk; ++i) cm = fmaxf(cm, sv[i]);
+      if (cm == -INFINITY) continue;  // nothing to add from this chunk
+      u32x4 raw[kStateChunk][NQ];
+#pragma unroll
+      for (int i = 0; i < kStateChunk; ++i) {
+        const int off = sv[i] == -INFINITY
+                            ? past_end
+                            : (int)((((int64_t)(st0 + i) * h + head) * d + c) * (int64_t)sizeof(T));
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) raw[i][q] = bload128(rv, off + 16 * q);
+      }
+      const float nm = fmaxf(m, cm);
+      const float r = __builtin_amdgcn_exp2f((m - nm) * kLog2e);  // 0 while m is -inf
+      wsum *= r;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] *= r;
+#pragma unroll
+      for (int i = 0; i < kStateChunk; ++i) {
+        const float w = sv[i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((sv[i] - nm) * kLog2e);
+        wsum += w;
+        if constexpr (sizeof(T) == 4) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] += w * __uint_as_float(raw[i][e / 4][e % 4]);
+        } else {
+          typedef T t8 __attribute__((ext_vector_type(8)));
+          const t8 a = __builtin_bit_cast(t8, raw[i][0]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] += w * (float)a[e];
+        }
+      }
+      m = nm;
     }
+    const float inv = m == -INFINITY ? 0.f : 1.0f / wsum;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= inv;
     store8_f32<T>(vo + c, acc);
   }
-  if (lane == 0 && sout != nullptr) sout[row * h + head] = m + logf(wsum);
+  if (lane == 0 && sout != nullptr) sout[row * h + head] = m == -INFINITY ? -INFINITY : m + logf(wsum);
 }
 
 }  // namespace
@@ -183,6 +223,8 @@ extern "C" int fa4cp_merge_states(const void* v, const float* s, void* v_out, fl
   if (rows < 0 || num_states <= 0 || h <= 0 || d <= 0 || (d % 8) != 0)
     return set_error(FA4CP_EINVAL, "merge_states: bad shape rows=%lld states=%d h=%d d=%d",
                      (long long)rows, num_states, h, d);
+  if ((int64_t)num_states * h * d * 4 + 32 > 0x7fffffffLL)
+    return set_error(FA4CP_EINVAL, "merge_states: one row of states exceeds 2 GiB");
   const int64_t n_groups = rows * h;
   if (n_groups == 0) return FA4CP_OK;
   const int64_t blocks = (n_groups + (kBlock / kGroup) - 1) / (kBlock / kGroup);
