@@ -268,13 +268,14 @@ __device__ __forceinline__ void decode_block(const AttnParams& p, int& hg, int& 
   rt = p.n_rt - 1 - (r - seq * p.n_rt);
 }
 
-// Number of leading key tiles that need no mask for any row of the workgroup.
+// Number of leading key tiles of BN keys that need no mask for any row of the workgroup.
+template <int BN = kBN>
 __device__ __forceinline__ int mask_free_tiles(int n_tiles, int Lk, bool causal, int row_tile0,
                                                int off) {
-  int n = Lk / kBN;
+  int n = Lk / BN;
   if (causal) {
     const int lim = row_tile0 + off + 1;  // keys < lim are visible to every row
-    n = min(n, lim > 0 ? lim / kBN : 0);
+    n = min(n, lim > 0 ? lim / BN : 0);
   }
   return min(n, n_tiles);
 }
@@ -1005,6 +1006,363 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_e4m3(At
 }
 
 //--------------------------------------------------------------------------------------
+// OCP e4m3 kernel, head dim 128: eight-wavefront ping-pong
+//
+// The schedule of attn_fwd_16bit_pp (two groups of four wavefronts one phase apart, K
+// triple-buffered, V transposed once per tile by group 0) with 128-key tiles, so a phase
+// is 16 fp8 MFMAs (8 for S^T = K Q^T, 8 for O^T += V^T P^T).
+//
+// Key order.  The A operand row rho of S^T tile mt is fed key
+//   sigma(mt, rho) = 64 (mt / 2) + 16 (mt % 2) + 32 ((rho / 4) % 2) + 4 (rho / 8) + rho % 4,
+// which puts key 64 (mt / 2) + 16 (mt % 2) + 32 h + i in accumulator register i of lane
+// half h.  P^T slot (h, j) of PV k-step u (register j % 16 of S^T tile 2u + j / 16) is
+// then key 64 u + 32 h + j: a lane's 32 slots are 32 consecutive keys, so the V^T A
+// fragment is 32 contiguous bytes of a V^T row.
+//
+// LDS tiles (16-byte chunks XOR-swizzled against bank conflicts):
+//   K    [128 keys][128 B], chunk c of row r at c ^ ((r & 3) | ((r >> 5 & 1) << 2)); for
+//        the rows a lane reads this is c ^ (rho & 7)
+//   V    [128 keys][128 B] as in HBM (LDS-DMA), chunk c of row r at c ^ (r & 7)
+//   V^T  [128 d][128 keys], chunk c of row d at c ^ (d & 7); written by group 0 from two
+//        ds_read_b64_tr_b8 of V per 16 keys x 16 columns
+//
+// P is rounded to e4m3.  Where few keys are visible (tiles on the causal diagonal, all
+// tiles of the first kPreciseRows rows of a causal launch) P is split into two e4m3 terms,
+// P = hi + lo with lo = e4m3(P - hi), and PV runs once per term (error ~2^-8 relative).
+//--------------------------------------------------------------------------------------
+constexpr int kE8BN = 128;
+
+__device__ __forceinline__ i32x8 cat8(i32x4 a, i32x4 b) {
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Packs probabilities of S^T registers into e4m3 P^T fragments: slot j of k-step u is
+// register j % 16 of tile 2u + j / 16.
+template <int NPS, int NMT>
+__device__ __forceinline__ void pack_e4m3(const f32x16 (&s)[NMT], i32x8 (&pf)[NPS]) {
+#pragma unroll
+  for (int u = 0; u < NPS; ++u)
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      const f32x16& t = s[2 * u + (w >> 2)];
+      const int i = 4 * (w & 3);
+      int x = __builtin_amdgcn_cvt_pk_fp8_f32(t[i], t[i + 1], 0, false);
+      x = __builtin_amdgcn_cvt_pk_fp8_f32(t[i + 2], t[i + 3], x, true);
+      pf[u][w] = x;
+    }
+}
+
+// The e4m3 rounding residual of s given its rounding hi: lo = e4m3(s - float(hi)).
+template <int NPS, int NMT>
+__device__ __forceinline__ void pack_e4m3_residual(const f32x16 (&s)[NMT], const i32x8 (&hi)[NPS],
+                                                   i32x8 (&lo)[NPS]) {
+#pragma unroll
+  for (int u = 0; u < NPS; ++u)
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      const f32x16& t = s[2 * u + (w >> 2)];
+      const int i = 4 * (w & 3);
+      const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(hi[u][w], false);
+      const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8(hi[u][w], true);
+      int x = __builtin_amdgcn_cvt_pk_fp8_f32(t[i] - a[0], t[i + 1] - a[1], 0, false);
+      x = __builtin_amdgcn_cvt_pk_fp8_f32(t[i + 2] - b[0], t[i + 3] - b[1], x, true);
+      lo[u][w] = x;
+    }
+}
+
+template <int HP>
+__global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_pp(AttnParams p) {
+  constexpr int D = 128;
+  constexpr int BN = kE8BN;
+  constexpr int RB = kPPWaves / HP;      // 32-row blocks per workgroup
+  constexpr int CH = D / 16;             // 16-byte chunks per K / V row
+  constexpr int NLD = BN * CH / 64;      // wave-wide LDS-DMA loads per K or V tile
+  constexpr int NMT = BN / 32;           // S^T tiles
+  constexpr int NKS = D / 64;            // S^T k-steps (64 d each)
+  constexpr int NDT = D / 32;            // O^T tiles
+  constexpr int NPS = BN / 64;           // O^T k-steps (64 keys each)
+  constexpr int NTR = (BN / 16) * (D / 16) / 16;  // transpose tasks per group-0 wavefront
+  static_assert(NLD % 4 == 0 && NLD % kPPWaves == 0, "tile loads must split over the wavefronts");
+  static_assert(CH == 8, "the K / V swizzles assume 8 chunks per row");
+
+  __shared__ __attribute__((aligned(1024))) uint8_t kl[3][BN * D];
+  __shared__ __attribute__((aligned(1024))) uint8_t vr[2][BN * D];
+  __shared__ __attribute__((aligned(1024))) uint8_t vt[2][D * BN];
+  // this wavefront's Q^T fragments (32 bytes per lane per k-step), kept in LDS instead of
+  // registers: they are read once per tile, and the registers hold the scores instead
+  __shared__ __attribute__((aligned(1024))) uint8_t qsm[kPPWaves][NKS][64 * 32];
+
+  int hg, seq, rt;
+  decode_block(p, hg, seq, rt);
+  int qs, Lq, ks, Lk;
+  seq_range(p.cu_q, seq, p.total_q, p.q_sel, qs, Lq);
+  seq_range(p.cu_k, seq, p.total_k, p.k_sel, ks, Lk);
+  const int row_tile0 = rt * RB * 32;
+  if (row_tile0 >= Lq) return;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2;
+  const int wi = wave & 3;
+  const int lane = tid & 63;
+  const int lq = lane & 31;
+  const int lh = lane >> 5;
+  const int groups_per_kv = p.group / HP;
+  const int kvh = hg / groups_per_kv;
+  const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
+  const int r0 = row_tile0 + (wave / HP) * 32;
+  const int off = Lk - Lq;
+
+  int n_tiles = (Lk + BN - 1) / BN;
+  if (p.causal) {
+    const int last_row = min(row_tile0 + RB * 32, Lq) - 1;
+    const int kmax = last_row + off;
+    n_tiles = kmax < 0 ? 0 : min(n_tiles, kmax / BN + 1);
+  }
+  const int n_free = mask_free_tiles<BN>(n_tiles, Lk, p.causal, row_tile0, off);
+
+  const uint8_t* __restrict__ qg = reinterpret_cast<const uint8_t*>(p.q);
+  const uint8_t* __restrict__ kg = reinterpret_cast<const uint8_t*>(p.k);
+  const uint8_t* __restrict__ vg = reinterpret_cast<const uint8_t*>(p.v);
+
+  {
+    const int rsb = (int)p.q_rs;
+    const auto rq = make_rsrc(qg + (int64_t)(qs + r0) * p.q_rs + (int64_t)head * p.q_hs,
+                              (int64_t)min(Lq - r0, 32) * rsb);
+#pragma unroll
+    for (int t = 0; t < NKS; ++t) {
+      const u32x4 a = bload128(rq, lq * rsb + 64 * t + 32 * lh);
+      const u32x4 b = bload128(rq, lq * rsb + 64 * t + 32 * lh + 16);
+      *reinterpret_cast<u32x4*>(&qsm[wave][t][32 * lane]) = a;
+      *reinterpret_cast<u32x4*>(&qsm[wave][t][32 * lane + 16]) = b;
+    }
+  }
+
+  const uint8_t* kbase = kg + (int64_t)ks * p.k_rs + (int64_t)kvh * p.k_hs;
+  const uint8_t* vbase = vg + (int64_t)ks * p.v_rs + (int64_t)kvh * p.v_hs;
+  const int k_rsb = (int)p.k_rs;
+  const int v_rsb = (int)p.v_rs;
+  // LDS-DMA of one K / V tile by `nw` wavefronts: load n of wavefront w fills LDS chunks
+  // [64 (w + nw n), +64) of the tile; LDS chunk P is row P / 8, swizzled position P % 8.
+  auto dma_k = [&](int tile, uint8_t* dst, int w, auto nw) __attribute__((always_inline)) {
+    const int kb = tile * BN;
+    const auto rk = make_rsrc(kbase + (int64_t)kb * p.k_rs, (int64_t)min(Lk - kb, BN) * k_rsb);
+#pragma unroll
+    for (int n = 0; n < NLD / decltype(nw)::value; ++n) {
+      const int P = 64 * (w + decltype(nw)::value * n) + lane;
+      const int row = P >> 3;
+      const int c = (P & 7) ^ ((row & 3) | (((row >> 5) & 1) << 2));
+      dma16(rk, dst + 1024 * (w + decltype(nw)::value * n), row * k_rsb + 16 * c);
+    }
+  };
+  auto dma_v = [&](int tile, uint8_t* dst, int w, auto nw) __attribute__((always_inline)) {
+    const int kb = tile * BN;
+    const auto rv = make_rsrc(vbase + (int64_t)kb * p.v_rs, (int64_t)min(Lk - kb, BN) * v_rsb);
+#pragma unroll
+    for (int n = 0; n < NLD / decltype(nw)::value; ++n) {
+      const int P = 64 * (w + decltype(nw)::value * n) + lane;
+      const int row = P >> 3;
+      const int c = (P & 7) ^ (row & 7);
+      dma16(rv, dst + 1024 * (w + decltype(nw)::value * n), row * v_rsb + 16 * c);
+    }
+  };
+
+  // fragment addresses (bytes): K row sigma(0, lq), chunks 4t + 2h + e; V^T row lq, chunks
+  // 4u + 2h + e; tiles mt and dt add compile-time offsets
+  const int k_row = 32 * ((lq >> 2) & 1) + 4 * (lq >> 3) + (lq & 3);
+  int k_off[NKS][2], v_off[NPS][2];
+#pragma unroll
+  for (int t = 0; t < NKS; ++t)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) k_off[t][e] = k_row * D + 16 * ((4 * t + 2 * lh + e) ^ (lq & 7));
+#pragma unroll
+  for (int u = 0; u < NPS; ++u)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) v_off[u][e] = lq * BN + 16 * ((4 * u + 2 * lh + e) ^ (lq & 7));
+
+  const float qd = p.qd ? p.qd[kvh] : 1.f;
+  const float kd = p.kd ? p.kd[kvh] : 1.f;
+  const float vd = p.vd ? p.vd[kvh] : 1.f;
+  const float c_log2 = p.scale * qd * kd * kLog2e;
+  const float c_nat = p.scale * qd * kd;
+
+  f32x16 o[NDT];
+#pragma unroll
+  for (int i = 0; i < NDT; ++i) o[i] = f32x16{};
+  float m = -INFINITY;
+  float lsum = 0.f;
+  f32x16 s[NMT];
+  i32x8 pf[NPS], pl[NPS];
+
+  auto qk = [&](const uint8_t* ksrc) __attribute__((always_inline)) {
+    i32x8 qf[NKS];
+#pragma unroll
+    for (int t = 0; t < NKS; ++t)
+      qf[t] = cat8(*reinterpret_cast<const i32x4*>(&qsm[wave][t][32 * lane]),
+                   *reinterpret_cast<const i32x4*>(&qsm[wave][t][32 * lane + 16]));
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt) {
+      s[mt] = f32x16{};
+      const int mo = (64 * (mt >> 1) + 16 * (mt & 1)) * D;
+#pragma unroll
+      for (int t = 0; t < NKS; ++t) {
+        const i32x4 a0 = *reinterpret_cast<const i32x4*>(ksrc + mo + k_off[t][0]);
+        const i32x4 a1 = *reinterpret_cast<const i32x4*>(ksrc + mo + k_off[t][1]);
+        s[mt] = mma_fp8(cat8(a0, a1), qf[t], s[mt]);
+      }
+    }
+  };
+  auto pv = [&](const uint8_t* vsrc, auto two_terms) __attribute__((always_inline)) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int u = 0; u < NPS; ++u) {
+        const i32x4 a0 = *reinterpret_cast<const i32x4*>(vsrc + 32 * dt * BN + v_off[u][0]);
+        const i32x4 a1 = *reinterpret_cast<const i32x4*>(vsrc + 32 * dt * BN + v_off[u][1]);
+        const i32x8 a = cat8(a0, a1);
+        o[dt] = mma_fp8(a, pf[u], o[dt]);
+        if constexpr (decltype(two_terms)::value) o[dt] = mma_fp8(a, pl[u], o[dt]);
+      }
+  };
+  // Transposes the V tile at vsrc into vt layout at vdst.  Task id (16 keys kb x 16
+  // columns cb) = 4 (wi + 4 n) + lane / 16; lane j of the 16 reads rows 16 kb + j / 2
+  // (+ 8), bytes 8 (j % 2) of column chunk cb, and receives column 16 cb + j.
+  const int tj = lane & 15;
+  auto transpose_v = [&](const uint8_t* vsrc, uint8_t* vdst) __attribute__((always_inline)) {
+#pragma unroll
+    for (int n = 0; n < NTR; ++n) {
+      const int id = 4 * (wi + 4 * n) + (lane >> 4);
+      const int kb = id & (BN / 16 - 1), cb = id / (BN / 16);
+      const int row = 16 * kb + (tj >> 1);
+      const uint8_t* src = vsrc + row * D + 16 * (cb ^ (row & 7)) + 8 * (tj & 1);
+      const i32x2 lo = lds_tr8(src);
+      const i32x2 hi = lds_tr8(src + 8 * D);
+      const int d = 16 * cb + tj;
+      *reinterpret_cast<i32x4*>(vdst + d * BN + 16 * (kb ^ (d & 7))) =
+          __builtin_shufflevector(lo, hi, 0, 1, 2, 3);
+    }
+  };
+  auto mask = [&](int kb0) __attribute__((always_inline)) {
+    const int qq = r0 + lq + off;
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kk = kb0 + 64 * (mt >> 1) + 16 * (mt & 1) + 32 * lh + i;
+        const bool dead = kk >= Lk || (p.causal && kk > qq);
+        s[mt][i] = dead ? -INFINITY : s[mt][i];
+      }
+  };
+
+  std::integral_constant<int, kPPWaves> all8;
+  std::integral_constant<int, 4> four;
+  if (n_tiles > 0) {
+    dma_k(0, kl[0], wave, all8);
+    dma_k(1, kl[1], wave, all8);
+    dma_k(2, kl[2], wave, all8);
+    dma_v(0, vr[0], wave, all8);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (grp == 1) __syncthreads();  // group 1 runs one phase behind group 0
+
+  // One tile j.  MFMA phase: PV of tile j - 1 (PREV = 1: one e4m3 term, 2: with the
+  // residual term, 0: none), then S^T of tile j -- PV first, since it consumes P before QK
+  // defines the new scores, so the two never hold registers at the same time.  VALU phase:
+  // mask (MASKED), online softmax, P of tile j (with its residual when SPLIT).  Every
+  // variant is a separate instance, so no phase carries code or registers of another.
+  auto tile = [&](int j, auto prev, auto masked, auto split) __attribute__((always_inline)) {
+    constexpr int PREV = decltype(prev)::value;
+    __builtin_amdgcn_s_setprio(1);
+    if constexpr (PREV == 0) {
+      qk(kl[j % 3]);
+    } else {
+      pv(vt[(j - 1) & 1], std::integral_constant<bool, PREV == 2>{});
+      qk(kl[j % 3]);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kPPReadAhead, 0);
+#pragma unroll
+      for (int i = 0; i < NDT * NPS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, PREV, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < NMT * NKS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's LDS-DMA from its previous VALU phase
+    __syncthreads();
+    if (grp == 1) {
+      dma_k(j + 3, kl[j % 3], wi, four);
+    } else {
+      transpose_v(vr[j & 1], vt[j & 1]);
+      dma_v(j + 1, vr[(j + 1) & 1], wi, four);
+    }
+    if constexpr (decltype(masked)::value) mask(j * BN);
+    tile_max_rescale<NMT, NDT>(s, o, m, lsum, c_log2);
+    tile_exp<NMT>(s, m, lsum, c_log2);
+    pack_e4m3<NPS, NMT>(s, pf);
+    if constexpr (decltype(split)::value) pack_e4m3_residual<NPS, NMT>(s, pf, pl);
+    __syncthreads();
+  };
+  // SP = 0: no residual terms (non-causal); 1: on the masked (diagonal) tiles of a causal
+  // launch; 2: on every tile (the first kPreciseRows rows of a causal launch).
+  auto run = [&](auto sp) __attribute__((always_inline)) {
+    constexpr int SP = decltype(sp)::value;
+    using SA = std::integral_constant<bool, SP == 2>;  // residual on mask-free tiles
+    using SB = std::integral_constant<bool, SP >= 1>;  // residual on masked tiles
+    using P0 = std::integral_constant<int, 0>;
+    using PA = std::integral_constant<int, SA::value ? 2 : 1>;
+    using PB = std::integral_constant<int, SB::value ? 2 : 1>;
+    using F = std::false_type;
+    using T = std::true_type;
+    int j = 0;
+    if (n_free > 0) {
+      tile(0, P0{}, F{}, SA{});
+      for (j = 1; j < n_free; ++j) tile(j, PA{}, F{}, SA{});
+    }
+    if (j < n_tiles) {
+      if (j == 0) tile(0, P0{}, T{}, SB{});
+      else tile(j, PA{}, T{}, SB{});
+      for (++j; j < n_tiles; ++j) tile(j, PB{}, T{}, SB{});
+    }
+    if (n_tiles > 0) {
+      __builtin_amdgcn_s_setprio(1);
+      if (n_tiles > n_free) pv(vt[(n_tiles - 1) & 1], std::integral_constant<bool, SB::value>{});
+      else pv(vt[(n_tiles - 1) & 1], std::integral_constant<bool, SA::value>{});
+      __builtin_amdgcn_s_setprio(0);
+    }
+  };
+  if (!p.causal) run(std::integral_constant<int, 0>{});
+  else if (r0 >= kPreciseRows) run(std::integral_constant<int, 1>{});
+  else run(std::integral_constant<int, 2>{});
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (grp == 0) __syncthreads();  // both groups pass the same number of barriers
+
+  const float ltot = pair_sum(lsum);
+  const float inv = ltot > 0.f ? vd / ltot : 0.f;
+  const int row = r0 + lq;
+  if (row < Lq) {
+    __bf16* og = reinterpret_cast<__bf16*>(p.out) + (int64_t)(qs + row) * p.o_rs + (int64_t)head * p.o_hs;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        bf16x4 w = {(__bf16)(o[dt][4 * g + 0] * inv), (__bf16)(o[dt][4 * g + 1] * inv),
+                    (__bf16)(o[dt][4 * g + 2] * inv), (__bf16)(o[dt][4 * g + 3] * inv)};
+        *reinterpret_cast<bf16x4*>(og + 32 * dt + 8 * g + 4 * lh) = w;
+      }
+    if (lh == 0) {
+      const float lse = ltot > 0.f ? m * c_nat + logf(ltot) : -INFINITY;
+      p.lse[(int64_t)(qs + row) * p.lse_rs + head] = lse;
+    }
+  }
+}
+
+//--------------------------------------------------------------------------------------
 // host dispatch
 //--------------------------------------------------------------------------------------
 int heads_per_wg(int group) {
@@ -1048,17 +1406,19 @@ KernelChoice pick16(int d, int hp) {
 
 KernelChoice pick8(int d, int hp) {
   KernelChoice k;
-  k.threads = kThreads;
-  k.rows = 32 * kWaves / hp;
-#define FA4CP_PICK(DD)                                \
-  if (d == DD) {                                      \
-    if (hp == 4) k.fn = attn_fwd_e4m3<DD, 4>;         \
-    else if (hp == 2) k.fn = attn_fwd_e4m3<DD, 2>;    \
-    else k.fn = attn_fwd_e4m3<DD, 1>;                 \
+  if (d == 128) {
+    k.threads = kPPThreads;
+    k.rows = 32 * kPPWaves / hp;
+    if (hp == 4) k.fn = attn_fwd_e4m3_pp<4>;
+    else if (hp == 2) k.fn = attn_fwd_e4m3_pp<2>;
+    else k.fn = attn_fwd_e4m3_pp<1>;
+  } else if (d == 256) {
+    k.threads = kThreads;
+    k.rows = 32 * kWaves / hp;
+    if (hp == 4) k.fn = attn_fwd_e4m3<256, 4>;
+    else if (hp == 2) k.fn = attn_fwd_e4m3<256, 2>;
+    else k.fn = attn_fwd_e4m3<256, 1>;
   }
-  FA4CP_PICK(128)
-  FA4CP_PICK(256)
-#undef FA4CP_PICK
   return k;
 }
 

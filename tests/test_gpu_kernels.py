@@ -218,6 +218,10 @@ FP8_CASES = [
     (384, 384, 16, 2, 256, False, SEL_BACK_HALF, SEL_ALL, None),
     (None, None, 8, 8, 128, True, SEL_ALL, SEL_ALL, [0, 128, 136, 520]),
     (None, None, 8, 2, 128, False, SEL_BACK_HALF, SEL_ALL, [0, 0, 256, 256, 390]),
+    (333, 333, 8, 4, 128, True, SEL_ALL, SEL_ALL, None),          # 2 heads per kv head, tails
+    (64, 200, 4, 4, 128, True, SEL_ALL, SEL_ALL, None),           # bottom-right causal, MHA
+    (700, 700, 4, 1, 128, False, SEL_ALL, SEL_FRONT_HALF, None),  # MQA, partial key tile
+    (1100, 1100, 4, 1, 128, True, SEL_ALL, SEL_ALL, None),        # rows past the precise block
 ]
 
 
