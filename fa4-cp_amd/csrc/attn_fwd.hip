@@ -65,6 +65,8 @@ struct AttnParams {
   const float* qd;
   const float* kd;
   const float* vd;
+  const void* vt;  // V^T (fa4cp_transpose_v layout) or null
+  int64_t vt_ds;   // V^T row stride (elements)
   int n_rt;  // row tiles per sequence (of 32 * RB rows)
   int n_hg;  // head groups: h_kv * group / HP
   int n_blocks;
@@ -74,20 +76,6 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 
-// Query / key row range [start, start + len) of sequence j after the half selection.
-__device__ __forceinline__ void seq_range(const int32_t* cu, int j, int total, int sel,
-                                          int& start, int& len) {
-  int s = 0, e = total;
-  if (cu != nullptr) {
-    s = cu[j];
-    e = cu[j + 1];
-  }
-  const int mid = (s + e) >> 1;
-  if (sel == FA4CP_SEL_FRONT_HALF) e = mid;
-  if (sel == FA4CP_SEL_BACK_HALF) s = mid;
-  start = s;
-  len = e - s;
-}
 
 // Pair reduction across lanes l and l ^ 32 (v_permlane32_swap: lanes 0-31 receive the
 // upper half's value in the second result, lanes 32-63 the lower half's in the first).
@@ -119,6 +107,11 @@ __device__ __forceinline__ i32x2 lds_tr8(const void* p) {
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff,
                                            0, 0, 0);
+}
+// The same with a wave-uniform byte offset `soff` added in the scalar offset field.
+__device__ __forceinline__ void dma16s(__amdgpu_buffer_rsrc_t r, void* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff,
+                                           soff, 0, 0);
 }
 
 // Instruction-scheduling groups for __builtin_amdgcn_sched_group_barrier.
@@ -767,6 +760,238 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_pp(AttnParams p)
 }
 
 //--------------------------------------------------------------------------------------
+// bf16 / fp16 kernel, head dim <= 128, V^T given: eight-wavefront ping-pong
+//
+// attn_fwd_16bit_pp with V^T tiles loaded straight from the fa4cp_transpose_v layout, so
+// no wavefront transposes V.  For a lane's P^T slots to be consecutive keys, the A operand
+// row rho of S^T tile mt is fed key 32 mt + sw(rho), sw swapping bits 2 and 3 of rho:
+// accumulator register i of lane half h then holds key 32 mt + 16 (i / 8) + 8 h + i % 8,
+// and P^T k-step t (registers 8 (t % 2) + 0..7 of tile t / 2) covers keys 16 t + 8 h + 0..7,
+// the 16 bytes at V^T row d, keys 16 t + 8 h.
+//
+// LDS: K [BN][D] in three slots, chunk c of row r at c ^ ksw(r); V^T [D][BN] in two slots,
+// chunk c of row d at c ^ ((d >> 1) & 7) (16 distinct 16-byte slots per 256 bytes for the
+// 16 lanes of every fragment read).  Counting phases from 0 (group 0's first MFMA phase):
+// group 0 loads K_{j+2} into slot (j + 2) % 3 in its VALU phase j (phase 2j + 1; the slot
+// last held K_{j-1}, read in phase 2j - 1); group 1 loads V^T_{j+1} into slot (j + 1) % 2
+// in its VALU phase j (phase 2j + 2; the slot last held V^T_{j-1}, read in phase 2j + 1).
+// Each wavefront waits for its loads at the end of its next phase, whose barrier publishes
+// them before phase 2j + 4, the first that reads them.
+//--------------------------------------------------------------------------------------
+__device__ __forceinline__ int swap_bits23(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+template <int CH>
+__device__ __forceinline__ int ksw16(int r) { return CH >= 16 ? (r & 15) : ((r >> 1) & 7); }
+
+template <typename T, int D, int HP>
+__global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_vt(AttnParams p) {
+  using Ops = MfmaOps<T>;
+  using frag = typename Ops::frag;
+  constexpr int BN = kBN;
+  constexpr int RB = kPPWaves / HP;     // 32-row blocks per workgroup
+  constexpr int CH = D / 8;             // 16-byte chunks per K row
+  constexpr int NLD = BN * CH / 64;     // wave-wide LDS-DMA loads per K (or V^T) tile
+  constexpr int NMT = BN / 32;
+  constexpr int NDT = D / 32;
+  constexpr int NKS = D / 16;
+  constexpr int NPS = BN / 16;
+  static_assert(D <= 128, "ping-pong kernel holds one 32 x D output tile per wavefront");
+  static_assert(BN * (int)sizeof(T) == 128, "V^T rows are 8 chunks");
+  static_assert(NLD % 4 == 0 && NLD % kPPWaves == 0, "tile loads must split over the wavefronts");
+
+  __shared__ __attribute__((aligned(1024))) T kl[3][BN * D];
+  __shared__ __attribute__((aligned(1024))) T vtl[2][D * BN];
+
+  int hg, seq, rt;
+  decode_block(p, hg, seq, rt);
+  int qs, Lq, ks, Lk;
+  seq_range(p.cu_q, seq, p.total_q, p.q_sel, qs, Lq);
+  seq_range(p.cu_k, seq, p.total_k, p.k_sel, ks, Lk);
+  const int row_tile0 = rt * RB * 32;
+  if (row_tile0 >= Lq) return;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2;
+  const int wi = wave & 3;
+  const int lane = tid & 63;
+  const int lq = lane & 31;
+  const int lh = lane >> 5;
+  const int groups_per_kv = p.group / HP;
+  const int kvh = hg / groups_per_kv;
+  const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
+  const int r0 = row_tile0 + (wave / HP) * 32;
+  const int off = Lk - Lq;
+
+  int n_tiles = (Lk + BN - 1) / BN;
+  if (p.causal) {
+    const int last_row = min(row_tile0 + RB * 32, Lq) - 1;
+    const int kmax = last_row + off;
+    n_tiles = kmax < 0 ? 0 : min(n_tiles, kmax / BN + 1);
+  }
+  const int n_free = mask_free_tiles(n_tiles, Lk, p.causal, row_tile0, off);
+
+  const T* __restrict__ qg = reinterpret_cast<const T*>(p.q);
+  const T* __restrict__ kg = reinterpret_cast<const T*>(p.k);
+
+  frag qf[NKS];
+  {
+    const int64_t rsb = p.q_rs * (int64_t)sizeof(T);
+    const auto rq = make_rsrc(qg + (int64_t)(qs + r0) * p.q_rs + (int64_t)head * p.q_hs,
+                              (int64_t)min(Lq - r0, 32) * rsb);
+#pragma unroll
+    for (int t = 0; t < NKS; ++t)
+      qf[t] = __builtin_bit_cast(frag, bload128(rq, lq * (int)rsb + (int)sizeof(T) * (16 * t + 8 * lh)));
+  }
+
+  const T* kbase = kg + (int64_t)ks * p.k_rs + (int64_t)kvh * p.k_hs;
+  const int k_rsb = (int)(p.k_rs * (int64_t)sizeof(T));
+  // V^T of this kv head and sequence: row d at vtbase + d * vt_ds
+  const int64_t vt_pos = p.cu_k ? vt_seq_start(p.cu_k, seq, p.k_sel) : 0;
+  const T* vtbase = reinterpret_cast<const T*>(p.vt) + (int64_t)kvh * D * p.vt_ds + vt_pos;
+  const int64_t vt_left = (int64_t)D * p.vt_ds - vt_pos;  // elements to the end of this head
+  const int vt_rsb = (int)(p.vt_ds * (int64_t)sizeof(T));
+  // LDS-DMA of one tile by `nw` wavefronts: load n of wavefront w fills LDS chunks
+  // [64 (w + nw n), +64) of the tile.
+  auto dma_k = [&](int tile, T* dst, int w, auto nw) __attribute__((always_inline)) {
+    const int kb = tile * BN;
+    const auto rk = make_rsrc(kbase + (int64_t)kb * p.k_rs, (int64_t)min(Lk - kb, BN) * k_rsb);
+#pragma unroll
+    for (int n = 0; n < NLD / decltype(nw)::value; ++n) {
+      const int P = 64 * (w + decltype(nw)::value * n) + lane;
+      const int row = P / CH, c = (P % CH) ^ ksw16<CH>(row);
+      dma16(rk, dst + 512 * (w + decltype(nw)::value * n), row * k_rsb + 16 * c);
+    }
+  };
+  auto dma_vt = [&](int tile, T* dst, int w, auto nw) __attribute__((always_inline)) {
+    const int kb = tile * BN;
+    const auto rv = make_rsrc(vtbase + kb, (vt_left - kb) * (int64_t)sizeof(T));
+#pragma unroll
+    for (int n = 0; n < NLD / decltype(nw)::value; ++n) {
+      const int P = 64 * (w + decltype(nw)::value * n) + lane;
+      const int d = P >> 3, c = (P & 7) ^ ((d >> 1) & 7);
+      dma16(rv, dst + 512 * (w + decltype(nw)::value * n), d * vt_rsb + 16 * c);
+    }
+  };
+
+  const int kr = swap_bits23(lq);  // K row fed by this lane (tile 0)
+  int k_off[NKS];
+#pragma unroll
+  for (int t = 0; t < NKS; ++t) k_off[t] = kr * D + 8 * ((2 * t + lh) ^ ksw16<CH>(kr));
+  int v_off[NPS];
+#pragma unroll
+  for (int t = 0; t < NPS; ++t) v_off[t] = lq * BN + 8 * ((2 * t + lh) ^ ((lq >> 1) & 7));
+
+  const float c_log2 = p.scale * kLog2e;
+  f32x16 o[NDT];
+#pragma unroll
+  for (int i = 0; i < NDT; ++i) o[i] = f32x16{};
+  float m = -INFINITY;
+  float lsum = 0.f;
+  f32x16 s[NMT];
+  frag pf[NPS];
+
+  auto qk = [&](const T* ksrc) __attribute__((always_inline)) {
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt) {
+      s[mt] = f32x16{};
+#pragma unroll
+      for (int t = 0; t < NKS; ++t) {
+        const frag a = *reinterpret_cast<const frag*>(ksrc + k_off[t] + 32 * mt * D);
+        s[mt] = Ops::mma(a, qf[t], s[mt]);
+      }
+    }
+  };
+  auto pv = [&](const T* vsrc) __attribute__((always_inline)) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int t = 0; t < NPS; ++t) {
+        const frag a = *reinterpret_cast<const frag*>(vsrc + 32 * dt * BN + v_off[t]);
+        o[dt] = Ops::mma(a, pf[t], o[dt]);
+      }
+  };
+  auto mask = [&](int kb0) __attribute__((always_inline)) {
+    const int qq = r0 + lq + off;
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kk = kb0 + 32 * mt + 16 * (i >> 3) + 8 * lh + (i & 7);
+        const bool dead = kk >= Lk || (p.causal && kk > qq);
+        s[mt][i] = dead ? -INFINITY : s[mt][i];
+      }
+  };
+
+  std::integral_constant<int, kPPWaves> all8;
+  std::integral_constant<int, 4> four;
+  if (n_tiles > 0) {
+    dma_k(0, kl[0], wave, all8);
+    dma_k(1, kl[1], wave, all8);
+    dma_vt(0, vtl[0], wave, all8);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (grp == 1) __syncthreads();  // group 1 runs one phase behind group 0
+
+  for (int j = 0; j < n_tiles; ++j) {
+    // MFMA phase
+    __builtin_amdgcn_s_setprio(1);
+    qk(kl[j % 3]);
+    if (j > 0) {
+      pv(vtl[(j - 1) & 1]);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kPPReadAhead, 0);
+#pragma unroll
+      for (int i = 0; i < NMT * NKS + NDT * NPS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's LDS-DMA from its previous VALU phase
+    __syncthreads();
+    // VALU phase
+    if (grp == 0) dma_k(j + 2, kl[(j + 2) % 3], wi, four);
+    else dma_vt(j + 1, vtl[(j + 1) & 1], wi, four);
+    if (j >= n_free) mask(j * BN);
+    tile_max_rescale<NMT, NDT>(s, o, m, lsum, c_log2);
+    tile_exp<NMT>(s, m, lsum, c_log2);
+#pragma unroll
+    for (int t = 0; t < NPS; ++t)
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) pf[t][jj] = (T)s[t >> 1][8 * (t & 1) + jj];
+    __syncthreads();
+  }
+  if (n_tiles > 0) {
+    __builtin_amdgcn_s_setprio(1);
+    pv(vtl[(n_tiles - 1) & 1]);
+    __builtin_amdgcn_s_setprio(0);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (grp == 0) __syncthreads();  // both groups pass the same number of barriers
+
+  const float ltot = pair_sum(lsum);
+  const float inv = ltot > 0.f ? 1.0f / ltot : 0.f;
+  const int row = r0 + lq;
+  if (row < Lq) {
+    T* og = reinterpret_cast<T*>(p.out) + (int64_t)(qs + row) * p.o_rs + (int64_t)head * p.o_hs;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        typedef T t4 __attribute__((ext_vector_type(4)));
+        t4 w = {(T)(o[dt][4 * g + 0] * inv), (T)(o[dt][4 * g + 1] * inv),
+                (T)(o[dt][4 * g + 2] * inv), (T)(o[dt][4 * g + 3] * inv)};
+        *reinterpret_cast<t4*>(og + 32 * dt + 8 * g + 4 * lh) = w;
+      }
+    if (lh == 0) {
+      const float lse = ltot > 0.f ? m * p.scale + logf(ltot) : -INFINITY;
+      p.lse[(int64_t)(qs + row) * p.lse_rs + head] = lse;
+    }
+  }
+}
+
+//--------------------------------------------------------------------------------------
 // OCP e4m3 kernel
 //
 // QK^T and PV run on v_mfma_f32_32x32x64_f8f6f4 (fp8 x fp8, 64-deep).  The MFMA pairs
@@ -1363,6 +1588,308 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_pp(AttnParams p) 
 }
 
 //--------------------------------------------------------------------------------------
+// OCP e4m3 kernel, head dim 128, V^T given: eight-wavefront ping-pong
+//
+// attn_fwd_e4m3_pp with V^T tiles loaded straight from the fa4cp_transpose_v layout (no V
+// transposition), loads and swizzles sized for an LDS that serves 256 bytes per cycle (64
+// banks; a 16-byte access in groups of 16 lanes, which must hit 16 distinct 16-byte slots
+// modulo 256 bytes -- two 128-byte rows share a window):
+//   K    [128 keys][128 B], chunk c of row r at c ^ kswz(r)
+//   V^T  [128 d][128 keys], chunk c of row d at c ^ ((d >> 1) & 7)
+//   Q    per wavefront, lane-contiguous 16-byte halves of the Q^T fragments
+// Group 0 loads K_{j+2} into slot (j + 2) % 3 in its VALU phase j (phase 2j + 1; the slot
+// last held K_{j-1}, read in phase 2j - 1); group 1 loads V^T_{j+1} into slot (j + 1) % 2 in
+// its VALU phase j (phase 2j + 2; the slot last held V^T_{j-1}, read in phase 2j + 1).  Each
+// wavefront waits for its loads at the end of its next phase, whose barrier publishes them
+// before phase 2j + 4, the first that reads them.  The per-lane load offsets are computed
+// once, so the VALU phase issues only the loads themselves.
+//--------------------------------------------------------------------------------------
+// K tile swizzle: the 16 rows read by a 16-lane group are k_row(rho) + const (rows
+// {0-3, 32-35, 4-7, 36-39} + 8 g + 16 (mt % 2) + 64 (mt / 2)), which bits 1-2 and 5 tell
+// apart within each row parity.
+__device__ __forceinline__ int kswz(int r) { return ((r >> 1) & 3) | (((r >> 5) & 1) << 2); }
+
+template <int HP>
+__global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_vt(AttnParams p) {
+  constexpr int D = 128;
+  constexpr int BN = kE8BN;
+  constexpr int RB = kPPWaves / HP;      // 32-row blocks per workgroup
+  constexpr int CH = D / 16;             // 16-byte chunks per K / V row
+  constexpr int NLD = BN * CH / 64;      // wave-wide LDS-DMA loads per K or V tile
+  constexpr int NMT = BN / 32;           // S^T tiles
+  constexpr int NKS = D / 64;            // S^T k-steps (64 d each)
+  constexpr int NDT = D / 32;            // O^T tiles
+  constexpr int NPS = BN / 64;           // O^T k-steps (64 keys each)
+  static_assert(NLD % 4 == 0 && NLD % kPPWaves == 0, "tile loads must split over the wavefronts");
+  static_assert(CH == 8, "the K / V swizzles assume 8 chunks per row");
+
+  __shared__ __attribute__((aligned(1024))) uint8_t kl[3][BN * D];
+  __shared__ __attribute__((aligned(1024))) uint8_t vt[2][D * BN];
+  // this wavefront's Q^T fragments (16 bytes per lane per half k-step), kept in LDS instead
+  // of registers: they are read once per tile, and the registers hold the scores instead
+  __shared__ __attribute__((aligned(1024))) uint8_t qsm[kPPWaves][NKS][2][64 * 16];
+
+  int hg, seq, rt;
+  decode_block(p, hg, seq, rt);
+  int qs, Lq, ks, Lk;
+  seq_range(p.cu_q, seq, p.total_q, p.q_sel, qs, Lq);
+  seq_range(p.cu_k, seq, p.total_k, p.k_sel, ks, Lk);
+  const int row_tile0 = rt * RB * 32;
+  if (row_tile0 >= Lq) return;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2;
+  const int wi = wave & 3;
+  const int lane = tid & 63;
+  const int lq = lane & 31;
+  const int lh = lane >> 5;
+  const int groups_per_kv = p.group / HP;
+  const int kvh = hg / groups_per_kv;
+  const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
+  const int r0 = row_tile0 + (wave / HP) * 32;
+  const int off = Lk - Lq;
+
+  int n_tiles = (Lk + BN - 1) / BN;
+  if (p.causal) {
+    const int last_row = min(row_tile0 + RB * 32, Lq) - 1;
+    const int kmax = last_row + off;
+    n_tiles = kmax < 0 ? 0 : min(n_tiles, kmax / BN + 1);
+  }
+  const int n_free = mask_free_tiles<BN>(n_tiles, Lk, p.causal, row_tile0, off);
+
+  const uint8_t* __restrict__ qg = reinterpret_cast<const uint8_t*>(p.q);
+  const uint8_t* __restrict__ kg = reinterpret_cast<const uint8_t*>(p.k);
+  const uint8_t* __restrict__ vg = reinterpret_cast<const uint8_t*>(p.v);
+
+  {
+    const int rsb = (int)p.q_rs;
+    const auto rq = make_rsrc(qg + (int64_t)(qs + r0) * p.q_rs + (int64_t)head * p.q_hs,
+                              (int64_t)min(Lq - r0, 32) * rsb);
+#pragma unroll
+    for (int t = 0; t < NKS; ++t) {
+      const u32x4 a = bload128(rq, lq * rsb + 64 * t + 32 * lh);
+      const u32x4 b = bload128(rq, lq * rsb + 64 * t + 32 * lh + 16);
+      *reinterpret_cast<u32x4*>(&qsm[wave][t][0][16 * lane]) = a;
+      *reinterpret_cast<u32x4*>(&qsm[wave][t][1][16 * lane]) = b;
+    }
+  }
+
+  const uint8_t* kbase = kg + (int64_t)ks * p.k_rs + (int64_t)kvh * p.k_hs;
+  const int k_rsb = (int)p.k_rs;
+  const int64_t vt_pos = p.cu_k ? vt_seq_start(p.cu_k, seq, p.k_sel) : 0;
+  const uint8_t* vtbase = reinterpret_cast<const uint8_t*>(p.vt) + (int64_t)kvh * D * p.vt_ds + vt_pos;
+  const int64_t vt_left = (int64_t)D * p.vt_ds - vt_pos;  // bytes to the end of this head
+  const int vt_rsb = (int)p.vt_ds;
+  // LDS-DMA: load n of wavefront wi of a group fills LDS chunks [64 (wi + 4 n), +64) of a
+  // tile; chunk P is row r = P / 8 = 8 (wi + 4 n) + lane / 8 at swizzled position P % 8.
+  // Row r's swizzle bits 0-1 are lane bits 4-5 for both tiles; bit 2 is n % 2 (K: bit 5 of
+  // r) or wi % 2 (V^T: bit 3 of r).  So two lane offsets for K, one for V^T, and the row
+  // term 8 (wi + 4 n) * row_bytes as a scalar offset.
+  constexpr int NG = NLD / 4;  // loads per wavefront of a group
+  const int lsw = (lane >> 4) & 3;
+  int k_lane[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) k_lane[u] = (lane >> 3) * k_rsb + 16 * ((lane & 7) ^ (lsw | (u << 2)));
+  const int vt_lane = (lane >> 3) * vt_rsb + 16 * ((lane & 7) ^ (lsw | ((wi & 1) << 2)));
+  auto dma_k_group = [&](int tile, uint8_t* dst) __attribute__((always_inline)) {
+    const int kb = tile * BN;
+    const auto rk = make_rsrc(kbase + (int64_t)kb * p.k_rs, (int64_t)min(Lk - kb, BN) * k_rsb);
+#pragma unroll
+    for (int n = 0; n < NG; ++n)
+      dma16s(rk, dst + 1024 * (wi + 4 * n), k_lane[n & 1], 8 * (wi + 4 * n) * k_rsb);
+  };
+  auto dma_vt_group = [&](int tile, uint8_t* dst) __attribute__((always_inline)) {
+    const int kb = tile * BN;
+    const auto rv = make_rsrc(vtbase + kb, vt_left - kb);
+#pragma unroll
+    for (int n = 0; n < NG; ++n) dma16s(rv, dst + 1024 * (wi + 4 * n), vt_lane, 8 * (wi + 4 * n) * vt_rsb);
+  };
+  // the same by all eight wavefronts (prologue)
+  auto dma_all = [&](int tile, uint8_t* kdst, uint8_t* vdst) __attribute__((always_inline)) {
+    const int kb = tile * BN;
+    const auto rk = make_rsrc(kbase + (int64_t)kb * p.k_rs, (int64_t)min(Lk - kb, BN) * k_rsb);
+    const auto rv = make_rsrc(vtbase + kb, vt_left - kb);
+#pragma unroll
+    for (int n = 0; n < NLD / kPPWaves; ++n) {
+      const int P = 64 * (wave + kPPWaves * n) + lane;
+      const int r = P >> 3;
+      dma16(rk, kdst + 1024 * (wave + kPPWaves * n), r * k_rsb + 16 * ((P & 7) ^ kswz(r)));
+      if (vdst != nullptr)
+        dma16(rv, vdst + 1024 * (wave + kPPWaves * n), r * vt_rsb + 16 * ((P & 7) ^ ((r >> 1) & 7)));
+    }
+  };
+
+  // fragment addresses (bytes): K row sigma(0, lq), chunks 4t + 2h + e; V^T row lq, chunks
+  // 4u + 2h + e; tiles mt and dt add compile-time offsets
+  const int k_row = 32 * ((lq >> 2) & 1) + 4 * (lq >> 3) + (lq & 3);
+  int k_off[NKS][2], v_off[NPS][2];
+#pragma unroll
+  for (int t = 0; t < NKS; ++t)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) k_off[t][e] = k_row * D + 16 * ((4 * t + 2 * lh + e) ^ kswz(k_row));
+#pragma unroll
+  for (int u = 0; u < NPS; ++u)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) v_off[u][e] = lq * BN + 16 * ((4 * u + 2 * lh + e) ^ ((lq >> 1) & 7));
+
+  const float qd = p.qd ? p.qd[kvh] : 1.f;
+  const float kd = p.kd ? p.kd[kvh] : 1.f;
+  const float vd = p.vd ? p.vd[kvh] : 1.f;
+  const float c_log2 = p.scale * qd * kd * kLog2e;
+  const float c_nat = p.scale * qd * kd;
+
+  f32x16 o[NDT];
+#pragma unroll
+  for (int i = 0; i < NDT; ++i) o[i] = f32x16{};
+  float m = -INFINITY;
+  float lsum = 0.f;
+  f32x16 s[NMT];
+  i32x8 pf[NPS], pl[NPS];
+
+  auto qk = [&](const uint8_t* ksrc) __attribute__((always_inline)) {
+    i32x8 qf[NKS];
+#pragma unroll
+    for (int t = 0; t < NKS; ++t)
+      qf[t] = cat8(*reinterpret_cast<const i32x4*>(&qsm[wave][t][0][16 * lane]),
+                   *reinterpret_cast<const i32x4*>(&qsm[wave][t][1][16 * lane]));
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt) {
+      s[mt] = f32x16{};
+      const int mo = (64 * (mt >> 1) + 16 * (mt & 1)) * D;
+#pragma unroll
+      for (int t = 0; t < NKS; ++t) {
+        const i32x4 a0 = *reinterpret_cast<const i32x4*>(ksrc + mo + k_off[t][0]);
+        const i32x4 a1 = *reinterpret_cast<const i32x4*>(ksrc + mo + k_off[t][1]);
+        s[mt] = mma_fp8(cat8(a0, a1), qf[t], s[mt]);
+      }
+    }
+  };
+  auto pv = [&](const uint8_t* vsrc, auto two_terms) __attribute__((always_inline)) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int u = 0; u < NPS; ++u) {
+        const i32x4 a0 = *reinterpret_cast<const i32x4*>(vsrc + 32 * dt * BN + v_off[u][0]);
+        const i32x4 a1 = *reinterpret_cast<const i32x4*>(vsrc + 32 * dt * BN + v_off[u][1]);
+        const i32x8 a = cat8(a0, a1);
+        o[dt] = mma_fp8(a, pf[u], o[dt]);
+        if constexpr (decltype(two_terms)::value) o[dt] = mma_fp8(a, pl[u], o[dt]);
+      }
+  };
+  auto mask = [&](int kb0) __attribute__((always_inline)) {
+    const int qq = r0 + lq + off;
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kk = kb0 + 64 * (mt >> 1) + 16 * (mt & 1) + 32 * lh + i;
+        const bool dead = kk >= Lk || (p.causal && kk > qq);
+        s[mt][i] = dead ? -INFINITY : s[mt][i];
+      }
+  };
+
+  if (n_tiles > 0) {
+    dma_all(0, kl[0], vt[0]);
+    dma_all(1, kl[1], nullptr);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (grp == 1) __syncthreads();  // group 1 runs one phase behind group 0
+
+  // One tile j.  MFMA phase: PV of tile j - 1 (PREV = 1: one e4m3 term, 2: with the
+  // residual term, 0: none), then S^T of tile j -- PV first, since it consumes P before QK
+  // defines the new scores, so the two never hold registers at the same time.  VALU phase:
+  // mask (MASKED), online softmax, P of tile j (with its residual when SPLIT).  Every
+  // variant is a separate instance, so no phase carries code or registers of another.
+  auto tile = [&](int j, auto prev, auto masked, auto split) __attribute__((always_inline)) {
+    constexpr int PREV = decltype(prev)::value;
+    __builtin_amdgcn_s_setprio(1);
+    if constexpr (PREV == 0) {
+      qk(kl[j % 3]);
+    } else {
+      pv(vt[(j - 1) & 1], std::integral_constant<bool, PREV == 2>{});
+      qk(kl[j % 3]);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kPPReadAhead, 0);
+#pragma unroll
+      for (int i = 0; i < NDT * NPS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, PREV, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < NMT * NKS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's LDS-DMA from its previous VALU phase
+    __syncthreads();
+    if (grp == 0) dma_k_group(j + 2, kl[(j + 2) % 3]);
+    else dma_vt_group(j + 1, vt[(j + 1) & 1]);
+    if constexpr (decltype(masked)::value) mask(j * BN);
+    tile_max_rescale<NMT, NDT>(s, o, m, lsum, c_log2);
+    tile_exp<NMT>(s, m, lsum, c_log2);
+    pack_e4m3<NPS, NMT>(s, pf);
+    if constexpr (decltype(split)::value) pack_e4m3_residual<NPS, NMT>(s, pf, pl);
+    __syncthreads();
+  };
+  // SP = 0: no residual terms (non-causal); 1: on the masked (diagonal) tiles of a causal
+  // launch; 2: on every tile (the first kPreciseRows rows of a causal launch).
+  auto run = [&](auto sp) __attribute__((always_inline)) {
+    constexpr int SP = decltype(sp)::value;
+    using SA = std::integral_constant<bool, SP == 2>;  // residual on mask-free tiles
+    using SB = std::integral_constant<bool, SP >= 1>;  // residual on masked tiles
+    using P0 = std::integral_constant<int, 0>;
+    using PA = std::integral_constant<int, SA::value ? 2 : 1>;
+    using PB = std::integral_constant<int, SB::value ? 2 : 1>;
+    using F = std::false_type;
+    using T = std::true_type;
+    int j = 0;
+    if (n_free > 0) {
+      tile(0, P0{}, F{}, SA{});
+      for (j = 1; j < n_free; ++j) tile(j, PA{}, F{}, SA{});
+    }
+    if (j < n_tiles) {
+      if (j == 0) tile(0, P0{}, T{}, SB{});
+      else tile(j, PA{}, T{}, SB{});
+      for (++j; j < n_tiles; ++j) tile(j, PB{}, T{}, SB{});
+    }
+    if (n_tiles > 0) {
+      __builtin_amdgcn_s_setprio(1);
+      if (n_tiles > n_free) pv(vt[(n_tiles - 1) & 1], std::integral_constant<bool, SB::value>{});
+      else pv(vt[(n_tiles - 1) & 1], std::integral_constant<bool, SA::value>{});
+      __builtin_amdgcn_s_setprio(0);
+    }
+  };
+  if (!p.causal) run(std::integral_constant<int, 0>{});
+  else if (r0 >= kPreciseRows) run(std::integral_constant<int, 1>{});
+  else run(std::integral_constant<int, 2>{});
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (grp == 0) __syncthreads();  // both groups pass the same number of barriers
+
+  const float ltot = pair_sum(lsum);
+  const float inv = ltot > 0.f ? vd / ltot : 0.f;
+  const int row = r0 + lq;
+  if (row < Lq) {
+    __bf16* og = reinterpret_cast<__bf16*>(p.out) + (int64_t)(qs + row) * p.o_rs + (int64_t)head * p.o_hs;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        bf16x4 w = {(__bf16)(o[dt][4 * g + 0] * inv), (__bf16)(o[dt][4 * g + 1] * inv),
+                    (__bf16)(o[dt][4 * g + 2] * inv), (__bf16)(o[dt][4 * g + 3] * inv)};
+        *reinterpret_cast<bf16x4*>(og + 32 * dt + 8 * g + 4 * lh) = w;
+      }
+    if (lh == 0) {
+      const float lse = ltot > 0.f ? m * c_nat + logf(ltot) : -INFINITY;
+      p.lse[(int64_t)(qs + row) * p.lse_rs + head] = lse;
+    }
+  }
+}
+
+//--------------------------------------------------------------------------------------
 // host dispatch
 //--------------------------------------------------------------------------------------
 int heads_per_wg(int group) {
@@ -1380,9 +1907,21 @@ struct KernelChoice {
 };
 
 template <typename T>
-KernelChoice pick16(int d, int hp) {
+KernelChoice pick16(int d, int hp, bool vt) {
   KernelChoice k;
-  if (d == 64 || d == 128) {
+  if (vt && (d == 64 || d == 128)) {
+    k.threads = kPPThreads;
+    k.rows = 32 * kPPWaves / hp;
+#define FA4CP_PICK(DD)                                  \
+  if (d == DD) {                                        \
+    if (hp == 4) k.fn = attn_fwd_16bit_vt<T, DD, 4>;    \
+    else if (hp == 2) k.fn = attn_fwd_16bit_vt<T, DD, 2>; \
+    else k.fn = attn_fwd_16bit_vt<T, DD, 1>;            \
+  }
+    FA4CP_PICK(64)
+    FA4CP_PICK(128)
+#undef FA4CP_PICK
+  } else if (d == 64 || d == 128) {
     k.threads = kPPThreads;
     k.rows = 32 * kPPWaves / hp;
 #define FA4CP_PICK(DD)                                  \
@@ -1404,9 +1943,15 @@ KernelChoice pick16(int d, int hp) {
   return k;
 }
 
-KernelChoice pick8(int d, int hp) {
+KernelChoice pick8(int d, int hp, bool vt) {
   KernelChoice k;
-  if (d == 128) {
+  if (vt && d == 128) {
+    k.threads = kPPThreads;
+    k.rows = 32 * kPPWaves / hp;
+    if (hp == 4) k.fn = attn_fwd_e4m3_vt<4>;
+    else if (hp == 2) k.fn = attn_fwd_e4m3_vt<2>;
+    else k.fn = attn_fwd_e4m3_vt<1>;
+  } else if (d == 128) {
     k.threads = kPPThreads;
     k.rows = 32 * kPPWaves / hp;
     if (hp == 4) k.fn = attn_fwd_e4m3_pp<4>;
@@ -1453,11 +1998,18 @@ extern "C" int fa4cp_attn_fwd(const fa4cp_attn_args* a, void* stream) {
   const int hp = heads_per_wg(group);
   const int d = a->d;
 
+  const bool use_vt = a->v_t != nullptr;
+  if (use_vt) {
+    if (a->vt_d_stride < fa4cp_vt_min_d_stride(a->total_k, nseq) || a->vt_d_stride % kVtPad != 0 ||
+        ((uintptr_t)a->v_t % 16) != 0)
+      return set_error(FA4CP_EINVAL, "attn_fwd: v_t must be 16-byte aligned with vt_d_stride a multiple "
+                       "of %d and >= %lld", kVtPad, (long long)fa4cp_vt_min_d_stride(a->total_k, nseq));
+  }
   KernelChoice kc;
   switch (a->dtype) {
-    case FA4CP_BF16: kc = pick16<__bf16>(d, hp); break;
-    case FA4CP_FP16: kc = pick16<_Float16>(d, hp); break;
-    case FA4CP_E4M3: kc = pick8(d, hp); break;
+    case FA4CP_BF16: kc = pick16<__bf16>(d, hp, use_vt); break;
+    case FA4CP_FP16: kc = pick16<_Float16>(d, hp, use_vt); break;
+    case FA4CP_E4M3: kc = pick8(d, hp, use_vt); break;
     default: return set_error(FA4CP_EUNSUPPORTED, "attn_fwd: unsupported dtype %d", a->dtype);
   }
   if (kc.fn == nullptr)
@@ -1493,6 +2045,7 @@ extern "C" int fa4cp_attn_fwd(const fa4cp_attn_args* a, void* stream) {
   p.causal = a->causal ? 1 : 0; p.q_sel = a->q_sel; p.k_sel = a->k_sel;
   p.scale = a->softmax_scale;
   p.qd = a->q_descale; p.kd = a->k_descale; p.vd = a->v_descale;
+  p.vt = a->v_t; p.vt_ds = a->vt_d_stride;
   p.n_rt = (max_q + kc.rows - 1) / kc.rows;
   p.n_hg = a->h_kv * (group / hp);
   const int64_t blocks = (int64_t)p.n_hg * nseq * p.n_rt;

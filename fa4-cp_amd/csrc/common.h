@@ -111,6 +111,40 @@ __device__ __forceinline__ void bload8_f32(__amdgpu_buffer_rsrc_t r, int off, fl
   }
 }
 
+// Row range [start, start + len) of sequence j after a half selection (FA4CP_SEL_*).
+__device__ __forceinline__ void seq_range(const int32_t* cu, int j, int total, int sel, int& start,
+                                          int& len) {
+  int s = 0, e = total;
+  if (cu != nullptr) {
+    s = cu[j];
+    e = cu[j + 1];
+  }
+  const int mid = (s + e) >> 1;
+  if (sel == FA4CP_SEL_FRONT_HALF) e = mid;
+  if (sel == FA4CP_SEL_BACK_HALF) s = mid;
+  start = s;
+  len = e - s;
+}
+__device__ __forceinline__ void vt_seq_range(const int32_t* cu, int j, int total, int sel, int& start,
+                                             int& len) {
+  seq_range(cu, j, total, sel, start, len);
+}
+
+// Keys of one sequence in V^T are padded to a multiple of kVtPad (zeros), so key tiles of up
+// to kVtPad keys never cross into the next sequence and every tile row is 16-byte aligned.
+constexpr int kVtPad = 128;
+
+// First V^T position of sequence j: the padded lengths of the sequences before it.
+__device__ __forceinline__ int64_t vt_seq_start(const int32_t* cu, int j, int sel) {
+  int64_t p = 0;
+  for (int i = 0; i < j; ++i) {
+    const int s = cu[i], e = cu[i + 1], mid = (s + e) >> 1;
+    const int len = sel == FA4CP_SEL_FRONT_HALF ? mid - s : sel == FA4CP_SEL_BACK_HALF ? e - mid : e - s;
+    p += (len + kVtPad - 1) / kVtPad * kVtPad;
+  }
+  return p;
+}
+
 // Index of the packed sequence that contains `row`: the largest j with cu[j] <= row
 // (binary search over cu[0..nseq]).
 __device__ __forceinline__ int find_seq(const int32_t* __restrict__ cu, int nseq, int64_t row) {

@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libfa4cp.so"
 # FA4CP_LIB selects another build of the library (the in-tree one by default)
 LIB_PATH = os.environ.get("FA4CP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # element types (FA4CP_*)
 BF16, FP16, E4M3, FP32 = 0, 1, 2, 3
@@ -67,6 +67,28 @@ class AttnArgs(ctypes.Structure):
         ("q_descale", ctypes.c_void_p),
         ("k_descale", ctypes.c_void_p),
         ("v_descale", ctypes.c_void_p),
+        ("v_t", ctypes.c_void_p),
+        ("vt_d_stride", ctypes.c_int64),
+    ]
+
+
+class TransposeArgs(ctypes.Structure):
+    """Mirror of fa4cp_transpose_args."""
+
+    _fields_ = [
+        ("v", ctypes.c_void_p),
+        ("v_row_stride", ctypes.c_int64),
+        ("v_head_stride", ctypes.c_int64),
+        ("cu_k", ctypes.c_void_p),
+        ("nseq", ctypes.c_int32),
+        ("total_k", ctypes.c_int32),
+        ("max_seqlen_k", ctypes.c_int32),
+        ("k_sel", ctypes.c_int32),
+        ("h_kv", ctypes.c_int32),
+        ("d", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("v_t", ctypes.c_void_p),
+        ("vt_d_stride", ctypes.c_int64),
     ]
 
 
@@ -94,6 +116,8 @@ SIGNATURES = {
         [ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
          ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p],
     ),
+    "fa4cp_transpose_v": (ctypes.c_int, [ctypes.POINTER(TransposeArgs), ctypes.c_void_p]),
+    "fa4cp_vt_min_d_stride": (ctypes.c_int64, [ctypes.c_int32, ctypes.c_int32]),
     "fa4cp_last_error": (ctypes.c_char_p, []),
     "fa4cp_abi_version": (ctypes.c_int, []),
 }

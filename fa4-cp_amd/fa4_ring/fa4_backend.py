@@ -25,6 +25,8 @@ from ._lib import SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF
 
 SUPPORTED_HEAD_DIMS = {torch.bfloat16: (64, 128, 256), torch.float16: (64, 128, 256),
                        torch.float8_e4m3fn: (128, 256)}
+# (dtype, head dim) pairs whose kernels read a pre-transposed V^T (fa4cp_transpose_v)
+VT_HEAD_DIMS = {torch.bfloat16: (64, 128), torch.float16: (64, 128), torch.float8_e4m3fn: (128,)}
 
 
 def has_fa4() -> bool:
@@ -68,6 +70,38 @@ def out_dtype_for(dt: torch.dtype) -> torch.dtype:
     return torch.bfloat16 if dt == torch.float8_e4m3fn else dt
 
 
+def transpose_v(v: torch.Tensor, *, cu_seqlens_k: Optional[torch.Tensor] = None,
+                max_seqlen_k: Optional[int] = None, k_sel: int = SEL_ALL) -> Tuple[torch.Tensor, int]:
+    """V [T_k, H_kv, D] -> (V^T, row stride): the keys selected by ``k_sel`` of every packed
+    sequence, transposed to [H_kv, D, positions] (fa4cp_transpose_v layout: each sequence
+    starts at a multiple of 128 positions, zero padded).  Runs on the current stream."""
+    lib = _lib.load()
+    _require(v.dim() == 3 and v.is_cuda, "v must be a [T, H_kv, D] device tensor")
+    _require(v.stride(2) == 1, "v must be contiguous in the head dim")
+    t_k, h_kv, d = v.shape
+    nseq = 1
+    if cu_seqlens_k is not None:
+        _cu_ok(cu_seqlens_k, v.device, "cu_seqlens_k")
+        _require(max_seqlen_k is not None, "max_seqlen_k required with cu_seqlens_k")
+        nseq = cu_seqlens_k.shape[0] - 1
+    stride = int(lib.fa4cp_vt_min_d_stride(t_k, nseq))
+    vt = torch.empty(h_kv * d * stride, dtype=v.dtype, device=v.device)
+    a = _lib.TransposeArgs()
+    a.v = v.data_ptr()
+    a.v_row_stride, a.v_head_stride = v.stride(0), v.stride(1)
+    a.cu_k = _lib.ptr(cu_seqlens_k)
+    a.nseq = nseq
+    a.total_k = t_k
+    a.max_seqlen_k = int(max_seqlen_k) if cu_seqlens_k is not None else t_k
+    a.k_sel = int(k_sel)
+    a.h_kv, a.d = h_kv, d
+    a.dtype = _lib.dtype_code(v.dtype)
+    a.v_t = vt.data_ptr()
+    a.vt_d_stride = stride
+    _lib.check(lib.fa4cp_transpose_v(ctypes.byref(a), _lib.stream_handle(v.device)), "fa4cp_transpose_v")
+    return vt, stride
+
+
 def fa4_attn(
     q: torch.Tensor,  # [T_q, H, D]
     k: torch.Tensor,  # [T_k, H_kv, D]
@@ -86,6 +120,8 @@ def fa4_attn(
     k_sel: int = SEL_ALL,
     out: Optional[torch.Tensor] = None,
     lse: Optional[torch.Tensor] = None,
+    v_t: Optional[Tuple[torch.Tensor, int]] = None,
+    use_vt: bool = True,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Varlen flash-attention forward.
 
@@ -95,7 +131,11 @@ def fa4_attn(
     sequence.  Causal masking is bottom-right aligned per sequence.  With
     ``q_sel=SEL_BACK_HALF`` only the back half of each query sequence is computed and
     written (at its own rows of ``out`` / ``lse``); with ``k_sel=SEL_FRONT_HALF`` only
-    the front half of each key sequence is attended."""
+    the front half of each key sequence is attended.
+
+    Where a kernel reading V^T exists (``VT_HEAD_DIMS``) and ``use_vt`` is set, V is first
+    transposed with ``transpose_v`` (or ``v_t`` from an earlier ``transpose_v`` call with
+    the same keys and selection is used)."""
     lib = _lib.load()
     _require(q.dim() == 3 and k.dim() == 3 and v.dim() == 3, "q, k, v must be [T, H, D]")
     _require(q.is_cuda, "fa4_attn runs on the GPU: q must be a device tensor")
@@ -147,6 +187,12 @@ def fa4_attn(
     _require(lse.shape == (t_q, h_q) and lse.dtype == torch.float32 and lse.stride(1) == 1,
              "lse must be [T_q, H] float32 with unit head stride")
 
+    vt_ptr, vt_stride = None, 0
+    if use_vt and d in VT_HEAD_DIMS.get(dt, ()):
+        if v_t is None:
+            v_t = transpose_v(v, cu_seqlens_k=cu_seqlens_k, max_seqlen_k=max_seqlen_k, k_sel=k_sel)
+        vt_ptr, vt_stride = v_t[0].data_ptr(), int(v_t[1])
+
     qd = _norm_descale(q_descale, h_kv, dev)
     kd = _norm_descale(k_descale, h_kv, dev)
     vd = _norm_descale(v_descale, h_kv, dev)
@@ -169,9 +215,11 @@ def fa4_attn(
     a.q_sel, a.k_sel = int(q_sel), int(k_sel)
     a.softmax_scale = float(softmax_scale)
     a.q_descale, a.k_descale, a.v_descale = _lib.ptr(qd), _lib.ptr(kd), _lib.ptr(vd)
+    a.v_t, a.vt_d_stride = vt_ptr, vt_stride
     rc = lib.fa4cp_attn_fwd(ctypes.byref(a), _lib.stream_handle(dev))
     _lib.check(rc, "fa4cp_attn_fwd")
     return out, lse
 
 
-__all__ = ["fa4_attn", "has_fa4", "out_dtype_for", "SEL_ALL", "SEL_BACK_HALF", "SEL_FRONT_HALF"]
+__all__ = ["fa4_attn", "transpose_v", "has_fa4", "out_dtype_for", "SEL_ALL", "SEL_BACK_HALF",
+           "SEL_FRONT_HALF"]

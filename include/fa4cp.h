@@ -18,6 +18,8 @@
  *   fa4cp_merge_states          <- fa4_ring/merge.py:39-42 (flashinfer.cascade.merge_states)
  *   fa4cp_zigzag_shard          <- fa4_ring/zigzag.py:31-39 and :82-97 (zigzag_shard, zigzag_shard_varlen)
  *   fa4cp_zigzag_unshard        <- fa4_ring/zigzag.py:42-50 (zigzag_unshard)
+ *   fa4cp_transpose_v           <- no counterpart: the V^T layout the fast attention kernels
+ *                                  load (FA4 reads V as given; see fa4cp_attn_args.v_t)
  */
 #ifndef FA4CP_H_
 #define FA4CP_H_
@@ -28,7 +30,7 @@
 extern "C" {
 #endif
 
-#define FA4CP_ABI_VERSION 1
+#define FA4CP_ABI_VERSION 2
 
 /* status codes */
 #define FA4CP_OK 0
@@ -96,9 +98,38 @@ typedef struct fa4cp_attn_args {
   const float* q_descale; /* [h_kv] or NULL */
   const float* k_descale; /* [h_kv] or NULL */
   const float* v_descale; /* [h_kv] or NULL */
+  /* Optional V^T of the selected keys, written by fa4cp_transpose_v with the same v, cu_k,
+   * nseq, total_k, max_seqlen_k, k_sel, h_kv, d and dtype.  When set (head dims 64 and 128
+   * for BF16 / FP16, 128 for E4M3), the kernels load V^T tiles directly instead of
+   * transposing V in LDS, which is markedly faster.  NULL: V alone is read. */
+  const void* v_t;
+  int64_t vt_d_stride;
 } fa4cp_attn_args;
 
 int fa4cp_attn_fwd(const fa4cp_attn_args* args, void* stream);
+
+/*
+ * V -> V^T for fa4cp_attn_args.v_t.  Element (kv head g, column c, position p) of V^T is at
+ * v_t[(g * d + c) * vt_d_stride + p] (elements of dtype).  Sequence j's keys selected by
+ * k_sel inside [cu_k[j], cu_k[j+1]) (cu_k == NULL: one sequence of total_k rows) sit at
+ * positions [P_j, P_j + L_j) in order, with P_j = sum over i < j of L_i rounded up to 128;
+ * the rest of each sequence's padded range holds zeros.  vt_d_stride must be a multiple of
+ * 128 and at least fa4cp_vt_min_d_stride(total_k, nseq); v_t then needs
+ * h_kv * d * vt_d_stride elements.  v, v_t and the v strides must be 16-byte aligned.
+ */
+typedef struct fa4cp_transpose_args {
+  const void* v;
+  int64_t v_row_stride, v_head_stride; /* in elements */
+  const int32_t* cu_k;                 /* [nseq + 1] or NULL */
+  int32_t nseq, total_k, max_seqlen_k;
+  int32_t k_sel;
+  int32_t h_kv, d, dtype; /* BF16, FP16 or E4M3; d = 64, 128 or 256 */
+  void* v_t;
+  int64_t vt_d_stride;
+} fa4cp_transpose_args;
+
+int fa4cp_transpose_v(const fa4cp_transpose_args* args, void* stream);
+int64_t fa4cp_vt_min_d_stride(int32_t total_k, int32_t nseq);
 
 /*
  * In-place online-softmax merge (flashinfer.cascade.merge_state_in_place semantics, natural

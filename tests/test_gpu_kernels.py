@@ -11,7 +11,7 @@ from fa4_ring import zigzag as Z
 from fa4_ring.fa4_backend import SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, fa4_attn
 from fa4_ring.merge import merge_state_in_place, merge_states
 from gpu_helpers import (DEV, TOL_BF16_OUT, TOL_FP8_OUT, TOL_LSE, TOL_MERGE_FP32, lse_err, max_err,
-                         oracle_attn, rounded, say, scale_for)
+                         oracle_attn, rounded, say, scale_for, seq_bounds)
 from oracle import ring_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -140,6 +140,36 @@ def test_merge_states(dtype, t, ns, h, d):
     assert lse_err(so, el) <= TOL_MERGE_FP32
 
 
+# ------------------------------------------------------------------------- V^T layout
+
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float16, 64),
+                                     (torch.float8_e4m3fn, 128), (torch.bfloat16, 256)])
+@pytest.mark.parametrize("cu,sel", [(None, SEL_ALL), (None, SEL_FRONT_HALF), ([0, 64, 64, 330, 402], SEL_ALL),
+                                    ([0, 64, 64, 330, 402], SEL_FRONT_HALF),
+                                    ([0, 200, 456], SEL_BACK_HALF)])
+def test_transpose_v_layout_bit_exact(dtype, d, cu, sel):
+    """V^T positions: sequence j's selected keys at P_j + i, P_j = sum of the earlier
+    sequences' selected lengths rounded up to 128, zeros up to the next multiple of 128."""
+    from fa4_ring.fa4_backend import transpose_v
+    say(f"transpose_v {dtype} d={d} cu={cu} sel={sel}")
+    total = cu[-1] if cu is not None else 300
+    hkv = 3
+    g = torch.Generator().manual_seed(5)
+    v = torch.randn(total, hkv, d, generator=g).to(dtype)
+    cud = None if cu is None else torch.tensor(cu, dtype=torch.int32, device=DEV)
+    mx = None if cu is None else max(b - a for a, b in zip(cu[:-1], cu[1:]))
+    vt, stride = transpose_v(v.to(DEV), cu_seqlens_k=cud, max_seqlen_k=mx, k_sel=sel)
+    got = vt.cpu().view(torch.uint8 if dtype == torch.float8_e4m3fn else torch.int16).reshape(hkv, d, stride)
+    raw = v.view(torch.uint8 if dtype == torch.float8_e4m3fn else torch.int16)
+    pos = 0
+    for (s0, e0) in seq_bounds(cu, total, sel):
+        n = e0 - s0
+        pad = (n + 127) // 128 * 128
+        assert torch.equal(got[:, :, pos:pos + n], raw[s0:e0].permute(1, 2, 0))
+        assert (got[:, :, pos + n:pos + pad] == 0).all()
+        pos += pad
+
+
 # ------------------------------------------------------------------------- attention
 
 def _qkv(tq, tk, h, hkv, d, seed, dtype):
@@ -171,13 +201,15 @@ ATTN_CASES = [
 ]
 
 
+@pytest.mark.parametrize("use_vt", [True, False])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("case", ATTN_CASES)
-def test_attention_16bit(dtype, case):
+def test_attention_16bit(dtype, case, use_vt):
     tq, tk, h, hkv, d, causal, q_sel, k_sel, cu = case
     if cu is not None:
         tq = tk = cu[-1]
-    say(f"attn {dtype} tq={tq} tk={tk} h={h}/{hkv} d={d} causal={causal} sel={q_sel},{k_sel} cu={cu}")
+    say(f"attn {dtype} tq={tq} tk={tk} h={h}/{hkv} d={d} causal={causal} sel={q_sel},{k_sel} "
+        f"cu={cu} vt={use_vt}")
     q, k, v = _qkv(tq, tk, h, hkv, d, 7, dtype)
     scale = scale_for(d)
     cud = None if cu is None else torch.tensor(cu, dtype=torch.int32, device=DEV)
@@ -186,7 +218,7 @@ def test_attention_16bit(dtype, case):
     lse = torch.full((tq, h), float("nan"), device=DEV)
     fa4_attn(q.to(dtype).to(DEV), k.to(dtype).to(DEV), v.to(dtype).to(DEV), causal=causal,
              softmax_scale=scale, cu_seqlens_q=cud, cu_seqlens_k=cud, max_seqlen_q=mx,
-             max_seqlen_k=mx, q_sel=q_sel, k_sel=k_sel, out=out, lse=lse)
+             max_seqlen_k=mx, q_sel=q_sel, k_sel=k_sel, out=out, lse=lse, use_vt=use_vt)
     eo, el = oracle_attn(q, k, v, causal, scale, cu, cu, q_sel, k_sel)
     sel = ~torch.isnan(el)
     # rows outside the selection are left untouched
@@ -225,8 +257,9 @@ FP8_CASES = [
 ]
 
 
+@pytest.mark.parametrize("use_vt", [True, False])
 @pytest.mark.parametrize("case", FP8_CASES)
-def test_attention_e4m3(case):
+def test_attention_e4m3(case, use_vt):
     tq, tk, h, hkv, d, causal, q_sel, k_sel, cu = case
     if cu is not None:
         tq = tk = cu[-1]
@@ -246,7 +279,7 @@ def test_attention_e4m3(case):
              cu_seqlens_q=cud, cu_seqlens_k=cud, max_seqlen_q=mx, max_seqlen_k=mx,
              q_descale=torch.tensor(sq, device=DEV), k_descale=torch.tensor([sk] * hkv, device=DEV),
              v_descale=torch.tensor(sv, device=DEV).reshape(1, 1).expand(1, hkv),
-             q_sel=q_sel, k_sel=k_sel, out=out, lse=lse)
+             q_sel=q_sel, k_sel=k_sel, out=out, lse=lse, use_vt=use_vt)
     eo, el = oracle_attn(O.dequantize_e4m3(q8, sq), O.dequantize_e4m3(k8, sk),
                          O.dequantize_e4m3(v8, sv), causal, scale, cu, cu, q_sel, k_sel)
     sel = ~torch.isnan(el)

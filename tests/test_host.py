@@ -53,11 +53,13 @@ def test_error_path_reports_message_without_gpu():
         _lib.check(rc, "fa4cp_attn_fwd")
 
 
-def test_attn_args_layout_matches_c_header():
-    fields = [f for f, _ in _lib.AttnArgs._fields_]
+@pytest.mark.parametrize("struct,cname", [(_lib.AttnArgs, "fa4cp_attn_args"),
+                                           (_lib.TransposeArgs, "fa4cp_transpose_args")])
+def test_args_layout_matches_c_header(struct, cname):
+    fields = [f for f, _ in struct._fields_]
     prog = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",
-            'printf("%zu\\n", sizeof(fa4cp_attn_args));']
-    prog += [f'printf("%zu\\n", offsetof(fa4cp_attn_args, {f}));' for f in fields]
+            f'printf("%zu\\n", sizeof({cname}));']
+    prog += [f'printf("%zu\\n", offsetof({cname}, {f}));' for f in fields]
     prog.append("return 0;}")
     with tempfile.TemporaryDirectory() as td:
         src, exe = os.path.join(td, "l.c"), os.path.join(td, "l")
@@ -65,9 +67,9 @@ def test_attn_args_layout_matches_c_header():
         subprocess.run(["gcc", "-o", exe, src], check=True)
         vals = [int(x) for x in subprocess.run([exe], check=True, capture_output=True,
                                                text=True).stdout.split()]
-    assert vals[0] == ctypes.sizeof(_lib.AttnArgs)
+    assert vals[0] == ctypes.sizeof(struct)
     for f, off in zip(fields, vals[1:]):
-        assert getattr(_lib.AttnArgs, f).offset == off, f
+        assert getattr(struct, f).offset == off, f
 
 
 def test_ring_config_checks():
