@@ -7,6 +7,9 @@ incremental LSE merges) over inputs already resident in HBM, at the bf16 benchma
 configuration: N = 131072 tokens, cp_size = 8 (local Q, K, V of 16384 tokens each),
 H_q = 32, H_kv = 8, D = 128, causal, rank 3 (all source ranks' KV shards in HBM).
 
+Every step first transposes the source's selected V keys (fa4cp_transpose_v) for the
+attention kernel that reads V^T; both are inside the timed sweep.
+
 Prints one JSON line.  `value` is causal-adjusted attention TFLOP/s of the sweep:
 F = sum over steps of 4 * Tq * Tk * D * H_q (halved for the causal step) = 17.592 TFLOP per
 sweep, divided by the measured sweep time.  Also reported: the same sweep in OCP e4m3
@@ -40,7 +43,7 @@ N, CP, HQ, HKV, D = 131072, 8, 32, 8, 128
 # rocprofv3 counter passes over this script: FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the
 # factors being what those counters read for the zig-zag gather (a plain copy of known size).
 # The summary with both commands is under profiles/.
-ATTN_TRAFFIC_BYTES_RANK3 = 466728 * 1024
+ATTN_TRAFFIC_BYTES_RANK3 = 467143 * 1024
 
 
 def sweep_flops(t_local: int, cp: int, hq: int, d: int) -> float:
@@ -131,11 +134,12 @@ def timed_sweeps(fn, steps: int, warmup: int, clock: KernelClock = None):
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    saved = (RA.fa4_attn, RA.merge_state_in_place, RA.merge_states)
+    saved = (RA.fa4_attn, RA.merge_state_in_place, RA.merge_states, RA.transpose_v)
     if clock is not None:
         RA.fa4_attn = clock.wrap("attn", saved[0])
         RA.merge_state_in_place = clock.wrap("merge_inplace", saved[1])
         RA.merge_states = clock.wrap("merge_states", saved[2])
+        RA.transpose_v = clock.wrap("transpose_v", saved[3])
     try:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -144,7 +148,7 @@ def timed_sweeps(fn, steps: int, warmup: int, clock: KernelClock = None):
         torch.cuda.synchronize()
         dt = (time.perf_counter() - t0) / steps
     finally:
-        RA.fa4_attn, RA.merge_state_in_place, RA.merge_states = saved
+        RA.fa4_attn, RA.merge_state_in_place, RA.merge_states, RA.transpose_v = saved
     return dt
 
 
@@ -239,6 +243,11 @@ def main():
     mbytes = (n_full * merge_bytes_inplace(t_local, HQ, D, 2) +
               n_back * merge_bytes_inplace(t_local // 2, HQ, D, 2)) / (CP - 1)
     merge_gbs = mbytes / (merge_ms * 1e-3) / 1e9
+    # V -> V^T per step: read the selected keys of V, write them transposed (steps 1..rank
+    # select the front half of the source's keys)
+    tr_ms = clock.mean_ms("transpose_v")
+    keys = (t_local * (1 + (CP - 1 - n_full)) + (t_local // 2) * n_full) / CP
+    tr_bytes = 2.0 * keys * HKV * D * 2
 
     result = {
         "metric": METRIC,
@@ -259,13 +268,18 @@ def main():
                    "global_batch": 1, "seq_len": N, "cp_size": CP, "cp_rank": rank,
                    "h_q": HQ, "h_kv": HKV, "head_dim": D, "parallelism": "cp8 (one rank's share on 1 GPU)"},
         "frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
-        "roofline": {"bound": "mfma", "kernel": "attn_fwd_16bit_pp<bf16,128,4>",
+        "roofline": {"bound": "mfma", "kernel": "attn_fwd_16bit_vt<bf16,128,4>",
                      "achieved": round(attn_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": ATTN_TRAFFIC_BYTES_RANK3 if rank == 3 else None,
                      "algorithmic_per_launch": f"{per_launch / 1e12:.4f} TFLOP "
                                                "(4*Tq*Tk*D*H_q, halved for the causal step)",
                      "avg_launch_ms": round(attn_ms, 4), "launches": clock.count("attn")},
+        "transpose_v": {"kernel": "transpose_v_kernel<u16,128>", "avg_launch_ms": round(tr_ms, 4),
+                        "algorithmic_bytes_per_launch": round(tr_bytes),
+                        "achieved_GBs": round(tr_bytes / (tr_ms * 1e-3) / 1e9, 1),
+                        "frac": round(tr_bytes / (tr_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                        "launches": clock.count("transpose_v")},
         "merge": {"kernel": "merge_inplace_kernel<bf16>", "avg_launch_ms": round(merge_ms, 4),
                   "algorithmic_bytes_per_launch": round(mbytes),
                   "achieved_GBs": round(merge_gbs, 1), "peak_GBs": PEAK_HBM_GBS,

@@ -70,6 +70,11 @@ def out_dtype_for(dt: torch.dtype) -> torch.dtype:
     return torch.bfloat16 if dt == torch.float8_e4m3fn else dt
 
 
+def uses_vt(dtype: torch.dtype, d: int) -> bool:
+    """True when fa4_attn runs a kernel that reads V^T for this input type and head dim."""
+    return d in VT_HEAD_DIMS.get(dtype, ())
+
+
 def transpose_v(v: torch.Tensor, *, cu_seqlens_k: Optional[torch.Tensor] = None,
                 max_seqlen_k: Optional[int] = None, k_sel: int = SEL_ALL) -> Tuple[torch.Tensor, int]:
     """V [T_k, H_kv, D] -> (V^T, row stride): the keys selected by ``k_sel`` of every packed
@@ -188,7 +193,7 @@ def fa4_attn(
              "lse must be [T_q, H] float32 with unit head stride")
 
     vt_ptr, vt_stride = None, 0
-    if use_vt and d in VT_HEAD_DIMS.get(dt, ()):
+    if use_vt and uses_vt(dt, d):
         if v_t is None:
             v_t = transpose_v(v, cu_seqlens_k=cu_seqlens_k, max_seqlen_k=max_seqlen_k, k_sel=k_sel)
         vt_ptr, vt_stride = v_t[0].data_ptr(), int(v_t[1])
@@ -221,5 +226,5 @@ def fa4_attn(
     return out, lse
 
 
-__all__ = ["fa4_attn", "transpose_v", "has_fa4", "out_dtype_for", "SEL_ALL", "SEL_BACK_HALF",
+__all__ = ["fa4_attn", "transpose_v", "uses_vt", "has_fa4", "out_dtype_for", "SEL_ALL", "SEL_BACK_HALF",
            "SEL_FRONT_HALF"]

@@ -31,7 +31,8 @@ from typing import List, Optional, Sequence, Tuple
 import torch
 
 from .config import RingConfig
-from .fa4_backend import SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, fa4_attn, out_dtype_for
+from .fa4_backend import (SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, fa4_attn, out_dtype_for, transpose_v,
+                          uses_vt)
 from .merge import merge_state_in_place, merge_states
 from .zigzag import zigzag_shard, zigzag_shard_varlen
 
@@ -122,30 +123,36 @@ def ring_flash_attn(
     dev = local_q.device
     common = dict(softmax_scale=scale, cu_seqlens_q=cu_seqlens, cu_seqlens_k=cu_seqlens,
                   max_seqlen_q=max_seqlen, max_seqlen_k=max_seqlen, q_descale=qd)
+    vt_kernels = uses_vt(local_q.dtype, d)
+
+    def attn(k, v, src, causal, k_sel=SEL_ALL, **kw):
+        """One ring step's attention; V is transposed first (only the selected keys) when the
+        kernel for this type reads V^T."""
+        v_t = None
+        if vt_kernels:
+            v_t = transpose_v(v, cu_seqlens_k=cu_seqlens, max_seqlen_k=max_seqlen, k_sel=k_sel)
+        return fa4_attn(local_q, k, v, causal=causal, k_sel=k_sel, k_descale=kd(src), v_descale=vd(src),
+                        v_t=v_t, **kw, **common)
 
     if cfg.merge_mode == "batched" and S > 1:
         # every step writes its partial straight into slot `step` of the merge buffer
         vbuf = torch.empty((total, S, h_q, d), dtype=odt, device=dev)
         sbuf = torch.empty((total, S, h_q), dtype=torch.float32, device=dev)
-        fa4_attn(local_q, local_k, local_v, causal=True, k_descale=kd(rank), v_descale=vd(rank),
-                 out=vbuf[:, 0], lse=sbuf[:, 0], **common)
+        attn(local_k, local_v, rank, True, out=vbuf[:, 0], lse=sbuf[:, 0])
         for step in range(1, S):
             src = (rank - step) % S
             k, v = group.kv(src)
             if step <= rank:
-                fa4_attn(local_q, k, v, causal=False, k_sel=SEL_FRONT_HALF, k_descale=kd(src),
-                         v_descale=vd(src), out=vbuf[:, step], lse=sbuf[:, step], **common)
+                attn(k, v, src, False, k_sel=SEL_FRONT_HALF, out=vbuf[:, step], lse=sbuf[:, step])
             else:
                 # front rows of this slot stay empty: -inf LSE makes them the identity
                 sbuf[:, step].fill_(float("-inf"))
-                fa4_attn(local_q, k, v, causal=False, q_sel=SEL_BACK_HALF, k_descale=kd(src),
-                         v_descale=vd(src), out=vbuf[:, step], lse=sbuf[:, step], **common)
+                attn(k, v, src, False, q_sel=SEL_BACK_HALF, out=vbuf[:, step], lse=sbuf[:, step])
         out, _ = merge_states(vbuf, sbuf)
         return out
 
     # incremental (and cp_size == 1): step 0 seeds the accumulator with every row finite
-    acc, acc_lse = fa4_attn(local_q, local_k, local_v, causal=True, k_descale=kd(rank),
-                            v_descale=vd(rank), **common)
+    acc, acc_lse = attn(local_k, local_v, rank, True)
     if S == 1:
         return acc
     part = torch.empty_like(acc)
@@ -154,12 +161,10 @@ def ring_flash_attn(
         src = (rank - step) % S
         k, v = group.kv(src)
         if step <= rank:
-            fa4_attn(local_q, k, v, causal=False, k_sel=SEL_FRONT_HALF, k_descale=kd(src),
-                     v_descale=vd(src), out=part, lse=part_lse, **common)
+            attn(k, v, src, False, k_sel=SEL_FRONT_HALF, out=part, lse=part_lse)
             merge_state_in_place(acc, acc_lse, part, part_lse)
         else:
-            fa4_attn(local_q, k, v, causal=False, q_sel=SEL_BACK_HALF, k_descale=kd(src),
-                     v_descale=vd(src), out=part, lse=part_lse, **common)
+            attn(k, v, src, False, q_sel=SEL_BACK_HALF, out=part, lse=part_lse)
             merge_state_in_place(acc, acc_lse, part, part_lse, cu_seqlens=cu_seqlens,
                                  row_sel=SEL_BACK_HALF)
     return acc
