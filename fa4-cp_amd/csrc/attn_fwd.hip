@@ -1823,12 +1823,14 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_vt(AttnParams p) 
       }
     }
     __builtin_amdgcn_s_setprio(0);
+    // mask, row max and rescale need only S_j: they end the MFMA phase, which is the
+    // shorter of the two, instead of lengthening the softmax phase
+    if constexpr (decltype(masked)::value) mask(j * BN);
+    tile_max_rescale<NMT, NDT>(s, o, m, lsum, c_log2);
     __builtin_amdgcn_s_waitcnt(0);  // this wavefront's LDS-DMA from its previous VALU phase
     __syncthreads();
     if (grp == 0) dma_k_group(j + 2, kl[(j + 2) % 3]);
     else dma_vt_group(j + 1, vt[(j + 1) & 1]);
-    if constexpr (decltype(masked)::value) mask(j * BN);
-    tile_max_rescale<NMT, NDT>(s, o, m, lsum, c_log2);
     tile_exp<NMT>(s, m, lsum, c_log2);
     pack_e4m3<NPS, NMT>(s, pf);
     if constexpr (decltype(split)::value) pack_e4m3_residual<NPS, NMT>(s, pf, pl);
