@@ -2,13 +2,13 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--rank 3] [--no-cpu-baseline]
 
-A step is one rank's full ring sweep (cp_size attention launches plus cp_size - 1
-incremental LSE merges) over inputs already resident in HBM, at the bf16 benchmark
-configuration: N = 131072 tokens, cp_size = 8 (local Q, K, V of 16384 tokens each),
-H_q = 32, H_kv = 8, D = 128, causal, rank 3 (all source ranks' KV shards in HBM).
-
-Every step first transposes the source's selected V keys (fa4cp_transpose_v) for the
-attention kernel that reads V^T; both are inside the timed sweep.
+A step is one rank's full ring sweep over inputs already resident in HBM, at the bf16
+benchmark configuration: N = 131072 tokens, cp_size = 8 (local Q, K, V of 16384 tokens
+each), H_q = 32, H_kv = 8, D = 128, causal, rank 3 (all source ranks' KV shards in HBM).
+The default sweep transposes every source shard's V once (fa4cp_transpose_v) and runs one
+fused kernel over all cp_size sources (fa4cp_ring_sweep_fwd); both are inside the timed
+step.  The reference's per-step form (one attention launch plus one LSE merge per step) is
+timed beside it as `per_step_bf16`.
 
 Prints one JSON line.  `value` is causal-adjusted attention TFLOP/s of the sweep:
 F = sum over steps of 4 * Tq * Tk * D * H_q (halved for the causal step) = 17.592 TFLOP per
@@ -44,6 +44,8 @@ N, CP, HQ, HKV, D = 131072, 8, 32, 8, 128
 # factors being what those counters read for the zig-zag gather (a plain copy of known size).
 # The summary with both commands is under profiles/.
 ATTN_TRAFFIC_BYTES_RANK3 = 467143 * 1024
+# The same for the fused sweep kernel (one launch per sweep).
+SWEEP_TRAFFIC_BYTES_RANK3 = None
 
 
 def sweep_flops(t_local: int, cp: int, hq: int, d: int) -> float:
@@ -134,12 +136,13 @@ def timed_sweeps(fn, steps: int, warmup: int, clock: KernelClock = None):
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    saved = (RA.fa4_attn, RA.merge_state_in_place, RA.merge_states, RA.transpose_v)
+    saved = (RA.fa4_attn, RA.merge_state_in_place, RA.merge_states, RA.transpose_v, RA.launch_sweep)
     if clock is not None:
         RA.fa4_attn = clock.wrap("attn", saved[0])
         RA.merge_state_in_place = clock.wrap("merge_inplace", saved[1])
         RA.merge_states = clock.wrap("merge_states", saved[2])
         RA.transpose_v = clock.wrap("transpose_v", saved[3])
+        RA.launch_sweep = clock.wrap("sweep_kernel", saved[4])
     try:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -148,7 +151,7 @@ def timed_sweeps(fn, steps: int, warmup: int, clock: KernelClock = None):
         torch.cuda.synchronize()
         dt = (time.perf_counter() - t0) / steps
     finally:
-        RA.fa4_attn, RA.merge_state_in_place, RA.merge_states, RA.transpose_v = saved
+        RA.fa4_attn, RA.merge_state_in_place, RA.merge_states, RA.transpose_v, RA.launch_sweep = saved
     return dt
 
 
@@ -224,7 +227,7 @@ def main():
     flops = sweep_flops(t_local, CP, HQ, D)
     per_launch = flops / CP
 
-    # ---------------- headline: bf16 incremental sweep
+    # ---------------- headline: bf16 sweep, one fused launch (V transposes + sweep kernel)
     q_full, lq, ring = make_bf16_inputs(rank)
     cfg = RingConfig(cp_size=CP, cp_rank=rank, merge_mode="incremental")
 
@@ -233,9 +236,19 @@ def main():
 
     clock = KernelClock()
     sec = timed_sweeps(sweep, args.steps, args.warmup, clock)
-    attn_ms = clock.mean_ms("attn")
-    merge_ms = clock.mean_ms("merge_inplace")
     value = flops / sec / 1e12
+    sw_ms = clock.mean_ms("sweep_kernel")
+    sw_tflops = flops / (sw_ms * 1e-3) / 1e12
+    # V -> V^T: every source's whole shard, read and written once
+    tr_ms = clock.mean_ms("transpose_v")
+    tr_bytes = 2.0 * t_local * HKV * D * 2
+
+    # ---------------- the reference's per-step sweep (attention + LSE merge per step)
+    clockp = KernelClock()
+    secp = timed_sweeps(lambda: ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, fused=False),
+                        args.steps, args.warmup, clockp)
+    attn_ms = clockp.mean_ms("attn")
+    merge_ms = clockp.mean_ms("merge_inplace")
     attn_tflops = per_launch / (attn_ms * 1e-3) / 1e12
     # merge bytes: steps 1..rank merge every row, steps rank+1.. only the back half
     n_full = min(rank, CP - 1)
@@ -243,11 +256,6 @@ def main():
     mbytes = (n_full * merge_bytes_inplace(t_local, HQ, D, 2) +
               n_back * merge_bytes_inplace(t_local // 2, HQ, D, 2)) / (CP - 1)
     merge_gbs = mbytes / (merge_ms * 1e-3) / 1e9
-    # V -> V^T per step: read the selected keys of V, write them transposed (steps 1..rank
-    # select the front half of the source's keys)
-    tr_ms = clock.mean_ms("transpose_v")
-    keys = (t_local * (1 + (CP - 1 - n_full)) + (t_local // 2) * n_full) / CP
-    tr_bytes = 2.0 * keys * HKV * D * 2
 
     result = {
         "metric": METRIC,
@@ -264,26 +272,34 @@ def main():
         "data": "synthetic (q/k/v ~ N(0,1) bf16, seeded on the GPU)",
         "config": {"workload": "bf16 causal zig-zag ring sweep, one rank's share of cp_size=8 over "
                                "N=131072 (local Q/K/V 16384 tokens), H_q=32, H_kv=8, D=128, "
-                               f"rank {rank}, incremental merge, all 8 source KV shards in HBM",
+                               f"rank {rank}, all 8 source KV shards in HBM, fused sweep kernel",
                    "global_batch": 1, "seq_len": N, "cp_size": CP, "cp_rank": rank,
                    "h_q": HQ, "h_kv": HKV, "head_dim": D, "parallelism": "cp8 (one rank's share on 1 GPU)"},
         "frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
-        "roofline": {"bound": "mfma", "kernel": "attn_fwd_16bit_vt<bf16,128,4>",
-                     "achieved": round(attn_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": ATTN_TRAFFIC_BYTES_RANK3 if rank == 3 else None,
-                     "algorithmic_per_launch": f"{per_launch / 1e12:.4f} TFLOP "
-                                               "(4*Tq*Tk*D*H_q, halved for the causal step)",
-                     "avg_launch_ms": round(attn_ms, 4), "launches": clock.count("attn")},
+        "roofline": {"bound": "mfma", "kernel": "attn_fwd_16bit_sweep<bf16,128,4>",
+                     "achieved": round(sw_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(sw_tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": SWEEP_TRAFFIC_BYTES_RANK3 if rank == 3 else None,
+                     "algorithmic_per_launch": f"{flops / 1e12:.4f} TFLOP (the whole sweep: "
+                                               "4*Tq*Tk*D*H_q per step, halved for the causal step)",
+                     "avg_launch_ms": round(sw_ms, 4), "launches": clock.count("sweep_kernel")},
         "transpose_v": {"kernel": "transpose_v_kernel<u16,128>", "avg_launch_ms": round(tr_ms, 4),
                         "algorithmic_bytes_per_launch": round(tr_bytes),
                         "achieved_GBs": round(tr_bytes / (tr_ms * 1e-3) / 1e9, 1),
                         "frac": round(tr_bytes / (tr_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                         "launches": clock.count("transpose_v")},
-        "merge": {"kernel": "merge_inplace_kernel<bf16>", "avg_launch_ms": round(merge_ms, 4),
-                  "algorithmic_bytes_per_launch": round(mbytes),
-                  "achieved_GBs": round(merge_gbs, 1), "peak_GBs": PEAK_HBM_GBS,
-                  "frac": round(merge_gbs / PEAK_HBM_GBS, 4), "launches": clock.count("merge_inplace")},
+        "per_step_bf16": {
+            "workload": "same sweep as the reference runs it: one attention launch per step "
+                        "(V transposed first) and an in-place LSE merge after each",
+            "ms_per_step": round(secp * 1e3, 3), "TFLOP/s": round(flops / secp / 1e12, 2),
+            "attn": {"kernel": "attn_fwd_16bit_vt<bf16,128,4>", "avg_launch_ms": round(attn_ms, 4),
+                     "TFLOP/s": round(attn_tflops, 2), "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": ATTN_TRAFFIC_BYTES_RANK3 if rank == 3 else None,
+                     "launches": clockp.count("attn")},
+            "merge": {"kernel": "merge_inplace_kernel<bf16>", "avg_launch_ms": round(merge_ms, 4),
+                      "algorithmic_bytes_per_launch": round(mbytes),
+                      "achieved_GBs": round(merge_gbs, 1), "peak_GBs": PEAK_HBM_GBS,
+                      "frac": round(merge_gbs / PEAK_HBM_GBS, 4), "launches": clockp.count("merge_inplace")}},
     }
 
     # zig-zag gather of the full q (bf16, 1 GiB -> 128 MiB)
@@ -312,7 +328,7 @@ def main():
         # batched merge mode and one merge_states launch at S = 8
         cfgb = RingConfig(cp_size=CP, cp_rank=rank, merge_mode="batched")
         clockb = KernelClock()
-        secb = timed_sweeps(lambda: ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfgb, group=ring),
+        secb = timed_sweeps(lambda: ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfgb, group=ring, fused=False),
                             max(3, args.steps // 2), 2, clockb)
         ms_ms = clockb.mean_ms("merge_states")
         bb = merge_bytes_batched(t_local, CP, HQ, D, 2)

@@ -37,6 +37,7 @@
 // Softmax runs in the exp2 domain with scale * log2(e) (times the q/k descales) folded
 // into one FMA per score, and rescales the output only when the running max grows by
 // more than 2^8; the LSE written is natural-log, as fa4_ring/merge.py expects.
+#include <algorithm>
 #include <cfloat>
 #include <type_traits>
 
@@ -252,7 +253,8 @@ struct MfmaOps<_Float16> {
 // Decodes the workgroup id into (head group, sequence, row tile).  Row tiles are handed
 // out longest-first (the causal diagonal makes late row tiles the most expensive), and
 // head groups are laid out so that each XCD works on few kv heads (shared L2).
-__device__ __forceinline__ void decode_block(const AttnParams& p, int& hg, int& seq, int& rt) {
+template <typename Params>
+__device__ __forceinline__ void decode_block(const Params& p, int& hg, int& seq, int& rt) {
   const int b = xcd_remap((int)blockIdx.x, p.n_blocks);
   const int per_hg = p.nseq * p.n_rt;
   hg = b / per_hg;
@@ -974,6 +976,378 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_vt(AttnParams p)
   const float inv = ltot > 0.f ? 1.0f / ltot : 0.f;
   const int row = r0 + lq;
   if (row < Lq) {
+    T* og = reinterpret_cast<T*>(p.out) + (int64_t)(qs + row) * p.o_rs + (int64_t)head * p.o_hs;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        typedef T t4 __attribute__((ext_vector_type(4)));
+        t4 w = {(T)(o[dt][4 * g + 0] * inv), (T)(o[dt][4 * g + 1] * inv),
+                (T)(o[dt][4 * g + 2] * inv), (T)(o[dt][4 * g + 3] * inv)};
+        *reinterpret_cast<t4*>(og + 32 * dt + 8 * g + 4 * lh) = w;
+      }
+    if (lh == 0) {
+      const float lse = ltot > 0.f ? m * p.scale + logf(ltot) : -INFINITY;
+      p.lse[(int64_t)(qs + row) * p.lse_rs + head] = lse;
+    }
+  }
+}
+
+//--------------------------------------------------------------------------------------
+// Whole ring sweep, bf16 / fp16, head dim <= 128
+//
+// A workgroup takes one row tile of the local q through the key segments of all ring steps
+// (step 0: own keys, causal; step s <= rank: front half of source (rank - s) mod S; step
+// s > rank: all keys of that source, back-half rows only), one online softmax across them,
+// and writes the final out / lse.  The MFMA / VALU phases and the LDS layouts are those of
+// attn_fwd_16bit_vt; what differs is the walk over segments, kept to a few scalar
+// instructions per tile because one wavefront's issue rate bounds the VALU phase:
+//  * every wavefront loads one operand, group 0 the K tiles (three ahead of the MFMA
+//    phase, four LDS slots) and group 1 the V^T tiles (two ahead, three slots), through a
+//    cursor that bumps a pointer per tile and looks at the segment list only when a
+//    segment ends;
+//  * a cursor past the last tile still issues its loads, with an empty buffer range: they
+//    write zeros into a slot nobody reads, so every VALU phase issues the same number of
+//    loads and the wait before the next phase's reads is one constant;
+//  * the mask bound is computed only for the tiles that need it (causal diagonal, partial
+//    last tiles, rows a back-half step does not cover).
+//--------------------------------------------------------------------------------------
+struct SweepParams {
+  const void* q;
+  void* out;
+  float* lse;
+  int64_t q_rs, q_hs, o_rs, o_hs, lse_rs;
+  const void* k[FA4CP_MAX_CP];
+  const void* vt[FA4CP_MAX_CP];
+  int64_t k_rs, k_hs, vt_ds;
+  const int32_t* cu;
+  int nseq, total;
+  int h_kv, group;
+  int rank, S;
+  float scale;
+  int n_rt, n_hg, n_blocks;
+};
+
+// A ring step's keys as one row tile sees them.
+struct StepSeg {
+  int src;         // source rank
+  int keys;        // keys of the segment (per sequence)
+  int tiles;       // BN-key tiles this row tile visits
+  int kind;        // 0 causal, 1 front-half keys, 2 back-half rows
+  int first_mask;  // first tile that needs a mask (== tiles when none does)
+};
+__device__ __forceinline__ StepSeg step_seg(int s, int rank, int S, int L, int row_tile0, int rows,
+                                            int BN) {
+  StepSeg g;
+  g.src = rank - s < 0 ? rank - s + S : rank - s;
+  const int half = L >> 1;
+  if (s == 0) {
+    g.kind = 0;
+    g.keys = L;
+    const int last_row = min(row_tile0 + rows, L) - 1;
+    g.tiles = min((L + BN - 1) / BN, last_row / BN + 1);
+    // keys <= row_tile0 are visible to every row of the tile
+    g.first_mask = min(min(L / BN, (row_tile0 + 1) / BN), g.tiles);
+  } else if (s <= rank) {
+    g.kind = 1;
+    g.keys = half;
+    g.tiles = (half + BN - 1) / BN;
+    g.first_mask = half / BN;
+  } else {
+    g.kind = 2;
+    g.keys = L;
+    g.tiles = row_tile0 + rows > half ? (L + BN - 1) / BN : 0;
+    g.first_mask = row_tile0 < half ? 0 : L / BN;
+  }
+  return g;
+}
+// Load cursor: step s, tile t of it, and the byte address of that tile's data.
+struct LoadCursor {
+  int s, t, tiles, keys;
+  const char* ptr;
+};
+// Mask cursor: step s, tile t of it.
+struct MaskCursor {
+  int s, t;
+  StepSeg g;
+};
+
+template <typename T, int D, int HP>
+__global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_sweep(SweepParams p) {
+  using Ops = MfmaOps<T>;
+  using frag = typename Ops::frag;
+  constexpr int BN = kBN;
+  constexpr int RB = kPPWaves / HP;
+  constexpr int CH = D / 8;
+  constexpr int NLD = BN * CH / 64;  // wave-wide LDS-DMA loads per K (or V^T) tile
+  constexpr int NMT = BN / 32;
+  constexpr int NDT = D / 32;
+  constexpr int NKS = D / 16;
+  constexpr int NPS = BN / 16;
+  constexpr int KS = 4, VS = 3;      // LDS slots of K and V^T tiles
+  constexpr int TILE = BN * D;       // elements of one K or V^T tile
+  static_assert(D <= 128, "ping-pong kernel holds one 32 x D output tile per wavefront");
+  static_assert(BN * (int)sizeof(T) == 128, "V^T rows are 8 chunks");
+  static_assert(NLD % 4 == 0 && NLD % kPPWaves == 0, "tile loads must split over the wavefronts");
+  // s_waitcnt: LDS reads done; this wavefront's loads of its latest VALU phase may remain
+  constexpr int kWaitOlder = (NLD / 4) | (7 << 4);
+  static_assert(NLD / 4 < 16, "vmcnt field");
+
+  __shared__ __attribute__((aligned(1024))) T kl[KS][TILE];
+  __shared__ __attribute__((aligned(1024))) T vtl[VS][TILE];
+
+  int hg, seq, rt;
+  decode_block(p, hg, seq, rt);
+  int qs, L;
+  seq_range(p.cu, seq, p.total, FA4CP_SEL_ALL, qs, L);
+  const int row_tile0 = rt * RB * 32;
+  if (row_tile0 >= L) return;
+  constexpr int rows = RB * 32;
+  const int half = L >> 1;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2;
+  const int wi = wave & 3;
+  const int lane = tid & 63;
+  const int lq = lane & 31;
+  const int lh = lane >> 5;
+  const int groups_per_kv = p.group / HP;
+  const int kvh = hg / groups_per_kv;
+  const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
+  const int r0 = row_tile0 + (wave / HP) * 32;
+
+  auto seg = [&](int s) __attribute__((always_inline)) {
+    return step_seg(s, p.rank, p.S, L, row_tile0, rows, BN);
+  };
+  int n_tiles = 0;
+  for (int s = 0; s < p.S; ++s) n_tiles += seg(s).tiles;
+
+  const T* __restrict__ qg = reinterpret_cast<const T*>(p.q);
+  frag qf[NKS];
+  {
+    const int64_t rsb = p.q_rs * (int64_t)sizeof(T);
+    const auto rq = make_rsrc(qg + (int64_t)(qs + r0) * p.q_rs + (int64_t)head * p.q_hs,
+                              (int64_t)min(L - r0, 32) * rsb);
+#pragma unroll
+    for (int t = 0; t < NKS; ++t)
+      qf[t] = __builtin_bit_cast(frag, bload128(rq, lq * (int)rsb + (int)sizeof(T) * (16 * t + 8 * lh)));
+  }
+
+  // ---- load cursors
+  const int k_rsb = (int)(p.k_rs * (int64_t)sizeof(T));
+  const int vt_rsb = (int)(p.vt_ds * (int64_t)sizeof(T));
+  const int64_t vt_pos = p.cu ? vt_seq_start(p.cu, seq, FA4CP_SEL_ALL) : 0;
+  const int64_t k_off = ((int64_t)qs * p.k_rs + (int64_t)kvh * p.k_hs) * (int64_t)sizeof(T);
+  const int64_t v_off = ((int64_t)kvh * D * p.vt_ds + vt_pos) * (int64_t)sizeof(T);
+  // a V^T tile spans rows d = 0..D-1 of BN keys; the 128-key padding of every sequence
+  // keeps it inside the source's V^T
+  const int vt_tile_bytes = (D - 1) * vt_rsb + BN * (int)sizeof(T);
+  auto seg_base = [&](int src, bool isk) __attribute__((always_inline)) {
+    return isk ? reinterpret_cast<const char*>(p.k[src]) + k_off
+               : reinterpret_cast<const char*>(p.vt[src]) + v_off;
+  };
+  auto fix = [&](LoadCursor& c, bool isk) __attribute__((always_inline)) {
+    while (c.t >= c.tiles && c.s < p.S) {
+      ++c.s;
+      c.t = 0;
+      if (c.s < p.S) {
+        const StepSeg g = seg(c.s);
+        c.tiles = g.tiles;
+        c.keys = g.keys;
+        c.ptr = seg_base(g.src, isk);
+      }
+    }
+  };
+  auto start = [&](bool isk) __attribute__((always_inline)) {
+    const StepSeg g = seg(0);
+    LoadCursor c{0, 0, g.tiles, g.keys, seg_base(g.src, isk)};
+    fix(c, isk);
+    return c;
+  };
+  auto step = [&](LoadCursor& c, bool isk) __attribute__((always_inline)) {
+    ++c.t;
+    c.ptr += isk ? BN * k_rsb : BN * (int)sizeof(T);
+    if (__builtin_expect(c.t >= c.tiles, 0)) fix(c, isk);
+  };
+  auto rsrc = [&](const LoadCursor& c, bool isk) __attribute__((always_inline)) {
+    const int n = c.s >= p.S ? 0 : isk ? min(c.keys - c.t * BN, BN) * k_rsb : vt_tile_bytes;
+    return make_rsrc32(c.ptr, n);
+  };
+  // LDS-DMA lane offsets of a tile split over `nw` wavefronts (load n of wavefront w fills
+  // LDS chunks [64 (w + nw n), +64) of the tile)
+  auto k_voff = [&](int w, int nw, int n) __attribute__((always_inline)) {
+    const int P = 64 * (w + nw * n) + lane;
+    const int row = P / CH, c = (P % CH) ^ ksw16<CH>(row);
+    return row * k_rsb + 16 * c;
+  };
+  auto v_voff = [&](int w, int nw, int n) __attribute__((always_inline)) {
+    const int P = 64 * (w + nw * n) + lane;
+    const int d = P >> 3, c = (P & 7) ^ ((d >> 1) & 7);
+    return d * vt_rsb + 16 * c;
+  };
+
+  // prologue: K_0 .. K_{KS-2} and V^T_0 .. V^T_{VS-2}, loaded by all eight wavefronts
+  LoadCursor kc = start(true), vc = start(false);
+#pragma unroll
+  for (int i = 0; i < KS - 1; ++i) {
+    const auto r = rsrc(kc, true);
+#pragma unroll
+    for (int n = 0; n < NLD / kPPWaves; ++n) dma16(r, kl[i] + 512 * (wave + kPPWaves * n), k_voff(wave, kPPWaves, n));
+    step(kc, true);
+  }
+#pragma unroll
+  for (int i = 0; i < VS - 1; ++i) {
+    const auto r = rsrc(vc, false);
+#pragma unroll
+    for (int n = 0; n < NLD / kPPWaves; ++n) dma16(r, vtl[i] + 512 * (wave + kPPWaves * n), v_voff(wave, kPPWaves, n));
+    step(vc, false);
+  }
+  // from here on group 0 loads K and group 1 V^T, four wavefronts per tile
+  const bool isk = grp == 0;
+  LoadCursor lc = isk ? kc : vc;
+  int ld_voff[NLD / 4];
+#pragma unroll
+  for (int n = 0; n < NLD / 4; ++n) ld_voff[n] = isk ? k_voff(wi, 4, n) : v_voff(wi, 4, n);
+  T* const ld_base = isk ? kl[0] : vtl[0];
+  const int ld_slots = isk ? KS : VS;
+  int ld_slot = ld_slots - 1;
+
+  const int kr = swap_bits23(lq);
+  int k_off_l[NKS];
+#pragma unroll
+  for (int t = 0; t < NKS; ++t) k_off_l[t] = kr * D + 8 * ((2 * t + lh) ^ ksw16<CH>(kr));
+  int v_off_l[NPS];
+#pragma unroll
+  for (int t = 0; t < NPS; ++t) v_off_l[t] = lq * BN + 8 * ((2 * t + lh) ^ ((lq >> 1) & 7));
+
+  const float c_log2 = p.scale * kLog2e;
+  f32x16 o[NDT];
+#pragma unroll
+  for (int i = 0; i < NDT; ++i) o[i] = f32x16{};
+  float m = -INFINITY;
+  float lsum = 0.f;
+  f32x16 s[NMT];
+  frag pf[NPS];
+
+  auto qk = [&](const T* ksrc) __attribute__((always_inline)) {
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt) {
+      s[mt] = f32x16{};
+#pragma unroll
+      for (int t = 0; t < NKS; ++t) {
+        const frag a = *reinterpret_cast<const frag*>(ksrc + k_off_l[t] + 32 * mt * D);
+        s[mt] = Ops::mma(a, qf[t], s[mt]);
+      }
+    }
+  };
+  auto pv = [&](const T* vsrc) __attribute__((always_inline)) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int t = 0; t < NPS; ++t) {
+        const frag a = *reinterpret_cast<const frag*>(vsrc + 32 * dt * BN + v_off_l[t]);
+        o[dt] = Ops::mma(a, pf[t], o[dt]);
+      }
+  };
+  // mask cursor (the tile in the MFMA phase)
+  MaskCursor mc{0, 0, seg(0)};
+  auto mfix = [&]() __attribute__((always_inline)) {
+    while (mc.t >= mc.g.tiles && mc.s < p.S) {
+      ++mc.s;
+      mc.t = 0;
+      if (mc.s < p.S) mc.g = seg(mc.s);
+    }
+  };
+  mfix();
+  const int qq = r0 + lq;
+  // keys past the segment, keys after the query (step 0), every key for the rows a
+  // back-half step does not cover
+  auto mask = [&]() __attribute__((always_inline)) {
+    const int kb0 = mc.t * BN;
+    const int lim_all = mc.g.keys - kb0;
+    const int lim0 = min(lim_all, qq + 1 - kb0);
+    const int lim2 = qq < half ? 0 : lim_all;
+    const int lim = mc.g.kind == 0 ? lim0 : mc.g.kind == 2 ? lim2 : lim_all;
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kk = 32 * mt + 16 * (i >> 3) + 8 * lh + (i & 7);
+        s[mt][i] = kk >= lim ? -INFINITY : s[mt][i];
+      }
+  };
+
+  std::integral_constant<int, 4> four;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (grp == 1) __syncthreads();  // group 1 runs one phase behind group 0
+
+  int vr = VS - 1;  // V^T slot of the tile before the one in the MFMA phase
+  // One tile: MFMA phase (S_j, and O += P_{j-1} V_{j-1} after the first tile), then the
+  // VALU phase.  Tile 0 is peeled so that every later MFMA phase is straight-line code in
+  // which the P V reads interleave with the Q K^T MFMAs.
+  auto tile = [&](int j, auto with_pv) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_setprio(1);
+    qk(kl[j & (KS - 1)]);
+    if constexpr (decltype(with_pv)::value) {
+      pv(vtl[vr]);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kPPReadAhead, 0);
+#pragma unroll
+      for (int i = 0; i < NMT * NKS + NDT * NPS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+    }
+    // cursor walk while the MFMAs drain
+    if constexpr (decltype(with_pv)::value) {
+      step(lc, isk);
+      ++mc.t;
+      if (__builtin_expect(mc.t >= mc.g.tiles, 0)) mfix();
+    }
+    const auto r = rsrc(lc, isk);
+    const bool masked = mc.t >= mc.g.first_mask;
+    __builtin_amdgcn_s_setprio(0);
+    // K_{j+1} / V^T_j, loaded two VALU phases ago, are read in the next phase
+    __builtin_amdgcn_s_waitcnt(kWaitOlder);
+    wg_barrier();
+    T* const dst = ld_base + ld_slot * TILE;
+#pragma unroll
+    for (int n = 0; n < NLD / 4; ++n) dma16(r, dst + 512 * (wi + 4 * n), ld_voff[n]);
+    ld_slot = ld_slot + 1 == ld_slots ? 0 : ld_slot + 1;
+    if (__builtin_expect(masked, 0)) mask();
+    tile_max_rescale<NMT, NDT>(s, o, m, lsum, c_log2);
+    tile_exp<NMT>(s, m, lsum, c_log2);
+#pragma unroll
+    for (int t = 0; t < NPS; ++t)
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) pf[t][jj] = (T)s[t >> 1][8 * (t & 1) + jj];
+    vr = vr + 1 == VS ? 0 : vr + 1;
+    // the softmax state is complete when the other group's MFMA phase ends
+#pragma unroll
+    for (int t = 0; t < NPS; ++t) pin(pf[t]);
+#pragma unroll
+    for (int i = 0; i < NDT; ++i) pin(o[i]);
+    pin(m);
+    pin(lsum);
+    wg_barrier();  // the VALU phase reads no LDS; its loads are waited for a phase later
+  };
+  if (n_tiles > 0) tile(0, std::false_type{});
+  for (int j = 1; j < n_tiles; ++j) tile(j, std::true_type{});
+  if (n_tiles > 0) {
+    __builtin_amdgcn_s_setprio(1);
+    pv(vtl[vr]);
+    __builtin_amdgcn_s_setprio(0);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (grp == 0) __syncthreads();  // both groups pass the same number of barriers
+  (void)four;
+
+  const float ltot = pair_sum(lsum);
+  const float inv = ltot > 0.f ? 1.0f / ltot : 0.f;
+  const int row = r0 + lq;
+  if (row < L) {
     T* og = reinterpret_cast<T*>(p.out) + (int64_t)(qs + row) * p.o_rs + (int64_t)head * p.o_hs;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
@@ -1974,6 +2348,13 @@ KernelChoice pick8(int d, int hp, bool vt) {
 
 using namespace fa4cp;
 
+// The kernels address within a tile by 32-bit byte offsets: up to 256 rows of a row-major
+// operand, and rows 0..d-1 of V^T.
+static bool tile_offsets_fit(int64_t row_stride, int esz, int d, int64_t vt_d_stride) {
+  constexpr int64_t kMax = 0x7fffffffLL;
+  return 256 * row_stride * esz < kMax && (int64_t)d * vt_d_stride * esz + 256 < kMax;
+}
+
 extern "C" int fa4cp_attn_fwd(const fa4cp_attn_args* a, void* stream) {
   clear_error();
   if (a == nullptr) return set_error(FA4CP_EINVAL, "attn_fwd: null args");
@@ -2033,6 +2414,9 @@ extern "C" int fa4cp_attn_fwd(const fa4cp_attn_args* a, void* stream) {
         !ok(a->out, a->o_row_stride, a->o_head_stride, 4, 2) || a->lse_row_stride < a->h_q)
       return set_error(FA4CP_EINVAL, "attn_fwd: misaligned pointer or stride (q/k rows and heads "
                        "need 16-byte alignment, v 8-byte for e4m3, out 8-byte; lse_row_stride >= h_q)");
+    const int64_t rs = std::max(a->q_row_stride, std::max(a->k_row_stride, a->v_row_stride));
+    if (!tile_offsets_fit(rs, esz, use_vt ? d : 0, a->vt_d_stride))
+      return set_error(FA4CP_EINVAL, "attn_fwd: row or V^T stride too large for 32-bit tile offsets");
   }
   AttnParams p;
   p.q = a->q; p.k = a->k; p.v = a->v; p.out = a->out; p.lse = a->lse;
@@ -2056,4 +2440,78 @@ extern "C" int fa4cp_attn_fwd(const fa4cp_attn_args* a, void* stream) {
   p.n_blocks = (int)blocks;
   hipLaunchKernelGGL(kc.fn, dim3((unsigned)blocks), dim3(kc.threads), 0, (hipStream_t)stream, p);
   return check_launch("attn_fwd");
+}
+
+extern "C" int fa4cp_ring_sweep_fwd(const fa4cp_sweep_args* a, void* stream) {
+  clear_error();
+  if (a == nullptr || !a->q || !a->out || !a->lse)
+    return set_error(FA4CP_EINVAL, "ring_sweep_fwd: null pointer");
+  if (a->cp_size < 1 || a->cp_size > FA4CP_MAX_CP || a->cp_rank < 0 || a->cp_rank >= a->cp_size)
+    return set_error(FA4CP_EINVAL, "ring_sweep_fwd: cp_rank %d / cp_size %d out of range (cp_size <= %d)",
+                     a->cp_rank, a->cp_size, FA4CP_MAX_CP);
+  for (int i = 0; i < a->cp_size; ++i)
+    if (!a->k[i] || !a->v_t[i]) return set_error(FA4CP_EINVAL, "ring_sweep_fwd: null K / V^T of source %d", i);
+  if (a->h_q <= 0 || a->h_kv <= 0 || a->h_q % a->h_kv != 0)
+    return set_error(FA4CP_EINVAL, "ring_sweep_fwd: h_q=%d must be a positive multiple of h_kv=%d", a->h_q, a->h_kv);
+  const int nseq = a->cu ? a->nseq : 1;
+  if (nseq < 1 || a->total < 0) return set_error(FA4CP_EINVAL, "ring_sweep_fwd: bad nseq / total");
+  if (a->vt_d_stride < fa4cp_vt_min_d_stride(a->total, nseq) || a->vt_d_stride % kVtPad != 0)
+    return set_error(FA4CP_EINVAL, "ring_sweep_fwd: vt_d_stride must be a multiple of %d and >= %lld", kVtPad,
+                     (long long)fa4cp_vt_min_d_stride(a->total, nseq));
+  const int max_len = a->cu ? a->max_seqlen : a->total;
+  const int group = a->h_q / a->h_kv;
+  const int hp = heads_per_wg(group);
+  const int d = a->d;
+  if (a->dtype != FA4CP_BF16 && a->dtype != FA4CP_FP16)
+    return set_error(FA4CP_EUNSUPPORTED, "ring_sweep_fwd: dtype %d (BF16 / FP16 only)", a->dtype);
+  if (d != 64 && d != 128) return set_error(FA4CP_EUNSUPPORTED, "ring_sweep_fwd: head dim %d (64 / 128 only)", d);
+  {
+    auto ok = [](const void* ptr, int64_t rs, int64_t hs, int64_t al) {
+      return rs > 0 && hs > 0 && rs % al == 0 && hs % al == 0 && ((uintptr_t)ptr % (uintptr_t)(al * 2)) == 0;
+    };
+    bool good = ok(a->q, a->q_row_stride, a->q_head_stride, 8) &&
+                ok(a->out, a->o_row_stride, a->o_head_stride, 4) && a->lse_row_stride >= a->h_q;
+    for (int i = 0; i < a->cp_size; ++i)
+      good = good && ok(a->k[i], a->k_row_stride, a->k_head_stride, 8) && ((uintptr_t)a->v_t[i] % 16) == 0;
+    if (!good) return set_error(FA4CP_EINVAL, "ring_sweep_fwd: misaligned pointer or stride");
+    if (!tile_offsets_fit(std::max(a->q_row_stride, a->k_row_stride), 2, d, a->vt_d_stride))
+      return set_error(FA4CP_EINVAL, "ring_sweep_fwd: row or V^T stride too large for 32-bit tile offsets");
+  }
+  SweepParams p;
+  p.q = a->q; p.out = a->out; p.lse = a->lse;
+  p.q_rs = a->q_row_stride; p.q_hs = a->q_head_stride;
+  p.o_rs = a->o_row_stride; p.o_hs = a->o_head_stride; p.lse_rs = a->lse_row_stride;
+  for (int i = 0; i < FA4CP_MAX_CP; ++i) {
+    p.k[i] = i < a->cp_size ? a->k[i] : nullptr;
+    p.vt[i] = i < a->cp_size ? a->v_t[i] : nullptr;
+  }
+  p.k_rs = a->k_row_stride; p.k_hs = a->k_head_stride; p.vt_ds = a->vt_d_stride;
+  p.cu = a->cu; p.nseq = nseq; p.total = a->total;
+  p.h_kv = a->h_kv; p.group = group;
+  p.rank = a->cp_rank; p.S = a->cp_size;
+  p.scale = a->softmax_scale;
+  const int rows = 32 * kPPWaves / hp;
+  p.n_rt = (max_len + rows - 1) / rows;
+  p.n_hg = a->h_kv * (group / hp);
+  const int64_t blocks = (int64_t)p.n_hg * nseq * p.n_rt;
+  if (blocks == 0) return FA4CP_OK;
+  if (blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "ring_sweep_fwd: grid too large");
+  p.n_blocks = (int)blocks;
+  void (*fn)(SweepParams) = nullptr;
+#define FA4CP_PICK(TT, DD)                                          \
+  if (d == DD) {                                                    \
+    if (hp == 4) fn = attn_fwd_16bit_sweep<TT, DD, 4>;              \
+    else if (hp == 2) fn = attn_fwd_16bit_sweep<TT, DD, 2>;         \
+    else fn = attn_fwd_16bit_sweep<TT, DD, 1>;                      \
+  }
+  if (a->dtype == FA4CP_BF16) {
+    FA4CP_PICK(__bf16, 64)
+    FA4CP_PICK(__bf16, 128)
+  } else {
+    FA4CP_PICK(_Float16, 64)
+    FA4CP_PICK(_Float16, 128)
+  }
+#undef FA4CP_PICK
+  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kPPThreads), 0, (hipStream_t)stream, p);
+  return check_launch("ring_sweep_fwd");
 }

@@ -88,6 +88,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
   const int n = bytes <= 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : (int)bytes);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
 }
+// The same for a size already known to lie in [0, 2^31).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc32(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
 __device__ __forceinline__ u32x4 bload128(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
@@ -108,6 +112,33 @@ __device__ __forceinline__ void bload8_f32(__amdgpu_buffer_rsrc_t r, int off, fl
     const t8 a = __builtin_bit_cast(t8, bload128(r, off));
 #pragma unroll
     for (int i = 0; i < 8; ++i) out[i] = (float)a[i];
+  }
+}
+
+// Workgroup barrier with no memory fence.  __syncthreads() also fences, which makes the
+// compiler wait for every outstanding load of the wavefront, LDS-DMA included, before the
+// barrier; the pipelined kernels instead wait (s_waitcnt) for exactly the loads the next
+// phase reads.  The "memory" clobber keeps the compiler from moving memory accesses across,
+// the scheduling barriers keep it from moving arithmetic across (which would shift one
+// phase's work into the next).
+__device__ __forceinline__ void wg_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Makes `x` be computed before the next volatile asm statement (such as wg_barrier): the
+// empty asm reads and rewrites it, and volatile asm statements keep their program order.
+template <typename V>
+__device__ __forceinline__ void pin(V& x) {
+  static_assert(sizeof(V) % 4 == 0, "pin: 32-bit lanes");
+  if constexpr (sizeof(V) == 4) {
+    asm volatile("" : "+v"(x));
+  } else {
+    typedef uint32_t W __attribute__((ext_vector_type(sizeof(V) / 4)));
+    W w = __builtin_bit_cast(W, x);
+    asm volatile("" : "+v"(w));
+    x = __builtin_bit_cast(V, w);
   }
 }
 

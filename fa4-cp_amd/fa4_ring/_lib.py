@@ -92,6 +92,40 @@ class TransposeArgs(ctypes.Structure):
     ]
 
 
+MAX_CP = 16  # FA4CP_MAX_CP
+
+
+class SweepArgs(ctypes.Structure):
+    """Mirror of fa4cp_sweep_args."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("q_row_stride", ctypes.c_int64),
+        ("q_head_stride", ctypes.c_int64),
+        ("o_row_stride", ctypes.c_int64),
+        ("o_head_stride", ctypes.c_int64),
+        ("lse_row_stride", ctypes.c_int64),
+        ("k", ctypes.c_void_p * MAX_CP),
+        ("v_t", ctypes.c_void_p * MAX_CP),
+        ("k_row_stride", ctypes.c_int64),
+        ("k_head_stride", ctypes.c_int64),
+        ("vt_d_stride", ctypes.c_int64),
+        ("cu", ctypes.c_void_p),
+        ("nseq", ctypes.c_int32),
+        ("max_seqlen", ctypes.c_int32),
+        ("total", ctypes.c_int32),
+        ("h_q", ctypes.c_int32),
+        ("h_kv", ctypes.c_int32),
+        ("d", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("cp_rank", ctypes.c_int32),
+        ("cp_size", ctypes.c_int32),
+        ("softmax_scale", ctypes.c_float),
+    ]
+
+
 # exported symbol -> (restype, argtypes)
 SIGNATURES = {
     "fa4cp_attn_fwd": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
@@ -118,6 +152,7 @@ SIGNATURES = {
     ),
     "fa4cp_transpose_v": (ctypes.c_int, [ctypes.POINTER(TransposeArgs), ctypes.c_void_p]),
     "fa4cp_vt_min_d_stride": (ctypes.c_int64, [ctypes.c_int32, ctypes.c_int32]),
+    "fa4cp_ring_sweep_fwd": (ctypes.c_int, [ctypes.POINTER(SweepArgs), ctypes.c_void_p]),
     "fa4cp_last_error": (ctypes.c_char_p, []),
     "fa4cp_abi_version": (ctypes.c_int, []),
 }

@@ -25,11 +25,14 @@ and every launch goes to torch's current stream.
 
 from __future__ import annotations
 
+import ctypes
+import math
 from dataclasses import dataclass
 from typing import List, Optional, Sequence, Tuple
 
 import torch
 
+from . import _lib
 from .config import RingConfig
 from .fa4_backend import (SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, fa4_attn, out_dtype_for, transpose_v,
                           uses_vt)
@@ -88,8 +91,15 @@ def ring_flash_attn(
     descales: Optional[Descales] = None,
     cu_seqlens: Optional[torch.Tensor] = None,  # local int32 [num_seq+1]; None -> one sequence
     max_seqlen: Optional[int] = None,
+    fused: Optional[bool] = None,
 ) -> torch.Tensor:
     """This rank's local causal ring-attention output ``[T, H, D]``.
+
+    ``fused`` (default: whenever supported) runs the whole sweep as one kernel over every
+    source's K / V^T (``ring_sweep``): no per-step partials, no merges.  It needs
+    cp_size > 1 with a LocalKVRing, bf16 / fp16, head dim 64 or 128 and no descales;
+    ``fused=False`` runs the per-step path of the reference (attention + LSE merge per
+    step), which covers every case.
 
     One sequence per rank: leave ``cu_seqlens=None``.  Packed sequences: pass the LOCAL
     ``cu_seqlens`` (each entry a zig-zag ``2*h_j`` shard length) on the device and
@@ -109,6 +119,16 @@ def ring_flash_attn(
                 "ring_flash_attn: cp_size > 1 needs group=LocalKVRing(k_shards, v_shards); "
                 "KV rotation between GPUs is not part of this single-GPU build")
         assert group.cp_size == S, f"LocalKVRing holds {group.cp_size} shards, cp_size is {S}"
+
+    can_fuse = (S > 1 and descales is None and local_q.dtype in (torch.bfloat16, torch.float16)
+                and local_q.shape[2] in (64, 128) and S <= _lib.MAX_CP)
+    if fused and not can_fuse:
+        raise AssertionError("fused ring sweep needs cp_size in [2, 16], bf16/fp16, head dim 64/128, "
+                             "no descales")
+    if fused is None:
+        fused = can_fuse
+    if fused:
+        return ring_sweep(local_q, local_k, local_v, cfg, group, cu_seqlens, max_seqlen)
 
     qd = descales.q if descales else None
 
@@ -168,3 +188,59 @@ def ring_flash_attn(
             merge_state_in_place(acc, acc_lse, part, part_lse, cu_seqlens=cu_seqlens,
                                  row_sel=SEL_BACK_HALF)
     return acc
+
+
+def ring_sweep(local_q: torch.Tensor, local_k: torch.Tensor, local_v: torch.Tensor, cfg: RingConfig,
+               group: "LocalKVRing", cu_seqlens: Optional[torch.Tensor] = None,
+               max_seqlen: Optional[int] = None, out: Optional[torch.Tensor] = None,
+               lse: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The whole sweep of ring_flash_attn (fa4_ring/ring_attention.py:61-174) in one
+    fa4cp_ring_sweep_fwd launch: every source's V is transposed (fa4cp_transpose_v), then one
+    kernel carries each row tile's online softmax through the causal local keys, the front
+    halves of the earlier sources and, for the back-half rows, all keys of the later ones.
+    Returns out [T, H, D] (``lse`` [T, H], if given, receives the natural-log LSE)."""
+    lib = _lib.load()
+    S, rank = cfg.cp_size, cfg.cp_rank
+    total, h_q, d = local_q.shape
+    dev = local_q.device
+    assert local_q.is_cuda and local_q.stride(2) == 1, "local_q must be a device tensor, contiguous in D"
+    nseq = 1 if cu_seqlens is None else cu_seqlens.shape[0] - 1
+    ks = [local_k if i == rank else group.k[i] for i in range(S)]
+    vs = [local_v if i == rank else group.v[i] for i in range(S)]
+    h_kv = ks[0].shape[1]
+    for k, v in zip(ks, vs):
+        assert k.shape == (total, h_kv, d) and v.shape == k.shape and k.dtype == local_q.dtype
+        assert k.stride() == ks[0].stride(), "all K shards must share strides"
+    vts = [transpose_v(v, cu_seqlens_k=cu_seqlens, max_seqlen_k=max_seqlen)[0] for v in vs]
+    stride = int(lib.fa4cp_vt_min_d_stride(total, nseq))
+    if out is None:
+        out = torch.empty_like(local_q)
+    if lse is None:
+        lse = torch.empty((total, h_q), dtype=torch.float32, device=dev)
+    a = _lib.SweepArgs()
+    a.q, a.out, a.lse = local_q.data_ptr(), out.data_ptr(), lse.data_ptr()
+    a.q_row_stride, a.q_head_stride = local_q.stride(0), local_q.stride(1)
+    a.o_row_stride, a.o_head_stride = out.stride(0), out.stride(1)
+    a.lse_row_stride = lse.stride(0)
+    for i in range(S):
+        a.k[i] = ks[i].data_ptr()
+        a.v_t[i] = vts[i].data_ptr()
+    a.k_row_stride, a.k_head_stride = ks[0].stride(0), ks[0].stride(1)
+    a.vt_d_stride = stride
+    a.cu = _lib.ptr(cu_seqlens)
+    a.nseq = nseq
+    a.max_seqlen = int(max_seqlen) if cu_seqlens is not None else total
+    a.total = total
+    a.h_q, a.h_kv, a.d = h_q, h_kv, d
+    a.dtype = _lib.dtype_code(local_q.dtype)
+    a.cp_rank, a.cp_size = rank, S
+    a.softmax_scale = float(cfg.softmax_scale if cfg.softmax_scale is not None else 1.0 / math.sqrt(d))
+    launch_sweep(a, dev)
+    return out
+
+
+def launch_sweep(args: "_lib.SweepArgs", device: torch.device) -> None:
+    """Queues the fused sweep kernel on the current stream of `device`."""
+    lib = _lib.load()
+    _lib.check(lib.fa4cp_ring_sweep_fwd(ctypes.byref(args), _lib.stream_handle(device)),
+               "fa4cp_ring_sweep_fwd")

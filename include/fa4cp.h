@@ -20,6 +20,8 @@
  *   fa4cp_zigzag_unshard        <- fa4_ring/zigzag.py:42-50 (zigzag_unshard)
  *   fa4cp_transpose_v           <- no counterpart: the V^T layout the fast attention kernels
  *                                  load (FA4 reads V as given; see fa4cp_attn_args.v_t)
+ *   fa4cp_ring_sweep_fwd        <- fa4_ring/ring_attention.py:61-174 (ring_flash_attn's step loop
+ *                                  and its merges, fused; every source's K/V on this GPU)
  */
 #ifndef FA4CP_H_
 #define FA4CP_H_
@@ -130,6 +132,37 @@ typedef struct fa4cp_transpose_args {
 
 int fa4cp_transpose_v(const fa4cp_transpose_args* args, void* stream);
 int64_t fa4cp_vt_min_d_stride(int32_t total_k, int32_t nseq);
+
+/*
+ * One rank's whole causal zig-zag ring sweep in a single launch (fa4_ring/ring_attention.py:61-174
+ * with every source rank's K/V already on this GPU): out / lse are the attention of the
+ * local q over the union of
+ *   step 0:          the rank's own keys, causal (bottom-right aligned per sequence);
+ *   step s <= rank:  the front half of source (rank - s) mod cp_size's keys, every local row;
+ *   step s >  rank:  all of that source's keys, the back half of the local rows only,
+ * which is what the per-step attention calls and their LSE merges produce.  There are no
+ * partial results and no merges: every workgroup carries its online softmax across the
+ * sources.  k[i] is source rank i's local K shard and v_t[i] its V^T (fa4cp_transpose_v with
+ * k_sel = ALL over the same cu); all shards share strides and the local sequence layout cu.
+ * BF16 / FP16, d = 64 or 128, cp_size <= FA4CP_MAX_CP.
+ */
+#define FA4CP_MAX_CP 16
+typedef struct fa4cp_sweep_args {
+  const void* q; /* [total rows] x h_q heads x d */
+  void* out;     /* [total rows] x h_q heads x d */
+  float* lse;    /* lse[row * lse_row_stride + head], natural log */
+  int64_t q_row_stride, q_head_stride, o_row_stride, o_head_stride, lse_row_stride;
+  const void* k[FA4CP_MAX_CP];   /* per source rank: [total rows] x h_kv heads x d */
+  const void* v_t[FA4CP_MAX_CP]; /* per source rank: V^T of all its keys */
+  int64_t k_row_stride, k_head_stride, vt_d_stride;
+  const int32_t* cu; /* local cu_seqlens [nseq + 1] or NULL (one sequence of `total` rows) */
+  int32_t nseq, max_seqlen, total;
+  int32_t h_q, h_kv, d, dtype;
+  int32_t cp_rank, cp_size;
+  float softmax_scale;
+} fa4cp_sweep_args;
+
+int fa4cp_ring_sweep_fwd(const fa4cp_sweep_args* args, void* stream);
 
 /*
  * In-place online-softmax merge (flashinfer.cascade.merge_state_in_place semantics, natural

@@ -31,10 +31,19 @@ def _device_ring(q, k, v, cp, dtype):
     return qd, LocalKVRing.from_full(kd, vd, cp)
 
 
-@pytest.mark.parametrize("mode", ["incremental", "batched"])
+PATHS = ["fused", "incremental", "batched"]  # one-kernel sweep; per-step paths with merges
+
+
+def _cfg_path(path, cp, rank):
+    """RingConfig and ring_flash_attn `fused` flag of a test path."""
+    mode = "incremental" if path == "fused" else path
+    return RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode), path == "fused"
+
+
+@pytest.mark.parametrize("mode", PATHS)
 @pytest.mark.parametrize("n,h,hkv,d,cp", SMALL_CASES)
 def test_ring_all_ranks_small(n, h, hkv, d, cp, mode):
-    say(f"ring bf16 n={n} h={h}/{hkv} d={d} cp={cp} mode={mode}")
+    say(f"ring bf16 n={n} h={h}/{hkv} d={d} cp={cp} path={mode}")
     q, k, v = O.random_qkv(n, h, hkv, d, seed=0)
     q, k, v = (rounded(t, torch.bfloat16) for t in (q, k, v))
     scale = scale_for(d)
@@ -43,10 +52,11 @@ def test_ring_all_ranks_small(n, h, hkv, d, cp, mode):
     vs = [O.zigzag_shard(v, r, cp) for r in range(cp)]
     outs = []
     for rank in range(cp):
-        cfg = RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode)
-        out = ring_flash_attn(zigzag_shard(qd, rank, cp), ring.k[rank], ring.v[rank], cfg, group=ring)
+        cfg, fused = _cfg_path(mode, cp, rank)
+        out = ring_flash_attn(zigzag_shard(qd, rank, cp), ring.k[rank], ring.v[rank], cfg, group=ring,
+                              fused=fused)
         assert out.dtype == torch.bfloat16 and out.shape == (n // cp, h, d)
-        ref, _ = O.ring_rank(O.zigzag_shard(q, rank, cp), ks, vs, rank, cp, scale, merge_mode=mode)
+        ref, _ = O.ring_rank(O.zigzag_shard(q, rank, cp), ks, vs, rank, cp, scale, merge_mode=cfg.merge_mode)
         assert max_err(out, ref) <= TOL_BF16_OUT, f"rank {rank}"
         outs.append(out.float().cpu())
     dense = O.dense_causal(q, k, v, scale)
@@ -62,11 +72,11 @@ def test_ring_cp1_is_causal_attention():
     assert max_err(out, O.dense_causal(q, k, v, scale_for(128))) <= TOL_BF16_OUT
 
 
-@pytest.mark.parametrize("mode", ["incremental", "batched"])
+@pytest.mark.parametrize("mode", PATHS)
 def test_ring_varlen_all_ranks(mode):
     lens = [608, 1216, 1072, 608, 232, 1928, 344, 200]  # the packed benchmark lengths / 8
     cp, h, hkv, d = 4, 8, 2, 128
-    say(f"ring varlen lens={lens} cp={cp} mode={mode}")
+    say(f"ring varlen lens={lens} cp={cp} path={mode}")
     full_cu = [0]
     for n in lens:
         full_cu.append(full_cu[-1] + n)
@@ -81,11 +91,11 @@ def test_ring_varlen_all_ranks(mode):
     for rank in range(cp):
         lq, local_cu = zigzag_shard_varlen(qd, full_cu, rank, cp)
         max_local = int((local_cu[1:] - local_cu[:-1]).max())
-        cfg = RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode)
+        cfg, fused = _cfg_path(mode, cp, rank)
         out = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring,
-                              cu_seqlens=local_cu, max_seqlen=max_local)
+                              cu_seqlens=local_cu, max_seqlen=max_local, fused=fused)
         oq, ocu = O.zigzag_shard_varlen(q, full_cu, rank, cp)
-        ref, _ = O.ring_rank(oq, ks, vs, rank, cp, scale, cu=ocu, merge_mode=mode)
+        ref, _ = O.ring_rank(oq, ks, vs, rank, cp, scale, cu=ocu, merge_mode=cfg.merge_mode)
         assert max_err(out, ref) <= TOL_BF16_OUT, f"rank {rank}"
         outs.append(out.float().cpu())
     lcu = O.local_cu_from_full(full_cu, cp)
@@ -170,12 +180,13 @@ def test_ring_c2_bf16_full_size(rank):
     ring = LocalKVRing.from_full(k, v, cp)
     lq = zigzag_shard(q, rank, cp)
     outs = {}
-    for mode in ("incremental", "batched"):
-        cfg = RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode)
-        outs[mode] = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring)
-    again = ring_flash_attn(lq, ring.k[rank], ring.v[rank], RingConfig(cp_size=cp, cp_rank=rank),
-                            group=ring)
-    assert torch.equal(again, outs["incremental"]), "sweep is not bit-reproducible"
+    for mode in PATHS:
+        cfg, fused = _cfg_path(mode, cp, rank)
+        outs[mode] = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, fused=fused)
+    for mode, fused in (("fused", True), ("incremental", False)):
+        again = ring_flash_attn(lq, ring.k[rank], ring.v[rank], RingConfig(cp_size=cp, cp_rank=rank),
+                                group=ring, fused=fused)
+        assert torch.equal(again, outs[mode]), f"{mode} sweep is not bit-reproducible"
     kc, vc = k.float().cpu(), v.float().cpu()
     grow = O.zigzag_rows(n, rank, cp)
     qc = torch.zeros(n, hq, d)
