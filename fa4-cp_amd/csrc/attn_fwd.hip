@@ -762,54 +762,91 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_pp(AttnParams p)
 }
 
 //--------------------------------------------------------------------------------------
-// bf16 / fp16 kernel, head dim <= 128, V^T given: eight-wavefront ping-pong
+// bf16 / fp16, head dim <= 128, V^T given: eight-wavefront ping-pong over key segments
 //
-// attn_fwd_16bit_pp with V^T tiles loaded straight from the fa4cp_transpose_v layout, so
-// no wavefront transposes V.  For a lane's P^T slots to be consecutive keys, the A operand
-// row rho of S^T tile mt is fed key 32 mt + sw(rho), sw swapping bits 2 and 3 of rho:
-// accumulator register i of lane half h then holds key 32 mt + 16 (i / 8) + 8 h + i % 8,
-// and P^T k-step t (registers 8 (t % 2) + 0..7 of tile t / 2) covers keys 16 t + 8 h + 0..7,
-// the 16 bytes at V^T row d, keys 16 t + 8 h.
+// The V^T tiles come straight from the fa4cp_transpose_v layout, so no wavefront
+// transposes V.  For a lane's P^T slots to be consecutive keys, the A operand row rho of
+// S^T tile mt is fed key 32 mt + sw(rho), sw swapping bits 2 and 3 of rho: accumulator
+// register i of lane half h then holds key 32 mt + 16 (i / 8) + 8 h + i % 8, and P^T k-step
+// t (registers 8 (t % 2) + 0..7 of tile t / 2) covers keys 16 t + 8 h + 0..7, the 16 bytes
+// at V^T row d, keys 16 t + 8 h.
 //
-// LDS: K [BN][D] in three slots, chunk c of row r at c ^ ksw(r); V^T [D][BN] in two slots,
-// chunk c of row d at c ^ ((d >> 1) & 7) (16 distinct 16-byte slots per 256 bytes for the
-// 16 lanes of every fragment read).  Counting phases from 0 (group 0's first MFMA phase):
-// group 0 loads K_{j+2} into slot (j + 2) % 3 in its VALU phase j (phase 2j + 1; the slot
-// last held K_{j-1}, read in phase 2j - 1); group 1 loads V^T_{j+1} into slot (j + 1) % 2
-// in its VALU phase j (phase 2j + 2; the slot last held V^T_{j-1}, read in phase 2j + 1).
-// Each wavefront waits for its loads at the end of its next phase, whose barrier publishes
-// them before phase 2j + 4, the first that reads them.
+// LDS: K [BN][D] in KS = 4 slots, chunk c of row r at c ^ ksw(r); V^T [D][BN] in VS = 3
+// slots, chunk c of row d at c ^ ((d >> 1) & 7) (16 distinct 16-byte slots per 256 bytes
+// for the 16 lanes of every fragment read).  Every wavefront loads one operand: group 0
+// the K tiles, group 1 the V^T tiles, four wavefronts per tile.  Counting phases from 0
+// (group 0's first MFMA phase), group 0 loads K_{j+3} into slot (j + 3) % 4 in its VALU
+// phase j (phase 2j + 1; the slot last held K_{j-1}, read in phases 2j - 2 and 2j - 1),
+// group 1 loads V^T_{j+2} into slot (j + 2) % 3 in its VALU phase j (phase 2j + 2; the
+// slot last held V^T_{j-1}, read in phases 2j and 2j + 1).  At the end of its MFMA phase
+// a wavefront waits for all but the loads of its latest VALU phase, i.e. for K_{j+1}
+// (first read in phase 2j + 2) or V^T_j (first read in phase 2j + 2); the barrier that
+// follows publishes them.  A cursor past the last tile still issues its loads, with an
+// empty buffer range: they write zeros into a slot nobody reads, so every VALU phase
+// issues the same number of loads and the wait is one constant.  The phase barriers carry
+// no memory fence (a fence would wait for the loads just issued).
+//
+// The keys are a list of segments (a ring sweep: one per step; one attention call: one),
+// each a run of BN-key tiles of one source.  The cursors bump a pointer per tile and look
+// at the segment list only when a segment ends, so the walk costs a few scalar
+// instructions per tile: one wavefront's issue rate bounds the VALU phase.
 //--------------------------------------------------------------------------------------
 __device__ __forceinline__ int swap_bits23(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 template <int CH>
 __device__ __forceinline__ int ksw16(int r) { return CH >= 16 ? (r & 15) : ((r >> 1) & 7); }
 
-template <typename T, int D, int HP>
-__global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_vt(AttnParams p) {
+constexpr int kNoCausal = 1 << 29;  // causal offset that masks nothing
+
+// One segment of keys as one row tile sees them.  Query row q (numbered within its query
+// range) sees key k < keys of the segment when q >= qmin and k <= q + off.
+struct StepSeg {
+  int src;         // source of the keys
+  int keys;        // keys of the segment (per sequence)
+  int tiles;       // BN-key tiles this row tile visits
+  int first_mask;  // first tile that needs a mask (== tiles when none does)
+  int off;         // causal offset, kNoCausal when not causal
+  int qmin;        // rows below see none of the segment
+};
+// Load cursor: segment s, tile t of it, and the byte address of that tile's data.
+struct LoadCursor {
+  int s, t, tiles, keys;
+  const char* ptr;
+};
+// Mask cursor: segment s, tile t of it.
+struct MaskCursor {
+  int s, t;
+  StepSeg g;
+};
+
+// The pipeline over a segment list.  Geo provides nseg(), seg(s) -> StepSeg and
+// base(src, is_k) -> byte address of the segment's first K row (of this kv head) or V^T
+// position (of this kv head and sequence).  q: Q row r0 of this wavefront's head; q_valid:
+// rows of Q from there (zeros beyond); out / lse: the same row of the outputs; Lq: rows of
+// the query range (rows from Lq on are not written).
+template <typename T, int D, int HP, typename Geo>
+__device__ __forceinline__ void vt_pipeline(const Geo& geo, const T* q, int64_t q_rs, int q_valid, T* out,
+                                            int64_t o_rs, float* lse, int64_t lse_rs, int r0, int Lq,
+                                            int k_rsb, int vt_rsb, float scale) {
   using Ops = MfmaOps<T>;
   using frag = typename Ops::frag;
   constexpr int BN = kBN;
-  constexpr int RB = kPPWaves / HP;     // 32-row blocks per workgroup
-  constexpr int CH = D / 8;             // 16-byte chunks per K row
-  constexpr int NLD = BN * CH / 64;     // wave-wide LDS-DMA loads per K (or V^T) tile
+  constexpr int CH = D / 8;
+  constexpr int NLD = BN * CH / 64;  // wave-wide LDS-DMA loads per K (or V^T) tile
   constexpr int NMT = BN / 32;
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
   constexpr int NPS = BN / 16;
+  constexpr int KS = 4, VS = 3;      // LDS slots of K and V^T tiles
+  constexpr int TILE = BN * D;       // elements of one K or V^T tile
   static_assert(D <= 128, "ping-pong kernel holds one 32 x D output tile per wavefront");
   static_assert(BN * (int)sizeof(T) == 128, "V^T rows are 8 chunks");
   static_assert(NLD % 4 == 0 && NLD % kPPWaves == 0, "tile loads must split over the wavefronts");
+  // s_waitcnt: LDS reads done; this wavefront's loads of its latest VALU phase may remain
+  constexpr int kWaitOlder = (NLD / 4) | (7 << 4);
+  static_assert(NLD / 4 < 16, "vmcnt field");
 
-  __shared__ __attribute__((aligned(1024))) T kl[3][BN * D];
-  __shared__ __attribute__((aligned(1024))) T vtl[2][D * BN];
-
-  int hg, seq, rt;
-  decode_block(p, hg, seq, rt);
-  int qs, Lq, ks, Lk;
-  seq_range(p.cu_q, seq, p.total_q, p.q_sel, qs, Lq);
-  seq_range(p.cu_k, seq, p.total_k, p.k_sel, ks, Lk);
-  const int row_tile0 = rt * RB * 32;
-  if (row_tile0 >= Lq) return;
+  __shared__ __attribute__((aligned(1024))) T kl[KS][TILE];
+  __shared__ __attribute__((aligned(1024))) T vtl[VS][TILE];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -818,64 +855,93 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_vt(AttnParams p)
   const int lane = tid & 63;
   const int lq = lane & 31;
   const int lh = lane >> 5;
-  const int groups_per_kv = p.group / HP;
-  const int kvh = hg / groups_per_kv;
-  const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
-  const int r0 = row_tile0 + (wave / HP) * 32;
-  const int off = Lk - Lq;
+  const int nseg = geo.nseg();
 
-  int n_tiles = (Lk + BN - 1) / BN;
-  if (p.causal) {
-    const int last_row = min(row_tile0 + RB * 32, Lq) - 1;
-    const int kmax = last_row + off;
-    n_tiles = kmax < 0 ? 0 : min(n_tiles, kmax / BN + 1);
-  }
-  const int n_free = mask_free_tiles(n_tiles, Lk, p.causal, row_tile0, off);
-
-  const T* __restrict__ qg = reinterpret_cast<const T*>(p.q);
-  const T* __restrict__ kg = reinterpret_cast<const T*>(p.k);
+  int n_tiles = 0;
+  for (int s = 0; s < nseg; ++s) n_tiles += geo.seg(s).tiles;
 
   frag qf[NKS];
   {
-    const int64_t rsb = p.q_rs * (int64_t)sizeof(T);
-    const auto rq = make_rsrc(qg + (int64_t)(qs + r0) * p.q_rs + (int64_t)head * p.q_hs,
-                              (int64_t)min(Lq - r0, 32) * rsb);
+    const int rsb = (int)(q_rs * (int64_t)sizeof(T));
+    const auto rq = make_rsrc(q, (int64_t)q_valid * rsb);
 #pragma unroll
     for (int t = 0; t < NKS; ++t)
-      qf[t] = __builtin_bit_cast(frag, bload128(rq, lq * (int)rsb + (int)sizeof(T) * (16 * t + 8 * lh)));
+      qf[t] = __builtin_bit_cast(frag, bload128(rq, lq * rsb + (int)sizeof(T) * (16 * t + 8 * lh)));
   }
 
-  const T* kbase = kg + (int64_t)ks * p.k_rs + (int64_t)kvh * p.k_hs;
-  const int k_rsb = (int)(p.k_rs * (int64_t)sizeof(T));
-  // V^T of this kv head and sequence: row d at vtbase + d * vt_ds
-  const int64_t vt_pos = p.cu_k ? vt_seq_start(p.cu_k, seq, p.k_sel) : 0;
-  const T* vtbase = reinterpret_cast<const T*>(p.vt) + (int64_t)kvh * D * p.vt_ds + vt_pos;
-  const int64_t vt_left = (int64_t)D * p.vt_ds - vt_pos;  // elements to the end of this head
-  const int vt_rsb = (int)(p.vt_ds * (int64_t)sizeof(T));
-  // LDS-DMA of one tile by `nw` wavefronts: load n of wavefront w fills LDS chunks
-  // [64 (w + nw n), +64) of the tile.
-  auto dma_k = [&](int tile, T* dst, int w, auto nw) __attribute__((always_inline)) {
-    const int kb = tile * BN;
-    const auto rk = make_rsrc(kbase + (int64_t)kb * p.k_rs, (int64_t)min(Lk - kb, BN) * k_rsb);
-#pragma unroll
-    for (int n = 0; n < NLD / decltype(nw)::value; ++n) {
-      const int P = 64 * (w + decltype(nw)::value * n) + lane;
-      const int row = P / CH, c = (P % CH) ^ ksw16<CH>(row);
-      dma16(rk, dst + 512 * (w + decltype(nw)::value * n), row * k_rsb + 16 * c);
+  // ---- load cursors
+  // a V^T tile spans rows d = 0..D-1 of BN keys; the 128-key padding of every sequence
+  // keeps it inside the source's V^T
+  const int vt_tile_bytes = (D - 1) * vt_rsb + BN * (int)sizeof(T);
+  auto fix = [&](LoadCursor& c, bool isk) __attribute__((always_inline)) {
+    while (c.t >= c.tiles && c.s < nseg) {
+      ++c.s;
+      c.t = 0;
+      if (c.s < nseg) {
+        const StepSeg g = geo.seg(c.s);
+        c.tiles = g.tiles;
+        c.keys = g.keys;
+        c.ptr = geo.base(g.src, isk);
+      }
     }
   };
-  auto dma_vt = [&](int tile, T* dst, int w, auto nw) __attribute__((always_inline)) {
-    const int kb = tile * BN;
-    const auto rv = make_rsrc(vtbase + kb, (vt_left - kb) * (int64_t)sizeof(T));
-#pragma unroll
-    for (int n = 0; n < NLD / decltype(nw)::value; ++n) {
-      const int P = 64 * (w + decltype(nw)::value * n) + lane;
-      const int d = P >> 3, c = (P & 7) ^ ((d >> 1) & 7);
-      dma16(rv, dst + 512 * (w + decltype(nw)::value * n), d * vt_rsb + 16 * c);
-    }
+  auto start = [&](bool isk) __attribute__((always_inline)) {
+    const StepSeg g = geo.seg(0);
+    LoadCursor c{0, 0, g.tiles, g.keys, geo.base(g.src, isk)};
+    fix(c, isk);
+    return c;
+  };
+  auto step = [&](LoadCursor& c, bool isk) __attribute__((always_inline)) {
+    ++c.t;
+    c.ptr += isk ? BN * k_rsb : BN * (int)sizeof(T);
+    if (__builtin_expect(c.t >= c.tiles, 0)) fix(c, isk);
+  };
+  auto rsrc = [&](const LoadCursor& c, bool isk) __attribute__((always_inline)) {
+    const int n = c.s >= nseg ? 0 : isk ? min(c.keys - c.t * BN, BN) * k_rsb : vt_tile_bytes;
+    return make_rsrc32(c.ptr, n);
+  };
+  // LDS-DMA lane offsets of a tile split over `nw` wavefronts (load n of wavefront w fills
+  // LDS chunks [64 (w + nw n), +64) of the tile)
+  auto k_voff = [&](int w, int nw, int n) __attribute__((always_inline)) {
+    const int P = 64 * (w + nw * n) + lane;
+    const int row = P / CH, c = (P % CH) ^ ksw16<CH>(row);
+    return row * k_rsb + 16 * c;
+  };
+  auto v_voff = [&](int w, int nw, int n) __attribute__((always_inline)) {
+    const int P = 64 * (w + nw * n) + lane;
+    const int d = P >> 3, c = (P & 7) ^ ((d >> 1) & 7);
+    return d * vt_rsb + 16 * c;
   };
 
-  const int kr = swap_bits23(lq);  // K row fed by this lane (tile 0)
+  // prologue: K_0 .. K_{KS-2} and V^T_0 .. V^T_{VS-2}, loaded by all eight wavefronts
+  LoadCursor kc = start(true), vc = start(false);
+#pragma unroll
+  for (int i = 0; i < KS - 1; ++i) {
+    const auto r = rsrc(kc, true);
+#pragma unroll
+    for (int n = 0; n < NLD / kPPWaves; ++n)
+      dma16(r, kl[i] + 512 * (wave + kPPWaves * n), k_voff(wave, kPPWaves, n));
+    step(kc, true);
+  }
+#pragma unroll
+  for (int i = 0; i < VS - 1; ++i) {
+    const auto r = rsrc(vc, false);
+#pragma unroll
+    for (int n = 0; n < NLD / kPPWaves; ++n)
+      dma16(r, vtl[i] + 512 * (wave + kPPWaves * n), v_voff(wave, kPPWaves, n));
+    step(vc, false);
+  }
+  // from here on group 0 loads K and group 1 V^T
+  const bool isk = grp == 0;
+  LoadCursor lc = isk ? kc : vc;
+  int ld_voff[NLD / 4];
+#pragma unroll
+  for (int n = 0; n < NLD / 4; ++n) ld_voff[n] = isk ? k_voff(wi, 4, n) : v_voff(wi, 4, n);
+  T* const ld_base = isk ? kl[0] : vtl[0];
+  const int ld_slots = isk ? KS : VS;
+  int ld_slot = ld_slots - 1;
+
+  const int kr = swap_bits23(lq);
   int k_off[NKS];
 #pragma unroll
   for (int t = 0; t < NKS; ++t) k_off[t] = kr * D + 8 * ((2 * t + lh) ^ ksw16<CH>(kr));
@@ -883,7 +949,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_vt(AttnParams p)
 #pragma unroll
   for (int t = 0; t < NPS; ++t) v_off[t] = lq * BN + 8 * ((2 * t + lh) ^ ((lq >> 1) & 7));
 
-  const float c_log2 = p.scale * kLog2e;
+  const float c_log2 = scale * kLog2e;
   f32x16 o[NDT];
 #pragma unroll
   for (int i = 0; i < NDT; ++i) o[i] = f32x16{};
@@ -912,363 +978,20 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_vt(AttnParams p)
         o[dt] = Ops::mma(a, pf[t], o[dt]);
       }
   };
-  auto mask = [&](int kb0) __attribute__((always_inline)) {
-    const int qq = r0 + lq + off;
-#pragma unroll
-    for (int mt = 0; mt < NMT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int kk = kb0 + 32 * mt + 16 * (i >> 3) + 8 * lh + (i & 7);
-        const bool dead = kk >= Lk || (p.causal && kk > qq);
-        s[mt][i] = dead ? -INFINITY : s[mt][i];
-      }
-  };
-
-  std::integral_constant<int, kPPWaves> all8;
-  std::integral_constant<int, 4> four;
-  if (n_tiles > 0) {
-    dma_k(0, kl[0], wave, all8);
-    dma_k(1, kl[1], wave, all8);
-    dma_vt(0, vtl[0], wave, all8);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (grp == 1) __syncthreads();  // group 1 runs one phase behind group 0
-
-  for (int j = 0; j < n_tiles; ++j) {
-    // MFMA phase
-    __builtin_amdgcn_s_setprio(1);
-    qk(kl[j % 3]);
-    if (j > 0) {
-      pv(vtl[(j - 1) & 1]);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kPPReadAhead, 0);
-#pragma unroll
-      for (int i = 0; i < NMT * NKS + NDT * NPS; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-      }
-    }
-    __builtin_amdgcn_s_setprio(0);
-    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's LDS-DMA from its previous VALU phase
-    __syncthreads();
-    // VALU phase
-    if (grp == 0) dma_k(j + 2, kl[(j + 2) % 3], wi, four);
-    else dma_vt(j + 1, vtl[(j + 1) & 1], wi, four);
-    if (j >= n_free) mask(j * BN);
-    tile_max_rescale<NMT, NDT>(s, o, m, lsum, c_log2);
-    tile_exp<NMT>(s, m, lsum, c_log2);
-#pragma unroll
-    for (int t = 0; t < NPS; ++t)
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) pf[t][jj] = (T)s[t >> 1][8 * (t & 1) + jj];
-    __syncthreads();
-  }
-  if (n_tiles > 0) {
-    __builtin_amdgcn_s_setprio(1);
-    pv(vtl[(n_tiles - 1) & 1]);
-    __builtin_amdgcn_s_setprio(0);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (grp == 0) __syncthreads();  // both groups pass the same number of barriers
-
-  const float ltot = pair_sum(lsum);
-  const float inv = ltot > 0.f ? 1.0f / ltot : 0.f;
-  const int row = r0 + lq;
-  if (row < Lq) {
-    T* og = reinterpret_cast<T*>(p.out) + (int64_t)(qs + row) * p.o_rs + (int64_t)head * p.o_hs;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        typedef T t4 __attribute__((ext_vector_type(4)));
-        t4 w = {(T)(o[dt][4 * g + 0] * inv), (T)(o[dt][4 * g + 1] * inv),
-                (T)(o[dt][4 * g + 2] * inv), (T)(o[dt][4 * g + 3] * inv)};
-        *reinterpret_cast<t4*>(og + 32 * dt + 8 * g + 4 * lh) = w;
-      }
-    if (lh == 0) {
-      const float lse = ltot > 0.f ? m * p.scale + logf(ltot) : -INFINITY;
-      p.lse[(int64_t)(qs + row) * p.lse_rs + head] = lse;
-    }
-  }
-}
-
-//--------------------------------------------------------------------------------------
-// Whole ring sweep, bf16 / fp16, head dim <= 128
-//
-// A workgroup takes one row tile of the local q through the key segments of all ring steps
-// (step 0: own keys, causal; step s <= rank: front half of source (rank - s) mod S; step
-// s > rank: all keys of that source, back-half rows only), one online softmax across them,
-// and writes the final out / lse.  The MFMA / VALU phases and the LDS layouts are those of
-// attn_fwd_16bit_vt; what differs is the walk over segments, kept to a few scalar
-// instructions per tile because one wavefront's issue rate bounds the VALU phase:
-//  * every wavefront loads one operand, group 0 the K tiles (three ahead of the MFMA
-//    phase, four LDS slots) and group 1 the V^T tiles (two ahead, three slots), through a
-//    cursor that bumps a pointer per tile and looks at the segment list only when a
-//    segment ends;
-//  * a cursor past the last tile still issues its loads, with an empty buffer range: they
-//    write zeros into a slot nobody reads, so every VALU phase issues the same number of
-//    loads and the wait before the next phase's reads is one constant;
-//  * the mask bound is computed only for the tiles that need it (causal diagonal, partial
-//    last tiles, rows a back-half step does not cover).
-//--------------------------------------------------------------------------------------
-struct SweepParams {
-  const void* q;
-  void* out;
-  float* lse;
-  int64_t q_rs, q_hs, o_rs, o_hs, lse_rs;
-  const void* k[FA4CP_MAX_CP];
-  const void* vt[FA4CP_MAX_CP];
-  int64_t k_rs, k_hs, vt_ds;
-  const int32_t* cu;
-  int nseq, total;
-  int h_kv, group;
-  int rank, S;
-  float scale;
-  int n_rt, n_hg, n_blocks;
-};
-
-// A ring step's keys as one row tile sees them.
-struct StepSeg {
-  int src;         // source rank
-  int keys;        // keys of the segment (per sequence)
-  int tiles;       // BN-key tiles this row tile visits
-  int kind;        // 0 causal, 1 front-half keys, 2 back-half rows
-  int first_mask;  // first tile that needs a mask (== tiles when none does)
-};
-__device__ __forceinline__ StepSeg step_seg(int s, int rank, int S, int L, int row_tile0, int rows,
-                                            int BN) {
-  StepSeg g;
-  g.src = rank - s < 0 ? rank - s + S : rank - s;
-  const int half = L >> 1;
-  if (s == 0) {
-    g.kind = 0;
-    g.keys = L;
-    const int last_row = min(row_tile0 + rows, L) - 1;
-    g.tiles = min((L + BN - 1) / BN, last_row / BN + 1);
-    // keys <= row_tile0 are visible to every row of the tile
-    g.first_mask = min(min(L / BN, (row_tile0 + 1) / BN), g.tiles);
-  } else if (s <= rank) {
-    g.kind = 1;
-    g.keys = half;
-    g.tiles = (half + BN - 1) / BN;
-    g.first_mask = half / BN;
-  } else {
-    g.kind = 2;
-    g.keys = L;
-    g.tiles = row_tile0 + rows > half ? (L + BN - 1) / BN : 0;
-    g.first_mask = row_tile0 < half ? 0 : L / BN;
-  }
-  return g;
-}
-// Load cursor: step s, tile t of it, and the byte address of that tile's data.
-struct LoadCursor {
-  int s, t, tiles, keys;
-  const char* ptr;
-};
-// Mask cursor: step s, tile t of it.
-struct MaskCursor {
-  int s, t;
-  StepSeg g;
-};
-
-template <typename T, int D, int HP>
-__global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_sweep(SweepParams p) {
-  using Ops = MfmaOps<T>;
-  using frag = typename Ops::frag;
-  constexpr int BN = kBN;
-  constexpr int RB = kPPWaves / HP;
-  constexpr int CH = D / 8;
-  constexpr int NLD = BN * CH / 64;  // wave-wide LDS-DMA loads per K (or V^T) tile
-  constexpr int NMT = BN / 32;
-  constexpr int NDT = D / 32;
-  constexpr int NKS = D / 16;
-  constexpr int NPS = BN / 16;
-  constexpr int KS = 4, VS = 3;      // LDS slots of K and V^T tiles
-  constexpr int TILE = BN * D;       // elements of one K or V^T tile
-  static_assert(D <= 128, "ping-pong kernel holds one 32 x D output tile per wavefront");
-  static_assert(BN * (int)sizeof(T) == 128, "V^T rows are 8 chunks");
-  static_assert(NLD % 4 == 0 && NLD % kPPWaves == 0, "tile loads must split over the wavefronts");
-  // s_waitcnt: LDS reads done; this wavefront's loads of its latest VALU phase may remain
-  constexpr int kWaitOlder = (NLD / 4) | (7 << 4);
-  static_assert(NLD / 4 < 16, "vmcnt field");
-
-  __shared__ __attribute__((aligned(1024))) T kl[KS][TILE];
-  __shared__ __attribute__((aligned(1024))) T vtl[VS][TILE];
-
-  int hg, seq, rt;
-  decode_block(p, hg, seq, rt);
-  int qs, L;
-  seq_range(p.cu, seq, p.total, FA4CP_SEL_ALL, qs, L);
-  const int row_tile0 = rt * RB * 32;
-  if (row_tile0 >= L) return;
-  constexpr int rows = RB * 32;
-  const int half = L >> 1;
-
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int grp = wave >> 2;
-  const int wi = wave & 3;
-  const int lane = tid & 63;
-  const int lq = lane & 31;
-  const int lh = lane >> 5;
-  const int groups_per_kv = p.group / HP;
-  const int kvh = hg / groups_per_kv;
-  const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
-  const int r0 = row_tile0 + (wave / HP) * 32;
-
-  auto seg = [&](int s) __attribute__((always_inline)) {
-    return step_seg(s, p.rank, p.S, L, row_tile0, rows, BN);
-  };
-  int n_tiles = 0;
-  for (int s = 0; s < p.S; ++s) n_tiles += seg(s).tiles;
-
-  const T* __restrict__ qg = reinterpret_cast<const T*>(p.q);
-  frag qf[NKS];
-  {
-    const int64_t rsb = p.q_rs * (int64_t)sizeof(T);
-    const auto rq = make_rsrc(qg + (int64_t)(qs + r0) * p.q_rs + (int64_t)head * p.q_hs,
-                              (int64_t)min(L - r0, 32) * rsb);
-#pragma unroll
-    for (int t = 0; t < NKS; ++t)
-      qf[t] = __builtin_bit_cast(frag, bload128(rq, lq * (int)rsb + (int)sizeof(T) * (16 * t + 8 * lh)));
-  }
-
-  // ---- load cursors
-  const int k_rsb = (int)(p.k_rs * (int64_t)sizeof(T));
-  const int vt_rsb = (int)(p.vt_ds * (int64_t)sizeof(T));
-  const int64_t vt_pos = p.cu ? vt_seq_start(p.cu, seq, FA4CP_SEL_ALL) : 0;
-  const int64_t k_off = ((int64_t)qs * p.k_rs + (int64_t)kvh * p.k_hs) * (int64_t)sizeof(T);
-  const int64_t v_off = ((int64_t)kvh * D * p.vt_ds + vt_pos) * (int64_t)sizeof(T);
-  // a V^T tile spans rows d = 0..D-1 of BN keys; the 128-key padding of every sequence
-  // keeps it inside the source's V^T
-  const int vt_tile_bytes = (D - 1) * vt_rsb + BN * (int)sizeof(T);
-  auto seg_base = [&](int src, bool isk) __attribute__((always_inline)) {
-    return isk ? reinterpret_cast<const char*>(p.k[src]) + k_off
-               : reinterpret_cast<const char*>(p.vt[src]) + v_off;
-  };
-  auto fix = [&](LoadCursor& c, bool isk) __attribute__((always_inline)) {
-    while (c.t >= c.tiles && c.s < p.S) {
-      ++c.s;
-      c.t = 0;
-      if (c.s < p.S) {
-        const StepSeg g = seg(c.s);
-        c.tiles = g.tiles;
-        c.keys = g.keys;
-        c.ptr = seg_base(g.src, isk);
-      }
-    }
-  };
-  auto start = [&](bool isk) __attribute__((always_inline)) {
-    const StepSeg g = seg(0);
-    LoadCursor c{0, 0, g.tiles, g.keys, seg_base(g.src, isk)};
-    fix(c, isk);
-    return c;
-  };
-  auto step = [&](LoadCursor& c, bool isk) __attribute__((always_inline)) {
-    ++c.t;
-    c.ptr += isk ? BN * k_rsb : BN * (int)sizeof(T);
-    if (__builtin_expect(c.t >= c.tiles, 0)) fix(c, isk);
-  };
-  auto rsrc = [&](const LoadCursor& c, bool isk) __attribute__((always_inline)) {
-    const int n = c.s >= p.S ? 0 : isk ? min(c.keys - c.t * BN, BN) * k_rsb : vt_tile_bytes;
-    return make_rsrc32(c.ptr, n);
-  };
-  // LDS-DMA lane offsets of a tile split over `nw` wavefronts (load n of wavefront w fills
-  // LDS chunks [64 (w + nw n), +64) of the tile)
-  auto k_voff = [&](int w, int nw, int n) __attribute__((always_inline)) {
-    const int P = 64 * (w + nw * n) + lane;
-    const int row = P / CH, c = (P % CH) ^ ksw16<CH>(row);
-    return row * k_rsb + 16 * c;
-  };
-  auto v_voff = [&](int w, int nw, int n) __attribute__((always_inline)) {
-    const int P = 64 * (w + nw * n) + lane;
-    const int d = P >> 3, c = (P & 7) ^ ((d >> 1) & 7);
-    return d * vt_rsb + 16 * c;
-  };
-
-  // prologue: K_0 .. K_{KS-2} and V^T_0 .. V^T_{VS-2}, loaded by all eight wavefronts
-  LoadCursor kc = start(true), vc = start(false);
-#pragma unroll
-  for (int i = 0; i < KS - 1; ++i) {
-    const auto r = rsrc(kc, true);
-#pragma unroll
-    for (int n = 0; n < NLD / kPPWaves; ++n) dma16(r, kl[i] + 512 * (wave + kPPWaves * n), k_voff(wave, kPPWaves, n));
-    step(kc, true);
-  }
-#pragma unroll
-  for (int i = 0; i < VS - 1; ++i) {
-    const auto r = rsrc(vc, false);
-#pragma unroll
-    for (int n = 0; n < NLD / kPPWaves; ++n) dma16(r, vtl[i] + 512 * (wave + kPPWaves * n), v_voff(wave, kPPWaves, n));
-    step(vc, false);
-  }
-  // from here on group 0 loads K and group 1 V^T, four wavefronts per tile
-  const bool isk = grp == 0;
-  LoadCursor lc = isk ? kc : vc;
-  int ld_voff[NLD / 4];
-#pragma unroll
-  for (int n = 0; n < NLD / 4; ++n) ld_voff[n] = isk ? k_voff(wi, 4, n) : v_voff(wi, 4, n);
-  T* const ld_base = isk ? kl[0] : vtl[0];
-  const int ld_slots = isk ? KS : VS;
-  int ld_slot = ld_slots - 1;
-
-  const int kr = swap_bits23(lq);
-  int k_off_l[NKS];
-#pragma unroll
-  for (int t = 0; t < NKS; ++t) k_off_l[t] = kr * D + 8 * ((2 * t + lh) ^ ksw16<CH>(kr));
-  int v_off_l[NPS];
-#pragma unroll
-  for (int t = 0; t < NPS; ++t) v_off_l[t] = lq * BN + 8 * ((2 * t + lh) ^ ((lq >> 1) & 7));
-
-  const float c_log2 = p.scale * kLog2e;
-  f32x16 o[NDT];
-#pragma unroll
-  for (int i = 0; i < NDT; ++i) o[i] = f32x16{};
-  float m = -INFINITY;
-  float lsum = 0.f;
-  f32x16 s[NMT];
-  frag pf[NPS];
-
-  auto qk = [&](const T* ksrc) __attribute__((always_inline)) {
-#pragma unroll
-    for (int mt = 0; mt < NMT; ++mt) {
-      s[mt] = f32x16{};
-#pragma unroll
-      for (int t = 0; t < NKS; ++t) {
-        const frag a = *reinterpret_cast<const frag*>(ksrc + k_off_l[t] + 32 * mt * D);
-        s[mt] = Ops::mma(a, qf[t], s[mt]);
-      }
-    }
-  };
-  auto pv = [&](const T* vsrc) __attribute__((always_inline)) {
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int t = 0; t < NPS; ++t) {
-        const frag a = *reinterpret_cast<const frag*>(vsrc + 32 * dt * BN + v_off_l[t]);
-        o[dt] = Ops::mma(a, pf[t], o[dt]);
-      }
-  };
   // mask cursor (the tile in the MFMA phase)
-  MaskCursor mc{0, 0, seg(0)};
+  MaskCursor mc{0, 0, geo.seg(0)};
   auto mfix = [&]() __attribute__((always_inline)) {
-    while (mc.t >= mc.g.tiles && mc.s < p.S) {
+    while (mc.t >= mc.g.tiles && mc.s < nseg) {
       ++mc.s;
       mc.t = 0;
-      if (mc.s < p.S) mc.g = seg(mc.s);
+      if (mc.s < nseg) mc.g = geo.seg(mc.s);
     }
   };
   mfix();
   const int qq = r0 + lq;
-  // keys past the segment, keys after the query (step 0), every key for the rows a
-  // back-half step does not cover
   auto mask = [&]() __attribute__((always_inline)) {
     const int kb0 = mc.t * BN;
-    const int lim_all = mc.g.keys - kb0;
-    const int lim0 = min(lim_all, qq + 1 - kb0);
-    const int lim2 = qq < half ? 0 : lim_all;
-    const int lim = mc.g.kind == 0 ? lim0 : mc.g.kind == 2 ? lim2 : lim_all;
+    const int lim = qq < mc.g.qmin ? 0 : min(mc.g.keys, qq + mc.g.off + 1) - kb0;
 #pragma unroll
     for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
@@ -1278,7 +1001,6 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_sweep(SweepParam
       }
   };
 
-  std::integral_constant<int, 4> four;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (grp == 1) __syncthreads();  // group 1 runs one phase behind group 0
@@ -1298,9 +1020,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_sweep(SweepParam
         __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
         __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
       }
-    }
-    // cursor walk while the MFMAs drain
-    if constexpr (decltype(with_pv)::value) {
+      // cursor walk while the MFMAs drain
       step(lc, isk);
       ++mc.t;
       if (__builtin_expect(mc.t >= mc.g.tiles, 0)) mfix();
@@ -1342,13 +1062,11 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_sweep(SweepParam
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (grp == 0) __syncthreads();  // both groups pass the same number of barriers
-  (void)four;
 
   const float ltot = pair_sum(lsum);
   const float inv = ltot > 0.f ? 1.0f / ltot : 0.f;
-  const int row = r0 + lq;
-  if (row < L) {
-    T* og = reinterpret_cast<T*>(p.out) + (int64_t)(qs + row) * p.o_rs + (int64_t)head * p.o_hs;
+  if (r0 + lq < Lq) {
+    T* og = out + (int64_t)lq * o_rs;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -1358,11 +1076,152 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_sweep(SweepParam
                 (T)(o[dt][4 * g + 2] * inv), (T)(o[dt][4 * g + 3] * inv)};
         *reinterpret_cast<t4*>(og + 32 * dt + 8 * g + 4 * lh) = w;
       }
-    if (lh == 0) {
-      const float lse = ltot > 0.f ? m * p.scale + logf(ltot) : -INFINITY;
-      p.lse[(int64_t)(qs + row) * p.lse_rs + head] = lse;
-    }
+    if (lh == 0) lse[(int64_t)lq * lse_rs] = ltot > 0.f ? m * scale + logf(ltot) : -INFINITY;
   }
+}
+
+// One attention call: a single segment.
+struct OneSegment {
+  StepSeg g;
+  const char* kb;
+  const char* vb;
+  __device__ __forceinline__ int nseg() const { return 1; }
+  __device__ __forceinline__ StepSeg seg(int) const { return g; }
+  __device__ __forceinline__ const char* base(int, bool isk) const { return isk ? kb : vb; }
+};
+
+template <typename T, int D, int HP>
+__global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_vt(AttnParams p) {
+  constexpr int BN = kBN;
+  constexpr int RB = kPPWaves / HP;  // 32-row blocks per workgroup
+  int hg, seq, rt;
+  decode_block(p, hg, seq, rt);
+  int qs, Lq, ks, Lk;
+  seq_range(p.cu_q, seq, p.total_q, p.q_sel, qs, Lq);
+  seq_range(p.cu_k, seq, p.total_k, p.k_sel, ks, Lk);
+  const int row_tile0 = rt * RB * 32;
+  if (row_tile0 >= Lq) return;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int groups_per_kv = p.group / HP;
+  const int kvh = hg / groups_per_kv;
+  const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
+  const int r0 = row_tile0 + (wave / HP) * 32;
+  const int off = Lk - Lq;
+
+  OneSegment geo;
+  geo.g.src = 0;
+  geo.g.keys = Lk;
+  geo.g.tiles = (Lk + BN - 1) / BN;
+  if (p.causal) {
+    const int kmax = min(row_tile0 + RB * 32, Lq) - 1 + off;
+    geo.g.tiles = kmax < 0 ? 0 : min(geo.g.tiles, kmax / BN + 1);
+  }
+  geo.g.first_mask = mask_free_tiles(geo.g.tiles, Lk, p.causal, row_tile0, off);
+  geo.g.off = p.causal ? off : kNoCausal;
+  geo.g.qmin = 0;
+  const int64_t vt_pos = p.cu_k ? vt_seq_start(p.cu_k, seq, p.k_sel) : 0;
+  geo.kb = reinterpret_cast<const char*>(reinterpret_cast<const T*>(p.k) + (int64_t)ks * p.k_rs +
+                                         (int64_t)kvh * p.k_hs);
+  geo.vb = reinterpret_cast<const char*>(reinterpret_cast<const T*>(p.vt) + (int64_t)kvh * D * p.vt_ds + vt_pos);
+
+  const T* q = reinterpret_cast<const T*>(p.q) + (int64_t)(qs + r0) * p.q_rs + (int64_t)head * p.q_hs;
+  T* out = reinterpret_cast<T*>(p.out) + (int64_t)(qs + r0) * p.o_rs + (int64_t)head * p.o_hs;
+  float* lse = p.lse + (int64_t)(qs + r0) * p.lse_rs + head;
+  vt_pipeline<T, D, HP>(geo, q, p.q_rs, min(Lq - r0, 32), out, p.o_rs, lse, p.lse_rs, r0, Lq,
+                        (int)(p.k_rs * (int64_t)sizeof(T)), (int)(p.vt_ds * (int64_t)sizeof(T)), p.scale);
+}
+
+//--------------------------------------------------------------------------------------
+// Whole ring sweep, bf16 / fp16, head dim <= 128
+//
+// A workgroup takes one row tile of the local q through the key segments of all ring steps
+// (step 0: own keys, causal; step s <= rank: front half of source (rank - s) mod S; step
+// s > rank: all keys of that source, back-half rows only) with one online softmax, and
+// writes the final out / lse: vt_pipeline over one segment per step.
+//--------------------------------------------------------------------------------------
+struct SweepParams {
+  const void* q;
+  void* out;
+  float* lse;
+  int64_t q_rs, q_hs, o_rs, o_hs, lse_rs;
+  const void* k[FA4CP_MAX_CP];
+  const void* vt[FA4CP_MAX_CP];
+  int64_t k_rs, k_hs, vt_ds;
+  const int32_t* cu;
+  int nseq, total;
+  int h_kv, group;
+  int rank, S;
+  float scale;
+  int n_rt, n_hg, n_blocks;
+};
+
+// The ring steps of one row tile (rows [row_tile0, row_tile0 + rows) of a sequence of L).
+struct RingSegments {
+  const SweepParams* p;
+  int L, row_tile0, rows;
+  int64_t k_off, v_off;  // bytes from a source's K / V^T to this sequence and kv head
+  __device__ __forceinline__ int nseg() const { return p->S; }
+  __device__ __forceinline__ StepSeg seg(int s) const {
+    constexpr int BN = kBN;
+    StepSeg g;
+    g.src = p->rank - s < 0 ? p->rank - s + p->S : p->rank - s;
+    const int half = L >> 1;
+    g.qmin = 0;
+    g.off = kNoCausal;
+    if (s == 0) {  // own keys, causal
+      g.keys = L;
+      g.off = 0;
+      const int last_row = min(row_tile0 + rows, L) - 1;
+      g.tiles = min((L + BN - 1) / BN, last_row / BN + 1);
+      g.first_mask = min(min(L / BN, (row_tile0 + 1) / BN), g.tiles);
+    } else if (s <= p->rank) {  // front half of the keys, every row
+      g.keys = half;
+      g.tiles = (half + BN - 1) / BN;
+      g.first_mask = half / BN;
+    } else {  // all keys, back-half rows
+      g.keys = L;
+      g.qmin = half;
+      g.tiles = row_tile0 + rows > half ? (L + BN - 1) / BN : 0;
+      g.first_mask = row_tile0 < half ? 0 : L / BN;
+    }
+    return g;
+  }
+  __device__ __forceinline__ const char* base(int src, bool isk) const {
+    return isk ? reinterpret_cast<const char*>(p->k[src]) + k_off : reinterpret_cast<const char*>(p->vt[src]) + v_off;
+  }
+};
+
+template <typename T, int D, int HP>
+__global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_sweep(SweepParams p) {
+  constexpr int RB = kPPWaves / HP;
+  int hg, seq, rt;
+  decode_block(p, hg, seq, rt);
+  int qs, L;
+  seq_range(p.cu, seq, p.total, FA4CP_SEL_ALL, qs, L);
+  const int row_tile0 = rt * RB * 32;
+  if (row_tile0 >= L) return;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int groups_per_kv = p.group / HP;
+  const int kvh = hg / groups_per_kv;
+  const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
+  const int r0 = row_tile0 + (wave / HP) * 32;
+
+  RingSegments geo;
+  geo.p = &p;
+  geo.L = L;
+  geo.row_tile0 = row_tile0;
+  geo.rows = RB * 32;
+  const int64_t vt_pos = p.cu ? vt_seq_start(p.cu, seq, FA4CP_SEL_ALL) : 0;
+  geo.k_off = ((int64_t)qs * p.k_rs + (int64_t)kvh * p.k_hs) * (int64_t)sizeof(T);
+  geo.v_off = ((int64_t)kvh * D * p.vt_ds + vt_pos) * (int64_t)sizeof(T);
+
+  const T* q = reinterpret_cast<const T*>(p.q) + (int64_t)(qs + r0) * p.q_rs + (int64_t)head * p.q_hs;
+  T* out = reinterpret_cast<T*>(p.out) + (int64_t)(qs + r0) * p.o_rs + (int64_t)head * p.o_hs;
+  float* lse = p.lse + (int64_t)(qs + r0) * p.lse_rs + head;
+  vt_pipeline<T, D, HP>(geo, q, p.q_rs, min(L - r0, 32), out, p.o_rs, lse, p.lse_rs, r0, L,
+                        (int)(p.k_rs * (int64_t)sizeof(T)), (int)(p.vt_ds * (int64_t)sizeof(T)), p.scale);
 }
 
 //--------------------------------------------------------------------------------------
