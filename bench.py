@@ -336,19 +336,30 @@ def main():
                                   "merge_states_ms": round(ms_ms, 4), "merge_states_bytes": round(bb),
                                   "merge_states_GBs": round(bb / (ms_ms * 1e-3) / 1e9, 1)}
         del lq7
-        # fp8 sweep
+        # fp8 sweep: fused (default) and per step
         q8, ring8, desc = make_fp8_inputs(rank)
         cfg8 = RingConfig(cp_size=CP, cp_rank=rank)
         clock8 = KernelClock()
         sec8 = timed_sweeps(lambda: ring_flash_attn(q8, ring8.k[rank], ring8.v[rank], cfg8, group=ring8,
                                                     descales=desc), args.steps, args.warmup, clock8)
-        a8 = clock8.mean_ms("attn")
+        s8 = clock8.mean_ms("sweep_kernel")
+        clock8p = KernelClock()
+        sec8p = timed_sweeps(lambda: ring_flash_attn(q8, ring8.k[rank], ring8.v[rank], cfg8, group=ring8,
+                                                     descales=desc, fused=False),
+                             max(3, args.steps // 2), 2, clock8p)
+        a8 = clock8p.mean_ms("attn")
         result["fp8"] = {"workload": "same shape, OCP e4m3 q/k/v, per-source-rank k/v descales, bf16 out",
                          "ms_per_step": round(sec8 * 1e3, 3), "TFLOP/s": round(flops / sec8 / 1e12, 2),
                          "frac_of_fp8_peak": round(flops / sec8 / 1e12 / PEAK_FP8_TFLOPS, 4),
-                         "attn_avg_launch_ms": round(a8, 4),
-                         "attn_TFLOP/s": round(per_launch / (a8 * 1e-3) / 1e12, 2),
-                         "attn_frac": round(per_launch / (a8 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)}
+                         "sweep_kernel": {"kernel": "attn_fwd_e4m3_sweep<4>", "avg_launch_ms": round(s8, 4),
+                                          "TFLOP/s": round(flops / (s8 * 1e-3) / 1e12, 2),
+                                          "frac": round(flops / (s8 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)},
+                         "per_step": {"ms_per_step": round(sec8p * 1e3, 3),
+                                      "TFLOP/s": round(flops / sec8p / 1e12, 2),
+                                      "attn_kernel": "attn_fwd_e4m3_vt<4>",
+                                      "attn_avg_launch_ms": round(a8, 4),
+                                      "attn_TFLOP/s": round(per_launch / (a8 * 1e-3) / 1e12, 2),
+                                      "attn_frac": round(per_launch / (a8 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)}}
         del q8, ring8
     del ring, lq, q_full
     torch.cuda.synchronize()

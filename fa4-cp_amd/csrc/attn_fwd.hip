@@ -806,6 +806,7 @@ struct StepSeg {
   int first_mask;  // first tile that needs a mask (== tiles when none does)
   int off;         // causal offset, kNoCausal when not causal
   int qmin;        // rows below see none of the segment
+  float kd, vd;    // k / v descales of the source (e4m3; 1 otherwise)
 };
 // Load cursor: segment s, tile t of it, and the byte address of that tile's data.
 struct LoadCursor {
@@ -1120,6 +1121,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_vt(AttnParams p)
   geo.g.first_mask = mask_free_tiles(geo.g.tiles, Lk, p.causal, row_tile0, off);
   geo.g.off = p.causal ? off : kNoCausal;
   geo.g.qmin = 0;
+  geo.g.kd = geo.g.vd = 1.f;
   const int64_t vt_pos = p.cu_k ? vt_seq_start(p.cu_k, seq, p.k_sel) : 0;
   geo.kb = reinterpret_cast<const char*>(reinterpret_cast<const T*>(p.k) + (int64_t)ks * p.k_rs +
                                          (int64_t)kvh * p.k_hs);
@@ -1153,22 +1155,28 @@ struct SweepParams {
   int h_kv, group;
   int rank, S;
   float scale;
+  const float* qd;  // [h_kv] (e4m3) or NULL
+  const float* kd;  // [S][h_kv] (e4m3) or NULL
+  const float* vd;  // [S][h_kv] (e4m3) or NULL
   int n_rt, n_hg, n_blocks;
 };
 
-// The ring steps of one row tile (rows [row_tile0, row_tile0 + rows) of a sequence of L).
+// The ring steps of one row tile (rows [row_tile0, row_tile0 + rows) of a sequence of L),
+// in tiles of BN keys.
+template <int BN>
 struct RingSegments {
   const SweepParams* p;
-  int L, row_tile0, rows;
+  int L, row_tile0, rows, kvh;
   int64_t k_off, v_off;  // bytes from a source's K / V^T to this sequence and kv head
   __device__ __forceinline__ int nseg() const { return p->S; }
   __device__ __forceinline__ StepSeg seg(int s) const {
-    constexpr int BN = kBN;
     StepSeg g;
     g.src = p->rank - s < 0 ? p->rank - s + p->S : p->rank - s;
     const int half = L >> 1;
     g.qmin = 0;
     g.off = kNoCausal;
+    g.kd = p->kd ? p->kd[g.src * p->h_kv + kvh] : 1.f;
+    g.vd = p->vd ? p->vd[g.src * p->h_kv + kvh] : 1.f;
     if (s == 0) {  // own keys, causal
       g.keys = L;
       g.off = 0;
@@ -1208,11 +1216,12 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_sweep(SweepParam
   const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
   const int r0 = row_tile0 + (wave / HP) * 32;
 
-  RingSegments geo;
+  RingSegments<kBN> geo;
   geo.p = &p;
   geo.L = L;
   geo.row_tile0 = row_tile0;
   geo.rows = RB * 32;
+  geo.kvh = kvh;
   const int64_t vt_pos = p.cu ? vt_seq_start(p.cu, seq, FA4CP_SEL_ALL) : 0;
   geo.k_off = ((int64_t)qs * p.k_rs + (int64_t)kvh * p.k_hs) * (int64_t)sizeof(T);
   geo.v_off = ((int64_t)kvh * D * p.vt_ds + vt_pos) * (int64_t)sizeof(T);
@@ -1821,7 +1830,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_pp(AttnParams p) 
 }
 
 //--------------------------------------------------------------------------------------
-// OCP e4m3 kernel, head dim 128, V^T given: eight-wavefront ping-pong
+// OCP e4m3, head dim 128, V^T given: eight-wavefront ping-pong over key segments
 //
 // attn_fwd_e4m3_pp with V^T tiles loaded straight from the fa4cp_transpose_v layout (no V
 // transposition), loads and swizzles sized for an LDS that serves 256 bytes per cycle (64
@@ -1830,45 +1839,56 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_pp(AttnParams p) 
 //   K    [128 keys][128 B], chunk c of row r at c ^ kswz(r)
 //   V^T  [128 d][128 keys], chunk c of row d at c ^ ((d >> 1) & 7)
 //   Q    per wavefront, lane-contiguous 16-byte halves of the Q^T fragments
-// Group 0 loads K_{j+2} into slot (j + 2) % 3 in its VALU phase j (phase 2j + 1; the slot
-// last held K_{j-1}, read in phase 2j - 1); group 1 loads V^T_{j+1} into slot (j + 1) % 2 in
-// its VALU phase j (phase 2j + 2; the slot last held V^T_{j-1}, read in phase 2j + 1).  Each
-// wavefront waits for its loads at the end of its next phase, whose barrier publishes them
-// before phase 2j + 4, the first that reads them.  The per-lane load offsets are computed
-// once, so the VALU phase issues only the loads themselves.
+// The load schedule, the constant wait and the fence-free barriers are those of
+// vt_pipeline: K in four slots three tiles ahead (group 0), V^T in three slots two tiles
+// ahead (group 1), the segment walk a few scalar instructions per tile.
+//
+// Segments may come from sources with different descales.  The running max is kept in
+// log2 units of the scaled scores (m2 = max of s * scale * qd * kd * log2 e), so each
+// segment's scores enter the softmax through its own factor; O is kept in units of the
+// current segment's v descale and rescaled by vd_old / vd_new when a segment starts.
 //--------------------------------------------------------------------------------------
 // K tile swizzle: the 16 rows read by a 16-lane group are k_row(rho) + const (rows
 // {0-3, 32-35, 4-7, 36-39} + 8 g + 16 (mt % 2) + 64 (mt / 2)), which bits 1-2 and 5 tell
 // apart within each row parity.
 __device__ __forceinline__ int kswz(int r) { return ((r >> 1) & 3) | (((r >> 5) & 1) << 2); }
 
-template <int HP>
-__global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_vt(AttnParams p) {
+// LDS of e8_pipeline: K tiles in four slots, V^T tiles in three, and every wavefront's Q^T
+// fragments (16 bytes per lane per half k-step), kept in LDS instead of registers: they are
+// read once per tile, and the registers hold the scores instead.
+struct E8Lds {
+  static constexpr int TILE = kE8BN * 128;
+  __attribute__((aligned(1024))) uint8_t kl[4][TILE];
+  __attribute__((aligned(1024))) uint8_t vt[3][TILE];
+  __attribute__((aligned(1024))) uint8_t qsm[kPPWaves][2][2][64 * 16];
+};
+
+// Geo as for vt_pipeline, in tiles of kE8BN keys.  q: this wavefront's Q row r0 (e4m3);
+// c_q: softmax scale x q descale.  sp: 0 = P in one e4m3 term everywhere, 1 = two terms on
+// the masked tiles, 2 = two terms on every tile; sp 1 needs a single segment.
+template <int HP, int SP, typename Geo>
+__device__ __forceinline__ void e8_pipeline(E8Lds& lds, const Geo& geo, const uint8_t* q, int64_t q_rs,
+                                            int q_valid, __bf16* out, int64_t o_rs, float* lse, int64_t lse_rs,
+                                            int r0, int Lq, int k_rsb, int vt_rsb, float c_q) {
   constexpr int D = 128;
   constexpr int BN = kE8BN;
-  constexpr int RB = kPPWaves / HP;      // 32-row blocks per workgroup
-  constexpr int CH = D / 16;             // 16-byte chunks per K / V row
-  constexpr int NLD = BN * CH / 64;      // wave-wide LDS-DMA loads per K or V tile
+  constexpr int CH = D / 16;             // 16-byte chunks per K / V^T row
+  constexpr int NLD = BN * CH / 64;      // wave-wide LDS-DMA loads per K or V^T tile
+  constexpr int NG = NLD / 4;            // loads per wavefront of a group
   constexpr int NMT = BN / 32;           // S^T tiles
   constexpr int NKS = D / 64;            // S^T k-steps (64 d each)
   constexpr int NDT = D / 32;            // O^T tiles
   constexpr int NPS = BN / 64;           // O^T k-steps (64 keys each)
+  constexpr int KS = 4, VS = 3;          // LDS slots of K and V^T tiles
+  constexpr int TILE = BN * D;           // bytes of one K or V^T tile
   static_assert(NLD % 4 == 0 && NLD % kPPWaves == 0, "tile loads must split over the wavefronts");
   static_assert(CH == 8, "the K / V swizzles assume 8 chunks per row");
-
-  __shared__ __attribute__((aligned(1024))) uint8_t kl[3][BN * D];
-  __shared__ __attribute__((aligned(1024))) uint8_t vt[2][D * BN];
-  // this wavefront's Q^T fragments (16 bytes per lane per half k-step), kept in LDS instead
-  // of registers: they are read once per tile, and the registers hold the scores instead
-  __shared__ __attribute__((aligned(1024))) uint8_t qsm[kPPWaves][NKS][2][64 * 16];
-
-  int hg, seq, rt;
-  decode_block(p, hg, seq, rt);
-  int qs, Lq, ks, Lk;
-  seq_range(p.cu_q, seq, p.total_q, p.q_sel, qs, Lq);
-  seq_range(p.cu_k, seq, p.total_k, p.k_sel, ks, Lk);
-  const int row_tile0 = rt * RB * 32;
-  if (row_tile0 >= Lq) return;
+  static_assert(E8Lds::TILE == TILE && NKS == 2, "E8Lds layout");
+  constexpr int kWaitOlder = NG | (7 << 4);
+  static_assert(NG < 16, "vmcnt field");
+  auto& kl = lds.kl;
+  auto& vt = lds.vt;
+  auto& qsm = lds.qsm;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1877,81 +1897,92 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_vt(AttnParams p) 
   const int lane = tid & 63;
   const int lq = lane & 31;
   const int lh = lane >> 5;
-  const int groups_per_kv = p.group / HP;
-  const int kvh = hg / groups_per_kv;
-  const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
-  const int r0 = row_tile0 + (wave / HP) * 32;
-  const int off = Lk - Lq;
+  const int nseg = geo.nseg();
 
-  int n_tiles = (Lk + BN - 1) / BN;
-  if (p.causal) {
-    const int last_row = min(row_tile0 + RB * 32, Lq) - 1;
-    const int kmax = last_row + off;
-    n_tiles = kmax < 0 ? 0 : min(n_tiles, kmax / BN + 1);
-  }
-  const int n_free = mask_free_tiles<BN>(n_tiles, Lk, p.causal, row_tile0, off);
-
-  const uint8_t* __restrict__ qg = reinterpret_cast<const uint8_t*>(p.q);
-  const uint8_t* __restrict__ kg = reinterpret_cast<const uint8_t*>(p.k);
-  const uint8_t* __restrict__ vg = reinterpret_cast<const uint8_t*>(p.v);
+  int n_tiles = 0;
+  for (int s = 0; s < nseg; ++s) n_tiles += geo.seg(s).tiles;
 
   {
-    const int rsb = (int)p.q_rs;
-    const auto rq = make_rsrc(qg + (int64_t)(qs + r0) * p.q_rs + (int64_t)head * p.q_hs,
-                              (int64_t)min(Lq - r0, 32) * rsb);
+    const int rsb = (int)q_rs;
+    const auto rq = make_rsrc(q, (int64_t)q_valid * rsb);
 #pragma unroll
     for (int t = 0; t < NKS; ++t) {
-      const u32x4 a = bload128(rq, lq * rsb + 64 * t + 32 * lh);
-      const u32x4 b = bload128(rq, lq * rsb + 64 * t + 32 * lh + 16);
-      *reinterpret_cast<u32x4*>(&qsm[wave][t][0][16 * lane]) = a;
-      *reinterpret_cast<u32x4*>(&qsm[wave][t][1][16 * lane]) = b;
+      const u32x4 x0 = bload128(rq, lq * rsb + 64 * t + 32 * lh);
+      const u32x4 x1 = bload128(rq, lq * rsb + 64 * t + 32 * lh + 16);
+      *reinterpret_cast<u32x4*>(&qsm[wave][t][0][16 * lane]) = x0;
+      *reinterpret_cast<u32x4*>(&qsm[wave][t][1][16 * lane]) = x1;
     }
   }
 
-  const uint8_t* kbase = kg + (int64_t)ks * p.k_rs + (int64_t)kvh * p.k_hs;
-  const int k_rsb = (int)p.k_rs;
-  const int64_t vt_pos = p.cu_k ? vt_seq_start(p.cu_k, seq, p.k_sel) : 0;
-  const uint8_t* vtbase = reinterpret_cast<const uint8_t*>(p.vt) + (int64_t)kvh * D * p.vt_ds + vt_pos;
-  const int64_t vt_left = (int64_t)D * p.vt_ds - vt_pos;  // bytes to the end of this head
-  const int vt_rsb = (int)p.vt_ds;
-  // LDS-DMA: load n of wavefront wi of a group fills LDS chunks [64 (wi + 4 n), +64) of a
-  // tile; chunk P is row r = P / 8 = 8 (wi + 4 n) + lane / 8 at swizzled position P % 8.
-  // Row r's swizzle bits 0-1 are lane bits 4-5 for both tiles; bit 2 is n % 2 (K: bit 5 of
-  // r) or wi % 2 (V^T: bit 3 of r).  So two lane offsets for K, one for V^T, and the row
-  // term 8 (wi + 4 n) * row_bytes as a scalar offset.
-  constexpr int NG = NLD / 4;  // loads per wavefront of a group
-  const int lsw = (lane >> 4) & 3;
-  int k_lane[2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) k_lane[u] = (lane >> 3) * k_rsb + 16 * ((lane & 7) ^ (lsw | (u << 2)));
-  const int vt_lane = (lane >> 3) * vt_rsb + 16 * ((lane & 7) ^ (lsw | ((wi & 1) << 2)));
-  auto dma_k_group = [&](int tile, uint8_t* dst) __attribute__((always_inline)) {
-    const int kb = tile * BN;
-    const auto rk = make_rsrc(kbase + (int64_t)kb * p.k_rs, (int64_t)min(Lk - kb, BN) * k_rsb);
-#pragma unroll
-    for (int n = 0; n < NG; ++n)
-      dma16s(rk, dst + 1024 * (wi + 4 * n), k_lane[n & 1], 8 * (wi + 4 * n) * k_rsb);
-  };
-  auto dma_vt_group = [&](int tile, uint8_t* dst) __attribute__((always_inline)) {
-    const int kb = tile * BN;
-    const auto rv = make_rsrc(vtbase + kb, vt_left - kb);
-#pragma unroll
-    for (int n = 0; n < NG; ++n) dma16s(rv, dst + 1024 * (wi + 4 * n), vt_lane, 8 * (wi + 4 * n) * vt_rsb);
-  };
-  // the same by all eight wavefronts (prologue)
-  auto dma_all = [&](int tile, uint8_t* kdst, uint8_t* vdst) __attribute__((always_inline)) {
-    const int kb = tile * BN;
-    const auto rk = make_rsrc(kbase + (int64_t)kb * p.k_rs, (int64_t)min(Lk - kb, BN) * k_rsb);
-    const auto rv = make_rsrc(vtbase + kb, vt_left - kb);
-#pragma unroll
-    for (int n = 0; n < NLD / kPPWaves; ++n) {
-      const int P = 64 * (wave + kPPWaves * n) + lane;
-      const int r = P >> 3;
-      dma16(rk, kdst + 1024 * (wave + kPPWaves * n), r * k_rsb + 16 * ((P & 7) ^ kswz(r)));
-      if (vdst != nullptr)
-        dma16(rv, vdst + 1024 * (wave + kPPWaves * n), r * vt_rsb + 16 * ((P & 7) ^ ((r >> 1) & 7)));
+  // ---- load cursors (as vt_pipeline)
+  const int vt_tile_bytes = (D - 1) * vt_rsb + BN;
+  auto fix = [&](LoadCursor& c, bool isk) __attribute__((always_inline)) {
+    while (c.t >= c.tiles && c.s < nseg) {
+      ++c.s;
+      c.t = 0;
+      if (c.s < nseg) {
+        const StepSeg g = geo.seg(c.s);
+        c.tiles = g.tiles;
+        c.keys = g.keys;
+        c.ptr = geo.base(g.src, isk);
+      }
     }
   };
+  auto start = [&](bool isk) __attribute__((always_inline)) {
+    const StepSeg g = geo.seg(0);
+    LoadCursor c{0, 0, g.tiles, g.keys, geo.base(g.src, isk)};
+    fix(c, isk);
+    return c;
+  };
+  auto step = [&](LoadCursor& c, bool isk) __attribute__((always_inline)) {
+    ++c.t;
+    c.ptr += isk ? BN * k_rsb : BN;
+    if (__builtin_expect(c.t >= c.tiles, 0)) fix(c, isk);
+  };
+  auto rsrc = [&](const LoadCursor& c, bool isk) __attribute__((always_inline)) {
+    const int n = c.s >= nseg ? 0 : isk ? min(c.keys - c.t * BN, BN) * k_rsb : vt_tile_bytes;
+    return make_rsrc32(c.ptr, n);
+  };
+  // LDS-DMA: load n of wavefront w (of nw) fills LDS chunks [64 (w + nw n), +64) of a tile;
+  // chunk P is row r = P / 8 at swizzled position P % 8.
+  auto k_voff = [&](int w, int nw, int n) __attribute__((always_inline)) {
+    const int P = 64 * (w + nw * n) + lane;
+    const int r = P >> 3;
+    return r * k_rsb + 16 * ((P & 7) ^ kswz(r));
+  };
+  auto v_voff = [&](int w, int nw, int n) __attribute__((always_inline)) {
+    const int P = 64 * (w + nw * n) + lane;
+    const int r = P >> 3;
+    return r * vt_rsb + 16 * ((P & 7) ^ ((r >> 1) & 7));
+  };
+
+  // prologue: K_0 .. K_{KS-2} and V^T_0 .. V^T_{VS-2}, loaded by all eight wavefronts
+  LoadCursor kc = start(true), vc = start(false);
+#pragma unroll
+  for (int i = 0; i < KS - 1; ++i) {
+    const auto r = rsrc(kc, true);
+#pragma unroll
+    for (int n = 0; n < NLD / kPPWaves; ++n)
+      dma16(r, kl[i] + 1024 * (wave + kPPWaves * n), k_voff(wave, kPPWaves, n));
+    step(kc, true);
+  }
+#pragma unroll
+  for (int i = 0; i < VS - 1; ++i) {
+    const auto r = rsrc(vc, false);
+#pragma unroll
+    for (int n = 0; n < NLD / kPPWaves; ++n)
+      dma16(r, vt[i] + 1024 * (wave + kPPWaves * n), v_voff(wave, kPPWaves, n));
+    step(vc, false);
+  }
+  // from here on group 0 loads K and group 1 V^T, four wavefronts per tile
+  const bool isk = grp == 0;
+  LoadCursor lc = isk ? kc : vc;
+  int ld_voff[NG];
+#pragma unroll
+  for (int n = 0; n < NG; ++n) ld_voff[n] = isk ? k_voff(wi, 4, n) : v_voff(wi, 4, n);
+  uint8_t* const ld_base = isk ? kl[0] : vt[0];
+  const int ld_slots = isk ? KS : VS;
+  int ld_slot = ld_slots - 1;
 
   // fragment addresses (bytes): K row sigma(0, lq), chunks 4t + 2h + e; V^T row lq, chunks
   // 4u + 2h + e; tiles mt and dt add compile-time offsets
@@ -1966,16 +1997,10 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_vt(AttnParams p) 
 #pragma unroll
     for (int e = 0; e < 2; ++e) v_off[u][e] = lq * BN + 16 * ((4 * u + 2 * lh + e) ^ ((lq >> 1) & 7));
 
-  const float qd = p.qd ? p.qd[kvh] : 1.f;
-  const float kd = p.kd ? p.kd[kvh] : 1.f;
-  const float vd = p.vd ? p.vd[kvh] : 1.f;
-  const float c_log2 = p.scale * qd * kd * kLog2e;
-  const float c_nat = p.scale * qd * kd;
-
   f32x16 o[NDT];
 #pragma unroll
   for (int i = 0; i < NDT; ++i) o[i] = f32x16{};
-  float m = -INFINITY;
+  float m2 = -INFINITY;  // running max, log2 units of the scaled scores
   float lsum = 0.f;
   f32x16 s[NMT];
   i32x8 pf[NPS], pl[NPS];
@@ -2010,39 +2035,87 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_vt(AttnParams p) 
         if constexpr (decltype(two_terms)::value) o[dt] = mma_fp8(a, pl[u], o[dt]);
       }
   };
-  auto mask = [&](int kb0) __attribute__((always_inline)) {
-    const int qq = r0 + lq + off;
+
+  // mask cursor (the tile in the MFMA phase) and the scale of its segment
+  MaskCursor mc{0, 0, geo.seg(0)};
+  bool seg_new = false;  // the tile in the MFMA phase starts a segment after the first
+  float v_ratio = 1.f;   // vd of the previous segment / vd of this one
+  auto mfix = [&]() __attribute__((always_inline)) {
+    const float vd_old = mc.g.vd;
+    while (mc.t >= mc.g.tiles && mc.s < nseg) {
+      ++mc.s;
+      mc.t = 0;
+      if (mc.s < nseg) mc.g = geo.seg(mc.s);
+    }
+    v_ratio = vd_old / mc.g.vd;
+  };
+  mfix();
+  v_ratio = 1.f;
+  const int qq = r0 + lq;
+  auto mask = [&]() __attribute__((always_inline)) {
+    const int kb0 = mc.t * BN;
+    const int lim = qq < mc.g.qmin ? 0 : min(mc.g.keys, qq + mc.g.off + 1) - kb0;
 #pragma unroll
     for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int kk = kb0 + 64 * (mt >> 1) + 16 * (mt & 1) + 32 * lh + i;
-        const bool dead = kk >= Lk || (p.causal && kk > qq);
-        s[mt][i] = dead ? -INFINITY : s[mt][i];
+        const int kk = 64 * (mt >> 1) + 16 * (mt & 1) + 32 * lh + i;
+        s[mt][i] = kk >= lim ? -INFINITY : s[mt][i];
       }
   };
+  // row max in log2 units; lazy rescale of O and the row sum (and O's change of v descale)
+  auto max_rescale = [&](float c) __attribute__((always_inline)) {
+    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx[i & 3] = fmaxf(mx[i & 3], s[mt][i]);
+    const float tmax = pair_max(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]))) * c;
+    const bool grow = tmax > m2 && (m2 == -INFINITY || tmax - m2 > kLazyLog2);
+    if (wave_any(grow) || seg_new) {
+      const float m_new = fmaxf(m2, tmax);
+      const float alpha = m2 == -INFINITY ? 0.f : fast_exp2(m2 - m_new);
+      m2 = m_new;
+      lsum *= alpha;
+      const float ao = alpha * v_ratio;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[dt] *= ao;
+    }
+  };
+  auto exp_tile = [&](float c) __attribute__((always_inline)) {
+    const float mc2 = m2 == -INFINITY ? 0.f : m2;
+    float rs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float e = fast_exp2(fmaf(s[mt][i], c, -mc2));
+        s[mt][i] = e;
+        rs[i & 3] += e;
+      }
+    lsum += (rs[0] + rs[1]) + (rs[2] + rs[3]);
+  };
 
-  if (n_tiles > 0) {
-    dma_all(0, kl[0], vt[0]);
-    dma_all(1, kl[1], nullptr);
-  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (grp == 1) __syncthreads();  // group 1 runs one phase behind group 0
 
+  int vr = VS - 1;  // V^T slot of the tile before the one in the MFMA phase
   // One tile j.  MFMA phase: PV of tile j - 1 (PREV = 1: one e4m3 term, 2: with the
   // residual term, 0: none), then S^T of tile j -- PV first, since it consumes P before QK
-  // defines the new scores, so the two never hold registers at the same time.  VALU phase:
-  // mask (MASKED), online softmax, P of tile j (with its residual when SPLIT).  Every
-  // variant is a separate instance, so no phase carries code or registers of another.
-  auto tile = [&](int j, auto prev, auto masked, auto split) __attribute__((always_inline)) {
+  // defines the new scores, so the two never hold registers at the same time -- then the
+  // cursor walk, mask, row max and rescale (they need only S_j and end the MFMA phase,
+  // the shorter of the two).  VALU phase: the loads, exponentials, P of tile j (with its
+  // residual when SPLIT).  Every variant is a separate instance, so no phase carries code
+  // or registers of another.
+  auto tile = [&](int j, auto prev, auto split) __attribute__((always_inline)) {
     constexpr int PREV = decltype(prev)::value;
     __builtin_amdgcn_s_setprio(1);
     if constexpr (PREV == 0) {
-      qk(kl[j % 3]);
+      qk(kl[j & (KS - 1)]);
     } else {
-      pv(vt[(j - 1) & 1], std::integral_constant<bool, PREV == 2>{});
-      qk(kl[j % 3]);
+      pv(vt[vr], std::integral_constant<bool, PREV == 2>{});
+      qk(kl[j & (KS - 1)]);
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kPPReadAhead, 0);
 #pragma unroll
       for (int i = 0; i < NDT * NPS; ++i) {
@@ -2054,61 +2127,83 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_vt(AttnParams p) 
         __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
         __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
       }
+      step(lc, isk);
+      ++mc.t;
+      seg_new = false;
+      if (__builtin_expect(mc.t >= mc.g.tiles, 0)) {
+        mfix();
+        seg_new = true;
+      }
     }
+    const auto r = rsrc(lc, isk);
+    const float c = c_q * mc.g.kd * kLog2e;
     __builtin_amdgcn_s_setprio(0);
-    // mask, row max and rescale need only S_j: they end the MFMA phase, which is the
-    // shorter of the two, instead of lengthening the softmax phase
-    if constexpr (decltype(masked)::value) mask(j * BN);
-    tile_max_rescale<NMT, NDT>(s, o, m, lsum, c_log2);
-    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's LDS-DMA from its previous VALU phase
-    __syncthreads();
-    if (grp == 0) dma_k_group(j + 2, kl[(j + 2) % 3]);
-    else dma_vt_group(j + 1, vt[(j + 1) & 1]);
-    tile_exp<NMT>(s, m, lsum, c_log2);
+    if (__builtin_expect(mc.t >= mc.g.first_mask, 0)) mask();
+    max_rescale(c);
+    // K_{j+1} / V^T_j, loaded two VALU phases ago, are read in the next phase
+    __builtin_amdgcn_s_waitcnt(kWaitOlder);
+    wg_barrier();
+    uint8_t* const dst = ld_base + ld_slot * TILE;
+#pragma unroll
+    for (int n = 0; n < NG; ++n) dma16(r, dst + 1024 * (wi + 4 * n), ld_voff[n]);
+    ld_slot = ld_slot + 1 == ld_slots ? 0 : ld_slot + 1;
+    exp_tile(c);
     pack_e4m3<NPS, NMT>(s, pf);
     if constexpr (decltype(split)::value) pack_e4m3_residual<NPS, NMT>(s, pf, pl);
-    __syncthreads();
+    vr = vr + 1 == VS ? 0 : vr + 1;
+#pragma unroll
+    for (int u = 0; u < NPS; ++u) pin(pf[u]);
+    if constexpr (decltype(split)::value) {
+#pragma unroll
+      for (int u = 0; u < NPS; ++u) pin(pl[u]);
+    }
+#pragma unroll
+    for (int i = 0; i < NDT; ++i) pin(o[i]);
+    pin(m2);
+    pin(lsum);
+    wg_barrier();  // the VALU phase reads no LDS; its loads are waited for a phase later
   };
-  // SP = 0: no residual terms (non-causal); 1: on the masked (diagonal) tiles of a causal
-  // launch; 2: on every tile (the first kPreciseRows rows of a causal launch).
-  auto run = [&](auto sp) __attribute__((always_inline)) {
-    constexpr int SP = decltype(sp)::value;
-    using SA = std::integral_constant<bool, SP == 2>;  // residual on mask-free tiles
-    using SB = std::integral_constant<bool, SP >= 1>;  // residual on masked tiles
-    using P0 = std::integral_constant<int, 0>;
-    using PA = std::integral_constant<int, SA::value ? 2 : 1>;
-    using PB = std::integral_constant<int, SB::value ? 2 : 1>;
-    using F = std::false_type;
-    using T = std::true_type;
+  using P0 = std::integral_constant<int, 0>;
+  using F = std::false_type;
+  using T = std::true_type;
+  if constexpr (SP == 1) {
+    // one segment: mask-free tiles with one e4m3 term, then masked tiles with two
+    const int n_free = mc.g.first_mask;
     int j = 0;
     if (n_free > 0) {
-      tile(0, P0{}, F{}, SA{});
-      for (j = 1; j < n_free; ++j) tile(j, PA{}, F{}, SA{});
+      tile(0, P0{}, F{});
+      for (j = 1; j < n_free; ++j) tile(j, std::integral_constant<int, 1>{}, F{});
     }
     if (j < n_tiles) {
-      if (j == 0) tile(0, P0{}, T{}, SB{});
-      else tile(j, PA{}, T{}, SB{});
-      for (++j; j < n_tiles; ++j) tile(j, PB{}, T{}, SB{});
+      if (j == 0) tile(0, P0{}, T{});
+      else tile(j, std::integral_constant<int, 1>{}, T{});
+      for (++j; j < n_tiles; ++j) tile(j, std::integral_constant<int, 2>{}, T{});
     }
     if (n_tiles > 0) {
       __builtin_amdgcn_s_setprio(1);
-      if (n_tiles > n_free) pv(vt[(n_tiles - 1) & 1], std::integral_constant<bool, SB::value>{});
-      else pv(vt[(n_tiles - 1) & 1], std::integral_constant<bool, SA::value>{});
+      if (n_tiles > n_free) pv(vt[vr], T{});
+      else pv(vt[vr], F{});
       __builtin_amdgcn_s_setprio(0);
     }
-  };
-  if (!p.causal) run(std::integral_constant<int, 0>{});
-  else if (r0 >= kPreciseRows) run(std::integral_constant<int, 1>{});
-  else run(std::integral_constant<int, 2>{});
+  } else {
+    using SPL = std::integral_constant<bool, SP == 2>;
+    using PN = std::integral_constant<int, SP == 2 ? 2 : 1>;
+    if (n_tiles > 0) tile(0, P0{}, SPL{});
+    for (int j = 1; j < n_tiles; ++j) tile(j, PN{}, SPL{});
+    if (n_tiles > 0) {
+      __builtin_amdgcn_s_setprio(1);
+      pv(vt[vr], SPL{});
+      __builtin_amdgcn_s_setprio(0);
+    }
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (grp == 0) __syncthreads();  // both groups pass the same number of barriers
 
   const float ltot = pair_sum(lsum);
-  const float inv = ltot > 0.f ? vd / ltot : 0.f;
-  const int row = r0 + lq;
-  if (row < Lq) {
-    __bf16* og = reinterpret_cast<__bf16*>(p.out) + (int64_t)(qs + row) * p.o_rs + (int64_t)head * p.o_hs;
+  const float inv = ltot > 0.f ? mc.g.vd / ltot : 0.f;
+  if (r0 + lq < Lq) {
+    __bf16* og = out + (int64_t)lq * o_rs;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -2117,11 +2212,108 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_vt(AttnParams p) 
                     (__bf16)(o[dt][4 * g + 2] * inv), (__bf16)(o[dt][4 * g + 3] * inv)};
         *reinterpret_cast<bf16x4*>(og + 32 * dt + 8 * g + 4 * lh) = w;
       }
-    if (lh == 0) {
-      const float lse = ltot > 0.f ? m * c_nat + logf(ltot) : -INFINITY;
-      p.lse[(int64_t)(qs + row) * p.lse_rs + head] = lse;
-    }
+    if (lh == 0) lse[(int64_t)lq * lse_rs] = ltot > 0.f ? m2 * kLn2 + logf(ltot) : -INFINITY;
   }
+}
+
+template <int HP>
+__global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_vt(AttnParams p) {
+  constexpr int D = 128;
+  constexpr int BN = kE8BN;
+  constexpr int RB = kPPWaves / HP;  // 32-row blocks per workgroup
+  int hg, seq, rt;
+  decode_block(p, hg, seq, rt);
+  int qs, Lq, ks, Lk;
+  seq_range(p.cu_q, seq, p.total_q, p.q_sel, qs, Lq);
+  seq_range(p.cu_k, seq, p.total_k, p.k_sel, ks, Lk);
+  const int row_tile0 = rt * RB * 32;
+  if (row_tile0 >= Lq) return;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int groups_per_kv = p.group / HP;
+  const int kvh = hg / groups_per_kv;
+  const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
+  const int r0 = row_tile0 + (wave / HP) * 32;
+  const int off = Lk - Lq;
+
+  OneSegment geo;
+  geo.g.src = 0;
+  geo.g.keys = Lk;
+  geo.g.tiles = (Lk + BN - 1) / BN;
+  if (p.causal) {
+    const int kmax = min(row_tile0 + RB * 32, Lq) - 1 + off;
+    geo.g.tiles = kmax < 0 ? 0 : min(geo.g.tiles, kmax / BN + 1);
+  }
+  geo.g.first_mask = mask_free_tiles<BN>(geo.g.tiles, Lk, p.causal, row_tile0, off);
+  geo.g.off = p.causal ? off : kNoCausal;
+  geo.g.qmin = 0;
+  geo.g.kd = p.kd ? p.kd[kvh] : 1.f;
+  geo.g.vd = p.vd ? p.vd[kvh] : 1.f;
+  const int64_t vt_pos = p.cu_k ? vt_seq_start(p.cu_k, seq, p.k_sel) : 0;
+  geo.kb = reinterpret_cast<const char*>(p.k) + (int64_t)ks * p.k_rs + (int64_t)kvh * p.k_hs;
+  geo.vb = reinterpret_cast<const char*>(p.vt) + (int64_t)kvh * D * p.vt_ds + vt_pos;
+
+  const uint8_t* q = reinterpret_cast<const uint8_t*>(p.q) + (int64_t)(qs + r0) * p.q_rs + (int64_t)head * p.q_hs;
+  __bf16* out = reinterpret_cast<__bf16*>(p.out) + (int64_t)(qs + r0) * p.o_rs + (int64_t)head * p.o_hs;
+  float* lse = p.lse + (int64_t)(qs + r0) * p.lse_rs + head;
+  const float c_q = p.scale * (p.qd ? p.qd[kvh] : 1.f);
+  const int k_rsb = (int)p.k_rs, vt_rsb = (int)p.vt_ds;
+  const int qv = min(Lq - r0, 32);
+  __shared__ E8Lds lds;
+  if (!p.causal)
+    e8_pipeline<HP, 0>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, Lq, k_rsb, vt_rsb, c_q);
+  else if (r0 >= kPreciseRows)
+    e8_pipeline<HP, 1>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, Lq, k_rsb, vt_rsb, c_q);
+  else
+    e8_pipeline<HP, 2>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, Lq, k_rsb, vt_rsb, c_q);
+}
+
+// The whole ring sweep in e4m3 (head dim 128): RingSegments in tiles of kE8BN keys, each
+// source with its own k / v descales.  Row tiles whose keys are all their own (rank 0, front
+// half) take the precision rules of a causal attention call; every other row tile sees at
+// least half a shard of other sources' keys and uses one e4m3 term for P.
+template <int HP>
+__global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_sweep(SweepParams p) {
+  constexpr int D = 128;
+  constexpr int RB = kPPWaves / HP;
+  int hg, seq, rt;
+  decode_block(p, hg, seq, rt);
+  int qs, L;
+  seq_range(p.cu, seq, p.total, FA4CP_SEL_ALL, qs, L);
+  const int row_tile0 = rt * RB * 32;
+  if (row_tile0 >= L) return;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int groups_per_kv = p.group / HP;
+  const int kvh = hg / groups_per_kv;
+  const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
+  const int r0 = row_tile0 + (wave / HP) * 32;
+
+  RingSegments<kE8BN> geo;
+  geo.p = &p;
+  geo.L = L;
+  geo.row_tile0 = row_tile0;
+  geo.rows = RB * 32;
+  geo.kvh = kvh;
+  const int64_t vt_pos = p.cu ? vt_seq_start(p.cu, seq, FA4CP_SEL_ALL) : 0;
+  geo.k_off = (int64_t)qs * p.k_rs + (int64_t)kvh * p.k_hs;
+  geo.v_off = (int64_t)kvh * D * p.vt_ds + vt_pos;
+
+  const uint8_t* q = reinterpret_cast<const uint8_t*>(p.q) + (int64_t)(qs + r0) * p.q_rs + (int64_t)head * p.q_hs;
+  __bf16* out = reinterpret_cast<__bf16*>(p.out) + (int64_t)(qs + r0) * p.o_rs + (int64_t)head * p.o_hs;
+  float* lse = p.lse + (int64_t)(qs + r0) * p.lse_rs + head;
+  const float c_q = p.scale * (p.qd ? p.qd[kvh] : 1.f);
+  const int k_rsb = (int)p.k_rs, vt_rsb = (int)p.vt_ds;
+  const int qv = min(L - r0, 32);
+  int with_keys = 0;
+  for (int s = 1; s < p.S; ++s) with_keys += geo.seg(s).tiles > 0;
+  __shared__ E8Lds lds;
+  if (with_keys > 0)
+    e8_pipeline<HP, 0>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, L, k_rsb, vt_rsb, c_q);
+  else if (r0 >= kPreciseRows)
+    e8_pipeline<HP, 1>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, L, k_rsb, vt_rsb, c_q);
+  else
+    e8_pipeline<HP, 2>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, L, k_rsb, vt_rsb, c_q);
 }
 
 //--------------------------------------------------------------------------------------
@@ -2321,19 +2513,24 @@ extern "C" int fa4cp_ring_sweep_fwd(const fa4cp_sweep_args* a, void* stream) {
   const int group = a->h_q / a->h_kv;
   const int hp = heads_per_wg(group);
   const int d = a->d;
-  if (a->dtype != FA4CP_BF16 && a->dtype != FA4CP_FP16)
-    return set_error(FA4CP_EUNSUPPORTED, "ring_sweep_fwd: dtype %d (BF16 / FP16 only)", a->dtype);
-  if (d != 64 && d != 128) return set_error(FA4CP_EUNSUPPORTED, "ring_sweep_fwd: head dim %d (64 / 128 only)", d);
+  const bool fp8 = a->dtype == FA4CP_E4M3;
+  if (a->dtype != FA4CP_BF16 && a->dtype != FA4CP_FP16 && !fp8)
+    return set_error(FA4CP_EUNSUPPORTED, "ring_sweep_fwd: dtype %d (BF16 / FP16 / E4M3 only)", a->dtype);
+  if (fp8 ? d != 128 : (d != 64 && d != 128))
+    return set_error(FA4CP_EUNSUPPORTED, "ring_sweep_fwd: head dim %d (64 / 128 for BF16 / FP16, 128 for E4M3)", d);
   {
-    auto ok = [](const void* ptr, int64_t rs, int64_t hs, int64_t al) {
-      return rs > 0 && hs > 0 && rs % al == 0 && hs % al == 0 && ((uintptr_t)ptr % (uintptr_t)(al * 2)) == 0;
+    // element sizes: q / k 1 (e4m3) or 2; out 2 (bf16 for e4m3)
+    const int esz = fp8 ? 1 : 2;
+    auto ok = [](const void* ptr, int64_t rs, int64_t hs, int64_t al, int es) {
+      return rs > 0 && hs > 0 && rs % al == 0 && hs % al == 0 && ((uintptr_t)ptr % (uintptr_t)(al * es)) == 0;
     };
-    bool good = ok(a->q, a->q_row_stride, a->q_head_stride, 8) &&
-                ok(a->out, a->o_row_stride, a->o_head_stride, 4) && a->lse_row_stride >= a->h_q;
+    const int64_t qa = 16 / esz;  // 16-byte rows
+    bool good = ok(a->q, a->q_row_stride, a->q_head_stride, qa, esz) &&
+                ok(a->out, a->o_row_stride, a->o_head_stride, 4, 2) && a->lse_row_stride >= a->h_q;
     for (int i = 0; i < a->cp_size; ++i)
-      good = good && ok(a->k[i], a->k_row_stride, a->k_head_stride, 8) && ((uintptr_t)a->v_t[i] % 16) == 0;
+      good = good && ok(a->k[i], a->k_row_stride, a->k_head_stride, qa, esz) && ((uintptr_t)a->v_t[i] % 16) == 0;
     if (!good) return set_error(FA4CP_EINVAL, "ring_sweep_fwd: misaligned pointer or stride");
-    if (!tile_offsets_fit(std::max(a->q_row_stride, a->k_row_stride), 2, d, a->vt_d_stride))
+    if (!tile_offsets_fit(std::max(a->q_row_stride, a->k_row_stride), esz, d, a->vt_d_stride))
       return set_error(FA4CP_EINVAL, "ring_sweep_fwd: row or V^T stride too large for 32-bit tile offsets");
   }
   SweepParams p;
@@ -2349,6 +2546,9 @@ extern "C" int fa4cp_ring_sweep_fwd(const fa4cp_sweep_args* a, void* stream) {
   p.h_kv = a->h_kv; p.group = group;
   p.rank = a->cp_rank; p.S = a->cp_size;
   p.scale = a->softmax_scale;
+  p.qd = fp8 ? a->q_descale : nullptr;
+  p.kd = fp8 ? a->k_descale : nullptr;
+  p.vd = fp8 ? a->v_descale : nullptr;
   const int rows = 32 * kPPWaves / hp;
   p.n_rt = (max_len + rows - 1) / rows;
   p.n_hg = a->h_kv * (group / hp);
@@ -2363,7 +2563,11 @@ extern "C" int fa4cp_ring_sweep_fwd(const fa4cp_sweep_args* a, void* stream) {
     else if (hp == 2) fn = attn_fwd_16bit_sweep<TT, DD, 2>;         \
     else fn = attn_fwd_16bit_sweep<TT, DD, 1>;                      \
   }
-  if (a->dtype == FA4CP_BF16) {
+  if (fp8) {
+    if (hp == 4) fn = attn_fwd_e4m3_sweep<4>;
+    else if (hp == 2) fn = attn_fwd_e4m3_sweep<2>;
+    else fn = attn_fwd_e4m3_sweep<1>;
+  } else if (a->dtype == FA4CP_BF16) {
     FA4CP_PICK(__bf16, 64)
     FA4CP_PICK(__bf16, 128)
   } else {

@@ -34,8 +34,8 @@ import torch
 
 from . import _lib
 from .config import RingConfig
-from .fa4_backend import (SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, fa4_attn, out_dtype_for, transpose_v,
-                          uses_vt)
+from .fa4_backend import (SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, _norm_descale, fa4_attn, out_dtype_for,
+                          transpose_v, uses_vt)
 from .merge import merge_state_in_place, merge_states
 from .zigzag import zigzag_shard, zigzag_shard_varlen
 
@@ -97,9 +97,10 @@ def ring_flash_attn(
 
     ``fused`` (default: whenever supported) runs the whole sweep as one kernel over every
     source's K / V^T (``ring_sweep``): no per-step partials, no merges.  It needs
-    cp_size > 1 with a LocalKVRing, bf16 / fp16, head dim 64 or 128 and no descales;
-    ``fused=False`` runs the per-step path of the reference (attention + LSE merge per
-    step), which covers every case.
+    cp_size in [2, 16] with a LocalKVRing and either bf16 / fp16 with head dim 64 or 128 and
+    no descales, or e4m3 with head dim 128 (any descales); ``fused=False`` runs the
+    per-step path of the reference (attention + LSE merge per step), which covers every
+    case.
 
     One sequence per rank: leave ``cu_seqlens=None``.  Packed sequences: pass the LOCAL
     ``cu_seqlens`` (each entry a zig-zag ``2*h_j`` shard length) on the device and
@@ -120,15 +121,19 @@ def ring_flash_attn(
                 "KV rotation between GPUs is not part of this single-GPU build")
         assert group.cp_size == S, f"LocalKVRing holds {group.cp_size} shards, cp_size is {S}"
 
-    can_fuse = (S > 1 and descales is None and local_q.dtype in (torch.bfloat16, torch.float16)
-                and local_q.shape[2] in (64, 128) and S <= _lib.MAX_CP)
+    d = local_q.shape[2]
+    e4m3 = local_q.dtype == torch.float8_e4m3fn
+    can_fuse = 1 < S <= _lib.MAX_CP and (
+        (descales is None and local_q.dtype in (torch.bfloat16, torch.float16) and d in (64, 128))
+        or (e4m3 and d == 128))
     if fused and not can_fuse:
-        raise AssertionError("fused ring sweep needs cp_size in [2, 16], bf16/fp16, head dim 64/128, "
-                             "no descales")
+        raise AssertionError("fused ring sweep needs cp_size in [2, 16] and bf16/fp16 with head dim "
+                             "64/128 and no descales, or e4m3 with head dim 128")
     if fused is None:
         fused = can_fuse
     if fused:
-        return ring_sweep(local_q, local_k, local_v, cfg, group, cu_seqlens, max_seqlen)
+        return ring_sweep(local_q, local_k, local_v, cfg, group, cu_seqlens, max_seqlen,
+                          descales=descales)
 
     qd = descales.q if descales else None
 
@@ -193,12 +198,14 @@ def ring_flash_attn(
 def ring_sweep(local_q: torch.Tensor, local_k: torch.Tensor, local_v: torch.Tensor, cfg: RingConfig,
                group: "LocalKVRing", cu_seqlens: Optional[torch.Tensor] = None,
                max_seqlen: Optional[int] = None, out: Optional[torch.Tensor] = None,
-               lse: Optional[torch.Tensor] = None) -> torch.Tensor:
+               lse: Optional[torch.Tensor] = None, descales: Optional[Descales] = None) -> torch.Tensor:
     """The whole sweep of ring_flash_attn (fa4_ring/ring_attention.py:61-174) in one
     fa4cp_ring_sweep_fwd launch: every source's V is transposed (fa4cp_transpose_v), then one
     kernel carries each row tile's online softmax through the causal local keys, the front
     halves of the earlier sources and, for the back-half rows, all keys of the later ones.
-    Returns out [T, H, D] (``lse`` [T, H], if given, receives the natural-log LSE)."""
+    e4m3 inputs take ``descales`` (the k / v descales per source rank, as ring_flash_attn)
+    and give a bf16 out.  Returns out [T, H, D] (``lse`` [T, H], if given, receives the
+    natural-log LSE)."""
     lib = _lib.load()
     S, rank = cfg.cp_size, cfg.cp_rank
     total, h_q, d = local_q.shape
@@ -213,8 +220,16 @@ def ring_sweep(local_q: torch.Tensor, local_k: torch.Tensor, local_v: torch.Tens
         assert k.stride() == ks[0].stride(), "all K shards must share strides"
     vts = [transpose_v(v, cu_seqlens_k=cu_seqlens, max_seqlen_k=max_seqlen)[0] for v in vs]
     stride = int(lib.fa4cp_vt_min_d_stride(total, nseq))
+    e4m3 = local_q.dtype == torch.float8_e4m3fn
     if out is None:
-        out = torch.empty_like(local_q)
+        out = torch.empty(local_q.shape, dtype=torch.bfloat16 if e4m3 else local_q.dtype, device=dev)
+    qd = kd = vd = None
+    if e4m3 and descales is not None:
+        qd = _norm_descale(descales.q, h_kv, dev)
+        if descales.k is not None:
+            kd = torch.stack([_norm_descale(descales.k[i], h_kv, dev) for i in range(S)]).contiguous()
+        if descales.v is not None:
+            vd = torch.stack([_norm_descale(descales.v[i], h_kv, dev) for i in range(S)]).contiguous()
     if lse is None:
         lse = torch.empty((total, h_q), dtype=torch.float32, device=dev)
     a = _lib.SweepArgs()
@@ -235,6 +250,7 @@ def ring_sweep(local_q: torch.Tensor, local_k: torch.Tensor, local_v: torch.Tens
     a.dtype = _lib.dtype_code(local_q.dtype)
     a.cp_rank, a.cp_size = rank, S
     a.softmax_scale = float(cfg.softmax_scale if cfg.softmax_scale is not None else 1.0 / math.sqrt(d))
+    a.q_descale, a.k_descale, a.v_descale = _lib.ptr(qd), _lib.ptr(kd), _lib.ptr(vd)
     launch_sweep(a, dev)
     return out
 

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define FA4CP_ABI_VERSION 2
+#define FA4CP_ABI_VERSION 3
 
 /* status codes */
 #define FA4CP_OK 0
@@ -144,7 +144,10 @@ int64_t fa4cp_vt_min_d_stride(int32_t total_k, int32_t nseq);
  * partial results and no merges: every workgroup carries its online softmax across the
  * sources.  k[i] is source rank i's local K shard and v_t[i] its V^T (fa4cp_transpose_v with
  * k_sel = ALL over the same cu); all shards share strides and the local sequence layout cu.
- * BF16 / FP16, d = 64 or 128, cp_size <= FA4CP_MAX_CP.
+ * BF16 / FP16 with d = 64 or 128, or E4M3 with d = 128 (bf16 out; q_descale [h_kv] and the
+ * per-source k_descale / v_descale [cp_size][h_kv], any of them NULL for 1, as the
+ * reference's Descales: ring_attention.py:43-52, fa4_backend.py:45-55); cp_size <=
+ * FA4CP_MAX_CP.
  */
 #define FA4CP_MAX_CP 16
 typedef struct fa4cp_sweep_args {
@@ -160,6 +163,9 @@ typedef struct fa4cp_sweep_args {
   int32_t h_q, h_kv, d, dtype;
   int32_t cp_rank, cp_size;
   float softmax_scale;
+  const float* q_descale; /* E4M3: [h_kv] or NULL */
+  const float* k_descale; /* E4M3: [cp_size][h_kv] or NULL */
+  const float* v_descale; /* E4M3: [cp_size][h_kv] or NULL */
 } fa4cp_sweep_args;
 
 int fa4cp_ring_sweep_fwd(const fa4cp_sweep_args* args, void* stream);

@@ -126,10 +126,12 @@ def _fp8_ring_inputs(q, k, v, cp, rank, full_cu=None):
     return (q8, k8, v8, sq, sk, sv), deq
 
 
-@pytest.mark.parametrize("mode", ["incremental", "batched"])
+@pytest.mark.parametrize("mode", PATHS)
 @pytest.mark.parametrize("n,h,hkv,d,cp", [(2048, 8, 2, 128, 8), (1024, 16, 2, 256, 4),
                                           (1024, 8, 8, 128, 2)])
 def test_ring_fp8_all_ranks(n, h, hkv, d, cp, mode):
+    if mode == "fused" and d != 128:
+        pytest.skip("the fused e4m3 sweep is head dim 128 only")
     say(f"ring e4m3 n={n} h={h}/{hkv} d={d} cp={cp} mode={mode}")
     q, k, v = O.random_qkv(n, h, hkv, d, seed=4)
     scale = scale_for(d)
@@ -139,10 +141,11 @@ def test_ring_fp8_all_ranks(n, h, hkv, d, cp, mode):
         desc = Descales(q=torch.tensor(sq, device=DEV),
                         k=[torch.tensor(s, device=DEV) for s in sk],
                         v=[torch.tensor([s] * hkv, device=DEV) for s in sv])
-        cfg = RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode)
-        out = ring_flash_attn(q8.to(DEV), ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc)
+        cfg, fused = _cfg_path(mode, cp, rank)
+        out = ring_flash_attn(q8.to(DEV), ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc,
+                              fused=fused)
         assert out.dtype == torch.bfloat16
-        ref, _ = O.ring_rank(dq, dk, dv, rank, cp, scale, merge_mode=mode)
+        ref, _ = O.ring_rank(dq, dk, dv, rank, cp, scale, merge_mode=cfg.merge_mode)
         assert max_err(out, ref) <= TOL_FP8_OUT, f"rank {rank}"
 
 
@@ -215,8 +218,9 @@ def _fp8_full_size(n, cp, hq, hkv, d, rank, modes, seed):
                     v=[torch.tensor(s, device=DEV) for s in sv])
     outs = {}
     for mode in modes:
-        cfg = RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode)
-        outs[mode] = ring_flash_attn(q8, ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc)
+        cfg, fused = _cfg_path(mode, cp, rank)
+        outs[mode] = ring_flash_attn(q8, ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc,
+                                     fused=fused)
     # dense reference on the dequantised tensors
     kf = O.zigzag_unshard([x.float().cpu() * s for x, s in zip(k8, sk)], cp)
     vf = O.zigzag_unshard([x.float().cpu() * s for x, s in zip(v8, sv)], cp)
@@ -229,7 +233,7 @@ def _fp8_full_size(n, cp, hq, hkv, d, rank, modes, seed):
 @pytest.mark.parametrize("rank", [0, 3, 7])
 def test_ring_c3_fp8_full_size(rank):
     say(f"ring C3 e4m3 n=131072 rank={rank}")
-    _fp8_full_size(131072, 8, 32, 8, 128, rank, ("incremental",), seed=1)
+    _fp8_full_size(131072, 8, 32, 8, 128, rank, ("fused", "incremental"), seed=1)
 
 
 def test_ring_c5_fp8_d256_full_size():
@@ -257,10 +261,10 @@ def test_ring_c4_varlen_full_size(rank):
     rng = np.random.default_rng(rank)
     rows = sorted(set(rng.integers(0, lq.shape[0], 40).tolist() + [0, lq.shape[0] - 1]))
     heads = rng.integers(0, hq, len(rows)).tolist()
-    for mode in ("incremental", "batched"):
-        cfg = RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode)
+    for mode in PATHS:
+        cfg, fused = _cfg_path(mode, cp, rank)
         out = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring,
-                              cu_seqlens=local_cu, max_seqlen=max_local)
+                              cu_seqlens=local_cu, max_seqlen=max_local, fused=fused)
         got = out[rows, heads].float().cpu()
         exp = []
         for i, hh in zip(rows, heads):
