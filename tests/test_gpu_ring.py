@@ -149,6 +149,31 @@ def test_ring_fp8_all_ranks(n, h, hkv, d, cp, mode):
         assert max_err(out, ref) <= TOL_FP8_OUT, f"rank {rank}"
 
 
+@pytest.mark.parametrize("mode", PATHS)
+def test_ring_fp8_varlen_all_ranks(mode):
+    lens = [608, 1216, 1072, 608, 232, 1928, 344, 200]
+    cp, h, hkv, d = 4, 8, 2, 128
+    say(f"ring e4m3 varlen lens={lens} cp={cp} path={mode}")
+    full_cu = [0]
+    for n in lens:
+        full_cu.append(full_cu[-1] + n)
+    q, k, v = O.random_qkv(full_cu[-1], h, hkv, d, seed=6)
+    scale = scale_for(d)
+    for rank in range(cp):
+        (q8, k8, v8, sq, sk, sv), (dq, dk, dv) = _fp8_ring_inputs(q, k, v, cp, rank, full_cu)
+        ring = LocalKVRing([x.to(DEV) for x in k8], [x.to(DEV) for x in v8])
+        desc = Descales(q=torch.tensor(sq, device=DEV), k=[torch.tensor(s, device=DEV) for s in sk],
+                        v=[torch.tensor([s] * hkv, device=DEV) for s in sv])
+        local_cu = torch.tensor(O.local_cu_from_full(full_cu, cp), dtype=torch.int32)
+        max_local = int((local_cu[1:] - local_cu[:-1]).max())
+        cfg, fused = _cfg_path(mode, cp, rank)
+        out = ring_flash_attn(q8.to(DEV), ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc,
+                              cu_seqlens=local_cu.to(DEV), max_seqlen=max_local, fused=fused)
+        assert out.dtype == torch.bfloat16
+        ref, _ = O.ring_rank(dq, dk, dv, rank, cp, scale, cu=local_cu.tolist(), merge_mode=cfg.merge_mode)
+        assert max_err(out, ref) <= TOL_FP8_OUT, f"rank {rank}"
+
+
 # ----------------------------------------------------------------- benchmark sizes
 
 def _sample_local_rows(t, n_random, seed):
