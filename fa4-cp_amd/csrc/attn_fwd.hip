@@ -156,7 +156,8 @@ __device__ __forceinline__ void softmax_tile(f32x16 (&s)[NMT], f32x16 (&o)[NDT],
 #pragma unroll
     for (int i = 0; i < 16; ++i) mx[i & 3] = fmaxf(mx[i & 3], s[mt][i]);
   const float tmax = pair_max(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])));
-  const bool grow = tmax > m && (m == -INFINITY || (tmax - m) * c_log2 > kLazyLog2);
+  // (an empty running max gives +inf here; an empty tile against one, -inf - -inf, never grows)
+  const bool grow = (tmax - m) * c_log2 > kLazyLog2;
   if (wave_any(grow)) {
     const float m_new = fmaxf(m, tmax);
     const float alpha = fast_exp2(m == -INFINITY ? -INFINITY : (m - m_new) * c_log2);
@@ -192,7 +193,8 @@ __device__ __forceinline__ void tile_max_rescale(const f32x16 (&s)[NMT], f32x16 
 #pragma unroll
     for (int i = 0; i < 16; ++i) mx[i & 3] = fmaxf(mx[i & 3], s[mt][i]);
   const float tmax = pair_max(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])));
-  const bool grow = tmax > m && (m == -INFINITY || (tmax - m) * c_log2 > kLazyLog2);
+  // (an empty running max gives +inf here; an empty tile against one, -inf - -inf, never grows)
+  const bool grow = (tmax - m) * c_log2 > kLazyLog2;
   if (wave_any(grow)) {
     const float m_new = fmaxf(m, tmax);
     const float alpha = fast_exp2(m == -INFINITY ? -INFINITY : (m - m_new) * c_log2);
@@ -2071,7 +2073,7 @@ __device__ __forceinline__ void e8_pipeline(E8Lds& lds, const Geo& geo, const ui
 #pragma unroll
       for (int i = 0; i < 16; ++i) mx[i & 3] = fmaxf(mx[i & 3], s[mt][i]);
     const float tmax = pair_max(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]))) * c;
-    const bool grow = tmax > m2 && (m2 == -INFINITY || tmax - m2 > kLazyLog2);
+    const bool grow = tmax - m2 > kLazyLog2;  // as tile_max_rescale
     if (wave_any(grow) || seg_new) {
       const float m_new = fmaxf(m2, tmax);
       const float alpha = m2 == -INFINITY ? 0.f : fast_exp2(m2 - m_new);
