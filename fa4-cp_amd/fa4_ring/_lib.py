@@ -92,6 +92,24 @@ class TransposeArgs(ctypes.Structure):
     ]
 
 
+class QuantArgs(ctypes.Structure):
+    """Mirror of fa4cp_quant_args."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("rows", ctypes.c_int64),
+        ("h", ctypes.c_int32),
+        ("d", ctypes.c_int32),
+        ("row_stride", ctypes.c_int64),
+        ("head_stride", ctypes.c_int64),
+        ("dtype", ctypes.c_int32),
+        ("heads_per_scale", ctypes.c_int32),
+        ("amax", ctypes.c_void_p),
+        ("descale", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+    ]
+
+
 MAX_CP = 16  # FA4CP_MAX_CP
 
 
@@ -156,6 +174,7 @@ SIGNATURES = {
     "fa4cp_transpose_v": (ctypes.c_int, [ctypes.POINTER(TransposeArgs), ctypes.c_void_p]),
     "fa4cp_vt_min_d_stride": (ctypes.c_int64, [ctypes.c_int32, ctypes.c_int32]),
     "fa4cp_ring_sweep_fwd": (ctypes.c_int, [ctypes.POINTER(SweepArgs), ctypes.c_void_p]),
+    "fa4cp_quantize_e4m3": (ctypes.c_int, [ctypes.POINTER(QuantArgs), ctypes.c_void_p]),
     "fa4cp_last_error": (ctypes.c_char_p, []),
     "fa4cp_abi_version": (ctypes.c_int, []),
 }

@@ -22,6 +22,8 @@
  *                                  load (FA4 reads V as given; see fa4cp_attn_args.v_t)
  *   fa4cp_ring_sweep_fwd        <- fa4_ring/ring_attention.py:61-174 (ring_flash_attn's step loop
  *                                  and its merges, fused; every source's K/V on this GPU)
+ *   fa4cp_quantize_e4m3         <- the caller-side FP8 step before it (README.md:63-70: e4m3
+ *                                  shards plus their descales, Descales ring_attention.py:43-52)
  */
 #ifndef FA4CP_H_
 #define FA4CP_H_
@@ -192,6 +194,31 @@ int fa4cp_merge_state_inplace(void* v, float* s, const void* v_other, const floa
  */
 int fa4cp_merge_states(const void* v, const float* s, void* v_out, float* s_out, int64_t rows,
                        int32_t num_states, int32_t h, int32_t d, int32_t dtype, void* stream);
+
+/*
+ * FP8 producer: OCP e4m3 quantisation of x [rows, h, d] (BF16, FP16 or FP32; any row and head
+ * stride, unit stride in d, 16-byte aligned) with scales from its absolute maximum:
+ *   heads_per_scale = 0:  one scale;  g > 0: one scale per g consecutive heads (h / g scales;
+ *                         g = 1 per head, g = h_q / h_kv gives the (1, H_kv) layout of FA4's
+ *                         q_descale);
+ *   scale = amax / 448 (1 where amax == 0);  y = e4m3(clamp(x / scale, -448, 448)),
+ * x / scale the correctly rounded fp32 quotient, the conversion round-to-nearest-even.
+ * descale[i] receives scale i (the dequantisation multiplier the sweep takes); amax is a
+ * caller-owned workspace of as many float words, overwritten.  y is [rows, h, d] contiguous.
+ */
+typedef struct fa4cp_quant_args {
+  const void* x;
+  int64_t rows;
+  int32_t h, d;
+  int64_t row_stride, head_stride; /* elements */
+  int32_t dtype;
+  int32_t heads_per_scale;
+  float* amax;    /* [nscale] workspace */
+  float* descale; /* [nscale] */
+  void* y;        /* [rows, h, d] e4m3 */
+} fa4cp_quant_args;
+
+int fa4cp_quantize_e4m3(const fa4cp_quant_args* args, void* stream);
 
 /*
  * Zig-zag shard for one rank: sequence j of the full packed tensor (rows

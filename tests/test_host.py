@@ -55,7 +55,8 @@ def test_error_path_reports_message_without_gpu():
 
 @pytest.mark.parametrize("struct,cname", [(_lib.AttnArgs, "fa4cp_attn_args"),
                                            (_lib.TransposeArgs, "fa4cp_transpose_args"),
-                                           (_lib.SweepArgs, "fa4cp_sweep_args")])
+                                           (_lib.SweepArgs, "fa4cp_sweep_args"),
+                                           (_lib.QuantArgs, "fa4cp_quant_args")])
 def test_args_layout_matches_c_header(struct, cname):
     fields = [f for f, _ in struct._fields_]
     prog = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",
