@@ -255,12 +255,24 @@ struct MfmaOps<_Float16> {
 // Decodes the workgroup id into (head group, sequence, row tile).  Row tiles are handed
 // out longest-first (the causal diagonal makes late row tiles the most expensive), and
 // head groups are laid out so that each XCD works on few kv heads (shared L2).
+//
+// With fewer head groups than XCDs, each head group spans k = 8 / n_hg XCDs; a contiguous
+// split would hand one XCD the heavy back-half row tiles and another the light front half,
+// so the k XCDs take every k-th row tile instead (still longest first on each).
 template <typename Params>
 __device__ __forceinline__ void decode_block(const Params& p, int& hg, int& seq, int& rt) {
-  const int b = xcd_remap((int)blockIdx.x, p.n_blocks);
   const int per_hg = p.nseq * p.n_rt;
-  hg = b / per_hg;
-  const int r = b - hg * per_hg;
+  const int k = p.n_hg < 8 ? 8 / p.n_hg : 1;
+  int r;
+  if (k > 1 && p.n_hg * k == 8 && p.n_blocks % 8 == 0 && per_hg % k == 0) {
+    const int x = (int)blockIdx.x & 7;  // the XCD the hardware sends this workgroup to
+    hg = x / k;
+    r = x % k + k * (int)(blockIdx.x >> 3);
+  } else {
+    const int b = xcd_remap((int)blockIdx.x, p.n_blocks);
+    hg = b / per_hg;
+    r = b - hg * per_hg;
+  }
   seq = r / p.n_rt;
   rt = p.n_rt - 1 - (r - seq * p.n_rt);
 }
@@ -1855,42 +1867,83 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_pp(AttnParams p) 
 // apart within each row parity.
 __device__ __forceinline__ int kswz(int r) { return ((r >> 1) & 3) | (((r >> 5) & 1) << 2); }
 
-// LDS of e8_pipeline: K tiles in four slots, V^T tiles in three, and every wavefront's Q^T
-// fragments (16 bytes per lane per half k-step), kept in LDS instead of registers: they are
-// read once per tile, and the registers hold the scores instead.
+// Tile layouts of e8_pipeline, one per (head dim, keys per tile).  In both, A-operand row
+// rho of S^T tile mt is fed K row krow(mt, rho), so that accumulator register i of lane half
+// h holds tile-relative key key(mt, i, h) and a lane's 32 P^T bytes of PV k-step u are the
+// consecutive keys 64 u + 32 h + 0..31, the bytes of one V^T row; kpos / vpos are the LDS
+// chunk slots of chunk c of a K row r / V^T row d (XOR swizzles, their own inverses), which
+// give the 16 lanes of every fragment read 16 distinct 16-byte slots per 256 bytes.
+template <int D, int BN>
+struct E8Layout;
+// D = 128, 128-key tiles: 128-byte K and V^T rows, four S^T tiles.
+template <>
+struct E8Layout<128, 128> {
+  static constexpr int KCH = 8, VCH = 8;  // 16-byte chunks per K / V^T row
+  __device__ static int krow(int mt, int rho) {
+    return 64 * (mt >> 1) + 16 * (mt & 1) + 32 * ((rho >> 2) & 1) + 4 * (rho >> 3) + (rho & 3);
+  }
+  __device__ static int key(int mt, int i, int h) { return 64 * (mt >> 1) + 16 * (mt & 1) + 32 * h + i; }
+  __device__ static int kpos(int r, int c) { return c ^ kswz(r); }
+  __device__ static int vpos(int d, int c) { return c ^ ((d >> 1) & 7); }
+};
+// D = 256, 64-key tiles: 256-byte K rows (a 16-lane read touches rows {0-7, 32-39} + 8 g +
+// 16 mt, told apart by bits 0-2 and 5), 64-byte V^T rows (four to a 256-byte window: rows
+// d .. d + 15 need bits 2-3 of d in the slot), two S^T tiles.
+template <>
+struct E8Layout<256, 64> {
+  static constexpr int KCH = 16, VCH = 4;
+  __device__ static int krow(int mt, int rho) {
+    return 16 * mt + 32 * ((rho >> 2) & 1) + 4 * (rho >> 3) + (rho & 3);
+  }
+  __device__ static int key(int mt, int i, int h) { return 16 * mt + 32 * h + i; }
+  __device__ static int kpos(int r, int c) { return c ^ ((r & 7) | (((r >> 5) & 1) << 3)); }
+  __device__ static int vpos(int d, int c) { return c ^ ((d >> 2) & 3); }
+};
+template <int D>
+constexpr int e8_bn() { return D == 256 ? 64 : 128; }
+
+// LDS of e8_pipeline: K tiles in four slots and V^T tiles in VS (16 KB each in both
+// layouts), and every wavefront's Q^T fragments (16 bytes per lane per half k-step), kept
+// in LDS instead of registers: they are read once per tile, and the registers hold the
+// scores (D = 128: 64 per lane) or O (D = 256: 128 registers) instead.  D = 256 keeps two
+// V^T slots so that the 64 KB of Q^T fit: 64 + 32 + 64 KB.
+template <int D>
 struct E8Lds {
-  static constexpr int TILE = kE8BN * 128;
+  static constexpr int TILE = 16384;
+  static constexpr int VS = D == 256 ? 2 : 3;
   __attribute__((aligned(1024))) uint8_t kl[4][TILE];
-  __attribute__((aligned(1024))) uint8_t vt[3][TILE];
-  __attribute__((aligned(1024))) uint8_t qsm[kPPWaves][2][2][64 * 16];
+  __attribute__((aligned(1024))) uint8_t vt[VS][TILE];
+  __attribute__((aligned(1024))) uint8_t qsm[kPPWaves][D / 64][2][64 * 16];
 };
 
-// Geo as for vt_pipeline, in tiles of kE8BN keys.  q: this wavefront's Q row r0 (e4m3);
-// c_q: softmax scale x q descale.  sp: 0 = P in one e4m3 term everywhere, 1 = two terms on
-// the masked tiles, 2 = two terms on every tile; sp 1 needs a single segment.
-template <int HP, int SP, typename Geo>
-__device__ __forceinline__ void e8_pipeline(E8Lds& lds, const Geo& geo, const uint8_t* q, int64_t q_rs,
-                                            int q_valid, __bf16* out, int64_t o_rs, float* lse, int64_t lse_rs,
-                                            int r0, int Lq, int k_rsb, int vt_rsb, float c_q) {
-  constexpr int D = 128;
-  constexpr int BN = kE8BN;
-  constexpr int CH = D / 16;             // 16-byte chunks per K / V^T row
-  constexpr int NLD = BN * CH / 64;      // wave-wide LDS-DMA loads per K or V^T tile
+// Geo as for vt_pipeline, in tiles of e8_bn<D>() keys.  q: this wavefront's Q row r0
+// (e4m3); c_q: softmax scale x q descale.  sp: 0 = P in one e4m3 term everywhere, 1 = two
+// terms on the masked tiles, 2 = two terms on every tile; sp 1 needs a single segment.
+template <int D, int HP, int SP, typename Geo>
+__device__ __forceinline__ void e8_pipeline(E8Lds<D>& lds, const Geo& geo,
+                                            const uint8_t* q, int64_t q_rs, int q_valid, __bf16* out,
+                                            int64_t o_rs, float* lse, int64_t lse_rs, int r0, int Lq, int k_rsb,
+                                            int vt_rsb, float c_q) {
+  constexpr int BN = e8_bn<D>();
+  using Lay = E8Layout<D, BN>;
+  constexpr int NLD = BN * D / 16 / 64;  // wave-wide LDS-DMA loads (1 KB) per K or V^T tile
   constexpr int NG = NLD / 4;            // loads per wavefront of a group
   constexpr int NMT = BN / 32;           // S^T tiles
   constexpr int NKS = D / 64;            // S^T k-steps (64 d each)
   constexpr int NDT = D / 32;            // O^T tiles
   constexpr int NPS = BN / 64;           // O^T k-steps (64 keys each)
-  constexpr int KS = 4, VS = 3;          // LDS slots of K and V^T tiles
+  constexpr int KS = 4, VS = E8Lds<D>::VS;  // LDS slots of K and V^T tiles
   constexpr int TILE = BN * D;           // bytes of one K or V^T tile
+  constexpr int KRB = Lay::KCH * 16, VRB = Lay::VCH * 16;  // LDS bytes per K / V^T row
+  static_assert(KRB == D && VRB == BN, "tile rows");
   static_assert(NLD % 4 == 0 && NLD % kPPWaves == 0, "tile loads must split over the wavefronts");
-  static_assert(CH == 8, "the K / V swizzles assume 8 chunks per row");
-  static_assert(E8Lds::TILE == TILE && NKS == 2, "E8Lds layout");
+  static_assert(E8Lds<D>::TILE == TILE, "E8Lds layout");
   constexpr int kWaitOlder = NG | (7 << 4);
   static_assert(NG < 16, "vmcnt field");
+  // MFMAs whose fragments are read ahead (D = 256 keeps 128 registers of O and 32 of Q^T)
+  constexpr int RA = D == 256 ? 1 : kPPReadAhead;
   auto& kl = lds.kl;
   auto& vt = lds.vt;
-  auto& qsm = lds.qsm;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1904,6 +1957,7 @@ __device__ __forceinline__ void e8_pipeline(E8Lds& lds, const Geo& geo, const ui
   int n_tiles = 0;
   for (int s = 0; s < nseg; ++s) n_tiles += geo.seg(s).tiles;
 
+  // Q^T fragments: lane (query lq, half lh) holds d = 64 t + 32 lh + 0..31 of k-step t
   {
     const int rsb = (int)q_rs;
     const auto rq = make_rsrc(q, (int64_t)q_valid * rsb);
@@ -1911,8 +1965,8 @@ __device__ __forceinline__ void e8_pipeline(E8Lds& lds, const Geo& geo, const ui
     for (int t = 0; t < NKS; ++t) {
       const u32x4 x0 = bload128(rq, lq * rsb + 64 * t + 32 * lh);
       const u32x4 x1 = bload128(rq, lq * rsb + 64 * t + 32 * lh + 16);
-      *reinterpret_cast<u32x4*>(&qsm[wave][t][0][16 * lane]) = x0;
-      *reinterpret_cast<u32x4*>(&qsm[wave][t][1][16 * lane]) = x1;
+      *reinterpret_cast<u32x4*>(&lds.qsm[wave][t][0][16 * lane]) = x0;
+      *reinterpret_cast<u32x4*>(&lds.qsm[wave][t][1][16 * lane]) = x1;
     }
   }
 
@@ -1945,17 +1999,17 @@ __device__ __forceinline__ void e8_pipeline(E8Lds& lds, const Geo& geo, const ui
     const int n = c.s >= nseg ? 0 : isk ? min(c.keys - c.t * BN, BN) * k_rsb : vt_tile_bytes;
     return make_rsrc32(c.ptr, n);
   };
-  // LDS-DMA: load n of wavefront w (of nw) fills LDS chunks [64 (w + nw n), +64) of a tile;
-  // chunk P is row r = P / 8 at swizzled position P % 8.
+  // LDS-DMA: load n of wavefront w (of nw) fills LDS chunk slots [64 (w + nw n), +64) of a
+  // tile; slot P is row P / CH, position P % CH, which holds chunk kpos / vpos(row, P % CH).
   auto k_voff = [&](int w, int nw, int n) __attribute__((always_inline)) {
     const int P = 64 * (w + nw * n) + lane;
-    const int r = P >> 3;
-    return r * k_rsb + 16 * ((P & 7) ^ kswz(r));
+    const int r = P / Lay::KCH;
+    return r * k_rsb + 16 * Lay::kpos(r, P % Lay::KCH);
   };
   auto v_voff = [&](int w, int nw, int n) __attribute__((always_inline)) {
     const int P = 64 * (w + nw * n) + lane;
-    const int r = P >> 3;
-    return r * vt_rsb + 16 * ((P & 7) ^ ((r >> 1) & 7));
+    const int r = P / Lay::VCH;
+    return r * vt_rsb + 16 * Lay::vpos(r, P % Lay::VCH);
   };
 
   // prologue: K_0 .. K_{KS-2} and V^T_0 .. V^T_{VS-2}, loaded by all eight wavefronts
@@ -1986,18 +2040,19 @@ __device__ __forceinline__ void e8_pipeline(E8Lds& lds, const Geo& geo, const ui
   const int ld_slots = isk ? KS : VS;
   int ld_slot = ld_slots - 1;
 
-  // fragment addresses (bytes): K row sigma(0, lq), chunks 4t + 2h + e; V^T row lq, chunks
-  // 4u + 2h + e; tiles mt and dt add compile-time offsets
-  const int k_row = 32 * ((lq >> 2) & 1) + 4 * (lq >> 3) + (lq & 3);
+  // fragment addresses (bytes): K row krow(0, lq), chunks 4t + 2h + e; V^T row lq, chunks
+  // 4u + 2h + e; tiles mt and dt add compile-time offsets (krow(mt, .) - krow(0, .) and
+  // 32 dt rows change no swizzle bit)
+  const int k_row = Lay::krow(0, lq);
   int k_off[NKS][2], v_off[NPS][2];
 #pragma unroll
   for (int t = 0; t < NKS; ++t)
 #pragma unroll
-    for (int e = 0; e < 2; ++e) k_off[t][e] = k_row * D + 16 * ((4 * t + 2 * lh + e) ^ kswz(k_row));
+    for (int e = 0; e < 2; ++e) k_off[t][e] = k_row * KRB + 16 * Lay::kpos(k_row, 4 * t + 2 * lh + e);
 #pragma unroll
   for (int u = 0; u < NPS; ++u)
 #pragma unroll
-    for (int e = 0; e < 2; ++e) v_off[u][e] = lq * BN + 16 * ((4 * u + 2 * lh + e) ^ ((lq >> 1) & 7));
+    for (int e = 0; e < 2; ++e) v_off[u][e] = lq * VRB + 16 * Lay::vpos(lq, 4 * u + 2 * lh + e);
 
   f32x16 o[NDT];
 #pragma unroll
@@ -2011,12 +2066,12 @@ __device__ __forceinline__ void e8_pipeline(E8Lds& lds, const Geo& geo, const ui
     i32x8 qf[NKS];
 #pragma unroll
     for (int t = 0; t < NKS; ++t)
-      qf[t] = cat8(*reinterpret_cast<const i32x4*>(&qsm[wave][t][0][16 * lane]),
-                   *reinterpret_cast<const i32x4*>(&qsm[wave][t][1][16 * lane]));
+      qf[t] = cat8(*reinterpret_cast<const i32x4*>(&lds.qsm[wave][t][0][16 * lane]),
+                   *reinterpret_cast<const i32x4*>(&lds.qsm[wave][t][1][16 * lane]));
 #pragma unroll
     for (int mt = 0; mt < NMT; ++mt) {
       s[mt] = f32x16{};
-      const int mo = (64 * (mt >> 1) + 16 * (mt & 1)) * D;
+      const int mo = (Lay::krow(mt, 0) - Lay::krow(0, 0)) * KRB;
 #pragma unroll
       for (int t = 0; t < NKS; ++t) {
         const i32x4 a0 = *reinterpret_cast<const i32x4*>(ksrc + mo + k_off[t][0]);
@@ -2061,7 +2116,7 @@ __device__ __forceinline__ void e8_pipeline(E8Lds& lds, const Geo& geo, const ui
     for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int kk = 64 * (mt >> 1) + 16 * (mt & 1) + 32 * lh + i;
+        const int kk = Lay::key(mt, i, lh);
         s[mt][i] = kk >= lim ? -INFINITY : s[mt][i];
       }
   };
@@ -2118,7 +2173,7 @@ __device__ __forceinline__ void e8_pipeline(E8Lds& lds, const Geo& geo, const ui
     } else {
       pv(vt[vr], std::integral_constant<bool, PREV == 2>{});
       qk(kl[j & (KS - 1)]);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kPPReadAhead, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * RA, 0);
 #pragma unroll
       for (int i = 0; i < NDT * NPS; ++i) {
         __builtin_amdgcn_sched_group_barrier(kSchedMfma, PREV, 0);
@@ -2142,8 +2197,10 @@ __device__ __forceinline__ void e8_pipeline(E8Lds& lds, const Geo& geo, const ui
     __builtin_amdgcn_s_setprio(0);
     if (__builtin_expect(mc.t >= mc.g.first_mask, 0)) mask();
     max_rescale(c);
-    // K_{j+1} / V^T_j, loaded two VALU phases ago, are read in the next phase
-    __builtin_amdgcn_s_waitcnt(kWaitOlder);
+    // K_{j+1} / V^T_j, loaded two VALU phases ago, are read in the next phase; with two
+    // V^T slots V^T_j is group 1's latest load
+    if (VS == 2 && !isk) __builtin_amdgcn_s_waitcnt(0);
+    else __builtin_amdgcn_s_waitcnt(kWaitOlder);
     wg_barrier();
     uint8_t* const dst = ld_base + ld_slot * TILE;
 #pragma unroll
@@ -2218,10 +2275,9 @@ __device__ __forceinline__ void e8_pipeline(E8Lds& lds, const Geo& geo, const ui
   }
 }
 
-template <int HP>
+template <int D, int HP>
 __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_vt(AttnParams p) {
-  constexpr int D = 128;
-  constexpr int BN = kE8BN;
+  constexpr int BN = e8_bn<D>();
   constexpr int RB = kPPWaves / HP;  // 32-row blocks per workgroup
   int hg, seq, rt;
   decode_block(p, hg, seq, rt);
@@ -2261,22 +2317,27 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_vt(AttnParams p) 
   const float c_q = p.scale * (p.qd ? p.qd[kvh] : 1.f);
   const int k_rsb = (int)p.k_rs, vt_rsb = (int)p.vt_ds;
   const int qv = min(Lq - r0, 32);
-  __shared__ E8Lds lds;
+  __shared__ E8Lds<D> lds;
+  // (D = 256: the two loop variants of sp 1 do not fit the registers with O's 128; causal
+  // launches split P on every tile instead)
   if (!p.causal)
-    e8_pipeline<HP, 0>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, Lq, k_rsb, vt_rsb, c_q);
-  else if (r0 >= kPreciseRows)
-    e8_pipeline<HP, 1>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, Lq, k_rsb, vt_rsb, c_q);
-  else
-    e8_pipeline<HP, 2>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, Lq, k_rsb, vt_rsb, c_q);
+    e8_pipeline<D, HP, 0>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, Lq, k_rsb, vt_rsb, c_q);
+  else if constexpr (D == 128) {
+    if (r0 >= kPreciseRows)
+      e8_pipeline<D, HP, 1>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, Lq, k_rsb, vt_rsb, c_q);
+    else
+      e8_pipeline<D, HP, 2>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, Lq, k_rsb, vt_rsb, c_q);
+  } else {
+    e8_pipeline<D, HP, 2>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, Lq, k_rsb, vt_rsb, c_q);
+  }
 }
 
-// The whole ring sweep in e4m3 (head dim 128): RingSegments in tiles of kE8BN keys, each
+// The whole ring sweep in e4m3 (head dim 128 or 256): RingSegments in tiles of e8_bn keys, each
 // source with its own k / v descales.  Row tiles whose keys are all their own (rank 0, front
 // half) take the precision rules of a causal attention call; every other row tile sees at
 // least half a shard of other sources' keys and uses one e4m3 term for P.
-template <int HP>
+template <int D, int HP>
 __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_sweep(SweepParams p) {
-  constexpr int D = 128;
   constexpr int RB = kPPWaves / HP;
   int hg, seq, rt;
   decode_block(p, hg, seq, rt);
@@ -2291,7 +2352,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_sweep(SweepParams
   const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
   const int r0 = row_tile0 + (wave / HP) * 32;
 
-  RingSegments<kE8BN> geo;
+  RingSegments<e8_bn<D>()> geo;
   geo.p = &p;
   geo.L = L;
   geo.row_tile0 = row_tile0;
@@ -2309,13 +2370,17 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_sweep(SweepParams
   const int qv = min(L - r0, 32);
   int with_keys = 0;
   for (int s = 1; s < p.S; ++s) with_keys += geo.seg(s).tiles > 0;
-  __shared__ E8Lds lds;
+  __shared__ E8Lds<D> lds;
   if (with_keys > 0)
-    e8_pipeline<HP, 0>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, L, k_rsb, vt_rsb, c_q);
-  else if (r0 >= kPreciseRows)
-    e8_pipeline<HP, 1>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, L, k_rsb, vt_rsb, c_q);
-  else
-    e8_pipeline<HP, 2>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, L, k_rsb, vt_rsb, c_q);
+    e8_pipeline<D, HP, 0>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, L, k_rsb, vt_rsb, c_q);
+  else if constexpr (D == 128) {
+    if (r0 >= kPreciseRows)
+      e8_pipeline<D, HP, 1>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, L, k_rsb, vt_rsb, c_q);
+    else
+      e8_pipeline<D, HP, 2>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, L, k_rsb, vt_rsb, c_q);
+  } else {
+    e8_pipeline<D, HP, 2>(lds, geo, q, p.q_rs, qv, out, p.o_rs, lse, p.lse_rs, r0, L, k_rsb, vt_rsb, c_q);
+  }
 }
 
 //--------------------------------------------------------------------------------------
@@ -2374,12 +2439,18 @@ KernelChoice pick16(int d, int hp, bool vt) {
 
 KernelChoice pick8(int d, int hp, bool vt) {
   KernelChoice k;
-  if (vt && d == 128) {
+  if (vt && (d == 128 || d == 256)) {
     k.threads = kPPThreads;
     k.rows = 32 * kPPWaves / hp;
-    if (hp == 4) k.fn = attn_fwd_e4m3_vt<4>;
-    else if (hp == 2) k.fn = attn_fwd_e4m3_vt<2>;
-    else k.fn = attn_fwd_e4m3_vt<1>;
+    if (d == 128) {
+      if (hp == 4) k.fn = attn_fwd_e4m3_vt<128, 4>;
+      else if (hp == 2) k.fn = attn_fwd_e4m3_vt<128, 2>;
+      else k.fn = attn_fwd_e4m3_vt<128, 1>;
+    } else {
+      if (hp == 4) k.fn = attn_fwd_e4m3_vt<256, 4>;
+      else if (hp == 2) k.fn = attn_fwd_e4m3_vt<256, 2>;
+      else k.fn = attn_fwd_e4m3_vt<256, 1>;
+    }
   } else if (d == 128) {
     k.threads = kPPThreads;
     k.rows = 32 * kPPWaves / hp;
@@ -2518,8 +2589,8 @@ extern "C" int fa4cp_ring_sweep_fwd(const fa4cp_sweep_args* a, void* stream) {
   const bool fp8 = a->dtype == FA4CP_E4M3;
   if (a->dtype != FA4CP_BF16 && a->dtype != FA4CP_FP16 && !fp8)
     return set_error(FA4CP_EUNSUPPORTED, "ring_sweep_fwd: dtype %d (BF16 / FP16 / E4M3 only)", a->dtype);
-  if (fp8 ? d != 128 : (d != 64 && d != 128))
-    return set_error(FA4CP_EUNSUPPORTED, "ring_sweep_fwd: head dim %d (64 / 128 for BF16 / FP16, 128 for E4M3)", d);
+  if (fp8 ? (d != 128 && d != 256) : (d != 64 && d != 128))
+    return set_error(FA4CP_EUNSUPPORTED, "ring_sweep_fwd: head dim %d (64 / 128 for BF16 / FP16, 128 / 256 for E4M3)", d);
   {
     // element sizes: q / k 1 (e4m3) or 2; out 2 (bf16 for e4m3)
     const int esz = fp8 ? 1 : 2;
@@ -2566,9 +2637,15 @@ extern "C" int fa4cp_ring_sweep_fwd(const fa4cp_sweep_args* a, void* stream) {
     else fn = attn_fwd_16bit_sweep<TT, DD, 1>;                      \
   }
   if (fp8) {
-    if (hp == 4) fn = attn_fwd_e4m3_sweep<4>;
-    else if (hp == 2) fn = attn_fwd_e4m3_sweep<2>;
-    else fn = attn_fwd_e4m3_sweep<1>;
+    if (d == 128) {
+      if (hp == 4) fn = attn_fwd_e4m3_sweep<128, 4>;
+      else if (hp == 2) fn = attn_fwd_e4m3_sweep<128, 2>;
+      else fn = attn_fwd_e4m3_sweep<128, 1>;
+    } else {
+      if (hp == 4) fn = attn_fwd_e4m3_sweep<256, 4>;
+      else if (hp == 2) fn = attn_fwd_e4m3_sweep<256, 2>;
+      else fn = attn_fwd_e4m3_sweep<256, 1>;
+    }
   } else if (a->dtype == FA4CP_BF16) {
     FA4CP_PICK(__bf16, 64)
     FA4CP_PICK(__bf16, 128)

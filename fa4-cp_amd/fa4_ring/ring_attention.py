@@ -98,7 +98,7 @@ def ring_flash_attn(
     ``fused`` (default: whenever supported) runs the whole sweep as one kernel over every
     source's K / V^T (``ring_sweep``): no per-step partials, no merges.  It needs
     cp_size in [2, 16] with a LocalKVRing and either bf16 / fp16 with head dim 64 or 128 and
-    no descales, or e4m3 with head dim 128 (any descales); ``fused=False`` runs the
+    no descales, or e4m3 with head dim 128 or 256 (any descales); ``fused=False`` runs the
     per-step path of the reference (attention + LSE merge per step), which covers every
     case.
 
@@ -125,10 +125,10 @@ def ring_flash_attn(
     e4m3 = local_q.dtype == torch.float8_e4m3fn
     can_fuse = 1 < S <= _lib.MAX_CP and (
         (descales is None and local_q.dtype in (torch.bfloat16, torch.float16) and d in (64, 128))
-        or (e4m3 and d == 128))
+        or (e4m3 and d in (128, 256)))
     if fused and not can_fuse:
         raise AssertionError("fused ring sweep needs cp_size in [2, 16] and bf16/fp16 with head dim "
-                             "64/128 and no descales, or e4m3 with head dim 128")
+                             "64/128 and no descales, or e4m3 with head dim 128/256")
     if fused is None:
         fused = can_fuse
     if fused:

@@ -130,8 +130,6 @@ def _fp8_ring_inputs(q, k, v, cp, rank, full_cu=None):
 @pytest.mark.parametrize("n,h,hkv,d,cp", [(2048, 8, 2, 128, 8), (1024, 16, 2, 256, 4),
                                           (1024, 8, 8, 128, 2)])
 def test_ring_fp8_all_ranks(n, h, hkv, d, cp, mode):
-    if mode == "fused" and d != 128:
-        pytest.skip("the fused e4m3 sweep is head dim 128 only")
     say(f"ring e4m3 n={n} h={h}/{hkv} d={d} cp={cp} mode={mode}")
     q, k, v = O.random_qkv(n, h, hkv, d, seed=4)
     scale = scale_for(d)
@@ -263,7 +261,7 @@ def test_ring_c3_fp8_full_size(rank):
 
 def test_ring_c5_fp8_d256_full_size():
     say("ring C5 e4m3 d=256 n=262144 rank=3")
-    _fp8_full_size(262144, 8, 16, 2, 256, 3, ("batched", "incremental"), seed=2)
+    _fp8_full_size(262144, 8, 16, 2, 256, 3, ("fused", "batched", "incremental"), seed=2)
 
 
 @pytest.mark.parametrize("rank", [0, 3])
