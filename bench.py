@@ -191,6 +191,56 @@ def cpu_baseline(rank: int, rows: int) -> dict:
             "full_sweep_s_extrapolated": round(sweep_flops(t, CP, HQ, D) / (flops / dt), 1)}
 
 
+def bench_c5(args) -> int:
+    """The e4m3 head-dim-256 sweep: N = 262144, cp_size = 8 (local 32768 tokens), H_q = 16,
+    H_kv = 2, D = 256, q scale per local shard and k / v scales per source shard (the FP8
+    producer), bf16 out; fused sweep timed, the per-step form beside it."""
+    import torch
+
+    from fa4_ring import LocalKVRing, RingConfig, quantize_ring, ring_flash_attn, zigzag_shard
+
+    n, cp, hq, hkv, d, rank = 262144, 8, 16, 2, 256, args.rank
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(2)
+    q = torch.randn(n, hq, d, device=dev, generator=g, dtype=torch.bfloat16)
+    k = torch.randn(n, hkv, d, device=dev, generator=g, dtype=torch.bfloat16)
+    v = torch.randn(n, hkv, d, device=dev, generator=g, dtype=torch.bfloat16)
+    lq = zigzag_shard(q, rank, cp)
+    del q
+    ks = [zigzag_shard(k, r, cp) for r in range(cp)]
+    vs = [zigzag_shard(v, r, cp) for r in range(cp)]
+    del k, v
+    q8, k8, v8, desc = quantize_ring(lq, ks, vs)
+    del ks, vs, lq
+    ring = LocalKVRing(k8, v8)
+    flops = sweep_flops(n // cp, cp, hq, d)
+    cfg = RingConfig(cp_size=cp, cp_rank=rank)
+    clock = KernelClock()
+    sec = timed_sweeps(lambda: ring_flash_attn(q8, ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc),
+                       args.steps, args.warmup, clock)
+    sw_ms = clock.mean_ms("sweep_kernel")
+    secp = timed_sweeps(lambda: ring_flash_attn(q8, ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc,
+                                                fused=False), max(3, args.steps // 2), 2)
+    value = flops / sec / 1e12
+    kt = flops / (sw_ms * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "e4m3", "data": "synthetic (N(0,1) bf16 quantised to OCP e4m3 on the GPU)",
+        "config": {"workload": f"e4m3 causal zig-zag ring sweep, one rank's share of cp_size={cp} over N={n} "
+                               f"(local 32768 tokens), H_q={hq}, H_kv={hkv}, D={d}, rank {rank}, fused sweep kernel",
+                   "global_batch": 1, "seq_len": n, "cp_size": cp, "cp_rank": rank, "h_q": hq, "h_kv": hkv,
+                   "head_dim": d, "parallelism": "cp8 (one rank's share on 1 GPU)"},
+        "frac_of_peak": round(value / PEAK_FP8_TFLOPS, 4),
+        "roofline": {"bound": "mfma", "kernel": "attn_fwd_e4m3_sweep<256,4>", "achieved": round(kt, 2),
+                     "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s", "frac": round(kt / PEAK_FP8_TFLOPS, 4),
+                     "traffic": None, "algorithmic_per_launch": f"{flops / 1e12:.4f} TFLOP (the whole sweep)",
+                     "avg_launch_ms": round(sw_ms, 4), "launches": clock.count("sweep_kernel")},
+        "per_step": {"ms_per_step": round(secp * 1e3, 3), "TFLOP/s": round(flops / secp / 1e12, 2)},
+        "cpu_baseline": None}), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -200,11 +250,16 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=16384)
     ap.add_argument("--skip-extra", action="store_true", help="only the headline bf16 sweep")
+    ap.add_argument("--workload", default="c2", choices=["c2", "c5"],
+                    help="c2 (default): the bf16 N=131072 sweep with its extras; c5: the e4m3 "
+                         "N=262144, H_q=16, H_kv=2, D=256 sweep")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (one rank's sweep with every source "
               f"rank's KV resident in HBM); --gpus {args.gpus} is not supported", file=sys.stderr)
         return 2
+    if args.workload == "c5":
+        return bench_c5(args)
 
     import torch
 
