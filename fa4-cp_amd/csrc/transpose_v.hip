@@ -18,12 +18,20 @@ namespace {
 constexpr int kTK = 64;      // keys per workgroup
 constexpr int kTBlock = 256;
 
+// The tensors of one launch (blockIdx.y picks one).
+struct TransposeSet {
+  const void* v[FA4CP_MAX_CP];
+  void* vt[FA4CP_MAX_CP];
+};
+
 __device__ __forceinline__ int round_up_pad(int n) { return (n + kVtPad - 1) / kVtPad * kVtPad; }
 
 template <typename T, int D>
 __global__ __launch_bounds__(kTBlock) void transpose_v_kernel(
-    const T* __restrict__ v, int64_t v_rs, int64_t v_hs, const int32_t* __restrict__ cu, int nseq,
-    int total_k, int sel, int n_kt, T* __restrict__ vt, int64_t vt_ds) {
+    TransposeSet set, int64_t v_rs, int64_t v_hs, const int32_t* __restrict__ cu, int nseq,
+    int total_k, int sel, int n_kt, int64_t vt_ds) {
+  const T* __restrict__ v = reinterpret_cast<const T*>(set.v[blockIdx.y]);
+  T* __restrict__ vt = reinterpret_cast<T*>(set.vt[blockIdx.y]);
   constexpr int E = 16 / sizeof(T);  // elements per 16-byte unit
   constexpr int PITCH = D + E;       // LDS row pitch in elements (one unit of padding)
   __shared__ __attribute__((aligned(16))) T tile[kTK * PITCH];
@@ -64,23 +72,21 @@ __global__ __launch_bounds__(kTBlock) void transpose_v_kernel(
 }
 
 template <typename T>
-int launch(const fa4cp_transpose_args& a, int n_kt, hipStream_t st) {
-  const dim3 grid((unsigned)(n_kt * a.nseq * a.h_kv));
-  const T* v = reinterpret_cast<const T*>(a.v);
-  T* vt = reinterpret_cast<T*>(a.v_t);
+int launch(const fa4cp_transpose_args& a, const TransposeSet& set, int count, int n_kt, hipStream_t st) {
   const int nseq = a.cu_k ? a.nseq : 1;
+  const dim3 grid((unsigned)(n_kt * nseq * a.h_kv), (unsigned)count);
   switch (a.d) {
     case 64:
-      hipLaunchKernelGGL((transpose_v_kernel<T, 64>), grid, dim3(kTBlock), 0, st, v, a.v_row_stride,
-                         a.v_head_stride, a.cu_k, nseq, a.total_k, a.k_sel, n_kt, vt, a.vt_d_stride);
+      hipLaunchKernelGGL((transpose_v_kernel<T, 64>), grid, dim3(kTBlock), 0, st, set, a.v_row_stride,
+                         a.v_head_stride, a.cu_k, nseq, a.total_k, a.k_sel, n_kt, a.vt_d_stride);
       break;
     case 128:
-      hipLaunchKernelGGL((transpose_v_kernel<T, 128>), grid, dim3(kTBlock), 0, st, v, a.v_row_stride,
-                         a.v_head_stride, a.cu_k, nseq, a.total_k, a.k_sel, n_kt, vt, a.vt_d_stride);
+      hipLaunchKernelGGL((transpose_v_kernel<T, 128>), grid, dim3(kTBlock), 0, st, set, a.v_row_stride,
+                         a.v_head_stride, a.cu_k, nseq, a.total_k, a.k_sel, n_kt, a.vt_d_stride);
       break;
     case 256:
-      hipLaunchKernelGGL((transpose_v_kernel<T, 256>), grid, dim3(kTBlock), 0, st, v, a.v_row_stride,
-                         a.v_head_stride, a.cu_k, nseq, a.total_k, a.k_sel, n_kt, vt, a.vt_d_stride);
+      hipLaunchKernelGGL((transpose_v_kernel<T, 256>), grid, dim3(kTBlock), 0, st, set, a.v_row_stride,
+                         a.v_head_stride, a.cu_k, nseq, a.total_k, a.k_sel, n_kt, a.vt_d_stride);
       break;
     default:
       return set_error(FA4CP_EUNSUPPORTED, "transpose_v: head dim %d not supported", a.d);
@@ -93,14 +99,9 @@ int launch(const fa4cp_transpose_args& a, int n_kt, hipStream_t st) {
 
 using namespace fa4cp;
 
-extern "C" int64_t fa4cp_vt_min_d_stride(int32_t total_k, int32_t nseq) {
-  return ((int64_t)total_k + (int64_t)kVtPad * (nseq < 1 ? 1 : nseq) + kVtPad - 1) / kVtPad * kVtPad;
-}
-
-extern "C" int fa4cp_transpose_v(const fa4cp_transpose_args* a, void* stream) {
-  clear_error();
-  if (a == nullptr || a->v == nullptr || a->v_t == nullptr)
-    return set_error(FA4CP_EINVAL, "transpose_v: null pointer");
+// Checks the shared arguments of a transpose; returns the key tiles per sequence (0: nothing
+// to do) or a negative status.
+static int transpose_check(const fa4cp_transpose_args* a, int& esize) {
   if (a->h_kv <= 0 || a->total_k < 0 || a->max_seqlen_k < 0)
     return set_error(FA4CP_EINVAL, "transpose_v: bad shape");
   if (a->k_sel != FA4CP_SEL_ALL && a->k_sel != FA4CP_SEL_FRONT_HALF && a->k_sel != FA4CP_SEL_BACK_HALF)
@@ -110,21 +111,57 @@ extern "C" int fa4cp_transpose_v(const fa4cp_transpose_args* a, void* stream) {
   if (a->vt_d_stride < fa4cp_vt_min_d_stride(a->total_k, nseq) || a->vt_d_stride % kVtPad != 0)
     return set_error(FA4CP_EINVAL, "transpose_v: vt_d_stride %lld must be a multiple of %d and >= %lld",
                      (long long)a->vt_d_stride, kVtPad, (long long)fa4cp_vt_min_d_stride(a->total_k, nseq));
-  int esize = 0;
   switch (a->dtype) {
     case FA4CP_BF16: case FA4CP_FP16: esize = 2; break;
     case FA4CP_E4M3: esize = 1; break;
     default: return set_error(FA4CP_EUNSUPPORTED, "transpose_v: unsupported dtype %d", a->dtype);
   }
-  if ((reinterpret_cast<uintptr_t>(a->v) % 16) != 0 || (a->v_row_stride * esize) % 16 != 0 ||
-      (a->v_head_stride * esize) % 16 != 0 || (reinterpret_cast<uintptr_t>(a->v_t) % 16) != 0)
+  if ((a->v_row_stride * esize) % 16 != 0 || (a->v_head_stride * esize) % 16 != 0)
     return set_error(FA4CP_EINVAL, "transpose_v: v / v_t and the v strides must be 16-byte aligned");
   const int max_sel = a->cu_k ? (a->k_sel == FA4CP_SEL_ALL ? a->max_seqlen_k : (a->max_seqlen_k + 1) / 2)
                               : (a->k_sel == FA4CP_SEL_ALL ? a->total_k : (a->total_k + 1) / 2);
   const int n_kt = (max_sel + kVtPad - 1) / kVtPad * kVtPad / kTK;
-  if (n_kt == 0) return FA4CP_OK;
   if ((int64_t)n_kt * nseq * a->h_kv > 0x7fffffffLL)
     return set_error(FA4CP_EINVAL, "transpose_v: too many tiles");
+  return n_kt;
+}
+
+static int transpose_launch(const fa4cp_transpose_args* a, const TransposeSet& set, int count, void* stream) {
+  int esize = 0;
+  const int n_kt = transpose_check(a, esize);
+  if (n_kt <= 0) return n_kt;
+  for (int i = 0; i < count; ++i) {
+    if (set.v[i] == nullptr || set.vt[i] == nullptr) return set_error(FA4CP_EINVAL, "transpose_v: null pointer");
+    if ((reinterpret_cast<uintptr_t>(set.v[i]) % 16) != 0 || (reinterpret_cast<uintptr_t>(set.vt[i]) % 16) != 0)
+      return set_error(FA4CP_EINVAL, "transpose_v: v / v_t and the v strides must be 16-byte aligned");
+  }
   hipStream_t st = (hipStream_t)stream;
-  return a->dtype == FA4CP_E4M3 ? launch<uint8_t>(*a, n_kt, st) : launch<uint16_t>(*a, n_kt, st);
+  return esize == 1 ? launch<uint8_t>(*a, set, count, n_kt, st) : launch<uint16_t>(*a, set, count, n_kt, st);
+}
+
+extern "C" int64_t fa4cp_vt_min_d_stride(int32_t total_k, int32_t nseq) {
+  return ((int64_t)total_k + (int64_t)kVtPad * (nseq < 1 ? 1 : nseq) + kVtPad - 1) / kVtPad * kVtPad;
+}
+
+extern "C" int fa4cp_transpose_v(const fa4cp_transpose_args* a, void* stream) {
+  clear_error();
+  if (a == nullptr) return set_error(FA4CP_EINVAL, "transpose_v: null pointer");
+  TransposeSet set{};
+  set.v[0] = a->v;
+  set.vt[0] = a->v_t;
+  return transpose_launch(a, set, 1, stream);
+}
+
+extern "C" int fa4cp_transpose_v_many(const fa4cp_transpose_args* a, const void* const* v, void* const* v_t,
+                                      int32_t count, void* stream) {
+  clear_error();
+  if (a == nullptr || v == nullptr || v_t == nullptr) return set_error(FA4CP_EINVAL, "transpose_v: null pointer");
+  if (count < 1 || count > FA4CP_MAX_CP)
+    return set_error(FA4CP_EINVAL, "transpose_v_many: count %d out of [1, %d]", count, FA4CP_MAX_CP);
+  TransposeSet set{};
+  for (int i = 0; i < count; ++i) {
+    set.v[i] = v[i];
+    set.vt[i] = v_t[i];
+  }
+  return transpose_launch(a, set, count, stream);
 }

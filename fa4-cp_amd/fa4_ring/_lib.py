@@ -173,6 +173,11 @@ SIGNATURES = {
     ),
     "fa4cp_transpose_v": (ctypes.c_int, [ctypes.POINTER(TransposeArgs), ctypes.c_void_p]),
     "fa4cp_vt_min_d_stride": (ctypes.c_int64, [ctypes.c_int32, ctypes.c_int32]),
+    "fa4cp_transpose_v_many": (
+        ctypes.c_int,
+        [ctypes.POINTER(TransposeArgs), ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p),
+         ctypes.c_int32, ctypes.c_void_p],
+    ),
     "fa4cp_ring_sweep_fwd": (ctypes.c_int, [ctypes.POINTER(SweepArgs), ctypes.c_void_p]),
     "fa4cp_quantize_e4m3": (ctypes.c_int, [ctypes.POINTER(QuantArgs), ctypes.c_void_p]),
     "fa4cp_last_error": (ctypes.c_char_p, []),

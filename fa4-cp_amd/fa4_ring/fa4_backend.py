@@ -16,7 +16,7 @@ from __future__ import annotations
 
 import ctypes
 import math
-from typing import Optional, Tuple
+from typing import List, Optional, Sequence, Tuple
 
 import torch
 
@@ -105,6 +105,41 @@ def transpose_v(v: torch.Tensor, *, cu_seqlens_k: Optional[torch.Tensor] = None,
     a.vt_d_stride = stride
     _lib.check(lib.fa4cp_transpose_v(ctypes.byref(a), _lib.stream_handle(v.device)), "fa4cp_transpose_v")
     return vt, stride
+
+
+def transpose_v_many(vs: Sequence[torch.Tensor], *, cu_seqlens_k: Optional[torch.Tensor] = None,
+                     max_seqlen_k: Optional[int] = None) -> Tuple[List[torch.Tensor], int]:
+    """transpose_v (k_sel = all) of up to 16 tensors of one shape and stride in one launch
+    (fa4cp_transpose_v_many), e.g. every source rank's V before a fused sweep."""
+    lib = _lib.load()
+    _require(1 <= len(vs) <= _lib.MAX_CP, f"1..{_lib.MAX_CP} tensors")
+    v = vs[0]
+    _require(v.dim() == 3 and v.is_cuda and v.stride(2) == 1, "v must be a [T, H_kv, D] device tensor, unit stride in D")
+    for x in vs:
+        _require(x.shape == v.shape and x.stride() == v.stride() and x.dtype == v.dtype, "tensors must share shape, strides and dtype")
+    t_k, h_kv, d = v.shape
+    nseq = 1
+    if cu_seqlens_k is not None:
+        _cu_ok(cu_seqlens_k, v.device, "cu_seqlens_k")
+        _require(max_seqlen_k is not None, "max_seqlen_k required with cu_seqlens_k")
+        nseq = cu_seqlens_k.shape[0] - 1
+    stride = int(lib.fa4cp_vt_min_d_stride(t_k, nseq))
+    vts = [torch.empty(h_kv * d * stride, dtype=v.dtype, device=v.device) for _ in vs]
+    a = _lib.TransposeArgs()
+    a.v_row_stride, a.v_head_stride = v.stride(0), v.stride(1)
+    a.cu_k = _lib.ptr(cu_seqlens_k)
+    a.nseq = nseq
+    a.total_k = t_k
+    a.max_seqlen_k = int(max_seqlen_k) if cu_seqlens_k is not None else t_k
+    a.k_sel = SEL_ALL
+    a.h_kv, a.d = h_kv, d
+    a.dtype = _lib.dtype_code(v.dtype)
+    a.vt_d_stride = stride
+    src = (ctypes.c_void_p * len(vs))(*[x.data_ptr() for x in vs])
+    dst = (ctypes.c_void_p * len(vs))(*[x.data_ptr() for x in vts])
+    _lib.check(lib.fa4cp_transpose_v_many(ctypes.byref(a), src, dst, len(vs), _lib.stream_handle(v.device)),
+               "fa4cp_transpose_v_many")
+    return vts, stride
 
 
 def fa4_attn(

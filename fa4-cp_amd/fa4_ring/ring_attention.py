@@ -35,7 +35,7 @@ import torch
 from . import _lib
 from .config import RingConfig
 from .fa4_backend import (SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, _norm_descale, fa4_attn, out_dtype_for,
-                          transpose_v, uses_vt)
+                          transpose_v, transpose_v_many, uses_vt)
 from .merge import merge_state_in_place, merge_states
 from .zigzag import zigzag_shard, zigzag_shard_varlen
 
@@ -218,8 +218,8 @@ def ring_sweep(local_q: torch.Tensor, local_k: torch.Tensor, local_v: torch.Tens
     for k, v in zip(ks, vs):
         assert k.shape == (total, h_kv, d) and v.shape == k.shape and k.dtype == local_q.dtype
         assert k.stride() == ks[0].stride(), "all K shards must share strides"
-    vts = [transpose_v(v, cu_seqlens_k=cu_seqlens, max_seqlen_k=max_seqlen)[0] for v in vs]
-    stride = int(lib.fa4cp_vt_min_d_stride(total, nseq))
+    assert all(v.stride() == vs[0].stride() for v in vs), "all V shards must share strides"
+    vts, stride = transpose_v_many(vs, cu_seqlens_k=cu_seqlens, max_seqlen_k=max_seqlen)
     e4m3 = local_q.dtype == torch.float8_e4m3fn
     if out is None:
         out = torch.empty(local_q.shape, dtype=torch.bfloat16 if e4m3 else local_q.dtype, device=dev)

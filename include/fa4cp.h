@@ -18,7 +18,7 @@
  *   fa4cp_merge_states          <- fa4_ring/merge.py:39-42 (flashinfer.cascade.merge_states)
  *   fa4cp_zigzag_shard          <- fa4_ring/zigzag.py:31-39 and :82-97 (zigzag_shard, zigzag_shard_varlen)
  *   fa4cp_zigzag_unshard        <- fa4_ring/zigzag.py:42-50 (zigzag_unshard)
- *   fa4cp_transpose_v           <- no counterpart: the V^T layout the fast attention kernels
+ *   fa4cp_transpose_v(_many)    <- no counterpart: the V^T layout the fast attention kernels
  *                                  load (FA4 reads V as given; see fa4cp_attn_args.v_t)
  *   fa4cp_ring_sweep_fwd        <- fa4_ring/ring_attention.py:61-174 (ring_flash_attn's step loop
  *                                  and its merges, fused; every source's K/V on this GPU)
@@ -112,6 +112,8 @@ typedef struct fa4cp_attn_args {
 
 int fa4cp_attn_fwd(const fa4cp_attn_args* args, void* stream);
 
+#define FA4CP_MAX_CP 16 /* source ranks of one sweep; tensors of one batched transpose */
+
 /*
  * V -> V^T for fa4cp_attn_args.v_t.  Element (kv head g, column c, position p) of V^T is at
  * v_t[(g * d + c) * vt_d_stride + p] (elements of dtype).  Sequence j's keys selected by
@@ -136,6 +138,14 @@ int fa4cp_transpose_v(const fa4cp_transpose_args* args, void* stream);
 int64_t fa4cp_vt_min_d_stride(int32_t total_k, int32_t nseq);
 
 /*
+ * The same for `count` (1..FA4CP_MAX_CP) tensors of one shape in one launch: v[i] -> v_t[i]
+ * (host arrays of device pointers; args->v and args->v_t are ignored), e.g. every source
+ * rank's V before fa4cp_ring_sweep_fwd.
+ */
+int fa4cp_transpose_v_many(const fa4cp_transpose_args* args, const void* const* v, void* const* v_t,
+                           int32_t count, void* stream);
+
+/*
  * One rank's whole causal zig-zag ring sweep in a single launch (fa4_ring/ring_attention.py:61-174
  * with every source rank's K/V already on this GPU): out / lse are the attention of the
  * local q over the union of
@@ -151,7 +161,6 @@ int64_t fa4cp_vt_min_d_stride(int32_t total_k, int32_t nseq);
  * reference's Descales: ring_attention.py:43-52, fa4_backend.py:45-55); cp_size <=
  * FA4CP_MAX_CP.
  */
-#define FA4CP_MAX_CP 16
 typedef struct fa4cp_sweep_args {
   const void* q; /* [total rows] x h_q heads x d */
   void* out;     /* [total rows] x h_q heads x d */

@@ -170,6 +170,30 @@ def test_transpose_v_layout_bit_exact(dtype, d, cu, sel):
         pos += pad
 
 
+@pytest.mark.parametrize("dtype,d,count", [(torch.bfloat16, 128, 8), (torch.float8_e4m3fn, 256, 3),
+                                           (torch.float16, 64, 16), (torch.bfloat16, 128, 1)])
+@pytest.mark.parametrize("cu", [None, [0, 200, 200, 713]])
+def test_transpose_v_many_equals_one_by_one(dtype, d, count, cu):
+    """One launch over `count` tensors writes what `count` single transposes write."""
+    from fa4_ring.fa4_backend import transpose_v, transpose_v_many
+    say(f"transpose_v_many {dtype} d={d} count={count} cu={cu}")
+    total = cu[-1] if cu is not None else 300
+    g = torch.Generator().manual_seed(6)
+    vs = [torch.randn(total, 2, d, generator=g).to(dtype).to(DEV) for _ in range(count)]
+    cud = None if cu is None else torch.tensor(cu, dtype=torch.int32, device=DEV)
+    mx = None if cu is None else max(b - a for a, b in zip(cu[:-1], cu[1:]))
+    many, stride = transpose_v_many(vs, cu_seqlens_k=cud, max_seqlen_k=mx)
+    for v, got in zip(vs, many):
+        one, s1 = transpose_v(v, cu_seqlens_k=cud, max_seqlen_k=mx)
+        assert s1 == stride
+        iv = torch.uint8 if dtype == torch.float8_e4m3fn else torch.int16
+        # positions past the last sequence's padding are never written (workspace)
+        used = sum((b - a + 127) // 128 * 128 for a, b in seq_bounds(cu, total, 0))
+        a_ = one.view(iv).reshape(2, d, stride)[:, :, :used]
+        b_ = got.view(iv).reshape(2, d, stride)[:, :, :used]
+        assert torch.equal(a_.cpu(), b_.cpu())
+
+
 # ------------------------------------------------------------------------- attention
 
 def _qkv(tq, tk, h, hkv, d, seed, dtype):
