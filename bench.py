@@ -43,9 +43,9 @@ N, CP, HQ, HKV, D = 131072, 8, 32, 8, 128
 # rocprofv3 counter passes over this script: FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the
 # factors being what those counters read for the zig-zag gather (a plain copy of known size).
 # The summary with both commands is under profiles/.
-ATTN_TRAFFIC_BYTES_RANK3 = 467135 * 1024
+ATTN_TRAFFIC_BYTES_RANK3 = 466593 * 1024
 # The same for the fused sweep kernel (one launch per sweep).
-SWEEP_TRAFFIC_BYTES_RANK3 = 2395580 * 1024
+SWEEP_TRAFFIC_BYTES_RANK3 = 2395694 * 1024
 
 
 def sweep_flops(t_local: int, cp: int, hq: int, d: int) -> float:
