@@ -194,6 +194,61 @@ def cpu_baseline(rank: int, rows: int) -> dict:
             "full_sweep_s_extrapolated": round(sweep_flops(t, CP, HQ, D) / (flops / dt), 1)}
 
 
+C4_LENGTHS = [4856, 9720, 8592, 4864, 1832, 15456, 2784, 1576]  # 8 * randint(128, 2049), seed 0
+
+
+def bench_c4(args) -> int:
+    """Packed sequences: the 8 lengths above (49680 tokens), cp_size = 4, H_q = 32, H_kv = 8,
+    D = 128, bf16, one rank's fused varlen sweep (the per-step form beside it)."""
+    import torch
+
+    from fa4_ring import LocalKVRing, RingConfig, ring_flash_attn
+    from fa4_ring.zigzag import zigzag_shard_varlen
+
+    cp, hq, hkv, d, rank = 4, HQ, HKV, D, args.rank % 4
+    full_cu = [0]
+    for n in C4_LENGTHS:
+        full_cu.append(full_cu[-1] + n)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(5)
+    q = torch.randn(full_cu[-1], hq, d, device=dev, generator=g, dtype=torch.bfloat16)
+    k = torch.randn(full_cu[-1], hkv, d, device=dev, generator=g, dtype=torch.bfloat16)
+    v = torch.randn(full_cu[-1], hkv, d, device=dev, generator=g, dtype=torch.bfloat16)
+    ring = LocalKVRing.from_full(k, v, cp, full_cu)
+    lq, local_cu = zigzag_shard_varlen(q, full_cu, rank, cp)
+    max_local = int((local_cu[1:] - local_cu[:-1]).max())
+    flops = sum(cp * 8.0 * (n // (2 * cp)) ** 2 * d * hq for n in C4_LENGTHS)
+    cfg = RingConfig(cp_size=cp, cp_rank=rank)
+
+    def run(fused):
+        return ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, cu_seqlens=local_cu,
+                               max_seqlen=max_local, fused=fused)
+
+    clock = KernelClock()
+    sec = timed_sweeps(lambda: run(None), args.steps, args.warmup, clock)
+    sw_ms = clock.mean_ms("sweep_kernel")
+    secp = timed_sweeps(lambda: run(False), args.steps, args.warmup)
+    value = flops / sec / 1e12
+    kt = flops / (sw_ms * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (q/k/v ~ N(0,1) bf16, seeded on the GPU)",
+        "config": {"workload": f"bf16 causal zig-zag ring sweep over packed sequences {C4_LENGTHS} "
+                               f"({full_cu[-1]} tokens), cp_size={cp}, rank {rank}, H_q={hq}, H_kv={hkv}, D={d}, "
+                               "fused sweep kernel",
+                   "global_batch": len(C4_LENGTHS), "seq_len": max(C4_LENGTHS), "cp_size": cp, "cp_rank": rank,
+                   "h_q": hq, "h_kv": hkv, "head_dim": d, "parallelism": "cp4 (one rank's share on 1 GPU)"},
+        "frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
+        "roofline": {"bound": "mfma", "kernel": "attn_fwd_16bit_sweep<bf16,128,4>", "achieved": round(kt, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(kt / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "algorithmic_per_launch": f"{flops / 1e12:.4f} TFLOP (the whole sweep)",
+                     "avg_launch_ms": round(sw_ms, 4), "launches": clock.count("sweep_kernel")},
+        "per_step": {"ms_per_step": round(secp * 1e3, 3), "TFLOP/s": round(flops / secp / 1e12, 2)},
+        "cpu_baseline": None}), flush=True)
+    return 0
+
+
 def bench_c5(args) -> int:
     """The e4m3 head-dim-256 sweep: N = 262144, cp_size = 8 (local 32768 tokens), H_q = 16,
     H_kv = 2, D = 256, q scale per local shard and k / v scales per source shard (the FP8
@@ -253,9 +308,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=16384)
     ap.add_argument("--skip-extra", action="store_true", help="only the headline bf16 sweep")
-    ap.add_argument("--workload", default="c2", choices=["c2", "c5"],
-                    help="c2 (default): the bf16 N=131072 sweep with its extras; c5: the e4m3 "
-                         "N=262144, H_q=16, H_kv=2, D=256 sweep")
+    ap.add_argument("--workload", default="c2", choices=["c2", "c4", "c5"],
+                    help="c2 (default): the bf16 N=131072 sweep with its extras; c4: packed bf16 "
+                         "sequences (8 lengths, cp_size 4); c5: the e4m3 N=262144, H_q=16, "
+                         "H_kv=2, D=256 sweep")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (one rank's sweep with every source "
@@ -263,6 +319,8 @@ def main():
         return 2
     if args.workload == "c5":
         return bench_c5(args)
+    if args.workload == "c4":
+        return bench_c4(args)
 
     import torch
 
