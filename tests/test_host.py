@@ -16,7 +16,7 @@ from fa4_ring import _lib
 from fa4_ring.config import RingConfig
 from fa4_ring.fa4_backend import _norm_descale, fa4_attn
 from fa4_ring.merge import BatchedMerger, IncrementalMerger, make_merger
-from fa4_ring.ring_attention import LocalKVRing, ring_flash_attn
+from fa4_ring.ring_attention import Descales, LocalKVRing, ring_flash_attn
 from fa4_ring.zigzag import get_half_index, half_indices, local_seqlen
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -143,9 +143,33 @@ def test_ring_without_local_kv_source_raises():
         ring_flash_attn(q, q, q, cfg, group=ring)
 
 
+def test_fused_sweep_rejects_what_it_does_not_cover():
+    """fused=True is refused (AssertionError, before any device work) outside the fused
+    kernel's cases: fp32, a head dim other than 64/128 (bf16) or 128/256 (e4m3), cp_size 1 or
+    above 16, bf16 with descales."""
+    cfg = RingConfig(cp_size=2, cp_rank=0)
+
+    def ring_of(x):
+        return LocalKVRing([x, x], [x, x])
+
+    for dt, d in [(torch.float32, 128), (torch.bfloat16, 256), (torch.float8_e4m3fn, 64)]:
+        x = torch.zeros(16, 2, d, dtype=dt)
+        with pytest.raises(AssertionError, match="fused ring sweep"):
+            ring_flash_attn(x, x, x, cfg, group=ring_of(x), fused=True)
+    x = torch.zeros(16, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="fused ring sweep"):
+        ring_flash_attn(x, x, x, cfg, group=ring_of(x), fused=True, descales=Descales(q=torch.tensor(1.0)))
+    with pytest.raises(AssertionError, match="fused ring sweep"):
+        ring_flash_attn(x, x, x, RingConfig(cp_size=1, cp_rank=0), fused=True)
+    big = RingConfig(cp_size=17, cp_rank=0)
+    with pytest.raises(AssertionError, match="fused ring sweep"):
+        ring_flash_attn(x, x, x, big, group=LocalKVRing([x] * 17, [x] * 17), fused=True)
+
+
 def test_public_api_names():
     for name in ["RingConfig", "ring_flash_attn", "Descales", "zigzag_shard", "zigzag_unshard",
-                 "IncrementalMerger", "BatchedMerger", "make_merger", "LocalKVRing"]:
+                 "IncrementalMerger", "BatchedMerger", "make_merger", "LocalKVRing", "quantize_e4m3",
+                 "quantize_ring"]:
         assert hasattr(fa4_ring, name)
     from fa4_ring.zigzag import zigzag_shard_varlen  # noqa: F401
     from fa4_ring.reference import full_causal_reference  # noqa: F401
