@@ -2134,7 +2134,8 @@ __device__ __forceinline__ void e8_pipeline(E8Lds<D>& lds, const Geo& geo,
       const float alpha = m2 == -INFINITY ? 0.f : fast_exp2(m2 - m_new);
       m2 = m_new;
       lsum *= alpha;
-      const float ao = alpha * v_ratio;
+      // the change of v descale applies once, on the segment's first tile
+      const float ao = seg_new ? alpha * v_ratio : alpha;
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) o[dt] *= ao;
     }

@@ -172,6 +172,39 @@ def test_ring_fp8_varlen_all_ranks(mode):
         assert max_err(out, ref) <= TOL_FP8_OUT, f"rank {rank}"
 
 
+@pytest.mark.parametrize("mode", PATHS)
+@pytest.mark.parametrize("growth", [5.0, 8.8, 150.0])
+def test_ring_fp8_row_max_grows_inside_a_later_source(growth, mode):
+    """The row max jumps by `growth` (log2 units) on the third key tile of the second source
+    (rank 1 of 2: local causal keys, then the front half of source 0), whose v descale is
+    ten times the first source's: 5 stays under the lazy-rescale bound, 8.8 moves the
+    reference max mid-segment (O must change units once, at the segment start, not again
+    here), 150 overflows the exponentials taken against the old max."""
+    n, h, hkv, d, cp, rank = 2048, 2, 1, 128, 2, 1
+    say(f"ring e4m3 late max growth={growth} path={mode}")
+    g = torch.Generator().manual_seed(8)
+    u = torch.randn(d, generator=g)
+    u = u / u.norm()
+    a = 4.0
+    scale = scale_for(d)
+    q = (a * u).expand(n, h, d).clone()
+    k = 1e-3 * torch.randn(n, hkv, d, generator=g)
+    k[300, 0] = u * (growth * math.log(2) / (a * scale))  # source 0, local key 300: tile 2
+    v = 4 * torch.randn(n, hkv, d, generator=g)
+    v[512:1536] = 1 + 0.1 * torch.randn(1024, hkv, d, generator=g)  # source 1's keys, mean 1
+    (q8, k8, v8, sq, sk, sv), (dq, dk, dv) = _fp8_ring_inputs(q, k, v, cp, rank)
+    assert sv[0] > 5 * sv[1]
+    ring = LocalKVRing([x.to(DEV) for x in k8], [x.to(DEV) for x in v8])
+    desc = Descales(q=torch.tensor(sq, device=DEV), k=[torch.tensor(s, device=DEV) for s in sk],
+                    v=[torch.tensor(s, device=DEV) for s in sv])
+    cfg, fused = _cfg_path(mode, cp, rank)
+    out = ring_flash_attn(q8.to(DEV), ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc,
+                          fused=fused)
+    ref, _ = O.ring_rank(dq, dk, dv, rank, cp, scale, merge_mode=cfg.merge_mode)
+    assert torch.isfinite(out.float()).all()
+    assert max_err(out, ref) <= TOL_FP8_OUT
+
+
 # ----------------------------------------------------------------- benchmark sizes
 
 def _sample_local_rows(t, n_random, seed):
