@@ -7,31 +7,63 @@
 // x / scale is the correctly rounded fp32 quotient and the conversion rounds to nearest
 // even, so y equals torch's `(x / scale).clamp(-448, 448).to(torch.float8_e4m3fn)`.
 //
-// Three launches: clear the amax words, reduce (per-thread maxima of fixed 16-byte chunk
-// slots of every row, then LDS and global atomic maxima on the bit patterns, which order
-// like the values for x >= 0), quantise (reads x again, writes y and the descales).  Both
-// passes over x are HBM-bound: a workgroup streams whole rows, 16 bytes per lane.
+// Three launches: clear the amax words, reduce |x| (per-thread maxima, then LDS and global
+// atomic maxima on the bit patterns, which order like the values for x >= 0), quantise
+// (reads x again, writes y and the descales).  Both passes over x are HBM-bound.  A
+// workgroup works on groups of `rb` whole rows, rb * (chunks per row) <= 2048 16-byte
+// chunks, and every thread owns the same NS chunk slots of every group: slot k of thread t
+// is chunk t + 256 k of the group.  Its row, head, position and scale are fixed, so they are
+// computed once, and a thread issues the loads of all its slots before it uses any.
 #include "common.h"
 
 namespace fa4cp {
 namespace {
 
 constexpr int kQBlock = 256;
-constexpr int kQSlots = 16;       // 16-byte chunks of a row one thread handles
+constexpr int kQSpan = 2048;      // 16-byte chunks per row group (8 per thread)
+constexpr int kQMaxSlots = 16;    // chunk slots per thread: rows of up to 4096 chunks
 constexpr int kQMaxScales = 1024;
-constexpr int kQMaxGrid = 2048;   // workgroups; each loops over rows
+constexpr int kQMaxGrid = 1024;   // workgroups (4 per CU); each loops over row groups
+
+// Where the chunks of a row group lie: group g covers rows [g rb, g rb + rb).
+struct QuantGeo {
+  int64_t rows, rs, hs;  // rows; row and head strides (elements)
+  int64_t groups;
+  int cph, cpr, cps;     // 16-byte chunks per head, per row, per scale (0: one scale)
+  int rb;                // rows per group
+};
 
 __global__ void clear_words(unsigned* p, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0u;
 }
 
-// Chunk c of a row (16 bytes, E elements): head c / cph, element (c % cph) * E.
+// The slots of this thread: x offset in a group (elements), y offset (bytes), row in the
+// group (or -1 for a slot past the group's chunks) and scale index.
+template <typename T, int NS>
+struct Slots {
+  int64_t xo[NS];
+  int yo[NS], ro[NS], si[NS];
+  __device__ explicit Slots(const QuantGeo& g) {
+    constexpr int E = 16 / sizeof(T);
+    const int span = g.rb * g.cpr;
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+      const int p = threadIdx.x + kQBlock * k;
+      const int r = p / g.cpr, c = p - r * g.cpr;
+      const int hh = c / g.cph;
+      ro[k] = p < span ? r : -1;
+      xo[k] = (int64_t)r * g.rs + (int64_t)hh * g.hs + (c - hh * g.cph) * E;
+      yo[k] = p * E;  // y is [rows, h, d] contiguous: a group is span * E bytes
+      si[k] = g.cps ? c / g.cps : 0;
+    }
+  }
+  // live: slot k of group row base r0 lies in the tensor
+  __device__ bool live(int k, int64_t r0, int64_t rows) const { return ro[k] >= 0 && r0 + ro[k] < rows; }
+};
+
 template <typename T>
-__device__ __forceinline__ void load_chunk(const T* row, int64_t hs, int c, int cph, float (&f)[16 / sizeof(T)]) {
-  constexpr int E = 16 / sizeof(T);
-  const int hh = c / cph, e = (c - hh * cph) * E;
-  const u32x4 w = *reinterpret_cast<const u32x4*>(row + hh * hs + e);
+__device__ __forceinline__ void widen(const u32x4& w, float (&f)[16 / sizeof(T)]) {
   if constexpr (sizeof(T) == 4) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(w[i]);
@@ -43,38 +75,54 @@ __device__ __forceinline__ void load_chunk(const T* row, int64_t hs, int c, int 
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(kQBlock) void amax_kernel(const T* __restrict__ x, int64_t rows, int cph, int cpr,
-                                                       int64_t rs, int64_t hs, int cps, unsigned* amax) {
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+template <typename T, int NS>
+__global__ __launch_bounds__(kQBlock) void amax_kernel(const T* __restrict__ x, QuantGeo g, unsigned* amax) {
   constexpr int E = 16 / sizeof(T);
-  const int nscale = cps ? cpr / cps : 1;  // cps: chunks per scale (0: one scale)
+  const int nscale = g.cps ? g.cpr / g.cps : 1;
   __shared__ unsigned smax[kQMaxScales];
   for (int i = threadIdx.x; i < nscale; i += kQBlock) smax[i] = 0u;
-  __syncthreads();
-  float acc[kQSlots];
+  const Slots<T, NS> sl(g);
+  float acc[NS];
 #pragma unroll
-  for (int k = 0; k < kQSlots; ++k) acc[k] = 0.f;
-  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-    const T* row = x + r * rs;
+  for (int k = 0; k < NS; ++k) acc[k] = 0.f;
+  for (int64_t grp = blockIdx.x; grp < g.groups; grp += gridDim.x) {
+    const int64_t r0 = grp * g.rb;
+    const T* xb = x + r0 * g.rs;
+    u32x4 w[NS];
 #pragma unroll
-    for (int k = 0; k < kQSlots; ++k) {
-      const int c = threadIdx.x + k * kQBlock;
-      if (c < cpr) {
-        float f[E];
-        load_chunk<T>(row, hs, c, cph, f);
+    for (int k = 0; k < NS; ++k)
+      w[k] = sl.live(k, r0, g.rows) ? *reinterpret_cast<const u32x4*>(xb + sl.xo[k]) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int i = 0; i < E; ++i) acc[k] = fmaxf(acc[k], fabsf(f[i]));
-      }
+    for (int k = 0; k < NS; ++k) {
+      float f[E];
+      widen<T>(w[k], f);
+#pragma unroll
+      for (int i = 0; i < E; ++i) acc[k] = fmaxf(acc[k], fabsf(f[i]));
     }
   }
+  __syncthreads();
+  if (g.cps == 0) {
+    float m = acc[0];
 #pragma unroll
-  for (int k = 0; k < kQSlots; ++k) {
-    const int c = threadIdx.x + k * kQBlock;
-    if (c < cpr) atomicMax(&smax[cps ? c / cps : 0], __float_as_uint(acc[k]));
+    for (int k = 1; k < NS; ++k) m = fmaxf(m, acc[k]);
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) atomicMax(&smax[0], __float_as_uint(m));
+  } else {
+#pragma unroll
+    for (int k = 0; k < NS; ++k)
+      if (sl.ro[k] >= 0) atomicMax(&smax[sl.si[k]], __float_as_uint(acc[k]));
   }
   __syncthreads();
+  // one atomic per scale and workgroup, and none where the maximum already stands higher:
+  // the atomics on one word serialise, and after the first workgroups most are redundant
   for (int i = threadIdx.x; i < nscale; i += kQBlock)
-    if (smax[i] != 0u) atomicMax(&amax[i], smax[i]);
+    if (smax[i] > __hip_atomic_load(&amax[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) atomicMax(&amax[i], smax[i]);
 }
 
 __device__ __forceinline__ float scale_of(unsigned amax_bits) {
@@ -82,63 +130,89 @@ __device__ __forceinline__ float scale_of(unsigned amax_bits) {
   return a > 0.f ? a / 448.f : 1.f;
 }
 
-template <typename T>
-__global__ __launch_bounds__(kQBlock) void quant_kernel(const T* __restrict__ x, int64_t rows, int cph, int cpr,
-                                                        int64_t rs, int64_t hs, int cps, const unsigned* amax,
+// x / s rounded to nearest, from rc = 1 / s rounded to nearest: q = x rc is within an ulp of
+// the quotient, its remainder x - q s is exact in one fma, and q + (x - q s) rc rounds to
+// the correctly rounded quotient (Markstein's theorem; no overflow here, since |x| <= 448 s
+// up to rounding, and quotients small enough to underflow quantise to 0 either way).  The
+// remainder is formed as -(q s - x), which is -0 for x = -0 (x - q s would be +0), so that
+// the quotient keeps the sign of a zero x as x / s does.
+__device__ __forceinline__ float div_rn(float x, float s, float rc) {
+  const float q = x * rc;
+  return fmaf(-fmaf(q, s, -x), rc, q);
+}
+
+template <typename T, int NS>
+__global__ __launch_bounds__(kQBlock) void quant_kernel(const T* __restrict__ x, QuantGeo g, const unsigned* amax,
                                                         float* descale, uint8_t* __restrict__ y) {
   constexpr int E = 16 / sizeof(T);
-  const int nscale = cps ? cpr / cps : 1;
+  const int nscale = g.cps ? g.cpr / g.cps : 1;
   if (blockIdx.x == 0)
     for (int i = threadIdx.x; i < nscale; i += kQBlock) descale[i] = scale_of(amax[i]);
-  float sc[kQSlots];
+  const Slots<T, NS> sl(g);
+  float sc[NS], rc[NS];
 #pragma unroll
-  for (int k = 0; k < kQSlots; ++k) {
-    const int c = threadIdx.x + k * kQBlock;
-    sc[k] = c < cpr ? scale_of(amax[cps ? c / cps : 0]) : 1.f;
+  for (int k = 0; k < NS; ++k) {
+    sc[k] = scale_of(amax[sl.si[k]]);
+    rc[k] = 1.f / sc[k];  // correctly rounded
   }
-  const int64_t y_rs = (int64_t)cpr * E;  // y is [rows, h, d] contiguous
-  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-    const T* row = x + r * rs;
-    uint8_t* yr = y + r * y_rs;
+  const int64_t y_gs = (int64_t)g.rb * g.cpr * E;  // y bytes per row group
+  for (int64_t grp = blockIdx.x; grp < g.groups; grp += gridDim.x) {
+    const int64_t r0 = grp * g.rb;
+    const T* xb = x + r0 * g.rs;
+    uint8_t* yb = y + grp * y_gs;
+    u32x4 w[NS];
 #pragma unroll
-    for (int k = 0; k < kQSlots; ++k) {
-      const int c = threadIdx.x + k * kQBlock;
-      if (c < cpr) {
-        float f[E];
-        load_chunk<T>(row, hs, c, cph, f);
+    for (int k = 0; k < NS; ++k)
+      w[k] = sl.live(k, r0, g.rows) ? *reinterpret_cast<const u32x4*>(xb + sl.xo[k]) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int i = 0; i < E; ++i) f[i] = fminf(fmaxf(f[i] / sc[k], -448.f), 448.f);
-        unsigned w[E / 4];
+    for (int k = 0; k < NS; ++k) {
+      if (!sl.live(k, r0, g.rows)) continue;
+      float f[E];
+      widen<T>(w[k], f);
 #pragma unroll
-        for (int j = 0; j < E / 4; ++j) {
-          int v = __builtin_amdgcn_cvt_pk_fp8_f32(f[4 * j], f[4 * j + 1], 0, false);
-          v = __builtin_amdgcn_cvt_pk_fp8_f32(f[4 * j + 2], f[4 * j + 3], v, true);
-          w[j] = (unsigned)v;
-        }
-        if constexpr (E == 8) {
-          *reinterpret_cast<u32x2*>(yr + (int64_t)c * E) = u32x2{w[0], w[1]};
-        } else {
-          *reinterpret_cast<unsigned*>(yr + (int64_t)c * E) = w[0];
-        }
+      for (int i = 0; i < E; ++i) f[i] = fminf(fmaxf(div_rn(f[i], sc[k], rc[k]), -448.f), 448.f);
+      unsigned o[E / 4];
+#pragma unroll
+      for (int j = 0; j < E / 4; ++j) {
+        int v = __builtin_amdgcn_cvt_pk_fp8_f32(f[4 * j], f[4 * j + 1], 0, false);
+        v = __builtin_amdgcn_cvt_pk_fp8_f32(f[4 * j + 2], f[4 * j + 3], v, true);
+        o[j] = (unsigned)v;
+      }
+      if constexpr (E == 8) {
+        __builtin_nontemporal_store(u32x2{o[0], o[1]}, reinterpret_cast<u32x2*>(yb + sl.yo[k]));
+      } else {
+        __builtin_nontemporal_store(o[0], reinterpret_cast<unsigned*>(yb + sl.yo[k]));
       }
     }
   }
 }
 
-template <typename T>
-int launch(const fa4cp_quant_args& a, int cps, hipStream_t st) {
-  constexpr int E = 16 / sizeof(T);
-  const int cph = a.d / E, cpr = a.h * cph;
-  const int nscale = cps ? cpr / cps : 1;
+template <typename T, int NS>
+void launch_ns(const fa4cp_quant_args& a, const QuantGeo& g, int nscale, hipStream_t st) {
   unsigned* amax = reinterpret_cast<unsigned*>(a.amax);
   hipLaunchKernelGGL(clear_words, dim3((nscale + kQBlock - 1) / kQBlock), dim3(kQBlock), 0, st, amax, nscale);
   const T* x = reinterpret_cast<const T*>(a.x);
-  const int grid = (int)(a.rows < kQMaxGrid ? (a.rows > 0 ? a.rows : 1) : kQMaxGrid);
-  if (a.rows > 0)
-    hipLaunchKernelGGL((amax_kernel<T>), dim3(grid), dim3(kQBlock), 0, st, x, a.rows, cph, cpr, a.row_stride,
-                       a.head_stride, cps, amax);
-  hipLaunchKernelGGL((quant_kernel<T>), dim3(grid), dim3(kQBlock), 0, st, x, a.rows, cph, cpr, a.row_stride,
-                     a.head_stride, cps, amax, a.descale, reinterpret_cast<uint8_t*>(a.y));
+  const int grid = (int)(g.groups < kQMaxGrid ? (g.groups > 0 ? g.groups : 1) : kQMaxGrid);
+  if (g.rows > 0) hipLaunchKernelGGL((amax_kernel<T, NS>), dim3(grid), dim3(kQBlock), 0, st, x, g, amax);
+  hipLaunchKernelGGL((quant_kernel<T, NS>), dim3(grid), dim3(kQBlock), 0, st, x, g, amax, a.descale,
+                     reinterpret_cast<uint8_t*>(a.y));
+}
+
+template <typename T>
+int launch(const fa4cp_quant_args& a, int cps, hipStream_t st) {
+  constexpr int E = 16 / sizeof(T);
+  QuantGeo g;
+  g.rows = a.rows;
+  g.rs = a.row_stride;
+  g.hs = a.head_stride;
+  g.cph = a.d / E;
+  g.cpr = a.h * g.cph;
+  g.cps = cps;
+  g.rb = g.cpr <= kQSpan ? kQSpan / g.cpr : 1;
+  g.groups = (a.rows + g.rb - 1) / g.rb;
+  const int nscale = cps ? g.cpr / cps : 1;
+  if (g.rb * g.cpr <= kQSpan) launch_ns<T, kQSpan / kQBlock>(a, g, nscale, st);
+  else launch_ns<T, kQMaxSlots>(a, g, nscale, st);
   return check_launch("quantize_e4m3");
 }
 
@@ -166,9 +240,9 @@ extern "C" int fa4cp_quantize_e4m3(const fa4cp_quant_args* a, void* stream) {
       (a->head_stride * esz) % 16 != 0 || (reinterpret_cast<uintptr_t>(a->y) % 8) != 0)
     return set_error(FA4CP_EINVAL, "quantize_e4m3: x and its strides must be 16-byte aligned, y 8-byte aligned");
   const int64_t cpr = (int64_t)a->h * (a->d / E);
-  if (cpr > (int64_t)kQBlock * kQSlots)
+  if (cpr > (int64_t)kQBlock * kQMaxSlots)
     return set_error(FA4CP_EUNSUPPORTED, "quantize_e4m3: h * d = %lld elements per row (at most %d)",
-                     (long long)a->h * a->d, kQBlock * kQSlots * E);
+                     (long long)a->h * a->d, kQBlock * kQMaxSlots * E);
   const int g = a->heads_per_scale;
   if (g < 0 || (g > 0 && a->h % g != 0))
     return set_error(FA4CP_EINVAL, "quantize_e4m3: heads_per_scale %d must be 0 or divide h = %d", g, a->h);

@@ -35,10 +35,17 @@ def _heads_scaled(rows, h, d, dtype, seed):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("rows,h,d,g", [(1000, 8, 128, 0), (333, 32, 128, 4), (17, 2, 256, 1),
-                                        (64, 16, 64, 2), (5, 1, 16, 0), (4096, 8, 128, 1)])
+                                        (64, 16, 64, 2), (5, 1, 16, 0), (4096, 8, 128, 1),
+                                        (9, 24, 512, 6), (9, 48, 512, 6)])
 def test_quantize_matches_oracle(dtype, rows, h, d, g):
+    """The last two cases have rows of more than 2048 16-byte chunks (fp32 / 16-bit); fp32
+    rows of more than 4096 chunks are refused."""
     say(f"quantize_e4m3 {dtype} rows={rows} h={h} d={d} heads_per_scale={g}")
     x = _heads_scaled(rows, h, d, dtype, seed=rows + h)
+    if h * d * x.element_size() > 16 * 4096:
+        with pytest.raises(RuntimeError, match="elements per row"):
+            quantize_e4m3(x.to(DEV), heads_per_scale=g)
+        return
     y, ds = quantize_e4m3(x.to(DEV), heads_per_scale=g)
     y_ref, ds_ref = _oracle(x, g)
     assert y.dtype == torch.float8_e4m3fn and y.shape == (rows, h, d)
@@ -47,6 +54,38 @@ def test_quantize_matches_oracle(dtype, rows, h, d, g):
     assert torch.equal(y.view(torch.uint8).cpu(), y_ref), "e4m3 bytes"
     # the largest magnitude of every group maps to +-448
     assert int((y.view(torch.uint8).cpu() & 0x7F).max()) == 0x7E
+
+
+def _e4m3_midpoints() -> torch.Tensor:
+    """The 126 points halfway between consecutive non-negative e4m3 values (fp32, exact)."""
+    vals = torch.arange(0, 0x7F, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn).float()
+    vals = vals.sort().values
+    return (vals[:-1] + vals[1:]) / 2
+
+
+@pytest.mark.parametrize("amax", [1.0, 3.7, 0.0123, 1000.5, 1.3 * 2.0 ** -20])
+def test_quantize_rounds_at_every_e4m3_midpoint(amax):
+    """fp32 inputs a few ulps either side of every e4m3 rounding midpoint (times the scale),
+    both signs: the quotient x / scale must be the correctly rounded one wherever that decides
+    the e4m3 byte, as the oracle's fp32 division and round-to-nearest-even conversion give."""
+    say(f"quantize_e4m3 midpoint sweep amax={amax}")
+    s = torch.tensor(amax, dtype=torch.float32) / 448  # the producer's scale, in fp32
+    x0 = (_e4m3_midpoints() * s).float()
+    xs = [x0]
+    lo, hi = x0.clone(), x0.clone()
+    for _ in range(3):
+        lo = torch.nextafter(lo, torch.tensor(-float("inf")))
+        hi = torch.nextafter(hi, torch.tensor(float("inf")))
+        xs += [lo, hi]
+    x = torch.cat(xs)
+    x = torch.cat([x, -x, torch.tensor([amax], dtype=torch.float32)])
+    x = x[x.abs() <= amax]
+    pad = (-x.numel()) % 16
+    x = torch.cat([x, torch.zeros(pad)]).reshape(-1, 1, 16)
+    y, ds = quantize_e4m3(x.to(DEV))
+    y_ref, ds_ref = _oracle(x, 0)
+    assert float(ds) == float(ds_ref[0]) == float(s)
+    assert torch.equal(y.view(torch.uint8).cpu(), y_ref)
 
 
 def test_quantize_strided_input():

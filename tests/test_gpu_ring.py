@@ -205,6 +205,34 @@ def test_ring_fp8_row_max_grows_inside_a_later_source(growth, mode):
     assert max_err(out, ref) <= TOL_FP8_OUT
 
 
+@pytest.mark.parametrize("mode", PATHS)
+@pytest.mark.parametrize("growth", [5.0, 8.8, 150.0])
+def test_ring_bf16_row_max_grows_mid_sweep(growth, mode):
+    """As the e4m3 case above in bf16 (64-key tiles): the row max jumps by `growth` (log2
+    units) on key 300 of source 0, the fifth tile of rank 1's second step."""
+    n, h, hkv, d, cp, rank = 2048, 2, 1, 128, 2, 1
+    say(f"ring bf16 late max growth={growth} path={mode}")
+    g = torch.Generator().manual_seed(9)
+    u = torch.randn(d, generator=g)
+    u = u / u.norm()
+    a = 4.0
+    scale = scale_for(d)
+    q = (a * u).expand(n, h, d).clone()
+    k = 1e-3 * torch.randn(n, hkv, d, generator=g)
+    k[300, 0] = u * (growth * math.log(2) / (a * scale))
+    v = 4 * torch.randn(n, hkv, d, generator=g)
+    v[512:1536] = 1 + 0.1 * torch.randn(1024, hkv, d, generator=g)
+    q, k, v = (rounded(t, torch.bfloat16) for t in (q, k, v))
+    qd, ring = _device_ring(q, k, v, cp, torch.bfloat16)
+    cfg, fused = _cfg_path(mode, cp, rank)
+    out = ring_flash_attn(zigzag_shard(qd, rank, cp), ring.k[rank], ring.v[rank], cfg, group=ring, fused=fused)
+    ks = [O.zigzag_shard(k, r, cp) for r in range(cp)]
+    vs = [O.zigzag_shard(v, r, cp) for r in range(cp)]
+    ref, _ = O.ring_rank(O.zigzag_shard(q, rank, cp), ks, vs, rank, cp, scale, merge_mode=cfg.merge_mode)
+    assert torch.isfinite(out.float()).all()
+    assert max_err(out, ref) <= TOL_BF16_OUT
+
+
 # ----------------------------------------------------------------- benchmark sizes
 
 def _sample_local_rows(t, n_random, seed):
