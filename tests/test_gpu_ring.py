@@ -6,14 +6,16 @@ sampled rows against exact dense causal attention (a row's ring output must equa
 causal attention over every key before it), plus run-to-run bit reproducibility.
 """
 
+import functools
 import math
 
 import numpy as np
 import pytest
 import torch
 
-from fa4_ring import Descales, LocalKVRing, RingConfig, ring_flash_attn, zigzag_shard
-from fa4_ring.zigzag import zigzag_shard_varlen
+from fa4_ring import Descales, LocalKVRing, RingConfig, ring_flash_attn, zigzag_shard, zigzag_unshard
+from fa4_ring.reference import full_causal_reference
+from fa4_ring.zigzag import zigzag_shard_varlen, zigzag_unshard_varlen
 from gpu_helpers import DEV, TOL_BF16_OUT, TOL_FP8_OUT, max_err, rounded, say, scale_for
 from oracle import ring_oracle as O
 
@@ -61,6 +63,62 @@ def test_ring_all_ranks_small(n, h, hkv, d, cp, mode):
         outs.append(out.float().cpu())
     dense = O.dense_causal(q, k, v, scale)
     assert max_err(O.zigzag_unshard(outs, cp), dense) <= TOL_BF16_OUT
+
+
+@functools.lru_cache(maxsize=4)
+def _reference_gpu_case(dtype_name: str, num_seqs: int):
+    """Inputs and dense fp32 reference of the reference's own GPU test at its defaults
+    (tests/test_ring_correctness.py:41-47: N=4096, H=16, H_kv=4, D=128, 4 ranks, seed 1234,
+    ~N(0,1) in the test dtype; the generator here is the CPU one, so the draws differ), each
+    packed sequence compared on its own (block-diagonal causal, :96-103)."""
+    dtype = getattr(torch, dtype_name)
+    n, h, hkv, d = 4096, 16, 4, 128
+    gen = torch.Generator().manual_seed(1234)
+    q = torch.randn(n, h, d, generator=gen).to(dtype)
+    k = torch.randn(n, hkv, d, generator=gen).to(dtype)
+    v = torch.randn(n, hkv, d, generator=gen).to(dtype)
+    per = n // num_seqs
+    ref = torch.cat([full_causal_reference(q[i * per:(i + 1) * per], k[i * per:(i + 1) * per],
+                                           v[i * per:(i + 1) * per]) for i in range(num_seqs)]).float()
+    return q, k, v, ref
+
+
+@pytest.mark.parametrize("num_seqs", [1, 4])
+@pytest.mark.parametrize("mode", PATHS)
+@pytest.mark.parametrize("dtype_name", ["bfloat16", "float16"])
+def test_reference_gpu_test_configuration(dtype_name, mode, num_seqs):
+    """The reference's GPU correctness check (test_ring_correctness.py:55-116) on one GPU: every
+    rank's sweep over its zig-zag shard, the outputs stitched back and compared with dense
+    causal attention over the whole sequence, max error below 2e-2 (bf16) / 5e-3 (fp16) and
+    cosine similarity above 0.999 (:108-109)."""
+    world = 4
+    say(f"reference GPU test config dtype={dtype_name} path={mode} num_seqs={num_seqs}")
+    q, k, v, ref = _reference_gpu_case(dtype_name, num_seqs)
+    n = q.shape[0]
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    full_cu = list(range(0, n + 1, n // num_seqs))
+    ring = LocalKVRing.from_full(kd, vd, world, full_cu if num_seqs > 1 else None)
+    outs = []
+    for rank in range(world):
+        cfg, fused = _cfg_path(mode, world, rank)
+        if num_seqs > 1:
+            lq, local_cu = zigzag_shard_varlen(qd, full_cu, rank, world)
+            max_local = int((local_cu[1:] - local_cu[:-1]).max())
+            out = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, cu_seqlens=local_cu,
+                                  max_seqlen=max_local, fused=fused)
+        else:
+            out = ring_flash_attn(zigzag_shard(qd, rank, world), ring.k[rank], ring.v[rank], cfg, group=ring,
+                                  fused=fused)
+        assert out.dtype == q.dtype
+        outs.append(out)
+    full = (zigzag_unshard_varlen(outs, full_cu, world) if num_seqs > 1 else zigzag_unshard(outs, world))
+    full = full.float().cpu()
+    err = float((full - ref).abs().max())
+    # in float64: an fp32 cosine over 8M elements drifts above 1
+    cos = float(torch.nn.functional.cosine_similarity(full.double().flatten(), ref.double().flatten(), dim=0))
+    tol = 2e-2 if dtype_name == "bfloat16" else 5e-3
+    say(f"  max_err={err:.3e} cos={cos:.6f}")
+    assert err < tol and cos > 0.999
 
 
 def test_ring_cp1_is_causal_attention():
