@@ -200,13 +200,13 @@ def ring_sweep(local_q: torch.Tensor, local_k: torch.Tensor, local_v: torch.Tens
                max_seqlen: Optional[int] = None, out: Optional[torch.Tensor] = None,
                lse: Optional[torch.Tensor] = None, descales: Optional[Descales] = None) -> torch.Tensor:
     """The whole sweep of ring_flash_attn (fa4_ring/ring_attention.py:61-174) in one
-    fa4cp_ring_sweep_fwd launch: every source's V is transposed (fa4cp_transpose_v), then one
-    kernel carries each row tile's online softmax through the causal local keys, the front
+    fa4cp_ring_sweep_fwd launch: every source's V is transposed (one fa4cp_transpose_v_many
+    launch), then one kernel carries each row tile's online softmax through the causal local keys, the front
     halves of the earlier sources and, for the back-half rows, all keys of the later ones.
     e4m3 inputs take ``descales`` (the k / v descales per source rank, as ring_flash_attn)
     and give a bf16 out.  Returns out [T, H, D] (``lse`` [T, H], if given, receives the
     natural-log LSE)."""
-    lib = _lib.load()
+    _lib.load()  # fails here, before any allocation, without the library
     S, rank = cfg.cp_size, cfg.cp_rank
     total, h_q, d = local_q.shape
     dev = local_q.device

@@ -36,7 +36,6 @@ How each function is pinned (tests/test_oracle.py):
 
 from __future__ import annotations
 
-import math
 from typing import List, Optional, Sequence, Tuple
 
 import numpy as np

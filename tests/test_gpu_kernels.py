@@ -6,7 +6,6 @@ import math
 import pytest
 import torch
 
-import fa4_ring
 from fa4_ring import zigzag as Z
 from fa4_ring.fa4_backend import SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, fa4_attn
 from fa4_ring.merge import merge_state_in_place, merge_states
