@@ -409,22 +409,22 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
   // S^T = K Q^T for the K tile at ksrc
   auto qk = [&](f32x16 (&s)[NMT], const T* ksrc) {
 #pragma unroll
-    for (int mt = 0; mt < NMT; ++mt) {
-      s[mt] = f32x16{};
+    for (int mt = 0; mt < NMT; ++mt) s[mt] = f32x16{};
 #pragma unroll
-      for (int t = 0; t < NKS; ++t) {
+    for (int t = 0; t < NKS; ++t)
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt) {
         const frag a = *reinterpret_cast<const frag*>(ksrc + k_off[t] + 32 * mt * D);
         s[mt] = Ops::mma(a, qf[t], s[mt]);
       }
-    }
   };
   // O^T += V^T P^T for the V tile at vsrc; the A fragment of k-step t is rows 16t + 4h .. +3
   // and 16t + 8 + 4h .. +3 of column d, read transposed from the row-major V tile
   auto pv = [&](const frag (&pf)[NPS], const T* vsrc) {
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+    for (int t = 0; t < NPS; ++t)
 #pragma unroll
-      for (int t = 0; t < NPS; ++t) {
+      for (int dt = 0; dt < NDT; ++dt) {
         const s16x4 lo = lds_tr16(vsrc + v_off[dt] + 16 * t * D);
         const s16x4 hi = lds_tr16(vsrc + v_off[dt] + (16 * t + 8) * D);
         const frag a = __builtin_bit_cast(frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -663,21 +663,21 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_pp(AttnParams p)
 
   auto qk = [&](const T* ksrc) {
 #pragma unroll
-    for (int mt = 0; mt < NMT; ++mt) {
-      s[mt] = f32x16{};
+    for (int mt = 0; mt < NMT; ++mt) s[mt] = f32x16{};
 #pragma unroll
-      for (int t = 0; t < NKS; ++t) {
+    for (int t = 0; t < NKS; ++t)
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt) {
         const frag a = *reinterpret_cast<const frag*>(ksrc + k_off[t] + 32 * mt * D);
         s[mt] = Ops::mma(a, qf[t], s[mt]);
       }
-    }
   };
   const int vt_lane = lq * VTS + 8 * lh;
   auto pv = [&](const T* vsrc) {
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+    for (int t = 0; t < NPS; ++t)
 #pragma unroll
-      for (int t = 0; t < NPS; ++t) {
+      for (int dt = 0; dt < NDT; ++dt) {
         const frag a = *reinterpret_cast<const frag*>(vsrc + vt_lane + 32 * dt * VTS + 16 * t);
         o[dt] = Ops::mma(a, pf[t], o[dt]);
       }
@@ -973,22 +973,26 @@ __device__ __forceinline__ void vt_pipeline(const Geo& geo, const T* q, int64_t 
   f32x16 s[NMT];
   frag pf[NPS];
 
+  // MFMA order: consecutive MFMAs share their register operand (Q^T fragment t in S^T, P^T
+  // fragment t in O^T), so fewer operand bits switch between them.  The chip runs at its
+  // power limit, and this order measured 1.1 % (bf16) and 1.4 % (e4m3) faster than tile by
+  // tile.  Each accumulator still sums its k-steps in ascending order: same results.
   auto qk = [&](const T* ksrc) __attribute__((always_inline)) {
 #pragma unroll
-    for (int mt = 0; mt < NMT; ++mt) {
-      s[mt] = f32x16{};
+    for (int mt = 0; mt < NMT; ++mt) s[mt] = f32x16{};
 #pragma unroll
-      for (int t = 0; t < NKS; ++t) {
+    for (int t = 0; t < NKS; ++t)
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt) {
         const frag a = *reinterpret_cast<const frag*>(ksrc + k_off[t] + 32 * mt * D);
         s[mt] = Ops::mma(a, qf[t], s[mt]);
       }
-    }
   };
   auto pv = [&](const T* vsrc) __attribute__((always_inline)) {
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+    for (int t = 0; t < NPS; ++t)
 #pragma unroll
-      for (int t = 0; t < NPS; ++t) {
+      for (int dt = 0; dt < NDT; ++dt) {
         const frag a = *reinterpret_cast<const frag*>(vsrc + 32 * dt * BN + v_off[t]);
         o[dt] = Ops::mma(a, pf[t], o[dt]);
       }
@@ -1406,18 +1410,16 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_e4m3(At
     const uint8_t* ks_ = smem + buf * BUF;
     const uint8_t* vs_ = ks_ + BN * RS;
 
-    f32x16 s[2];
+    f32x16 s[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      s[mt] = f32x16{};
+    for (int t = 0; t < NKS; ++t)
 #pragma unroll
-      for (int t = 0; t < NKS; ++t) {
+      for (int mt = 0; mt < 2; ++mt) {
         const uint8_t* src = ks_ + k_lane + 32 * mt * RS + 64 * t;
         const i32x4 a0 = *reinterpret_cast<const i32x4*>(src);
         const i32x4 a1 = *reinterpret_cast<const i32x4*>(src + 16);
         s[mt] = mma_fp8(__builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7), qf[t], s[mt]);
       }
-    }
     const int kb = it * BN;
     if constexpr (decltype(masked)::value) mask_tile<2>(s, kb, Lk, r0 + lq + off, p.causal, lh);
 
@@ -1451,9 +1453,9 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_e4m3(At
 #pragma unroll
         for (int j = 0; j < 8; ++j) pb[t][j] = (__bf16)s[t >> 1][8 * (t & 1) + j];
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
+      for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int dt = 0; dt < NDT; ++dt) {
           const i32x2 raw = lds_tr8(vs_ + v_lane + 8 * t * RS + 32 * dt);
           o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(e4m3x8_to_bf16(raw), pb[t], o[dt], 0, 0, 0);
         }
@@ -1682,22 +1684,22 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_pp(AttnParams p) 
       qf[t] = cat8(*reinterpret_cast<const i32x4*>(&qsm[wave][t][32 * lane]),
                    *reinterpret_cast<const i32x4*>(&qsm[wave][t][32 * lane + 16]));
 #pragma unroll
-    for (int mt = 0; mt < NMT; ++mt) {
-      s[mt] = f32x16{};
-      const int mo = (64 * (mt >> 1) + 16 * (mt & 1)) * D;
+    for (int mt = 0; mt < NMT; ++mt) s[mt] = f32x16{};
 #pragma unroll
-      for (int t = 0; t < NKS; ++t) {
+    for (int t = 0; t < NKS; ++t)
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt) {
+        const int mo = (64 * (mt >> 1) + 16 * (mt & 1)) * D;
         const i32x4 a0 = *reinterpret_cast<const i32x4*>(ksrc + mo + k_off[t][0]);
         const i32x4 a1 = *reinterpret_cast<const i32x4*>(ksrc + mo + k_off[t][1]);
         s[mt] = mma_fp8(cat8(a0, a1), qf[t], s[mt]);
       }
-    }
   };
   auto pv = [&](const uint8_t* vsrc, auto two_terms) __attribute__((always_inline)) {
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+    for (int u = 0; u < NPS; ++u)
 #pragma unroll
-      for (int u = 0; u < NPS; ++u) {
+      for (int dt = 0; dt < NDT; ++dt) {
         const i32x4 a0 = *reinterpret_cast<const i32x4*>(vsrc + 32 * dt * BN + v_off[u][0]);
         const i32x4 a1 = *reinterpret_cast<const i32x4*>(vsrc + 32 * dt * BN + v_off[u][1]);
         const i32x8 a = cat8(a0, a1);
@@ -2062,6 +2064,7 @@ __device__ __forceinline__ void e8_pipeline(E8Lds<D>& lds, const Geo& geo,
   f32x16 s[NMT];
   i32x8 pf[NPS], pl[NPS];
 
+  // MFMA order: consecutive MFMAs share their register operand (as in vt_pipeline)
   auto qk = [&](const uint8_t* ksrc) __attribute__((always_inline)) {
     i32x8 qf[NKS];
 #pragma unroll
@@ -2069,22 +2072,22 @@ __device__ __forceinline__ void e8_pipeline(E8Lds<D>& lds, const Geo& geo,
       qf[t] = cat8(*reinterpret_cast<const i32x4*>(&lds.qsm[wave][t][0][16 * lane]),
                    *reinterpret_cast<const i32x4*>(&lds.qsm[wave][t][1][16 * lane]));
 #pragma unroll
-    for (int mt = 0; mt < NMT; ++mt) {
-      s[mt] = f32x16{};
-      const int mo = (Lay::krow(mt, 0) - Lay::krow(0, 0)) * KRB;
+    for (int mt = 0; mt < NMT; ++mt) s[mt] = f32x16{};
 #pragma unroll
-      for (int t = 0; t < NKS; ++t) {
+    for (int t = 0; t < NKS; ++t)
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt) {
+        const int mo = (Lay::krow(mt, 0) - Lay::krow(0, 0)) * KRB;
         const i32x4 a0 = *reinterpret_cast<const i32x4*>(ksrc + mo + k_off[t][0]);
         const i32x4 a1 = *reinterpret_cast<const i32x4*>(ksrc + mo + k_off[t][1]);
         s[mt] = mma_fp8(cat8(a0, a1), qf[t], s[mt]);
       }
-    }
   };
   auto pv = [&](const uint8_t* vsrc, auto two_terms) __attribute__((always_inline)) {
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+    for (int u = 0; u < NPS; ++u)
 #pragma unroll
-      for (int u = 0; u < NPS; ++u) {
+      for (int dt = 0; dt < NDT; ++dt) {
         const i32x4 a0 = *reinterpret_cast<const i32x4*>(vsrc + 32 * dt * BN + v_off[u][0]);
         const i32x4 a1 = *reinterpret_cast<const i32x4*>(vsrc + 32 * dt * BN + v_off[u][1]);
         const i32x8 a = cat8(a0, a1);
