@@ -25,6 +25,8 @@ SMALL_CASES = [  # (N, H, H_kv, D, cp): the reference's CPU cases' structure at 
     (256, 4, 4, 64, 2), (512, 8, 2, 128, 4), (1024, 8, 8, 64, 4), (1024, 4, 1, 128, 8),
     (2048, 8, 2, 128, 8), (768, 6, 3, 64, 2), (1536, 8, 8, 128, 4),
     (2048, 8, 2, 128, 4),  # the CPU benchmark configuration's shape
+    (1024, 16, 2, 128, 4), (1024, 16, 1, 64, 2),  # GQA 8 and 16 query heads per kv head
+    (2048, 4, 2, 128, 16),  # the largest ring the fused sweep takes
 ]
 
 
