@@ -188,7 +188,7 @@ def _fp8_ring_inputs(q, k, v, cp, rank, full_cu=None):
 
 @pytest.mark.parametrize("mode", PATHS)
 @pytest.mark.parametrize("n,h,hkv,d,cp", [(2048, 8, 2, 128, 8), (1024, 16, 2, 256, 4),
-                                          (1024, 8, 8, 128, 2)])
+                                          (1024, 8, 8, 128, 2), (2048, 16, 1, 128, 16)])
 def test_ring_fp8_all_ranks(n, h, hkv, d, cp, mode):
     say(f"ring e4m3 n={n} h={h}/{hkv} d={d} cp={cp} mode={mode}")
     q, k, v = O.random_qkv(n, h, hkv, d, seed=4)
