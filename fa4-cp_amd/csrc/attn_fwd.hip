@@ -2587,6 +2587,7 @@ extern "C" int fa4cp_ring_sweep_fwd(const fa4cp_sweep_args* a, void* stream) {
     return set_error(FA4CP_EINVAL, "ring_sweep_fwd: vt_d_stride must be a multiple of %d and >= %lld", kVtPad,
                      (long long)fa4cp_vt_min_d_stride(a->total, nseq));
   const int max_len = a->cu ? a->max_seqlen : a->total;
+  if (max_len < 0) return set_error(FA4CP_EINVAL, "ring_sweep_fwd: bad max_seqlen %d", max_len);
   const int group = a->h_q / a->h_kv;
   const int hp = heads_per_wg(group);
   const int d = a->d;

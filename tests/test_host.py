@@ -53,6 +53,45 @@ def test_error_path_reports_message_without_gpu():
         _lib.check(rc, "fa4cp_attn_fwd")
 
 
+def test_sweep_entry_point_validates_before_launching():
+    """fa4cp_ring_sweep_fwd rejects bad arguments with a message and no HIP call: null
+    sources, cp_rank / cp_size out of range, a negative max_seqlen, unsupported head dims.
+    The pointers are fake, so this never runs where a device is visible."""
+    if torch.cuda.device_count() > 0:
+        pytest.skip("fake device pointers: host-only test")
+    lib = _lib.load()
+    fake = 1 << 20  # never dereferenced: every case fails validation first
+
+    def args(**kw):
+        a = _lib.SweepArgs()
+        a.q = a.out = a.lse = fake
+        a.q_row_stride, a.q_head_stride = 8 * 128, 128
+        a.o_row_stride, a.o_head_stride = 8 * 128, 128
+        a.lse_row_stride = 8
+        a.k_row_stride, a.k_head_stride = 2 * 128, 128
+        a.vt_d_stride = int(lib.fa4cp_vt_min_d_stride(256, 1))
+        a.total, a.h_q, a.h_kv, a.d = 256, 8, 2, 128
+        a.dtype = _lib.dtype_code(torch.bfloat16)
+        a.cp_rank, a.cp_size = 0, 2
+        a.softmax_scale = 0.1
+        for i in range(2):
+            a.k[i] = a.v_t[i] = fake
+        for key, val in kw.items():
+            setattr(a, key, val)
+        return a
+
+    cases = [(dict(cp_size=0), b"out of range"), (dict(cp_rank=2), b"out of range"),
+             (dict(cp_size=_lib.MAX_CP + 1), b"out of range"), (dict(cu=fake, nseq=1, max_seqlen=-4), b"max_seqlen"),
+             (dict(d=96), b"head dim"), (dict(h_q=7), b"multiple")]
+    for kw, msg in cases:
+        a = args(**kw)
+        rc = lib.fa4cp_ring_sweep_fwd(ctypes.byref(a), None)
+        assert rc != 0 and msg in lib.fa4cp_last_error(), (kw, lib.fa4cp_last_error())
+    a = args()
+    a.k[1] = 0
+    assert lib.fa4cp_ring_sweep_fwd(ctypes.byref(a), None) != 0 and b"source 1" in lib.fa4cp_last_error()
+
+
 @pytest.mark.parametrize("struct,cname", [(_lib.AttnArgs, "fa4cp_attn_args"),
                                            (_lib.TransposeArgs, "fa4cp_transpose_args"),
                                            (_lib.SweepArgs, "fa4cp_sweep_args"),
