@@ -159,6 +159,7 @@ extern "C" int fa4cp_zigzag_shard(const void* src_full, void* dst_local, int64_t
   const int lanes = lanes_for(units);
   const int rows_per_block = kBlock / lanes;
   const int64_t blocks = (n_local + rows_per_block - 1) / rows_per_block;
+  if (blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "zigzag_shard: too many rows");
   hipStream_t st = (hipStream_t)stream;
   const char* s = (const char*)src_full;
   char* d = (char*)dst_local;
@@ -195,6 +196,7 @@ extern "C" int fa4cp_zigzag_unshard(const void* const* shard_ptrs, void* dst_ful
   const int lanes = lanes_for(units);
   const int rows_per_block = kBlock / lanes;
   const int64_t blocks = (total_full + rows_per_block - 1) / rows_per_block;
+  if (blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "zigzag_unshard: too many rows");
   hipStream_t st = (hipStream_t)stream;
   char* d = (char*)dst_full;
   if (ub == 16)
