@@ -299,6 +299,67 @@ def bench_c5(args) -> int:
     return 0
 
 
+def bench_c1(args) -> int:
+    """The reference's CPU-runnable case (N = 2048, cp_size = 4, H_q = 8, H_kv = 2, D = 128,
+    seed 0): every rank's sweep on the GPU in bf16 (fused; the per-step form beside it), and
+    as cpu_baseline the oracle's fp32 restatement of the reference CPU ring algorithm timed
+    in full, all four ranks, on the host cores."""
+    import torch
+
+    from fa4_ring import LocalKVRing, RingConfig, ring_flash_attn, zigzag_shard
+
+    n, cp, hq, hkv, d = 2048, 4, 8, 2, 128
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(n, hq, d, generator=g)
+    k = torch.randn(n, hkv, d, generator=g)
+    v = torch.randn(n, hkv, d, generator=g)
+    qd, kd, vd = (t.to(torch.bfloat16).to(dev) for t in (q, k, v))
+    ring = LocalKVRing.from_full(kd, vd, cp)
+    lqs = [zigzag_shard(qd, r, cp) for r in range(cp)]
+    cfgs = [RingConfig(cp_size=cp, cp_rank=r) for r in range(cp)]
+    flops = cp * sweep_flops(n // cp, cp, hq, d)  # all four ranks' sweeps
+
+    def job(fused):
+        return [ring_flash_attn(lqs[r], ring.k[r], ring.v[r], cfgs[r], group=ring, fused=fused) for r in range(cp)]
+
+    sec = timed_sweeps(lambda: job(None), args.steps, args.warmup)
+    secp = timed_sweeps(lambda: job(False), args.steps, args.warmup)
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import ring_oracle as O
+
+        threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+        threads = min(threads, int(os.environ.get("OMP_NUM_THREADS", threads)))
+        torch.set_num_threads(threads)
+        ks = [O.zigzag_shard(k, r, cp) for r in range(cp)]
+        vs = [O.zigzag_shard(v, r, cp) for r in range(cp)]
+        lq = [O.zigzag_shard(q, r, cp) for r in range(cp)]
+        O.ring_rank(lq[0], ks, vs, 0, cp, 1 / math.sqrt(d))  # warm the BLAS
+        t0 = time.perf_counter()
+        for r in range(cp):
+            O.ring_rank(lq[r], ks, vs, r, cp, 1 / math.sqrt(d))
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+               "sample": f"the whole job: the oracle's fp32 ring sweep of all {cp} ranks "
+                         f"({flops / 1e9:.3f} GFLOP) in {dt:.3f} s"}
+    value = flops / sec / 1e12
+    print(json.dumps({
+        "metric": METRIC, "value": round(value, 4), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (q/k/v ~ N(0,1) fp32 from a seed-0 CPU generator, "
+                                                      "rounded to bf16 for the GPU)",
+        "config": {"workload": f"the reference's CPU case: causal zig-zag ring sweep of all {cp} ranks of "
+                               f"N={n}, H_q={hq}, H_kv={hkv}, D={d}, one after another on one GPU, fused sweep",
+                   "global_batch": 1, "seq_len": n, "cp_size": cp, "h_q": hq, "h_kv": hkv, "head_dim": d,
+                   "parallelism": "cp4 (every rank's share on 1 GPU)"},
+        "frac_of_peak": round(value / PEAK_BF16_TFLOPS, 6),
+        "note": "launch-bound: 2.1 GFLOP per rank",
+        "per_step": {"ms_per_step": round(secp * 1e3, 4), "TFLOP/s": round(flops / secp / 1e12, 4)},
+        "cpu_baseline": cpu}), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -308,9 +369,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=16384)
     ap.add_argument("--skip-extra", action="store_true", help="only the headline bf16 sweep")
-    ap.add_argument("--workload", default="c2", choices=["c2", "c4", "c5"],
-                    help="c2 (default): the bf16 N=131072 sweep with its extras; c4: packed bf16 "
-                         "sequences (8 lengths, cp_size 4); c5: the e4m3 N=262144, H_q=16, "
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c4", "c5"],
+                    help="c2 (default): the bf16 N=131072 sweep with its extras; c1: the reference's "
+                         "CPU case (N=2048, cp_size 4) on every rank, with the oracle's CPU time; c4: "
+                         "packed bf16 sequences (8 lengths, cp_size 4); c5: the e4m3 N=262144, H_q=16, "
                          "H_kv=2, D=256 sweep")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -321,6 +383,8 @@ def main():
         return bench_c5(args)
     if args.workload == "c4":
         return bench_c4(args)
+    if args.workload == "c1":
+        return bench_c1(args)
 
     import torch
 

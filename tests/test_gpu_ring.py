@@ -341,7 +341,8 @@ def test_ring_c2_bf16_full_size(rank):
     qc = torch.zeros(n, hq, d)
     qc[torch.from_numpy(grow)] = lq.float().cpu()
     for mode, out in outs.items():
-        _check_sampled(out, rank, cp, n, qc, kc, vc, scale_for(d), TOL_BF16_OUT, seed=rank)
+        err = _check_sampled(out, rank, cp, n, qc, kc, vc, scale_for(d), TOL_BF16_OUT, seed=rank)
+        say(f"  C2 rank {rank} {mode}: sampled max |err| {err:.3e} (bar {TOL_BF16_OUT})")
 
 
 def _fp8_full_size(n, cp, hq, hkv, d, rank, modes, seed):
@@ -373,7 +374,8 @@ def _fp8_full_size(n, cp, hq, hkv, d, rank, modes, seed):
     qf = torch.zeros(n, hq, d)
     qf[torch.from_numpy(O.zigzag_rows(n, rank, cp))] = q8.float().cpu() * sq
     for mode, out in outs.items():
-        _check_sampled(out, rank, cp, n, qf, kf, vf, scale_for(d), TOL_FP8_OUT, seed=rank + 10)
+        err = _check_sampled(out, rank, cp, n, qf, kf, vf, scale_for(d), TOL_FP8_OUT, seed=rank + 10)
+        say(f"  e4m3 n={n} d={d} rank {rank} {mode}: sampled max |err| {err:.3e} (bar {TOL_FP8_OUT})")
 
 
 @pytest.mark.parametrize("rank", [0, 3, 7])
@@ -419,4 +421,5 @@ def test_ring_c4_varlen_full_size(rank):
             o, _ = O.dense_causal_rows(qc, kc, vc, [g], [hh], scale_for(d), seq_start=full_cu[j])
             exp.append(o[0])
         err = float((got - torch.stack(exp)).abs().max())
+        say(f"  C4 rank {rank} {mode}: sampled max |err| {err:.3e} (bar {TOL_BF16_OUT})")
         assert err <= TOL_BF16_OUT, f"{mode}: {err}"
