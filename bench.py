@@ -376,7 +376,7 @@ def main():
                          "H_kv=2, D=256 sweep")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (one rank's sweep with every source "
+        print(f"bench.py: measures one GPU only (one rank's sweep with every source "
               f"rank's KV resident in HBM); --gpus {args.gpus} is not supported", file=sys.stderr)
         return 2
     if args.workload == "c5":

@@ -105,7 +105,7 @@ def ring_flash_attn(
     One sequence per rank: leave ``cu_seqlens=None``.  Packed sequences: pass the LOCAL
     ``cu_seqlens`` (each entry a zig-zag ``2*h_j`` shard length) on the device and
     ``max_seqlen``.  For cp_size > 1 ``group`` must be a LocalKVRing holding every source
-    rank's KV shard (this build does not move KV between GPUs)."""
+    rank's KV shard (KV is not moved between GPUs here)."""
     S = cfg.cp_size
     rank = cfg.cp_rank
     scale = cfg.softmax_scale

@@ -2,7 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product (the ``fa4_ring`` package and its HIP
 library) may import, call or link this module; only ``tests/``, ``__graft_entry__.smoke()``
-and the ``cpu_baseline`` leg of ``bench.py`` use it, and only as the checker.
+and the ``cpu_baseline`` leg of ``bench.py`` use it, to check results or as the timed CPU
+baseline.
 
 It restates the reference's own CPU algorithm (hxy0118/fa4-cp) in fp32 torch on the CPU:
 
