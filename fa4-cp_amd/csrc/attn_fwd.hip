@@ -2486,7 +2486,7 @@ static bool tile_offsets_fit(int64_t row_stride, int esz, int d, int64_t vt_d_st
 extern "C" int fa4cp_attn_fwd(const fa4cp_attn_args* a, void* stream) {
   clear_error();
   if (a == nullptr) return set_error(FA4CP_EINVAL, "attn_fwd: null args");
-  if (!a->q || !a->k || !a->v || !a->out || !a->lse)
+  if (a->total_q > 0 && (!a->q || !a->k || !a->v || !a->out || !a->lse))  // NULL only with no query rows
     return set_error(FA4CP_EINVAL, "attn_fwd: null tensor pointer");
   if (a->h_q <= 0 || a->h_kv <= 0 || a->h_q % a->h_kv != 0)
     return set_error(FA4CP_EINVAL, "attn_fwd: h_q=%d must be a positive multiple of h_kv=%d",
@@ -2563,7 +2563,7 @@ extern "C" int fa4cp_attn_fwd(const fa4cp_attn_args* a, void* stream) {
   p.n_rt = (max_q + kc.rows - 1) / kc.rows;
   p.n_hg = a->h_kv * (group / hp);
   const int64_t blocks = (int64_t)p.n_hg * nseq * p.n_rt;
-  if (blocks == 0) return FA4CP_OK;
+  if (blocks == 0 || a->total_q == 0) return FA4CP_OK;
   if (blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "attn_fwd: grid too large");
   p.n_blocks = (int)blocks;
   hipLaunchKernelGGL(kc.fn, dim3((unsigned)blocks), dim3(kc.threads), 0, (hipStream_t)stream, p);
@@ -2572,13 +2572,14 @@ extern "C" int fa4cp_attn_fwd(const fa4cp_attn_args* a, void* stream) {
 
 extern "C" int fa4cp_ring_sweep_fwd(const fa4cp_sweep_args* a, void* stream) {
   clear_error();
-  if (a == nullptr || !a->q || !a->out || !a->lse)
-    return set_error(FA4CP_EINVAL, "ring_sweep_fwd: null pointer");
+  if (a == nullptr) return set_error(FA4CP_EINVAL, "ring_sweep_fwd: null args");
+  const bool empty = a->total == 0;  // no rows: every pointer may be NULL
+  if (!empty && (!a->q || !a->out || !a->lse)) return set_error(FA4CP_EINVAL, "ring_sweep_fwd: null pointer");
   if (a->cp_size < 1 || a->cp_size > FA4CP_MAX_CP || a->cp_rank < 0 || a->cp_rank >= a->cp_size)
     return set_error(FA4CP_EINVAL, "ring_sweep_fwd: cp_rank %d / cp_size %d out of range (cp_size <= %d)",
                      a->cp_rank, a->cp_size, FA4CP_MAX_CP);
   for (int i = 0; i < a->cp_size; ++i)
-    if (!a->k[i] || !a->v_t[i]) return set_error(FA4CP_EINVAL, "ring_sweep_fwd: null K / V^T of source %d", i);
+    if (!empty && (!a->k[i] || !a->v_t[i])) return set_error(FA4CP_EINVAL, "ring_sweep_fwd: null K / V^T of source %d", i);
   if (a->h_q <= 0 || a->h_kv <= 0 || a->h_q % a->h_kv != 0)
     return set_error(FA4CP_EINVAL, "ring_sweep_fwd: h_q=%d must be a positive multiple of h_kv=%d", a->h_q, a->h_kv);
   const int nseq = a->cu ? a->nseq : 1;
@@ -2631,7 +2632,7 @@ extern "C" int fa4cp_ring_sweep_fwd(const fa4cp_sweep_args* a, void* stream) {
   p.n_rt = (max_len + rows - 1) / rows;
   p.n_hg = a->h_kv * (group / hp);
   const int64_t blocks = (int64_t)p.n_hg * nseq * p.n_rt;
-  if (blocks == 0) return FA4CP_OK;
+  if (blocks == 0 || empty) return FA4CP_OK;
   if (blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "ring_sweep_fwd: grid too large");
   p.n_blocks = (int)blocks;
   void (*fn)(SweepParams) = nullptr;

@@ -175,7 +175,7 @@ extern "C" int fa4cp_merge_state_inplace(void* v, float* s, const void* v_other,
                                          int32_t d, int32_t dtype, const int32_t* cu,
                                          int32_t nseq, int32_t row_sel, void* stream) {
   clear_error();
-  if (!v || !s || !v_other || !s_other)
+  if (rows > 0 && (!v || !s || !v_other || !s_other))  // NULL only with no rows
     return set_error(FA4CP_EINVAL, "merge_state_inplace: null pointer");
   if (rows < 0 || h <= 0 || d <= 0 || (d % 8) != 0)
     return set_error(FA4CP_EINVAL, "merge_state_inplace: bad shape rows=%lld h=%d d=%d "
@@ -219,7 +219,8 @@ extern "C" int fa4cp_merge_states(const void* v, const float* s, void* v_out, fl
                                   int64_t rows, int32_t num_states, int32_t h, int32_t d,
                                   int32_t dtype, void* stream) {
   clear_error();
-  if (!v || !s || !v_out) return set_error(FA4CP_EINVAL, "merge_states: null pointer");
+  if (rows > 0 && (!v || !s || !v_out))  // NULL only with no rows
+    return set_error(FA4CP_EINVAL, "merge_states: null pointer");
   if (rows < 0 || num_states <= 0 || h <= 0 || d <= 0 || (d % 8) != 0)
     return set_error(FA4CP_EINVAL, "merge_states: bad shape rows=%lld states=%d h=%d d=%d",
                      (long long)rows, num_states, h, d);

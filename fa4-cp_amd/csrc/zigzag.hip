@@ -146,7 +146,8 @@ extern "C" int fa4cp_zigzag_shard(const void* src_full, void* dst_local, int64_t
                                   const int32_t* full_cu, int32_t nseq, int64_t total_full,
                                   int32_t cp_rank, int32_t cp_size, void* stream) {
   clear_error();
-  if (!src_full || !dst_local) return set_error(FA4CP_EINVAL, "zigzag_shard: null pointer");
+  if (total_full > 0 && (!src_full || !dst_local))  // NULL only with no rows
+    return set_error(FA4CP_EINVAL, "zigzag_shard: null pointer");
   int rc = check_zigzag_args(row_bytes, nseq, total_full, cp_size, full_cu, "zigzag_shard");
   if (rc) return rc;
   if (cp_rank < 0 || cp_rank >= cp_size)
@@ -179,13 +180,14 @@ extern "C" int fa4cp_zigzag_unshard(const void* const* shard_ptrs, void* dst_ful
                                     int64_t row_bytes, const int32_t* full_cu, int32_t nseq,
                                     int64_t total_full, int32_t cp_size, void* stream) {
   clear_error();
-  if (!shard_ptrs || !dst_full) return set_error(FA4CP_EINVAL, "zigzag_unshard: null pointer");
+  if (!shard_ptrs || (total_full > 0 && !dst_full))  // the tensors may be NULL with no rows
+    return set_error(FA4CP_EINVAL, "zigzag_unshard: null pointer");
   int rc = check_zigzag_args(row_bytes, nseq, total_full, cp_size, full_cu, "zigzag_unshard");
   if (rc) return rc;
   ShardTable tab = {};
   uintptr_t bits = (uintptr_t)dst_full;
   for (int r = 0; r < cp_size; ++r) {
-    if (!shard_ptrs[r]) return set_error(FA4CP_EINVAL, "zigzag_unshard: shard %d is null", r);
+    if (total_full > 0 && !shard_ptrs[r]) return set_error(FA4CP_EINVAL, "zigzag_unshard: shard %d is null", r);
     tab.p[r] = (const char*)shard_ptrs[r];
     bits |= (uintptr_t)shard_ptrs[r];
   }

@@ -7,6 +7,9 @@
  *   - nothing here allocates device memory, and nothing synchronises the host: every
  *     kernel is launched on the hipStream_t passed as `stream` (NULL = legacy default
  *     stream) and the call returns as soon as the launch is queued;
+ *   - a call with no rows to process (total_q, total, rows or total_full of 0) launches
+ *     nothing and returns 0; the pointers of its empty tensors may then be NULL (torch
+ *     hands out NULL for zero-element tensors);
  *   - the return value is 0 on success and a negative FA4CP_E* code otherwise; the
  *     message for the last failure on the calling thread is in fa4cp_last_error();
  *   - the library keeps no state besides that thread-local message, so every entry point

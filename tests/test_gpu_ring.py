@@ -423,3 +423,48 @@ def test_ring_c4_varlen_full_size(rank):
         err = float((got - torch.stack(exp)).abs().max())
         say(f"  C4 rank {rank} {mode}: sampled max |err| {err:.3e} (bar {TOL_BF16_OUT})")
         assert err <= TOL_BF16_OUT, f"{mode}: {err}"
+
+
+EMPTY_CASES = [(torch.bfloat16, p) for p in PATHS] + [(torch.float8_e4m3fn, "fused"),
+                                                       (torch.float8_e4m3fn, "incremental")]
+
+
+@pytest.mark.parametrize("packed", [False, True])
+@pytest.mark.parametrize("dtype,path", EMPTY_CASES)
+def test_ring_empty_shard(dtype, path, packed):
+    """A rank with no rows (N = 0, or packed sequences that are all empty) gets an empty out
+    of the output type: every kernel call sees no rows and launches nothing."""
+    say(f"ring empty shard {dtype} path={path} packed={packed}")
+    cp, rank, h, hkv, d = 4, 1, 8, 2, 128
+    q = torch.empty(0, h, d, dtype=dtype, device=DEV)
+    k = torch.empty(0, hkv, d, dtype=dtype, device=DEV)
+    cfg, fused = _cfg_path(path, cp, rank)
+    kw = dict(cu_seqlens=torch.zeros(3, dtype=torch.int32, device=DEV), max_seqlen=0) if packed else {}
+    out = ring_flash_attn(q, k, k, cfg, group=LocalKVRing([k] * cp, [k] * cp), fused=fused, **kw)
+    torch.cuda.synchronize()
+    assert out.shape == (0, h, d)
+    assert out.dtype == (torch.bfloat16 if dtype == torch.float8_e4m3fn else dtype)
+
+
+def test_empty_operators():
+    """The operator level on zero rows: zig-zag shard / unshard (one and packed sequences),
+    fa4_attn, both merges, all returning empty results."""
+    from fa4_ring.fa4_backend import fa4_attn
+    from fa4_ring.merge import merge_state_in_place, merge_states
+
+    say("operators on zero rows")
+    x = torch.empty(0, 4, 64, dtype=torch.bfloat16, device=DEV)
+    shards = [zigzag_shard(x, r, 4) for r in range(4)]
+    assert all(s.shape == (0, 4, 64) for s in shards)
+    assert zigzag_unshard(shards, 4).shape == (0, 4, 64)
+    local, local_cu = zigzag_shard_varlen(x, [0, 0, 0], 1, 4)
+    assert local.shape == (0, 4, 64) and local_cu.tolist() == [0, 0, 0]
+    kv = torch.empty(0, 2, 64, dtype=torch.bfloat16, device=DEV)
+    out, lse = fa4_attn(x, kv, kv, causal=True)
+    assert out.shape == (0, 4, 64) and lse.shape == (0, 4)
+    acc, acc_lse = out.clone(), lse.clone()
+    merge_state_in_place(acc, acc_lse, out, lse)
+    v, s = merge_states(torch.empty(0, 3, 4, 64, dtype=torch.bfloat16, device=DEV),
+                        torch.empty(0, 3, 4, dtype=torch.float32, device=DEV))
+    torch.cuda.synchronize()
+    assert v.shape == (0, 4, 64) and s.shape == (0, 4)

@@ -47,10 +47,47 @@ def test_error_path_reports_message_without_gpu():
     rc = lib.fa4cp_zigzag_shard(1, 1, 16, None, 1, 10, 0, 4, None)
     assert rc == -1 and b"divisible" in lib.fa4cp_last_error()
     a = _lib.AttnArgs()
+    a.total_q = 1
     rc = lib.fa4cp_attn_fwd(ctypes.byref(a), None)
     assert rc == -1 and b"null tensor" in lib.fa4cp_last_error()
     with pytest.raises(RuntimeError, match="null tensor"):
         _lib.check(rc, "fa4cp_attn_fwd")
+
+
+def test_empty_calls_launch_nothing_and_take_null_pointers():
+    """A call with no rows returns 0 before any HIP call, whatever the pointers of its empty
+    tensors (torch gives NULL for zero-element tensors); with rows, NULL is still an error."""
+    lib = _lib.load()
+    bf16 = _lib.dtype_code(torch.bfloat16)
+    a = _lib.AttnArgs()
+    a.q_row_stride, a.q_head_stride = 8 * 128, 128
+    a.k_row_stride, a.k_head_stride = 2 * 128, 128
+    a.v_row_stride, a.v_head_stride = 2 * 128, 128
+    a.o_row_stride, a.o_head_stride = 8 * 128, 128
+    a.lse_row_stride = 8
+    a.h_q, a.h_kv, a.d, a.dtype, a.causal = 8, 2, 128, bf16, 1
+    assert lib.fa4cp_attn_fwd(ctypes.byref(a), None) == 0
+    a.total_q = a.total_k = 64
+    assert lib.fa4cp_attn_fwd(ctypes.byref(a), None) == -1 and b"null" in lib.fa4cp_last_error()
+
+    s = _lib.SweepArgs()
+    s.q_row_stride, s.q_head_stride = 8 * 128, 128
+    s.o_row_stride, s.o_head_stride = 8 * 128, 128
+    s.lse_row_stride = 8
+    s.k_row_stride, s.k_head_stride = 2 * 128, 128
+    s.vt_d_stride = int(lib.fa4cp_vt_min_d_stride(0, 1))
+    s.h_q, s.h_kv, s.d, s.dtype = 8, 2, 128, bf16
+    s.cp_rank, s.cp_size, s.softmax_scale = 1, 4, 0.1
+    assert lib.fa4cp_ring_sweep_fwd(ctypes.byref(s), None) == 0
+    s.total = 64
+    assert lib.fa4cp_ring_sweep_fwd(ctypes.byref(s), None) == -1 and b"null" in lib.fa4cp_last_error()
+
+    for rows, want in ((0, 0), (4, -1)):
+        assert lib.fa4cp_merge_state_inplace(None, None, None, None, rows, 8, 128, bf16, None, 0, 0, None) == want
+        assert lib.fa4cp_merge_states(None, None, None, None, rows, 2, 8, 128, bf16, None) == want
+    for n, want in ((0, 0), (64, -1)):
+        assert lib.fa4cp_zigzag_shard(None, None, 256, None, 1, n, 0, 4, None) == want
+        assert lib.fa4cp_zigzag_unshard((ctypes.c_void_p * 4)(), None, 256, None, 1, n, 4, None) == want
 
 
 def test_sweep_entry_point_validates_before_launching():
