@@ -18,19 +18,35 @@ namespace {
 constexpr int kTK = 64;      // keys per workgroup
 constexpr int kTBlock = 256;
 
-// The tensors of one launch (blockIdx.y picks one).
+// The tensors of one launch (blockIdx.y picks one).  pt[i] != NULL: v[i] is a paged cache
+// and pt[i] its page table (fa4cp_paged_args).
 struct TransposeSet {
   const void* v[FA4CP_MAX_CP];
   void* vt[FA4CP_MAX_CP];
+  const int32_t* pt[FA4CP_MAX_CP];
 };
+
+// Page geometry of a paged launch.
+struct PageGeo {
+  int page_size, num_pages;
+  int64_t pt_stride;
+};
+
+// First cache row of rows [r0, r0 + n) of sequence `seq` (n <= page_size, r0 % n == 0, so
+// they share one page), or -1 when the table entry names no page of the cache.
+__device__ __forceinline__ int64_t paged_row(const int32_t* pt, const PageGeo& g, int seq, int r0) {
+  const int page = pt[(int64_t)seq * g.pt_stride + r0 / g.page_size];
+  return page >= 0 && page < g.num_pages ? (int64_t)page * g.page_size + r0 % g.page_size : -1;
+}
 
 __device__ __forceinline__ int round_up_pad(int n) { return (n + kVtPad - 1) / kVtPad * kVtPad; }
 
 template <typename T, int D>
 __global__ __launch_bounds__(kTBlock) void transpose_v_kernel(
     TransposeSet set, int64_t v_rs, int64_t v_hs, const int32_t* __restrict__ cu, int nseq,
-    int total_k, int sel, int n_kt, int64_t vt_ds) {
+    int total_k, int sel, int n_kt, int64_t vt_ds, PageGeo pg) {
   const T* __restrict__ v = reinterpret_cast<const T*>(set.v[blockIdx.y]);
+  const int32_t* __restrict__ pt = set.pt[blockIdx.y];
   T* __restrict__ vt = reinterpret_cast<T*>(set.vt[blockIdx.y]);
   constexpr int E = 16 / sizeof(T);  // elements per 16-byte unit
   constexpr int PITCH = D + E;       // LDS row pitch in elements (one unit of padding)
@@ -48,12 +64,15 @@ __global__ __launch_bounds__(kTBlock) void transpose_v_kernel(
   const int64_t P = vt_seq_start(cu, seq, sel);
 
   const int tid = threadIdx.x;
+  // cache row of key k0 (paged: the tile's kTK keys lie in one page); -1: zeros
+  int64_t row0 = s + k0;
+  if (pt != nullptr) row0 = k0 < L ? paged_row(pt, pg, seq, k0) : -1;
   // load kTK key rows (zeros past the sequence's end)
   for (int c = tid; c < kTK * (D / E); c += kTBlock) {
     const int key = c / (D / E), u = c % (D / E);
     u32x4 x = {0u, 0u, 0u, 0u};
-    if (k0 + key < L)
-      x = *reinterpret_cast<const u32x4*>(v + (int64_t)(s + k0 + key) * v_rs + (int64_t)kvh * v_hs + E * u);
+    if (k0 + key < L && row0 >= 0)
+      x = *reinterpret_cast<const u32x4*>(v + (row0 + key) * v_rs + (int64_t)kvh * v_hs + E * u);
     *reinterpret_cast<u32x4*>(tile + key * PITCH + E * u) = x;
   }
   __syncthreads();
@@ -72,21 +91,22 @@ __global__ __launch_bounds__(kTBlock) void transpose_v_kernel(
 }
 
 template <typename T>
-int launch(const fa4cp_transpose_args& a, const TransposeSet& set, int count, int n_kt, hipStream_t st) {
+int launch(const fa4cp_transpose_args& a, const TransposeSet& set, int count, int n_kt, hipStream_t st,
+           PageGeo pg = PageGeo{1, 0, 0}) {
   const int nseq = a.cu_k ? a.nseq : 1;
   const dim3 grid((unsigned)(n_kt * nseq * a.h_kv), (unsigned)count);
   switch (a.d) {
     case 64:
       hipLaunchKernelGGL((transpose_v_kernel<T, 64>), grid, dim3(kTBlock), 0, st, set, a.v_row_stride,
-                         a.v_head_stride, a.cu_k, nseq, a.total_k, a.k_sel, n_kt, a.vt_d_stride);
+                         a.v_head_stride, a.cu_k, nseq, a.total_k, a.k_sel, n_kt, a.vt_d_stride, pg);
       break;
     case 128:
       hipLaunchKernelGGL((transpose_v_kernel<T, 128>), grid, dim3(kTBlock), 0, st, set, a.v_row_stride,
-                         a.v_head_stride, a.cu_k, nseq, a.total_k, a.k_sel, n_kt, a.vt_d_stride);
+                         a.v_head_stride, a.cu_k, nseq, a.total_k, a.k_sel, n_kt, a.vt_d_stride, pg);
       break;
     case 256:
       hipLaunchKernelGGL((transpose_v_kernel<T, 256>), grid, dim3(kTBlock), 0, st, set, a.v_row_stride,
-                         a.v_head_stride, a.cu_k, nseq, a.total_k, a.k_sel, n_kt, a.vt_d_stride);
+                         a.v_head_stride, a.cu_k, nseq, a.total_k, a.k_sel, n_kt, a.vt_d_stride, pg);
       break;
     default:
       return set_error(FA4CP_EUNSUPPORTED, "transpose_v: head dim %d not supported", a.d);
@@ -94,10 +114,69 @@ int launch(const fa4cp_transpose_args& a, const TransposeSet& set, int count, in
   return check_launch("transpose_v");
 }
 
+// Paged cache rows -> contiguous rows (fa4cp_gather_kv_pages), 16-byte units.
+constexpr int kGRows = 64;  // rows per workgroup (inside one page)
+
+struct GatherSet {
+  const void* src[FA4CP_MAX_CP];
+  void* dst[FA4CP_MAX_CP];
+  const int32_t* pt[FA4CP_MAX_CP];
+};
+
+// Workgroup (sequence, row block) of tensor blockIdx.y; strides in bytes; uph = 16-byte
+// units per head row (a power of two, 1 << uph_log2).
+__global__ __launch_bounds__(kTBlock) void gather_pages_kernel(GatherSet set, int64_t c_rs, int64_t c_hs,
+                                                               int64_t d_rs, int64_t d_hs,
+                                                               const int32_t* __restrict__ cu, int total,
+                                                               int n_rb, PageGeo pg, int h_kv, int uph_log2) {
+  const int seq = blockIdx.x / n_rb;
+  const int r0 = (blockIdx.x - seq * n_rb) * kGRows;
+  int s, L;
+  seq_range(cu, seq, total, FA4CP_SEL_ALL, s, L);
+  if (r0 >= L) return;
+  const int64_t row0 = paged_row(set.pt[blockIdx.y], pg, seq, r0);
+  const char* __restrict__ src = reinterpret_cast<const char*>(set.src[blockIdx.y]);
+  char* __restrict__ dst = reinterpret_cast<char*>(set.dst[blockIdx.y]) + (int64_t)(s + r0) * d_rs;
+  const int rows = min(kGRows, L - r0);
+  const int per_row = h_kv << uph_log2;
+  for (int c = threadIdx.x; c < rows * per_row; c += kTBlock) {
+    const int r = c / per_row, w = c - r * per_row;
+    const int h = w >> uph_log2, u = w & ((1 << uph_log2) - 1);
+    u32x4 x = {0u, 0u, 0u, 0u};
+    if (row0 >= 0) x = *reinterpret_cast<const u32x4*>(src + (row0 + r) * c_rs + h * c_hs + 16 * u);
+    *reinterpret_cast<u32x4*>(dst + r * d_rs + h * d_hs + 16 * u) = x;
+  }
+}
+
 }  // namespace
 }  // namespace fa4cp
 
 using namespace fa4cp;
+
+// Checks what the paged calls share; returns 0 or a negative status.
+static int paged_check(const fa4cp_paged_args* a, int count, int& esize, const char* who) {
+  if (count < 1 || count > FA4CP_MAX_CP)
+    return set_error(FA4CP_EINVAL, "%s: count %d out of [1, %d]", who, count, FA4CP_MAX_CP);
+  if (a->h_kv <= 0 || a->d <= 0 || a->total < 0 || a->max_seqlen < 0 || a->num_pages < 0)
+    return set_error(FA4CP_EINVAL, "%s: bad shape", who);
+  if (a->cu != nullptr && a->nseq < 1) return set_error(FA4CP_EINVAL, "%s: nseq must be >= 1 with cu", who);
+  if (a->page_size <= 0 || a->page_size % kVtPad != 0)
+    return set_error(FA4CP_EINVAL, "%s: page_size %d must be a positive multiple of %d", who, a->page_size, kVtPad);
+  const int max_len = a->cu ? a->max_seqlen : a->total;
+  if (a->pt_stride < (max_len + a->page_size - 1) / a->page_size)
+    return set_error(FA4CP_EINVAL, "%s: pt_stride %lld holds fewer pages than a sequence of %d rows needs", who,
+                     (long long)a->pt_stride, max_len);
+  switch (a->dtype) {
+    case FA4CP_BF16: case FA4CP_FP16: esize = 2; break;
+    case FA4CP_E4M3: esize = 1; break;
+    case FA4CP_FP32: esize = 4; break;
+    default: return set_error(FA4CP_EUNSUPPORTED, "%s: unsupported dtype %d", who, a->dtype);
+  }
+  if ((a->cache_row_stride * esize) % 16 != 0 || (a->cache_head_stride * esize) % 16 != 0 ||
+      a->cache_row_stride <= 0 || a->cache_head_stride <= 0)
+    return set_error(FA4CP_EINVAL, "%s: cache strides must be positive and 16-byte aligned", who);
+  return 0;
+}
 
 // Checks the shared arguments of a transpose; returns the key tiles per sequence (0: nothing
 // to do) or a negative status.
@@ -126,7 +205,8 @@ static int transpose_check(const fa4cp_transpose_args* a, int& esize) {
   return n_kt;
 }
 
-static int transpose_launch(const fa4cp_transpose_args* a, const TransposeSet& set, int count, void* stream) {
+static int transpose_launch(const fa4cp_transpose_args* a, const TransposeSet& set, int count, void* stream,
+                            PageGeo pg = PageGeo{1, 0, 0}) {
   int esize = 0;
   const int n_kt = transpose_check(a, esize);
   if (n_kt <= 0) return n_kt;
@@ -136,7 +216,7 @@ static int transpose_launch(const fa4cp_transpose_args* a, const TransposeSet& s
       return set_error(FA4CP_EINVAL, "transpose_v: v / v_t and the v strides must be 16-byte aligned");
   }
   hipStream_t st = (hipStream_t)stream;
-  return esize == 1 ? launch<uint8_t>(*a, set, count, n_kt, st) : launch<uint16_t>(*a, set, count, n_kt, st);
+  return esize == 1 ? launch<uint8_t>(*a, set, count, n_kt, st, pg) : launch<uint16_t>(*a, set, count, n_kt, st, pg);
 }
 
 extern "C" int64_t fa4cp_vt_min_d_stride(int32_t total_k, int32_t nseq) {
@@ -164,4 +244,76 @@ extern "C" int fa4cp_transpose_v_many(const fa4cp_transpose_args* a, const void*
     set.vt[i] = v_t[i];
   }
   return transpose_launch(a, set, count, stream);
+}
+
+extern "C" int fa4cp_transpose_v_paged_many(const fa4cp_paged_args* a, const void* const* v_cache,
+                                            const int32_t* const* page_table, void* const* v_t, int64_t vt_d_stride,
+                                            int32_t count, void* stream) {
+  clear_error();
+  if (a == nullptr || v_cache == nullptr || page_table == nullptr || v_t == nullptr)
+    return set_error(FA4CP_EINVAL, "transpose_v_paged: null pointer");
+  int esize = 0;
+  if (int rc = paged_check(a, count, esize, "transpose_v_paged")) return rc;
+  if (esize == 4) return set_error(FA4CP_EUNSUPPORTED, "transpose_v_paged: FP32 not supported");
+  fa4cp_transpose_args t{};
+  t.v_row_stride = a->cache_row_stride;
+  t.v_head_stride = a->cache_head_stride;
+  t.cu_k = a->cu;
+  t.nseq = a->nseq;
+  t.total_k = a->total;
+  t.max_seqlen_k = a->max_seqlen;
+  t.k_sel = FA4CP_SEL_ALL;
+  t.h_kv = a->h_kv;
+  t.d = a->d;
+  t.dtype = a->dtype;
+  t.vt_d_stride = vt_d_stride;
+  TransposeSet set{};
+  for (int i = 0; i < count; ++i) {
+    if (a->total > 0 && page_table[i] == nullptr)
+      return set_error(FA4CP_EINVAL, "transpose_v_paged: page table %d is null", i);
+    set.v[i] = v_cache[i];
+    set.vt[i] = v_t[i];
+    set.pt[i] = page_table[i];
+  }
+  return transpose_launch(&t, set, count, stream, PageGeo{a->page_size, a->num_pages, a->pt_stride});
+}
+
+extern "C" int fa4cp_gather_kv_pages(const fa4cp_paged_args* a, const void* const* cache,
+                                     const int32_t* const* page_table, void* const* dst, int64_t dst_row_stride,
+                                     int64_t dst_head_stride, int32_t count, void* stream) {
+  clear_error();
+  if (a == nullptr || cache == nullptr || page_table == nullptr || dst == nullptr)
+    return set_error(FA4CP_EINVAL, "gather_kv_pages: null pointer");
+  int esize = 0;
+  if (int rc = paged_check(a, count, esize, "gather_kv_pages")) return rc;
+  const int64_t row_unit_bytes = (int64_t)a->d * esize;
+  if (row_unit_bytes % 16 != 0 || ((row_unit_bytes / 16) & (row_unit_bytes / 16 - 1)) != 0)
+    return set_error(FA4CP_EUNSUPPORTED, "gather_kv_pages: d * element size = %lld bytes (16 x a power of two)",
+                     (long long)row_unit_bytes);
+  if (dst_row_stride <= 0 || dst_head_stride <= 0 || (dst_row_stride * esize) % 16 != 0 ||
+      (dst_head_stride * esize) % 16 != 0)
+    return set_error(FA4CP_EINVAL, "gather_kv_pages: dst strides must be positive and 16-byte aligned");
+  const int nseq = a->cu ? a->nseq : 1;
+  const int max_len = a->cu ? a->max_seqlen : a->total;
+  if (a->total == 0 || max_len == 0) return FA4CP_OK;
+  GatherSet set{};
+  for (int i = 0; i < count; ++i) {
+    if (!cache[i] || !page_table[i] || !dst[i]) return set_error(FA4CP_EINVAL, "gather_kv_pages: null tensor %d", i);
+    if ((reinterpret_cast<uintptr_t>(cache[i]) | reinterpret_cast<uintptr_t>(dst[i])) % 16 != 0)
+      return set_error(FA4CP_EINVAL, "gather_kv_pages: tensors must be 16-byte aligned");
+    set.src[i] = cache[i];
+    set.dst[i] = dst[i];
+    set.pt[i] = page_table[i];
+  }
+  const int n_rb = (max_len + kGRows - 1) / kGRows;
+  const int64_t blocks = (int64_t)nseq * n_rb;
+  if (blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "gather_kv_pages: too many rows");
+  int uph_log2 = 0;
+  while ((16LL << uph_log2) < row_unit_bytes) ++uph_log2;
+  const PageGeo pg{a->page_size, a->num_pages, a->pt_stride};
+  hipLaunchKernelGGL(gather_pages_kernel, dim3((unsigned)blocks, (unsigned)count), dim3(kTBlock), 0,
+                     (hipStream_t)stream, set, a->cache_row_stride * esize, a->cache_head_stride * esize,
+                     dst_row_stride * esize, dst_head_stride * esize, a->cu, a->total, n_rb, pg, a->h_kv,
+                     uph_log2);
+  return check_launch("gather_kv_pages");
 }

@@ -8,12 +8,14 @@ Public API (the reference package's names):
     IncrementalMerger / BatchedMerger / make_merger   online-softmax mergers
 and, for the single-GPU ring:
     LocalKVRing         every source rank's KV shard resident in HBM
+    PagedKVRing         every source rank's paged K/V cache (fused sweep)
     quantize_e4m3 / quantize_ring   the FP8 producer (e4m3 shards and their descales)
 """
 
 from .config import RingConfig
 from .fp8 import quantize_e4m3, quantize_ring
 from .merge import BatchedMerger, IncrementalMerger, make_merger
+from .paged import PagedKVRing
 from .ring_attention import Descales, LocalKVRing, ring_flash_attn
 from .zigzag import zigzag_shard, zigzag_unshard
 
@@ -22,6 +24,7 @@ __all__ = [
     "ring_flash_attn",
     "Descales",
     "LocalKVRing",
+    "PagedKVRing",
     "zigzag_shard",
     "zigzag_unshard",
     "IncrementalMerger",

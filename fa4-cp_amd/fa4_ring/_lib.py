@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libfa4cp.so"
 # FA4CP_LIB selects another build of the library (the in-tree one by default)
 LIB_PATH = os.environ.get("FA4CP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # element types (FA4CP_*)
 BF16, FP16, E4M3, FP32 = 0, 1, 2, 3
@@ -147,8 +147,36 @@ class SweepArgs(ctypes.Structure):
     ]
 
 
+class PagedArgs(ctypes.Structure):
+    """Mirror of fa4cp_paged_args."""
+    _fields_ = [
+        ("cu", ctypes.c_void_p),
+        ("nseq", ctypes.c_int32),
+        ("max_seqlen", ctypes.c_int32),
+        ("total", ctypes.c_int32),
+        ("h_kv", ctypes.c_int32),
+        ("d", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("num_pages", ctypes.c_int32),
+        ("cache_row_stride", ctypes.c_int64),
+        ("cache_head_stride", ctypes.c_int64),
+        ("pt_stride", ctypes.c_int64),
+    ]
+
+
 # exported symbol -> (restype, argtypes)
 SIGNATURES = {
+    "fa4cp_gather_kv_pages": (
+        ctypes.c_int,
+        [ctypes.POINTER(PagedArgs), ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p),
+         ctypes.POINTER(ctypes.c_void_p), ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p],
+    ),
+    "fa4cp_transpose_v_paged_many": (
+        ctypes.c_int,
+        [ctypes.POINTER(PagedArgs), ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p),
+         ctypes.POINTER(ctypes.c_void_p), ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p],
+    ),
     "fa4cp_attn_fwd": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
     "fa4cp_merge_state_inplace": (
         ctypes.c_int,

@@ -37,6 +37,7 @@ from .config import RingConfig
 from .fa4_backend import (SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, _norm_descale, fa4_attn, out_dtype_for,
                           transpose_v, transpose_v_many, uses_vt)
 from .merge import merge_state_in_place, merge_states
+from .paged import PagedKVRing, gather_kv_pages, transpose_v_paged_many
 from .zigzag import zigzag_shard, zigzag_shard_varlen
 
 
@@ -83,11 +84,11 @@ class LocalKVRing:
 
 def ring_flash_attn(
     local_q: torch.Tensor,  # [T, H, D] zig-zag local shard (T = sum of 2*h_j)
-    local_k: torch.Tensor,  # [T, H_kv, D]
-    local_v: torch.Tensor,  # [T, H_kv, D]
+    local_k: Optional[torch.Tensor],  # [T, H_kv, D] (None with a PagedKVRing)
+    local_v: Optional[torch.Tensor],  # [T, H_kv, D] (None with a PagedKVRing)
     cfg: RingConfig,
     *,
-    group: Optional[LocalKVRing] = None,
+    group=None,  # LocalKVRing or PagedKVRing holding every source rank's K/V
     descales: Optional[Descales] = None,
     cu_seqlens: Optional[torch.Tensor] = None,  # local int32 [num_seq+1]; None -> one sequence
     max_seqlen: Optional[int] = None,
@@ -105,7 +106,9 @@ def ring_flash_attn(
     One sequence per rank: leave ``cu_seqlens=None``.  Packed sequences: pass the LOCAL
     ``cu_seqlens`` (each entry a zig-zag ``2*h_j`` shard length) on the device and
     ``max_seqlen``.  For cp_size > 1 ``group`` must be a LocalKVRing holding every source
-    rank's KV shard (KV is not moved between GPUs here)."""
+    rank's KV shard (KV is not moved between GPUs here), or a PagedKVRing holding every
+    source's paged K/V cache (fused sweep only; the rank's own K/V come from it, so
+    ``local_k`` / ``local_v`` are ignored)."""
     S = cfg.cp_size
     rank = cfg.cp_rank
     scale = cfg.softmax_scale
@@ -114,11 +117,14 @@ def ring_flash_attn(
         assert max_seqlen is not None, "max_seqlen required when cu_seqlens is given"
     else:
         max_seqlen = total
-    if S > 1:
+    paged = isinstance(group, PagedKVRing)
+    if paged:
+        assert group.cp_size == S, f"PagedKVRing holds {group.cp_size} caches, cp_size is {S}"
+    elif S > 1:
         if not isinstance(group, LocalKVRing):
             raise RuntimeError(
-                "ring_flash_attn: cp_size > 1 needs group=LocalKVRing(k_shards, v_shards); "
-                "KV rotation between GPUs is not part of this single-GPU build")
+                "ring_flash_attn: cp_size > 1 needs group=LocalKVRing(k_shards, v_shards) or a "
+                "PagedKVRing: every source rank's K/V on this GPU (no KV rotation between GPUs)")
         assert group.cp_size == S, f"LocalKVRing holds {group.cp_size} shards, cp_size is {S}"
 
     d = local_q.shape[2]
@@ -126,6 +132,11 @@ def ring_flash_attn(
     can_fuse = 1 < S <= _lib.MAX_CP and (
         (descales is None and local_q.dtype in (torch.bfloat16, torch.float16) and d in (64, 128))
         or (e4m3 and d in (128, 256)))
+    if paged:
+        if fused is False or not can_fuse:
+            raise AssertionError("paged K/V caches run the fused sweep only (cp_size in [2, 16]; bf16/fp16 "
+                                 "with head dim 64/128 and no descales, or e4m3 with head dim 128/256)")
+        return ring_sweep_paged(local_q, cfg, group, cu_seqlens, max_seqlen, descales=descales)
     if fused and not can_fuse:
         raise AssertionError("fused ring sweep needs cp_size in [2, 16] and bf16/fp16 with head dim "
                              "64/128 and no descales, or e4m3 with head dim 128/256")
@@ -220,6 +231,40 @@ def ring_sweep(local_q: torch.Tensor, local_k: torch.Tensor, local_v: torch.Tens
         assert k.stride() == ks[0].stride(), "all K shards must share strides"
     assert all(v.stride() == vs[0].stride() for v in vs), "all V shards must share strides"
     vts, stride = transpose_v_many(vs, cu_seqlens_k=cu_seqlens, max_seqlen_k=max_seqlen)
+    return _sweep_launch(local_q, ks, vts, stride, cfg, cu_seqlens, max_seqlen, out, lse, descales)
+
+
+def ring_sweep_paged(local_q: torch.Tensor, cfg: RingConfig, ring: "PagedKVRing",
+                     cu_seqlens: Optional[torch.Tensor] = None, max_seqlen: Optional[int] = None,
+                     out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
+                     descales: Optional[Descales] = None) -> torch.Tensor:
+    """ring_sweep over paged K/V caches: one launch gathers every source's K pages into
+    contiguous rows, one writes every source's V^T from its V pages, then the same sweep
+    kernel runs.  The result is bit-identical to ring_sweep on the contiguous shards."""
+    _lib.load()  # fails here, before any allocation, without the library
+    total, _, d = local_q.shape
+    assert local_q.is_cuda and local_q.stride(2) == 1, "local_q must be a device tensor, contiguous in D"
+    kc = ring.k[0]
+    assert kc.dtype == local_q.dtype and kc.shape[3] == d and kc.device == local_q.device, \
+        "caches must match local_q's dtype, head dim and device"
+    nseq = 1 if cu_seqlens is None else cu_seqlens.shape[0] - 1
+    assert ring.page_tables[0].shape[0] == nseq, "page tables need one row per local sequence"
+    ks = gather_kv_pages(ring, "k", total, cu_seqlens, max_seqlen)
+    vts, stride = transpose_v_paged_many(ring, total, cu_seqlens, max_seqlen)
+    return _sweep_launch(local_q, ks, vts, stride, cfg, cu_seqlens, max_seqlen, out, lse, descales)
+
+
+def _sweep_launch(local_q: torch.Tensor, ks: List[torch.Tensor], vts: List[torch.Tensor], stride: int,
+                  cfg: RingConfig, cu_seqlens: Optional[torch.Tensor], max_seqlen: Optional[int],
+                  out: Optional[torch.Tensor], lse: Optional[torch.Tensor],
+                  descales: Optional[Descales]) -> torch.Tensor:
+    """Queues fa4cp_ring_sweep_fwd over K shards `ks` and V^T buffers `vts` (row stride
+    `stride`) of every source rank."""
+    S, rank = cfg.cp_size, cfg.cp_rank
+    total, h_q, d = local_q.shape
+    h_kv = ks[0].shape[1]
+    dev = local_q.device
+    nseq = 1 if cu_seqlens is None else cu_seqlens.shape[0] - 1
     e4m3 = local_q.dtype == torch.float8_e4m3fn
     if out is None:
         out = torch.empty(local_q.shape, dtype=torch.bfloat16 if e4m3 else local_q.dtype, device=dev)

@@ -27,6 +27,8 @@
  *                                  and its merges, fused; every source's K/V on this GPU)
  *   fa4cp_quantize_e4m3         <- the caller-side FP8 step before it (README.md:63-70: e4m3
  *                                  shards plus their descales, Descales ring_attention.py:43-52)
+ *   fa4cp_gather_kv_pages,      <- no counterpart: paged K/V caches in front of the sweep
+ *   fa4cp_transpose_v_paged_many   (README.md:139-140 lists paged KV as not supported)
  */
 #ifndef FA4CP_H_
 #define FA4CP_H_
@@ -37,7 +39,7 @@
 extern "C" {
 #endif
 
-#define FA4CP_ABI_VERSION 3
+#define FA4CP_ABI_VERSION 4
 
 /* status codes */
 #define FA4CP_OK 0
@@ -147,6 +149,44 @@ int64_t fa4cp_vt_min_d_stride(int32_t total_k, int32_t nseq);
  */
 int fa4cp_transpose_v_many(const fa4cp_transpose_args* args, const void* const* v, void* const* v_t,
                            int32_t count, void* stream);
+
+/*
+ * Paged K / V caches.  No counterpart in the reference, which keeps every rotated K/V shard
+ * contiguous (README.md:139-140: "no paged KV yet"); these two calls feed paged caches to
+ * fa4cp_ring_sweep_fwd.  A source rank's cache holds num_pages pages of page_size rows;
+ * a row is h_kv heads x d elements at cache_row_stride / cache_head_stride, and page p
+ * starts at row p * page_size.  page_table[j * pt_stride + k] names the page that holds
+ * rows [k * page_size, (k + 1) * page_size) of local sequence j (cu as for the sweep; cu ==
+ * NULL: one sequence of `total` rows).  An entry outside [0, num_pages) reads as zero rows.
+ * page_size is a multiple of 128, so a key tile never straddles two pages.
+ */
+typedef struct fa4cp_paged_args {
+  const int32_t* cu; /* local cu_seqlens [nseq + 1] or NULL */
+  int32_t nseq, max_seqlen, total;
+  int32_t h_kv, d, dtype;
+  int32_t page_size, num_pages;
+  int64_t cache_row_stride, cache_head_stride; /* elements */
+  int64_t pt_stride;                           /* entries per page-table row (>= pages of the longest sequence) */
+} fa4cp_paged_args;
+
+/*
+ * For each of `count` (1..FA4CP_MAX_CP) caches: dst[i] rows [cu[j], cu[j+1]) <- the rows of
+ * sequence j in cache[i] through page_table[i] (host arrays of device pointers), dst rows
+ * at dst_row_stride / dst_head_stride elements.  A bit-exact copy (the K shards of a sweep).
+ */
+int fa4cp_gather_kv_pages(const fa4cp_paged_args* args, const void* const* cache, const int32_t* const* page_table,
+                          void* const* dst, int64_t dst_row_stride, int64_t dst_head_stride, int32_t count,
+                          void* stream);
+
+/*
+ * V^T of `count` paged V caches: v_t[i] is what fa4cp_transpose_v_many with k_sel = ALL
+ * writes for the contiguous V of the same cu (vt_d_stride a multiple of 128 and >=
+ * fa4cp_vt_min_d_stride(total, nseq)).  Unused cache rows are never read: positions past a
+ * sequence's end are written as zeros.
+ */
+int fa4cp_transpose_v_paged_many(const fa4cp_paged_args* args, const void* const* v_cache,
+                                 const int32_t* const* page_table, void* const* v_t, int64_t vt_d_stride,
+                                 int32_t count, void* stream);
 
 /*
  * One rank's whole causal zig-zag ring sweep in a single launch (fa4_ring/ring_attention.py:61-174

@@ -90,6 +90,36 @@ def test_empty_calls_launch_nothing_and_take_null_pointers():
         assert lib.fa4cp_zigzag_unshard((ctypes.c_void_p * 4)(), None, 256, None, 1, n, 4, None) == want
 
 
+def test_paged_entry_points_validate_before_launching():
+    """fa4cp_gather_kv_pages / fa4cp_transpose_v_paged_many: nothing to do returns 0, bad
+    page geometry, strides, counts and types are rejected, all before any HIP call."""
+    lib = _lib.load()
+
+    def args(**kw):
+        a = _lib.PagedArgs()
+        a.total, a.h_kv, a.d, a.dtype = 0, 2, 128, _lib.dtype_code(torch.bfloat16)
+        a.page_size, a.num_pages, a.pt_stride = 128, 4, 1
+        a.cache_row_stride, a.cache_head_stride = 256, 128
+        for key, val in kw.items():
+            setattr(a, key, val)
+        return a
+
+    arr = (ctypes.c_void_p * 1)()
+    assert lib.fa4cp_gather_kv_pages(ctypes.byref(args()), arr, arr, arr, 256, 128, 1, None) == 0
+    assert lib.fa4cp_transpose_v_paged_many(ctypes.byref(args()), arr, arr, arr, 128, 1, None) == 0
+    cases = [(dict(page_size=96), b"page_size"), (dict(page_size=0), b"page_size"),
+             (dict(total=1000, pt_stride=7), b"pt_stride"), (dict(cache_row_stride=100), b"16-byte"),
+             (dict(dtype=9), b"dtype"), (dict(h_kv=0), b"bad shape")]
+    for kw, msg in cases:
+        for rc in (lib.fa4cp_gather_kv_pages(ctypes.byref(args(**kw)), arr, arr, arr, 256, 128, 1, None),
+                   lib.fa4cp_transpose_v_paged_many(ctypes.byref(args(**kw)), arr, arr, arr, 1024, 1, None)):
+            assert rc != 0 and msg in lib.fa4cp_last_error(), (kw, lib.fa4cp_last_error())
+    rc = lib.fa4cp_gather_kv_pages(ctypes.byref(args()), arr, arr, arr, 256, 128, 0, None)
+    assert rc != 0 and b"count" in lib.fa4cp_last_error()
+    rc = lib.fa4cp_gather_kv_pages(ctypes.byref(args(total=256, pt_stride=2)), arr, arr, arr, 256, 128, 1, None)
+    assert rc != 0 and b"null" in lib.fa4cp_last_error()
+
+
 def test_sweep_entry_point_validates_before_launching():
     """fa4cp_ring_sweep_fwd rejects bad arguments with a message and no HIP call: null
     sources, cp_rank / cp_size out of range, a negative max_seqlen, unsupported head dims.
@@ -132,7 +162,8 @@ def test_sweep_entry_point_validates_before_launching():
 @pytest.mark.parametrize("struct,cname", [(_lib.AttnArgs, "fa4cp_attn_args"),
                                            (_lib.TransposeArgs, "fa4cp_transpose_args"),
                                            (_lib.SweepArgs, "fa4cp_sweep_args"),
-                                           (_lib.QuantArgs, "fa4cp_quant_args")])
+                                           (_lib.QuantArgs, "fa4cp_quant_args"),
+                                           (_lib.PagedArgs, "fa4cp_paged_args")])
 def test_args_layout_matches_c_header(struct, cname):
     fields = [f for f, _ in struct._fields_]
     prog = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",
