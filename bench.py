@@ -553,6 +553,41 @@ def main():
                                       "attn_TFLOP/s": round(per_launch / (a8 * 1e-3) / 1e12, 2),
                                       "attn_frac": round(per_launch / (a8 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)}}
         del q8, ring8
+        # paged K/V caches (pages of 256 rows in a random order): page gather + paged V^T + sweep
+        from fa4_ring import PagedKVRing
+        from fa4_ring.paged import gather_kv_pages, transpose_v_paged_many
+        paged = PagedKVRing.from_shards(ring.k, ring.v, 256, spare_pages=8,
+                                        generator=torch.Generator().manual_seed(rank))
+        secpg = timed_sweeps(lambda: ring_flash_attn(lq, None, None, cfg, group=paged), args.steps, 2)
+
+        def event_ms(fn, n=10):
+            for _ in range(3):
+                fn()
+            evs = []
+            for _ in range(n):
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+                fn()
+                e.record()
+                evs.append((s, e))
+            torch.cuda.synchronize()
+            return sum(s.elapsed_time(e) for s, e in evs) / n
+
+        g_ms = event_ms(lambda: gather_kv_pages(paged, "k", t_local))
+        pt_ms = event_ms(lambda: transpose_v_paged_many(paged, t_local))
+        pbytes = CP * 2.0 * t_local * HKV * D * 2  # every source's K (or V): read once, written once
+        result["paged_bf16"] = {
+            "workload": "same sweep with every source's K/V in a paged cache (256-row pages, random "
+                        "page order): one K page gather, one paged V^T launch, the same sweep kernel",
+            "ms_per_step": round(secpg * 1e3, 3), "TFLOP/s": round(flops / secpg / 1e12, 2),
+            "gather_kv_pages": {"kernel": "gather_pages_kernel (8 caches per launch)", "avg_launch_ms": round(g_ms, 4),
+                                "bytes": round(pbytes), "achieved_GBs": round(pbytes / (g_ms * 1e-3) / 1e9, 1),
+                                "frac": round(pbytes / (g_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+            "transpose_v_paged": {"kernel": "transpose_v_kernel<u16,128>, paged (8 caches per launch)",
+                                  "avg_launch_ms": round(pt_ms, 4), "bytes": round(pbytes),
+                                  "achieved_GBs": round(pbytes / (pt_ms * 1e-3) / 1e9, 1),
+                                  "frac": round(pbytes / (pt_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}}
+        del paged
     del ring, lq, q_full
     torch.cuda.synchronize()
 
