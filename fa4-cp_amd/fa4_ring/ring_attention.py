@@ -107,8 +107,8 @@ def ring_flash_attn(
     ``cu_seqlens`` (each entry a zig-zag ``2*h_j`` shard length) on the device and
     ``max_seqlen``.  For cp_size > 1 ``group`` must be a LocalKVRing holding every source
     rank's KV shard (KV is not moved between GPUs here), or a PagedKVRing holding every
-    source's paged K/V cache (fused sweep only; the rank's own K/V come from it, so
-    ``local_k`` / ``local_v`` are ignored)."""
+    source's paged K/V cache (the rank's own K/V come from it, so ``local_k`` / ``local_v``
+    are ignored; the per-step form gathers the pages into contiguous shards first)."""
     S = cfg.cp_size
     rank = cfg.cp_rank
     scale = cfg.softmax_scale
@@ -133,10 +133,16 @@ def ring_flash_attn(
         (descales is None and local_q.dtype in (torch.bfloat16, torch.float16) and d in (64, 128))
         or (e4m3 and d in (128, 256)))
     if paged:
-        if fused is False or not can_fuse:
-            raise AssertionError("paged K/V caches run the fused sweep only (cp_size in [2, 16]; bf16/fp16 "
-                                 "with head dim 64/128 and no descales, or e4m3 with head dim 128/256)")
-        return ring_sweep_paged(local_q, cfg, group, cu_seqlens, max_seqlen, descales=descales)
+        if fused is not False and can_fuse:
+            return ring_sweep_paged(local_q, cfg, group, cu_seqlens, max_seqlen, descales=descales)
+        if fused:
+            raise AssertionError("fused ring sweep needs cp_size in [2, 16] and bf16/fp16 with head dim "
+                                 "64/128 and no descales, or e4m3 with head dim 128/256")
+        # the per-step form reads contiguous shards: gather every source's K and V pages first
+        group = LocalKVRing(gather_kv_pages(group, "k", total, cu_seqlens, max_seqlen),
+                            gather_kv_pages(group, "v", total, cu_seqlens, max_seqlen))
+        local_k, local_v = group.kv(rank)
+        fused = False
     if fused and not can_fuse:
         raise AssertionError("fused ring sweep needs cp_size in [2, 16] and bf16/fp16 with head dim "
                              "64/128 and no descales, or e4m3 with head dim 128/256")

@@ -180,3 +180,28 @@ def test_paged_sweep_full_size_bf16_rank3():
     want = ring_flash_attn(q, ks[rank], vs[rank], cfg, group=ring)
     got = ring_flash_attn(q, None, None, cfg, group=paged)
     assert torch.equal(bits(got), bits(want))
+
+
+PER_STEP_CASES = [  # (dtype, d, cp, merge mode): shapes the fused sweep does not take, and fused=False
+    (torch.bfloat16, 256, 2, "incremental"),
+    (torch.float16, 256, 4, "batched"),
+    (torch.bfloat16, 128, 4, "batched"),
+    (torch.bfloat16, 128, 1, "incremental"),
+]
+
+
+@pytest.mark.parametrize("dtype,d,cp,mode", PER_STEP_CASES)
+def test_paged_per_step_equals_contiguous(dtype, d, cp, mode):
+    say(f"paged per-step {dtype} d={d} cp={cp} {mode}")
+    n, h, h_kv = 1024, 4, 2
+    gen = torch.Generator().manual_seed(21)
+    q, k, v = (torch.randn(n, hh, d, generator=gen).to(dtype).to(DEV) for hh in (h, h_kv, h_kv))
+    ring = LocalKVRing.from_full(k, v, cp)
+    for rank in range(cp):
+        lq = zigzag_shard(q, rank, cp)
+        paged = PagedKVRing.from_shards(ring.k, ring.v, 128, spare_pages=1,
+                                        generator=torch.Generator().manual_seed(rank))
+        cfg = RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode)
+        want = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, fused=False)
+        got = ring_flash_attn(lq, None, None, cfg, group=paged, fused=False)
+        assert torch.equal(bits(got), bits(want)), f"rank {rank}"
