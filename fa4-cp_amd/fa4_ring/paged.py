@@ -120,6 +120,7 @@ def gather_kv_pages(ring: PagedKVRing, which: str, total: int, cu_seqlens: Optio
     """Every source's K (``which="k"``) or V rows as contiguous ``[total, H_kv, D]`` tensors in
     the local layout of ``cu_seqlens`` (one fa4cp_gather_kv_pages launch, current stream)."""
     lib = _lib.load()
+    _require(which in ("k", "v"), f"which must be 'k' or 'v', got {which!r}")
     caches = ring.k if which == "k" else ring.v
     n, (_, _, h_kv, d) = ring.cp_size, caches[0].shape
     outs = [torch.empty((total, h_kv, d), dtype=caches[0].dtype, device=caches[0].device) for _ in range(n)]
