@@ -177,6 +177,8 @@ extern "C" int fa4cp_merge_state_inplace(void* v, float* s, const void* v_other,
   clear_error();
   if (rows > 0 && (!v || !s || !v_other || !s_other))  // NULL only with no rows
     return set_error(FA4CP_EINVAL, "merge_state_inplace: null pointer");
+  if ((reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(v_other)) % 16 != 0)
+    return set_error(FA4CP_EINVAL, "merge_state_inplace: v and v_other must be 16-byte aligned");
   if (rows < 0 || h <= 0 || d <= 0 || (d % 8) != 0)
     return set_error(FA4CP_EINVAL, "merge_state_inplace: bad shape rows=%lld h=%d d=%d "
                      "(d must be a positive multiple of 8)", (long long)rows, h, d);
@@ -221,6 +223,8 @@ extern "C" int fa4cp_merge_states(const void* v, const float* s, void* v_out, fl
   clear_error();
   if (rows > 0 && (!v || !s || !v_out))  // NULL only with no rows
     return set_error(FA4CP_EINVAL, "merge_states: null pointer");
+  if ((reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(v_out)) % 16 != 0)
+    return set_error(FA4CP_EINVAL, "merge_states: v and v_out must be 16-byte aligned");
   if (rows < 0 || num_states <= 0 || h <= 0 || d <= 0 || (d % 8) != 0)
     return set_error(FA4CP_EINVAL, "merge_states: bad shape rows=%lld states=%d h=%d d=%d",
                      (long long)rows, num_states, h, d);

@@ -35,7 +35,8 @@ def quantize_e4m3(x: torch.Tensor, *, heads_per_scale: int = 0,
     nscale = 1 if g == 0 else h // g
     if out is None:
         out = torch.empty((rows, h, d), dtype=torch.float8_e4m3fn, device=x.device)
-    assert out.shape == (rows, h, d) and out.dtype == torch.float8_e4m3fn and out.is_contiguous()
+    assert out.shape == (rows, h, d) and out.dtype == torch.float8_e4m3fn and out.is_contiguous() \
+        and out.device == x.device, f"out must be a contiguous [{rows}, {h}, {d}] float8_e4m3fn tensor on {x.device}"
     amax = torch.empty(nscale, dtype=torch.float32, device=x.device)
     descale = torch.empty(nscale, dtype=torch.float32, device=x.device)
     a = _lib.QuantArgs()

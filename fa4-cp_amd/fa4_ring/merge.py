@@ -70,8 +70,10 @@ def merge_states(v: torch.Tensor, s: torch.Tensor,
         out = torch.empty((t, h, d), dtype=v.dtype, device=v.device)
     if s_out is None:
         s_out = torch.empty((t, h), dtype=torch.float32, device=v.device)
-    _require(out.shape == (t, h, d) and out.dtype == v.dtype and out.is_contiguous(), "bad out")
-    _require(s_out.shape == (t, h) and s_out.dtype == torch.float32 and s_out.is_contiguous(), "bad s_out")
+    _require(out.shape == (t, h, d) and out.dtype == v.dtype and out.is_contiguous() and out.device == v.device,
+             f"out must be a contiguous [{t}, {h}, {d}] {v.dtype} tensor on {v.device}")
+    _require(s_out.shape == (t, h) and s_out.dtype == torch.float32 and s_out.is_contiguous()
+             and s_out.device == v.device, f"s_out must be a contiguous [{t}, {h}] float32 tensor on {v.device}")
     rc = lib.fa4cp_merge_states(v.data_ptr(), s.data_ptr(), out.data_ptr(), s_out.data_ptr(), t, ns,
                                 h, d, _lib.dtype_code(v.dtype), _lib.stream_handle(v.device))
     _lib.check(rc, "fa4cp_merge_states")

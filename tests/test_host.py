@@ -46,6 +46,11 @@ def test_error_path_reports_message_without_gpu():
     assert b"null pointer" in lib.fa4cp_last_error()
     rc = lib.fa4cp_zigzag_shard(1, 1, 16, None, 1, 10, 0, 4, None)
     assert rc == -1 and b"divisible" in lib.fa4cp_last_error()
+    # the merges read 16-byte vectors of v: misaligned tensors are refused
+    rc = lib.fa4cp_merge_states(1 << 20 | 8, 1 << 20, 1 << 21, 1 << 21, 4, 2, 8, 128, 0, None)
+    assert rc == -1 and b"aligned" in lib.fa4cp_last_error()
+    rc = lib.fa4cp_merge_state_inplace(1 << 20, 1 << 20, 1 << 21 | 2, 1 << 21, 4, 8, 128, 0, None, 0, 0, None)
+    assert rc == -1 and b"aligned" in lib.fa4cp_last_error()
     a = _lib.AttnArgs()
     a.total_q = 1
     rc = lib.fa4cp_attn_fwd(ctypes.byref(a), None)
