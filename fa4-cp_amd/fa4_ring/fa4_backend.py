@@ -224,8 +224,8 @@ def fa4_attn(
     _require(out.shape == (t_q, h_q, d) and out.dtype == odt and out.device == dev,
              f"out must be [{t_q}, {h_q}, {d}] {odt}")
     _require(out.stride(2) == 1, "out must be contiguous in the head dim")
-    _require(lse.shape == (t_q, h_q) and lse.dtype == torch.float32 and lse.stride(1) == 1,
-             "lse must be [T_q, H] float32 with unit head stride")
+    _require(lse.shape == (t_q, h_q) and lse.dtype == torch.float32 and lse.stride(1) == 1
+             and lse.device == dev, "lse must be [T_q, H] float32 on q's device with unit head stride")
 
     vt_ptr, vt_stride = None, 0
     if use_vt and uses_vt(dt, d):

@@ -283,6 +283,17 @@ def _sweep_launch(local_q: torch.Tensor, ks: List[torch.Tensor], vts: List[torch
             vd = torch.stack([_norm_descale(descales.v[i], h_kv, dev) for i in range(S)]).contiguous()
     if lse is None:
         lse = torch.empty((total, h_q), dtype=torch.float32, device=dev)
+    odt = torch.bfloat16 if e4m3 else local_q.dtype
+    assert out.shape == local_q.shape and out.dtype == odt and out.device == dev and out.stride(2) == 1, \
+        f"out must be [{total}, {h_q}, {d}] {odt} on {dev}, contiguous in D"
+    assert lse.shape == (total, h_q) and lse.dtype == torch.float32 and lse.device == dev and lse.stride(1) == 1, \
+        f"lse must be [{total}, {h_q}] float32 on {dev} with unit head stride"
+    for i, (k, vt) in enumerate(zip(ks, vts)):
+        assert k.device == dev and vt.device == dev, f"source {i}'s K / V^T must be on {dev}"
+    if cu_seqlens is not None:
+        assert cu_seqlens.dtype == torch.int32 and cu_seqlens.device == dev and cu_seqlens.is_contiguous(), \
+            "cu_seqlens must be contiguous int32 on the device"
+        assert max_seqlen is not None, "max_seqlen required when cu_seqlens is given"
     a = _lib.SweepArgs()
     a.q, a.out, a.lse = local_q.data_ptr(), out.data_ptr(), lse.data_ptr()
     a.q_row_stride, a.q_head_stride = local_q.stride(0), local_q.stride(1)

@@ -468,3 +468,25 @@ def test_empty_operators():
                         torch.empty(0, 3, 4, dtype=torch.float32, device=DEV))
     torch.cuda.synchronize()
     assert v.shape == (0, 4, 64) and s.shape == (0, 4)
+
+
+def test_ring_sweep_rejects_bad_out_and_lse():
+    """Caller-provided out / lse of the wrong shape, type or layout are refused before the
+    sweep kernel is queued."""
+    from fa4_ring.ring_attention import ring_sweep
+
+    say("ring_sweep argument checks")
+    q = torch.randn(256, 4, 128, device=DEV).to(torch.bfloat16)
+    k = torch.randn(256, 2, 128, device=DEV).to(torch.bfloat16)
+    ring = LocalKVRing([k, k], [k, k])
+    cfg = RingConfig(cp_size=2, cp_rank=0)
+    bad_outs = [torch.empty(128, 4, 128, dtype=torch.bfloat16, device=DEV),
+                torch.empty(256, 4, 128, dtype=torch.float16, device=DEV),
+                torch.empty(256, 128, 4, dtype=torch.bfloat16, device=DEV).transpose(1, 2)]
+    for out in bad_outs:
+        with pytest.raises(AssertionError, match="out must be"):
+            ring_sweep(q, k, k, cfg, ring, out=out)
+    for lse in (torch.empty(256, 3, device=DEV), torch.empty(256, 4, dtype=torch.float16, device=DEV)):
+        with pytest.raises(AssertionError, match="lse must be"):
+            ring_sweep(q, k, k, cfg, ring, lse=lse)
+    torch.cuda.synchronize()
