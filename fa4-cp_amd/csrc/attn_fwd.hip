@@ -1140,7 +1140,8 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_vt(AttnParams p)
   geo.g.off = p.causal ? off : kNoCausal;
   geo.g.qmin = 0;
   geo.g.kd = geo.g.vd = 1.f;
-  const int64_t vt_pos = p.cu_k ? vt_seq_start(p.cu_k, seq, p.k_sel) : 0;
+  const int64_t vt_pos = p.cu_k ? vt_seq_start(p.cu_k, seq, p.total_k, p.k_sel) : 0;
+  if (vt_pos + (Lk + kVtPad - 1) / kVtPad * kVtPad > p.vt_ds) return;  // malformed cu_k: outside V^T
   geo.kb = reinterpret_cast<const char*>(reinterpret_cast<const T*>(p.k) + (int64_t)ks * p.k_rs +
                                          (int64_t)kvh * p.k_hs);
   geo.vb = reinterpret_cast<const char*>(reinterpret_cast<const T*>(p.vt) + (int64_t)kvh * D * p.vt_ds + vt_pos);
@@ -1240,7 +1241,8 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_sweep(SweepParam
   geo.row_tile0 = row_tile0;
   geo.rows = RB * 32;
   geo.kvh = kvh;
-  const int64_t vt_pos = p.cu ? vt_seq_start(p.cu, seq, FA4CP_SEL_ALL) : 0;
+  const int64_t vt_pos = p.cu ? vt_seq_start(p.cu, seq, p.total, FA4CP_SEL_ALL) : 0;
+  if (vt_pos + (L + kVtPad - 1) / kVtPad * kVtPad > p.vt_ds) return;  // malformed cu: outside V^T
   geo.k_off = ((int64_t)qs * p.k_rs + (int64_t)kvh * p.k_hs) * (int64_t)sizeof(T);
   geo.v_off = ((int64_t)kvh * D * p.vt_ds + vt_pos) * (int64_t)sizeof(T);
 
@@ -2311,7 +2313,8 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_vt(AttnParams p) 
   geo.g.qmin = 0;
   geo.g.kd = p.kd ? p.kd[kvh] : 1.f;
   geo.g.vd = p.vd ? p.vd[kvh] : 1.f;
-  const int64_t vt_pos = p.cu_k ? vt_seq_start(p.cu_k, seq, p.k_sel) : 0;
+  const int64_t vt_pos = p.cu_k ? vt_seq_start(p.cu_k, seq, p.total_k, p.k_sel) : 0;
+  if (vt_pos + (Lk + kVtPad - 1) / kVtPad * kVtPad > p.vt_ds) return;  // malformed cu_k: outside V^T
   geo.kb = reinterpret_cast<const char*>(p.k) + (int64_t)ks * p.k_rs + (int64_t)kvh * p.k_hs;
   geo.vb = reinterpret_cast<const char*>(p.vt) + (int64_t)kvh * D * p.vt_ds + vt_pos;
 
@@ -2362,7 +2365,8 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_sweep(SweepParams
   geo.row_tile0 = row_tile0;
   geo.rows = RB * 32;
   geo.kvh = kvh;
-  const int64_t vt_pos = p.cu ? vt_seq_start(p.cu, seq, FA4CP_SEL_ALL) : 0;
+  const int64_t vt_pos = p.cu ? vt_seq_start(p.cu, seq, p.total, FA4CP_SEL_ALL) : 0;
+  if (vt_pos + (L + kVtPad - 1) / kVtPad * kVtPad > p.vt_ds) return;  // malformed cu: outside V^T
   geo.k_off = (int64_t)qs * p.k_rs + (int64_t)kvh * p.k_hs;
   geo.v_off = (int64_t)kvh * D * p.vt_ds + vt_pos;
 

@@ -142,14 +142,22 @@ __device__ __forceinline__ void pin(V& x) {
   }
 }
 
+// Rows [s, e) of sequence j, clamped into [0, total]: a malformed cu (decreasing, or past
+// `total`) then gives wrong sequences but never an address outside the tensors.
+__device__ __forceinline__ void seq_bounds(const int32_t* cu, int j, int total, int& s, int& e) {
+  s = 0;
+  e = total;
+  if (cu != nullptr) {
+    s = min(max(cu[j], 0), total);
+    e = min(max(cu[j + 1], s), total);
+  }
+}
+
 // Row range [start, start + len) of sequence j after a half selection (FA4CP_SEL_*).
 __device__ __forceinline__ void seq_range(const int32_t* cu, int j, int total, int sel, int& start,
                                           int& len) {
-  int s = 0, e = total;
-  if (cu != nullptr) {
-    s = cu[j];
-    e = cu[j + 1];
-  }
+  int s, e;
+  seq_bounds(cu, j, total, s, e);
   const int mid = (s + e) >> 1;
   if (sel == FA4CP_SEL_FRONT_HALF) e = mid;
   if (sel == FA4CP_SEL_BACK_HALF) s = mid;
@@ -165,11 +173,14 @@ __device__ __forceinline__ void vt_seq_range(const int32_t* cu, int j, int total
 // to kVtPad keys never cross into the next sequence and every tile row is 16-byte aligned.
 constexpr int kVtPad = 128;
 
-// First V^T position of sequence j: the padded lengths of the sequences before it.
-__device__ __forceinline__ int64_t vt_seq_start(const int32_t* cu, int j, int sel) {
+// First V^T position of sequence j: the padded lengths of the sequences before it (ranges
+// clamped as seq_bounds, so the positions stay inside fa4cp_vt_min_d_stride(total, nseq)).
+__device__ __forceinline__ int64_t vt_seq_start(const int32_t* cu, int j, int total, int sel) {
   int64_t p = 0;
   for (int i = 0; i < j; ++i) {
-    const int s = cu[i], e = cu[i + 1], mid = (s + e) >> 1;
+    int s, e;
+    seq_bounds(cu, i, total, s, e);
+    const int mid = (s + e) >> 1;
     const int len = sel == FA4CP_SEL_FRONT_HALF ? mid - s : sel == FA4CP_SEL_BACK_HALF ? e - mid : e - s;
     p += (len + kVtPad - 1) / kVtPad * kVtPad;
   }

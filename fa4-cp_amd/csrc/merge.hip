@@ -51,6 +51,7 @@ __global__ __launch_bounds__(kBlock) void merge_inplace_kernel(
     row = (row_sel == FA4CP_SEL_BACK_HALF) ? single_rows / 2 + sel : sel;
   } else {
     row = selected_row(cu, nseq, row_sel, sel);
+    if (row < 0 || row >= single_rows) return;  // malformed cu: touch nothing outside the tensors
   }
   const int64_t sidx = row * h + head;
   const float sa = s[sidx];

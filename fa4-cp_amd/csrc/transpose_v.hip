@@ -61,7 +61,8 @@ __global__ __launch_bounds__(kTBlock) void transpose_v_kernel(
   const int k0 = kt * kTK;
   const int lpad = round_up_pad(L);
   if (k0 >= lpad) return;
-  const int64_t P = vt_seq_start(cu, seq, sel);
+  const int64_t P = vt_seq_start(cu, seq, total_k, sel);
+  if (P + lpad > vt_ds) return;  // malformed cu: the sequence would not fit V^T
 
   const int tid = threadIdx.x;
   // cache row of key k0 (paged: the tile's kTK keys lie in one page); -1: zeros

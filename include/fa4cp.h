@@ -10,6 +10,9 @@
  *   - a call with no rows to process (total_q, total, rows or total_full of 0) launches
  *     nothing and returns 0; the pointers of its empty tensors may then be NULL (torch
  *     hands out NULL for zero-element tensors);
+ *   - cu_seqlens tables (device int32) must start at 0, not decrease and end at most at
+ *     the tensor's row count; other contents give unspecified results, but every kernel
+ *     clamps the sequence ranges it derives from them, so no access leaves the tensors;
  *   - the return value is 0 on success and a negative FA4CP_E* code otherwise; the
  *     message for the last failure on the calling thread is in fa4cp_last_error();
  *   - the library keeps no state besides that thread-local message, so every entry point
