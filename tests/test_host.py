@@ -125,6 +125,21 @@ def test_paged_entry_points_validate_before_launching():
     assert rc != 0 and b"null" in lib.fa4cp_last_error()
 
 
+def test_paged_ring_checks_its_caches():
+    """PagedKVRing refuses caches that are not [num_pages, page_size, H_kv, D], host tensors
+    and mismatched lists before anything reaches the library."""
+    from fa4_ring import PagedKVRing
+
+    c = torch.zeros(4, 128, 2, 64, dtype=torch.bfloat16)
+    pt = torch.zeros(1, 4, dtype=torch.int32)
+    with pytest.raises(AssertionError, match="num_pages, page_size"):
+        PagedKVRing([c[0]], [c[0]], [pt])
+    with pytest.raises(AssertionError, match="device tensors"):
+        PagedKVRing([c], [c], [pt])
+    with pytest.raises(AssertionError, match="per source rank"):
+        PagedKVRing([c, c], [c], [pt, pt])
+
+
 def test_sweep_entry_point_validates_before_launching():
     """fa4cp_ring_sweep_fwd rejects bad arguments with a message and no HIP call: null
     sources, cp_rank / cp_size out of range, a negative max_seqlen, unsupported head dims.
