@@ -228,6 +228,21 @@ def bench_c4(args) -> int:
     sec = timed_sweeps(lambda: run(None), args.steps, args.warmup, clock)
     sw_ms = clock.mean_ms("sweep_kernel")
     secp = timed_sweeps(lambda: run(False), args.steps, args.warmup)
+    # zig-zag shard of the packed full q (per-sequence chunks r and 2cp-1-r), device cu
+    cu_dev = torch.tensor(full_cu, dtype=torch.int32, device=dev)
+    from fa4_ring.zigzag import _shard  # the launch alone (zigzag_shard_varlen checks cu on the host)
+    for _ in range(3):
+        _shard(q, rank, cp, cu_dev, len(C4_LENGTHS))
+    zev = []
+    for _ in range(10):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        _shard(q, rank, cp, cu_dev, len(C4_LENGTHS))
+        e.record()
+        zev.append((s, e))
+    torch.cuda.synchronize()
+    zms = sum(s.elapsed_time(e) for s, e in zev) / len(zev)
+    zbytes = 2.0 * (full_cu[-1] // cp) * hq * d * 2
     value = flops / sec / 1e12
     kt = flops / (sw_ms * 1e-3) / 1e12
     print(json.dumps({
@@ -245,6 +260,9 @@ def bench_c4(args) -> int:
                      "traffic": None, "algorithmic_per_launch": f"{flops / 1e12:.4f} TFLOP (the whole sweep)",
                      "avg_launch_ms": round(sw_ms, 4), "launches": clock.count("sweep_kernel")},
         "per_step": {"ms_per_step": round(secp * 1e3, 3), "TFLOP/s": round(flops / secp / 1e12, 2)},
+        "zigzag_varlen": {"kernel": "shard_kernel<u32x4> (packed sequences, full q)", "avg_launch_ms": round(zms, 4),
+                          "bytes": round(zbytes), "achieved_GBs": round(zbytes / (zms * 1e-3) / 1e9, 1),
+                          "frac": round(zbytes / (zms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
         "cpu_baseline": None}), flush=True)
     return 0
 
