@@ -33,11 +33,14 @@ __device__ __forceinline__ int64_t selected_row(const int32_t* __restrict__ cu, 
   return half_start + (i - (start >> 1));
 }
 
+// The result goes to (vd, sd), which is (v, s) itself for the in-place merge: every lane
+// reads its elements before it writes them, and lane 0 writes the LSE after the group's
+// lanes have read it (they are in one wavefront, which executes the read first).
 template <typename T>
 __global__ __launch_bounds__(kBlock) void merge_inplace_kernel(
-    T* __restrict__ v, float* __restrict__ s, const T* __restrict__ vo,
-    const float* __restrict__ so, int64_t n_groups, int h, int d, const int32_t* __restrict__ cu,
-    int nseq, int row_sel, int64_t single_rows) {
+    const T* v, const float* s, const T* __restrict__ vo, const float* __restrict__ so, T* vd,
+    float* sd, int64_t n_groups, int h, int d, const int32_t* __restrict__ cu, int nseq,
+    int row_sel, int64_t single_rows) {
   const int64_t g = (int64_t)blockIdx.x * (kBlock / kGroup) + (threadIdx.x / kGroup);
   const int lane = threadIdx.x % kGroup;
   if (g >= n_groups) return;
@@ -56,17 +59,30 @@ __global__ __launch_bounds__(kBlock) void merge_inplace_kernel(
   const int64_t sidx = row * h + head;
   const float sa = s[sidx];
   const float sb = so[sidx];
-  if (sb == -INFINITY) return;  // other side contributes nothing; row unchanged
-  T* va = v + sidx * (int64_t)d;
+  const T* va = v + sidx * (int64_t)d;
   const T* vb = vo + sidx * (int64_t)d;
-  if (sa == -INFINITY) {
-    // accumulator side is empty: take the other state verbatim
+  T* vr = vd + sidx * (int64_t)d;
+  if (sa == -INFINITY && sb == -INFINITY) {
+    // neither side has a key: the max-shifted formula gives 0/0, so v becomes NaN and the
+    // LSE stays -inf, as logaddexp(-inf, -inf) (the ring seeds every row with a finite LSE
+    // first and never gets here)
+    const float nan8[8] = {NAN, NAN, NAN, NAN, NAN, NAN, NAN, NAN};
+    for (int c = lane * 8; c < d; c += kGroup * 8) store8_f32<T>(vr + c, nan8);
+    if (lane == 0) sd[sidx] = -INFINITY;
+    return;
+  }
+  if (sb == -INFINITY || sa == -INFINITY) {
+    // one side contributes nothing: the result is the other state (nothing to do in place
+    // when the empty side is the other one)
+    const bool take_b = sb != -INFINITY;
+    if (!take_b && vr == va) return;
+    const T* src = take_b ? vb : va;
     for (int c = lane * 8; c < d; c += kGroup * 8) {
       float x[8];
-      load8_f32<T>(vb + c, x);
-      store8_f32<T>(va + c, x);
+      load8_f32<T>(src + c, x);
+      store8_f32<T>(vr + c, x);
     }
-    if (lane == 0) s[sidx] = sb;
+    if (lane == 0) sd[sidx] = take_b ? sb : sa;
     return;
   }
   const float m = fmaxf(sa, sb);
@@ -80,9 +96,9 @@ __global__ __launch_bounds__(kBlock) void merge_inplace_kernel(
     load8_f32<T>(vb + c, y);
 #pragma unroll
     for (int i = 0; i < 8; ++i) x[i] = x[i] * ca + y[i] * cb;
-    store8_f32<T>(va + c, x);
+    store8_f32<T>(vr + c, x);
   }
-  if (lane == 0) s[sidx] = m + logf(wa + wb);
+  if (lane == 0) sd[sidx] = m + logf(wa + wb);
 }
 
 constexpr int kStateChunk = 4;  // states whose loads are in flight together
@@ -166,6 +182,143 @@ __global__ __launch_bounds__(kBlock) void merge_states_kernel(
   if (lane == 0 && sout != nullptr) sout[row * h + head] = m == -INFINITY ? -INFINITY : m + logf(wsum);
 }
 
+// Device pointers of up to FA4CP_MAX_CP separate states, passed by value.
+struct StateList {
+  const void* v[FA4CP_MAX_CP];
+  const float* s[FA4CP_MAX_CP];
+};
+
+// S-way merge of states held in separate tensors (v[i] [rows, h, d], s[i] [rows, h]), so a
+// caller that keeps each step's partial in its own buffer merges them without stacking.
+// Same arithmetic as merge_states_kernel.  The state loop is unrolled over the array's
+// capacity so every pointer is read from the kernel arguments with a constant index.  A
+// state with LSE -inf is not read.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void merge_states_list_kernel(
+    StateList L, T* __restrict__ vout, float* __restrict__ sout, int64_t n_groups, int num_states,
+    int d) {
+  constexpr int NQ = sizeof(T) == 4 ? 2 : 1;  // 16-byte loads per 8 elements
+  const int64_t g = (int64_t)blockIdx.x * (kBlock / kGroup) + (threadIdx.x / kGroup);
+  const int lane = threadIdx.x % kGroup;
+  if (g >= n_groups) return;
+  float sv[FA4CP_MAX_CP];
+#pragma unroll
+  for (int i = 0; i < FA4CP_MAX_CP; ++i) sv[i] = i < num_states ? L.s[i][g] : -INFINITY;
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < FA4CP_MAX_CP; ++i) m = fmaxf(m, sv[i]);
+  T* vo = vout + g * (int64_t)d;
+  if (m == -INFINITY) {
+    const float zero8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int c = lane * 8; c < d; c += kGroup * 8) store8_f32<T>(vo + c, zero8);
+    if (lane == 0 && sout != nullptr) sout[g] = -INFINITY;
+    return;
+  }
+  float w[FA4CP_MAX_CP];
+  float wsum = 0.f;
+#pragma unroll
+  for (int i = 0; i < FA4CP_MAX_CP; ++i) {
+    w[i] = sv[i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((sv[i] - m) * kLog2e);
+    wsum += w[i];
+  }
+  const float inv = 1.0f / wsum;
+  for (int c = lane * 8; c < d; c += kGroup * 8) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int i0 = 0; i0 < FA4CP_MAX_CP; i0 += kStateChunk) {
+      if (i0 >= num_states) break;
+      u32x4 raw[kStateChunk][NQ];
+#pragma unroll
+      for (int i = 0; i < kStateChunk; ++i) {
+        const int st = i0 + i;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) raw[i][q] = u32x4{0, 0, 0, 0};
+        if (w[st] != 0.f) {
+          const T* p = static_cast<const T*>(L.v[st]) + g * (int64_t)d + c;
+#pragma unroll
+          for (int q = 0; q < NQ; ++q) raw[i][q] = reinterpret_cast<const u32x4*>(p)[q];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kStateChunk; ++i) {
+        const float wi = w[i0 + i];
+        if constexpr (sizeof(T) == 4) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] += wi * __uint_as_float(raw[i][e / 4][e % 4]);
+        } else {
+          typedef T t8 __attribute__((ext_vector_type(8)));
+          const t8 a = __builtin_bit_cast(t8, raw[i][0]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] += wi * (float)a[e];
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= inv;
+    store8_f32<T>(vo + c, acc);
+  }
+  if (lane == 0 && sout != nullptr) sout[g] = m + logf(wsum);
+}
+
+// Checks shared by the two-way merges; returns the number of (row, head) groups to merge
+// (>= 0) or a negative status.
+int merge2_check(const char* what, const void* v, const float* s, const void* v_other, const float* s_other,
+                 const void* v_dst, const float* s_dst, int64_t rows, int32_t h, int32_t d,
+                 const int32_t* cu, int32_t nseq, int32_t row_sel, int64_t* n_groups) {
+  if (rows > 0 && (!v || !s || !v_other || !s_other || !v_dst || !s_dst))  // NULL only with no rows
+    return set_error(FA4CP_EINVAL, "%s: null pointer", what);
+  if ((reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(v_other) |
+       reinterpret_cast<uintptr_t>(v_dst)) % 16 != 0)
+    return set_error(FA4CP_EINVAL, "%s: v and v_other must be 16-byte aligned", what);
+  if (rows < 0 || h <= 0 || d <= 0 || (d % 8) != 0)
+    return set_error(FA4CP_EINVAL, "%s: bad shape rows=%lld h=%d d=%d "
+                     "(d must be a positive multiple of 8)", what, (long long)rows, h, d);
+  if (row_sel != FA4CP_SEL_ALL && row_sel != FA4CP_SEL_FRONT_HALF &&
+      row_sel != FA4CP_SEL_BACK_HALF)
+    return set_error(FA4CP_EINVAL, "%s: bad row_sel %d", what, row_sel);
+  if (cu != nullptr && nseq <= 0)
+    return set_error(FA4CP_EINVAL, "%s: nseq must be >= 1 with cu", what);
+  if (row_sel != FA4CP_SEL_ALL && cu == nullptr && (rows % 2) != 0)
+    return set_error(FA4CP_EINVAL, "%s: half selection needs an even row count", what);
+  const int64_t sel_rows = (row_sel == FA4CP_SEL_ALL) ? rows : rows / 2;
+  *n_groups = sel_rows * h;
+  if ((*n_groups + (kBlock / kGroup) - 1) / (kBlock / kGroup) > 0x7fffffffLL)
+    return set_error(FA4CP_EINVAL, "%s: too many rows", what);
+  return FA4CP_OK;
+}
+
+int merge2_launch(const char* what, const void* v, const float* s, const void* v_other, const float* s_other,
+                  void* v_dst, float* s_dst, int64_t rows, int32_t h, int32_t d, int32_t dtype,
+                  const int32_t* cu, int32_t nseq, int32_t row_sel, void* stream) {
+  int64_t n_groups = 0;
+  const int rc = merge2_check(what, v, s, v_other, s_other, v_dst, s_dst, rows, h, d, cu, nseq, row_sel,
+                              &n_groups);
+  if (rc != FA4CP_OK) return rc;
+  if (n_groups == 0) return FA4CP_OK;
+  const dim3 grid((unsigned)((n_groups + (kBlock / kGroup) - 1) / (kBlock / kGroup)));
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case FA4CP_BF16:
+      hipLaunchKernelGGL(merge_inplace_kernel<__bf16>, grid, dim3(kBlock), 0, st, (const __bf16*)v, s,
+                         (const __bf16*)v_other, s_other, (__bf16*)v_dst, s_dst, n_groups, h, d, cu, nseq,
+                         row_sel, rows);
+      break;
+    case FA4CP_FP16:
+      hipLaunchKernelGGL(merge_inplace_kernel<_Float16>, grid, dim3(kBlock), 0, st, (const _Float16*)v, s,
+                         (const _Float16*)v_other, s_other, (_Float16*)v_dst, s_dst, n_groups, h, d, cu,
+                         nseq, row_sel, rows);
+      break;
+    case FA4CP_FP32:
+      hipLaunchKernelGGL(merge_inplace_kernel<float>, grid, dim3(kBlock), 0, st, (const float*)v, s,
+                         (const float*)v_other, s_other, (float*)v_dst, s_dst, n_groups, h, d, cu, nseq,
+                         row_sel, rows);
+      break;
+    default:
+      return set_error(FA4CP_EUNSUPPORTED, "%s: unsupported dtype %d", what, dtype);
+  }
+  return check_launch(what);
+}
+
 }  // namespace
 }  // namespace fa4cp
 
@@ -176,46 +329,17 @@ extern "C" int fa4cp_merge_state_inplace(void* v, float* s, const void* v_other,
                                          int32_t d, int32_t dtype, const int32_t* cu,
                                          int32_t nseq, int32_t row_sel, void* stream) {
   clear_error();
-  if (rows > 0 && (!v || !s || !v_other || !s_other))  // NULL only with no rows
-    return set_error(FA4CP_EINVAL, "merge_state_inplace: null pointer");
-  if ((reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(v_other)) % 16 != 0)
-    return set_error(FA4CP_EINVAL, "merge_state_inplace: v and v_other must be 16-byte aligned");
-  if (rows < 0 || h <= 0 || d <= 0 || (d % 8) != 0)
-    return set_error(FA4CP_EINVAL, "merge_state_inplace: bad shape rows=%lld h=%d d=%d "
-                     "(d must be a positive multiple of 8)", (long long)rows, h, d);
-  if (row_sel != FA4CP_SEL_ALL && row_sel != FA4CP_SEL_FRONT_HALF &&
-      row_sel != FA4CP_SEL_BACK_HALF)
-    return set_error(FA4CP_EINVAL, "merge_state_inplace: bad row_sel %d", row_sel);
-  if (cu != nullptr && nseq <= 0)
-    return set_error(FA4CP_EINVAL, "merge_state_inplace: nseq must be >= 1 with cu");
-  if (row_sel != FA4CP_SEL_ALL && cu == nullptr && (rows % 2) != 0)
-    return set_error(FA4CP_EINVAL, "merge_state_inplace: half selection needs even rows");
-  const int64_t sel_rows = (row_sel == FA4CP_SEL_ALL) ? rows : rows / 2;
-  const int64_t n_groups = sel_rows * h;
-  if (n_groups == 0) return FA4CP_OK;
-  const int64_t blocks = (n_groups + (kBlock / kGroup) - 1) / (kBlock / kGroup);
-  if (blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "merge_state_inplace: too many rows");
-  hipStream_t st = (hipStream_t)stream;
-  switch (dtype) {
-    case FA4CP_BF16:
-      hipLaunchKernelGGL(merge_inplace_kernel<__bf16>, dim3((unsigned)blocks), dim3(kBlock), 0, st,
-                         (__bf16*)v, s, (const __bf16*)v_other, s_other, n_groups, h, d, cu, nseq,
-                         row_sel, rows);
-      break;
-    case FA4CP_FP16:
-      hipLaunchKernelGGL(merge_inplace_kernel<_Float16>, dim3((unsigned)blocks), dim3(kBlock), 0,
-                         st, (_Float16*)v, s, (const _Float16*)v_other, s_other, n_groups, h, d,
-                         cu, nseq, row_sel, rows);
-      break;
-    case FA4CP_FP32:
-      hipLaunchKernelGGL(merge_inplace_kernel<float>, dim3((unsigned)blocks), dim3(kBlock), 0, st,
-                         (float*)v, s, (const float*)v_other, s_other, n_groups, h, d, cu, nseq,
-                         row_sel, rows);
-      break;
-    default:
-      return set_error(FA4CP_EUNSUPPORTED, "merge_state_inplace: unsupported dtype %d", dtype);
-  }
-  return check_launch("merge_state_inplace");
+  return merge2_launch("merge_state_inplace", v, s, v_other, s_other, v, s, rows, h, d, dtype, cu, nseq,
+                       row_sel, stream);
+}
+
+extern "C" int fa4cp_merge_state(const void* v, const float* s, const void* v_other, const float* s_other,
+                                 void* v_out, float* s_out, int64_t rows, int32_t h, int32_t d,
+                                 int32_t dtype, const int32_t* cu, int32_t nseq, int32_t row_sel,
+                                 void* stream) {
+  clear_error();
+  return merge2_launch("merge_state", v, s, v_other, s_other, v_out, s_out, rows, h, d, dtype, cu, nseq,
+                       row_sel, stream);
 }
 
 extern "C" int fa4cp_merge_states(const void* v, const float* s, void* v_out, float* s_out,
@@ -254,4 +378,49 @@ extern "C" int fa4cp_merge_states(const void* v, const float* s, void* v_out, fl
       return set_error(FA4CP_EUNSUPPORTED, "merge_states: unsupported dtype %d", dtype);
   }
   return check_launch("merge_states");
+}
+
+extern "C" int fa4cp_merge_states_list(const void* const* v, const float* const* s, int32_t num_states,
+                                       void* v_out, float* s_out, int64_t rows, int32_t h, int32_t d,
+                                       int32_t dtype, void* stream) {
+  clear_error();
+  if (num_states <= 0 || num_states > FA4CP_MAX_CP)
+    return set_error(FA4CP_EINVAL, "merge_states_list: num_states %d not in [1, %d]", num_states,
+                     FA4CP_MAX_CP);
+  if (rows < 0 || h <= 0 || d <= 0 || (d % 8) != 0)
+    return set_error(FA4CP_EINVAL, "merge_states_list: bad shape rows=%lld h=%d d=%d", (long long)rows, h, d);
+  const int64_t n_groups = rows * h;
+  if (n_groups == 0) return FA4CP_OK;
+  if (v == nullptr || s == nullptr || v_out == nullptr)
+    return set_error(FA4CP_EINVAL, "merge_states_list: null pointer");
+  StateList L{};
+  uintptr_t align = reinterpret_cast<uintptr_t>(v_out);
+  for (int i = 0; i < num_states; ++i) {
+    if (v[i] == nullptr || s[i] == nullptr)
+      return set_error(FA4CP_EINVAL, "merge_states_list: null pointer for state %d", i);
+    L.v[i] = v[i];
+    L.s[i] = s[i];
+    align |= reinterpret_cast<uintptr_t>(v[i]);
+  }
+  if (align % 16 != 0) return set_error(FA4CP_EINVAL, "merge_states_list: v tensors must be 16-byte aligned");
+  const int64_t blocks = (n_groups + (kBlock / kGroup) - 1) / (kBlock / kGroup);
+  if (blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "merge_states_list: too many rows");
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case FA4CP_BF16:
+      hipLaunchKernelGGL(merge_states_list_kernel<__bf16>, dim3((unsigned)blocks), dim3(kBlock), 0, st, L,
+                         (__bf16*)v_out, s_out, n_groups, num_states, d);
+      break;
+    case FA4CP_FP16:
+      hipLaunchKernelGGL(merge_states_list_kernel<_Float16>, dim3((unsigned)blocks), dim3(kBlock), 0, st, L,
+                         (_Float16*)v_out, s_out, n_groups, num_states, d);
+      break;
+    case FA4CP_FP32:
+      hipLaunchKernelGGL(merge_states_list_kernel<float>, dim3((unsigned)blocks), dim3(kBlock), 0, st, L,
+                         (float*)v_out, s_out, n_groups, num_states, d);
+      break;
+    default:
+      return set_error(FA4CP_EUNSUPPORTED, "merge_states_list: unsupported dtype %d", dtype);
+  }
+  return check_launch("merge_states_list");
 }

@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libfa4cp.so"
 # FA4CP_LIB selects another build of the library (the in-tree one by default)
 LIB_PATH = os.environ.get("FA4CP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # element types (FA4CP_*)
 BF16, FP16, E4M3, FP32 = 0, 1, 2, 3
@@ -183,6 +183,17 @@ SIGNATURES = {
         [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
          ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
          ctypes.c_int32, ctypes.c_void_p],
+    ),
+    "fa4cp_merge_state": (
+        ctypes.c_int,
+        [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+         ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
+         ctypes.c_int32, ctypes.c_void_p],
+    ),
+    "fa4cp_merge_states_list": (
+        ctypes.c_int,
+        [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p), ctypes.c_int32, ctypes.c_void_p,
+         ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p],
     ),
     "fa4cp_merge_states": (
         ctypes.c_int,

@@ -27,6 +27,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import weakref
 from dataclasses import dataclass
 from typing import List, Optional, Sequence, Tuple
 
@@ -60,6 +61,8 @@ class LocalKVRing:
         for k, v in zip(k_shards, v_shards):
             assert k.shape == v.shape == k_shards[0].shape, "every shard must have one shape"
             assert k.dtype == v.dtype == k_shards[0].dtype
+            assert k.dim() == 3 and k.stride(2) == 1 and v.stride(2) == 1, \
+                "K and V shards must be [T, H_kv, D] and contiguous in D"
         self.k = list(k_shards)
         self.v = list(v_shards)
 
@@ -82,6 +85,34 @@ class LocalKVRing:
         return cls(ks, vs)
 
 
+_checked_cu = {}  # id(cu tensor) -> (weak reference, tensor version) of cu tables found even
+
+
+def _check_even_lengths(cu_seqlens: Optional[torch.Tensor], total: int) -> None:
+    """Every local sequence is two zig-zag chunks of equal size, so its length must be even
+    (the reference asserts it through get_half_index, fa4_ring/zigzag.py:75, on every call).
+    The kernels split a sequence at (start + end) / 2 and the half-row merges at cu / 2,
+    which agree only for even lengths.  A device cu table is read once (one host
+    synchronisation) and remembered until it is modified or freed."""
+    if cu_seqlens is None:
+        if total % 2:
+            raise AssertionError(f"the local sequence has odd length {total}: a zig-zag shard is two "
+                                 "chunks of equal size")
+        return
+    key = id(cu_seqlens)
+    seen = _checked_cu.get(key)
+    if seen is not None and seen[0]() is cu_seqlens and seen[1] == cu_seqlens._version:
+        return
+    cu = cu_seqlens.to("cpu", torch.int64)
+    odd = ((cu[1:] - cu[:-1]) % 2 != 0).nonzero().flatten().tolist()
+    if odd:
+        raise AssertionError(f"local sequences {odd[:8]} have odd length: a zig-zag shard is two chunks of "
+                             "equal size")
+    if len(_checked_cu) > 256:
+        _checked_cu.clear()
+    _checked_cu[key] = (weakref.ref(cu_seqlens), cu_seqlens._version)
+
+
 def ring_flash_attn(
     local_q: torch.Tensor,  # [T, H, D] zig-zag local shard (T = sum of 2*h_j)
     local_k: Optional[torch.Tensor],  # [T, H_kv, D] (None with a PagedKVRing)
@@ -93,22 +124,29 @@ def ring_flash_attn(
     cu_seqlens: Optional[torch.Tensor] = None,  # local int32 [num_seq+1]; None -> one sequence
     max_seqlen: Optional[int] = None,
     fused: Optional[bool] = None,
-) -> torch.Tensor:
-    """This rank's local causal ring-attention output ``[T, H, D]``.
+    return_lse: bool = False,
+):
+    """This rank's local causal ring-attention output ``[T, H, D]`` (with ``return_lse``:
+    ``(out, lse)``, lse ``[T, H]`` float32, the natural-log LSE of every row over all the
+    keys it attends).
 
     ``fused`` (default: whenever supported) runs the whole sweep as one kernel over every
     source's K / V^T (``ring_sweep``): no per-step partials, no merges.  It needs
     cp_size in [2, 16] with a LocalKVRing and either bf16 / fp16 with head dim 64 or 128 and
     no descales, or e4m3 with head dim 128 or 256 (any descales); ``fused=False`` runs the
     per-step path of the reference (attention + LSE merge per step), which covers every
-    case.
+    case.  ``cfg.merge_mode`` chooses how the per-step path merges its partials
+    (incremental: in place after every step; batched: one merge_states at the end).  The
+    fused sweep has no partials to merge, so it runs for either mode; pass
+    ``fused=False`` to get the merge the mode names.
 
     One sequence per rank: leave ``cu_seqlens=None``.  Packed sequences: pass the LOCAL
     ``cu_seqlens`` (each entry a zig-zag ``2*h_j`` shard length) on the device and
-    ``max_seqlen``.  For cp_size > 1 ``group`` must be a LocalKVRing holding every source
-    rank's KV shard (KV is not moved between GPUs here), or a PagedKVRing holding every
-    source's paged K/V cache (the rank's own K/V come from it, so ``local_k`` / ``local_v``
-    are ignored; the per-step form gathers the pages into contiguous shards first)."""
+    ``max_seqlen``.  Every local sequence length must be even.  For cp_size > 1 ``group``
+    must be a LocalKVRing holding every source rank's KV shard (KV is not moved between
+    GPUs here), or a PagedKVRing holding every source's paged K/V cache (the rank's own K/V
+    come from it, so ``local_k`` / ``local_v`` are ignored; the per-step form gathers the
+    pages into contiguous shards first)."""
     S = cfg.cp_size
     rank = cfg.cp_rank
     scale = cfg.softmax_scale
@@ -117,6 +155,7 @@ def ring_flash_attn(
         assert max_seqlen is not None, "max_seqlen required when cu_seqlens is given"
     else:
         max_seqlen = total
+    _check_even_lengths(cu_seqlens, total)
     paged = isinstance(group, PagedKVRing)
     if paged:
         assert group.cp_size == S, f"PagedKVRing holds {group.cp_size} caches, cp_size is {S}"
@@ -132,9 +171,14 @@ def ring_flash_attn(
     can_fuse = 1 < S <= _lib.MAX_CP and (
         (descales is None and local_q.dtype in (torch.bfloat16, torch.float16) and d in (64, 128))
         or (e4m3 and d in (128, 256)))
+    def finish(out, lse):
+        return (out, lse) if return_lse else out
+
     if paged:
         if fused is not False and can_fuse:
-            return ring_sweep_paged(local_q, cfg, group, cu_seqlens, max_seqlen, descales=descales)
+            lse = _new_lse(local_q) if return_lse else None
+            return finish(ring_sweep_paged(local_q, cfg, group, cu_seqlens, max_seqlen, lse=lse,
+                                           descales=descales), lse)
         if fused:
             raise AssertionError("fused ring sweep needs cp_size in [2, 16] and bf16/fp16 with head dim "
                                  "64/128 and no descales, or e4m3 with head dim 128/256")
@@ -149,8 +193,9 @@ def ring_flash_attn(
     if fused is None:
         fused = can_fuse
     if fused:
-        return ring_sweep(local_q, local_k, local_v, cfg, group, cu_seqlens, max_seqlen,
-                          descales=descales)
+        lse = _new_lse(local_q) if return_lse else None
+        return finish(ring_sweep(local_q, local_k, local_v, cfg, group, cu_seqlens, max_seqlen, lse=lse,
+                                 descales=descales), lse)
 
     qd = descales.q if descales else None
 
@@ -190,13 +235,12 @@ def ring_flash_attn(
                 # front rows of this slot stay empty: -inf LSE makes them the identity
                 sbuf[:, step].fill_(float("-inf"))
                 attn(k, v, src, False, q_sel=SEL_BACK_HALF, out=vbuf[:, step], lse=sbuf[:, step])
-        out, _ = merge_states(vbuf, sbuf)
-        return out
+        return finish(*merge_states(vbuf, sbuf))
 
     # incremental (and cp_size == 1): step 0 seeds the accumulator with every row finite
     acc, acc_lse = attn(local_k, local_v, rank, True)
     if S == 1:
-        return acc
+        return finish(acc, acc_lse)
     part = torch.empty_like(acc)
     part_lse = torch.empty_like(acc_lse)
     for step in range(1, S):
@@ -209,7 +253,11 @@ def ring_flash_attn(
             attn(k, v, src, False, q_sel=SEL_BACK_HALF, out=part, lse=part_lse)
             merge_state_in_place(acc, acc_lse, part, part_lse, cu_seqlens=cu_seqlens,
                                  row_sel=SEL_BACK_HALF)
-    return acc
+    return finish(acc, acc_lse)
+
+
+def _new_lse(local_q: torch.Tensor) -> torch.Tensor:
+    return torch.empty(local_q.shape[:2], dtype=torch.float32, device=local_q.device)
 
 
 def ring_sweep(local_q: torch.Tensor, local_k: torch.Tensor, local_v: torch.Tensor, cfg: RingConfig,
@@ -235,6 +283,8 @@ def ring_sweep(local_q: torch.Tensor, local_k: torch.Tensor, local_v: torch.Tens
     for k, v in zip(ks, vs):
         assert k.shape == (total, h_kv, d) and v.shape == k.shape and k.dtype == local_q.dtype
         assert k.stride() == ks[0].stride(), "all K shards must share strides"
+        # the sweep's arguments carry K's row and head strides only: D must be contiguous
+        assert k.stride(2) == 1 and v.stride(2) == 1, "K and V shards must be contiguous in D"
     assert all(v.stride() == vs[0].stride() for v in vs), "all V shards must share strides"
     vts, stride = transpose_v_many(vs, cu_seqlens_k=cu_seqlens, max_seqlen_k=max_seqlen)
     return _sweep_launch(local_q, ks, vts, stride, cfg, cu_seqlens, max_seqlen, out, lse, descales)

@@ -27,8 +27,11 @@ def _require(cond: bool, msg: str) -> None:
 
 
 def local_seqlen(n: int, cp_size: int) -> int:
-    assert n % (2 * cp_size) == 0, f"seqlen {n} must be divisible by 2*cp_size={2 * cp_size}"
-    return n // cp_size
+    """Rows one rank holds of a length-n sequence: two zig-zag chunks of n / (2 cp_size)
+    (fa4_ring/zigzag.py:26-28)."""
+    chunks = 2 * cp_size
+    _require(n % chunks == 0, f"sequence length {n} is not a multiple of 2*cp_size = {chunks}")
+    return 2 * (n // chunks)
 
 
 def _row_bytes(x: torch.Tensor) -> int:
@@ -60,8 +63,8 @@ def _shard(x: torch.Tensor, cp_rank: int, cp_size: int, full_cu_dev, nseq: int) 
 def zigzag_shard(x: torch.Tensor, cp_rank: int, cp_size: int) -> torch.Tensor:
     """Full [N, ...] sequence -> this rank's local [2h, ...] shard."""
     n = x.shape[0]
-    assert n % (2 * cp_size) == 0, f"seqlen {n} must be divisible by 2*cp_size={2 * cp_size}"
-    assert 0 <= cp_rank < cp_size
+    local_seqlen(n, cp_size)
+    _require(0 <= cp_rank < cp_size, f"cp_rank {cp_rank} outside [0, {cp_size})")
     return _shard(x, cp_rank, cp_size, None, 1)
 
 
@@ -84,30 +87,35 @@ def _unshard(local_shards: Sequence[torch.Tensor], cp_size: int, full_cu_dev, ns
 
 def zigzag_unshard(local_shards: List[torch.Tensor], cp_size: int) -> torch.Tensor:
     """Inverse of zigzag_shard: stitch the cp_size per-rank [2h, ...] shards into [N, ...]."""
-    assert len(local_shards) == cp_size
+    _require(len(local_shards) == cp_size, f"{len(local_shards)} shards given for cp_size {cp_size}")
     return _unshard(local_shards, cp_size, None, 1, local_shards[0].shape[0] * cp_size)
 
 
 def half_indices(local_len: int, device) -> Tuple[torch.Tensor, torch.Tensor]:
-    """(first_half, second_half) row indices of a local [2h] sequence."""
-    h = local_len // 2
-    return (torch.arange(0, h, device=device), torch.arange(h, local_len, device=device))
+    """Row indices of the early and the late zig-zag chunk of one local sequence of
+    ``local_len`` rows (fa4_ring/zigzag.py:53-62)."""
+    rows = torch.arange(local_len, device=device)
+    return rows[:local_len // 2], rows[local_len // 2:]
 
 
 def get_half_index(cu_seqlens: torch.Tensor, *, front: bool) -> torch.Tensor:
-    """Long indices of the front (early) or back (late) half of each packed sequence of
-    ``cu_seqlens`` (int32 [num_seq+1]); each local sequence has even length and its
-    midpoint is (start + end) // 2."""
-    device = cu_seqlens.device
-    cu = _as_cu_list(cu_seqlens)
-    parts = []
-    for i in range(len(cu) - 1):
-        start, end = cu[i], cu[i + 1]
-        assert (end - start) % 2 == 0, "each local sequence length must be even (zig-zag)"
-        mid = (start + end) // 2
-        parts.append(torch.arange(start, mid, device=device) if front
-                     else torch.arange(mid, end, device=device))
-    return torch.cat(parts) if parts else torch.empty(0, dtype=torch.long, device=device)
+    """int64 row indices of the early (``front``) or late chunk of every packed local
+    sequence of ``cu_seqlens`` (int32 [num_seq+1]), in order (fa4_ring/zigzag.py:65-79).
+    Every local sequence is two chunks of equal size, so its length must be even.
+
+    Built in one pass without a per-sequence loop: sequence j contributes
+    ``first_j + [0, half_j)`` with ``half_j = len_j / 2`` and ``first_j = cu[j]`` (front) or
+    ``cu[j] + half_j`` (late).  Reads cu on the host (one synchronisation), as the reference
+    does."""
+    cu = torch.as_tensor(cu_seqlens).to("cpu", torch.int64)
+    lens = cu[1:] - cu[:-1]
+    _require(bool((lens % 2 == 0).all()), "every local sequence must have an even length "
+             "(two zig-zag chunks of equal size)")
+    half = lens // 2
+    first = cu[:-1] if front else cu[:-1] + half
+    offset_in_seq = torch.arange(int(half.sum())) - torch.repeat_interleave(torch.cumsum(half, 0) - half, half)
+    rows = torch.repeat_interleave(first, half) + offset_in_seq
+    return rows.to(torch.as_tensor(cu_seqlens).device)
 
 
 def zigzag_shard_varlen(x: torch.Tensor, full_cu_seqlens: Union[torch.Tensor, Sequence[int]],
@@ -117,12 +125,11 @@ def zigzag_shard_varlen(x: torch.Tensor, full_cu_seqlens: Union[torch.Tensor, Se
     ``full_cu_seqlens`` holds the FULL sequence boundaries (int list or tensor).  Returns
     (local_packed, local_cu_seqlens) with local_cu_seqlens int32 on x's device."""
     cu = _as_cu_list(full_cu_seqlens)
-    assert 0 <= cp_rank < cp_size
+    _require(0 <= cp_rank < cp_size, f"cp_rank {cp_rank} outside [0, {cp_size})")
     local_cu = [0]
     for j in range(len(cu) - 1):
         n = cu[j + 1] - cu[j]
-        assert n % (2 * cp_size) == 0, f"seqlen {n} must be divisible by 2*cp_size={2 * cp_size}"
-        local_cu.append(local_cu[-1] + n // cp_size)
+        local_cu.append(local_cu[-1] + local_seqlen(n, cp_size))
     _require(cu[0] == 0 and cu[-1] == x.shape[0], "full_cu_seqlens must span x from row 0")
     local_cu_t = torch.tensor(local_cu, dtype=torch.int32, device=x.device)
     if len(cu) < 2:
@@ -134,9 +141,9 @@ def zigzag_shard_varlen(x: torch.Tensor, full_cu_seqlens: Union[torch.Tensor, Se
 def zigzag_unshard_varlen(local_shards: List[torch.Tensor],
                           full_cu_seqlens: Union[torch.Tensor, Sequence[int]], cp_size: int):
     """Inverse of zigzag_shard_varlen over all ranks -> the packed full tensor."""
-    assert len(local_shards) == cp_size
+    _require(len(local_shards) == cp_size, f"{len(local_shards)} shards given for cp_size {cp_size}")
     cu = _as_cu_list(full_cu_seqlens)
     for j in range(len(cu) - 1):
-        assert (cu[j + 1] - cu[j]) % (2 * cp_size) == 0
+        local_seqlen(cu[j + 1] - cu[j], cp_size)
     return _unshard(local_shards, cp_size, _device_cu(full_cu_seqlens, local_shards[0].device),
                     len(cu) - 1, cu[-1])

@@ -21,7 +21,11 @@
  * Reference interfaces replaced (paths are in hxy0118/fa4-cp):
  *   fa4cp_attn_fwd              <- fa4_ring/fa4_backend.py:58-123 (fa4_attn -> FA4 _flash_attn_fwd)
  *   fa4cp_merge_state_inplace   <- fa4_ring/merge.py:31-36 (flashinfer.cascade.merge_state_in_place)
+ *   fa4cp_merge_state           <- fa4_ring/merge.py:45-64 (IncrementalMerger.add's first merge, which
+ *                                  the reference does as clone() + merge_state_in_place)
  *   fa4cp_merge_states          <- fa4_ring/merge.py:39-42 (flashinfer.cascade.merge_states)
+ *   fa4cp_merge_states_list     <- fa4_ring/merge.py:67-86 (BatchedMerger.result: torch.stack of the
+ *                                  partials, then merge_states)
  *   fa4cp_zigzag_shard          <- fa4_ring/zigzag.py:31-39 and :82-97 (zigzag_shard, zigzag_shard_varlen)
  *   fa4cp_zigzag_unshard        <- fa4_ring/zigzag.py:42-50 (zigzag_unshard)
  *   fa4cp_transpose_v(_many)    <- no counterpart: the V^T layout the fast attention kernels
@@ -42,7 +46,7 @@
 extern "C" {
 #endif
 
-#define FA4CP_ABI_VERSION 4
+#define FA4CP_ABI_VERSION 5
 
 /* status codes */
 #define FA4CP_OK 0
@@ -232,7 +236,8 @@ int fa4cp_ring_sweep_fwd(const fa4cp_sweep_args* args, void* stream);
  * log LSE):
  *     m = max(s, s_o);  w = e^(s-m);  w_o = e^(s_o-m)
  *     v <- (v*w + v_o*w_o) / (w + w_o);   s <- m + log(w + w_o)
- * A side whose s is -inf contributes nothing (its v is not read).  v, v_other: [rows, h, d]
+ * A side whose s is -inf contributes nothing (its v is not read); if both are -inf, v becomes
+ * NaN and s stays -inf (see fa4cp_merge_state).  v, v_other: [rows, h, d]
  * contiguous in dtype (BF16, FP16 or FP32); s, s_other: [rows, h] float32.  Math is fp32.
  * row_sel = SEL_ALL merges every row; BACK_HALF / FRONT_HALF merge only those rows of each
  * sequence of cu[0..nseq] (cu == NULL: one sequence of `rows` rows).
@@ -242,6 +247,16 @@ int fa4cp_merge_state_inplace(void* v, float* s, const void* v_other, const floa
                               const int32_t* cu, int32_t nseq, int32_t row_sel, void* stream);
 
 /*
+ * The same merge out of place: (v_out, s_out) <- merge((v, s), (v_other, s_other)); rows
+ * outside row_sel are not written.  (v_out, s_out) may be (v, s) (that is
+ * fa4cp_merge_state_inplace).  When both LSEs are -inf, v_out gets NaN and s_out -inf, the
+ * value of the max-shifted formula (the reference's mergers NaN-poison such rows).
+ */
+int fa4cp_merge_state(const void* v, const float* s, const void* v_other, const float* s_other,
+                      void* v_out, float* s_out, int64_t rows, int32_t h, int32_t d, int32_t dtype,
+                      const int32_t* cu, int32_t nseq, int32_t row_sel, void* stream);
+
+/*
  * Batched merge of num_states partial states (flashinfer.cascade.merge_states semantics):
  * v [rows, num_states, h, d] (dtype), s [rows, num_states, h] float32 ->
  * v_out [rows, h, d] (dtype), s_out [rows, h] float32 (s_out may be NULL).
@@ -249,6 +264,15 @@ int fa4cp_merge_state_inplace(void* v, float* s, const void* v_other, const floa
  */
 int fa4cp_merge_states(const void* v, const float* s, void* v_out, float* s_out, int64_t rows,
                        int32_t num_states, int32_t h, int32_t d, int32_t dtype, void* stream);
+
+/*
+ * merge_states over states kept in separate tensors: v[i] [rows, h, d] (dtype, contiguous,
+ * 16-byte aligned) and s[i] [rows, h] float32 for i < num_states (1..FA4CP_MAX_CP; host
+ * arrays of device pointers).  Same result as fa4cp_merge_states on the stacked tensors,
+ * without the stack.  A state whose s is -inf is not read; s_out may be NULL.
+ */
+int fa4cp_merge_states_list(const void* const* v, const float* const* s, int32_t num_states, void* v_out,
+                            float* s_out, int64_t rows, int32_t h, int32_t d, int32_t dtype, void* stream);
 
 /*
  * FP8 producer: OCP e4m3 quantisation of x [rows, h, d] (BF16, FP16 or FP32; any row and head

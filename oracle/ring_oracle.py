@@ -330,6 +330,57 @@ def dense_causal_rows(q_full, k_full, v_full, rows: Sequence[int], heads: Sequen
     return torch.stack(outs), torch.stack(lses)
 
 
+def dense_causal_rows_all_heads(q_rows: torch.Tensor, positions: Sequence[int], seq_starts: Sequence[int],
+                                k_full: torch.Tensor, v_full: torch.Tensor, scale: float,
+                                key_block: int = 8192):
+    """Exact fp32 causal attention of many query rows, every head: query row i (q_rows[i],
+    [H_q, D]) sits at packed position positions[i] of a sequence that starts at
+    seq_starts[i], so it sees keys seq_starts[i] .. positions[i] of k_full / v_full
+    [N, H_kv, D].  Returns (out [R, H_q, Dv], lse [R, H_q]).
+
+    The same arithmetic as dense_causal_rows (one row, one head at a time), batched: the
+    query heads of a kv head are stacked, and keys go in blocks of ``key_block`` folded with
+    the online-softmax merge (merge(), the identity this oracle's merge tests pin), each
+    block only for the rows that see part of it."""
+    r_count, h_q, d = q_rows.shape
+    h_kv = k_full.shape[1]
+    g = h_q // h_kv
+    pos = torch.as_tensor(list(positions), dtype=torch.int64)
+    start = torch.as_tensor(list(seq_starts), dtype=torch.int64)
+    out = torch.zeros(r_count, h_q, v_full.shape[2])
+    lse = torch.full((r_count, h_q), float("-inf"))
+    if r_count == 0:
+        return out, lse
+    qf = q_rows.float()
+    k0 = int(start.min())
+    k1 = int(pos.max()) + 1
+    for b0 in range(k0, k1, key_block):
+        b1 = min(k1, b0 + key_block)
+        rows = ((start < b1) & (pos >= b0)).nonzero().flatten()
+        if rows.numel() == 0:
+            continue
+        kb = k_full[b0:b1].float()  # [B, H_kv, D]
+        vb = v_full[b0:b1].float()
+        kpos = torch.arange(b0, b1)
+        visible = (kpos.unsqueeze(0) >= start[rows].unsqueeze(1)) & (kpos.unsqueeze(0) <= pos[rows].unsqueeze(1))
+        for gi in range(h_kv):
+            qh = qf[rows, gi * g:(gi + 1) * g, :]  # [r, g, D]
+            sc = torch.einsum("rgd,kd->rgk", qh, kb[:, gi]) * scale
+            sc = sc.masked_fill(~visible.unsqueeze(1), float("-inf"))
+            bl = torch.logsumexp(sc, dim=-1)  # [r, g]
+            p = torch.exp(sc - torch.where(torch.isinf(bl), torch.zeros_like(bl), bl).unsqueeze(-1))
+            bo = torch.einsum("rgk,kd->rgd", p, vb[:, gi])
+            mo, ml = merge(out[rows, gi * g:(gi + 1) * g], lse[rows, gi * g:(gi + 1) * g], bo, bl)
+            # a row with no visible key in this block keeps its state (merge would NaN it
+            # only if both were -inf, which happens before the first visible block)
+            keep = torch.isinf(bl) & (bl < 0)
+            mo = torch.where(keep.unsqueeze(-1), out[rows, gi * g:(gi + 1) * g], mo)
+            ml = torch.where(keep, lse[rows, gi * g:(gi + 1) * g], ml)
+            out[rows, gi * g:(gi + 1) * g] = mo
+            lse[rows, gi * g:(gi + 1) * g] = ml
+    return out, lse
+
+
 # --------------------------------------------------------------------------------------
 # OCP e4m3fn
 # --------------------------------------------------------------------------------------

@@ -8,7 +8,7 @@ import torch
 
 from fa4_ring import zigzag as Z
 from fa4_ring.fa4_backend import SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, fa4_attn
-from fa4_ring.merge import merge_state_in_place, merge_states
+from fa4_ring.merge import make_merger, merge_state, merge_state_in_place, merge_states, merge_states_list
 from gpu_helpers import (DEV, TOL_BF16_OUT, TOL_FP8_OUT, TOL_LSE, TOL_MERGE_FP32, lse_err, max_err,
                          oracle_attn, rounded, say, scale_for, seq_bounds)
 from oracle import ring_oracle as O
@@ -99,9 +99,136 @@ def test_merge_state_in_place(dtype, t, h, d):
     ok = ~both
     assert_rounded_close(vd, eo, dtype, ok.unsqueeze(-1).expand_as(eo))
     assert lse_err(sd.cpu()[ok], el[ok]) <= TOL_MERGE_FP32
-    # rows where both sides are empty keep the accumulator untouched (documented; the
-    # reference's merge would produce NaN there)
-    assert torch.equal(sd.cpu()[both], sa[both])
+    # rows where both sides are empty: the oracle's (the reference formula's) NaN out and
+    # -inf LSE
+    assert both.any()
+    assert torch.isnan(eo[both]).all() and torch.isnan(vd.cpu().float()[both]).all()
+    assert lse_err(sd.cpu()[both], el[both]) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_merge_state_out_of_place(dtype):
+    """merge_state writes a new state equal bit for bit to the in-place merge and leaves its
+    inputs alone."""
+    say(f"merge_state out of place dtype={dtype}")
+    t, h, d = 300, 4, 128
+    va, sa = _states(t, h, d, 5, dtype, inf_frac=0.1)
+    vb, sb = _states(t, h, d, 6, dtype, inf_frac=0.1)
+    a_v, a_s, b_v, b_s = va.to(dtype).to(DEV), sa.to(DEV), vb.to(dtype).to(DEV), sb.to(DEV)
+    keep = [x.clone() for x in (a_v, a_s, b_v, b_s)]
+    ov, os_ = merge_state(a_v, a_s, b_v, b_s)
+    for x, y in zip((a_v, a_s, b_v, b_s), keep):
+        assert torch.equal(x, y), "an input was modified"
+    iv, is_ = a_v.clone(), a_s.clone()
+    merge_state_in_place(iv, is_, b_v, b_s)
+    torch.cuda.synchronize()
+    assert torch.equal(ov.cpu().view(torch.uint8), iv.cpu().view(torch.uint8))
+    assert torch.equal(os_.cpu().view(torch.uint8), is_.cpu().view(torch.uint8))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("t,ns,h,d", [(50, 8, 4, 128), (17, 3, 2, 64), (64, 1, 1, 256), (40, 16, 2, 128),
+                                      (33, 21, 3, 64)])
+def test_merge_states_list(dtype, t, ns, h, d):
+    """The S-way merge over separate tensors equals the oracle's merge_states of their stack;
+    -inf states are not read (their v is NaN); more states than one launch takes are merged
+    in groups."""
+    say(f"merge_states_list dtype={dtype} t={t} S={ns} h={h} d={d}")
+    g = torch.Generator().manual_seed(100 + ns)
+    v = rounded(torch.randn(t, ns, h, d, generator=g), dtype)
+    s = torch.randn(t, ns, h, generator=g) * 3
+    s[torch.rand(t, ns, h, generator=g) < 0.2] = float("-inf")
+    s[0] = float("-inf")
+    vn = v.clone()
+    vn[torch.isinf(s)] = float("nan")
+    vs = [vn[:, i].contiguous().to(dtype).to(DEV) for i in range(ns)]
+    ss = [s[:, i].contiguous().to(DEV) for i in range(ns)]
+    out, so = merge_states_list(vs, ss)
+    eo, el = O.merge_states(v, s)
+    if ns <= 16:
+        assert_rounded_close(out, eo, dtype)
+    else:
+        # the first group's result is stored in the v type before the second merge: one more
+        # rounding, of a value no larger than max |v|
+        bound = TOL_MERGE_FP32 + 2 * _HALF_ULP[dtype] * float(v.abs().max())
+        assert max_err(out, eo) <= bound
+    assert lse_err(so, el) <= TOL_MERGE_FP32
+
+
+def _ring_partials(n, h, hkv, d, cp, rank, dtype=torch.bfloat16):
+    """Full-size per-step partials of one rank's small ring, as the reference's loop builds
+    them (fa4_ring/ring_attention.py:112-172, the late-Q steps padded with zeros / -inf),
+    from this library's attention kernel, plus the oracle's partials of the same steps."""
+    from fa4_ring.fa4_backend import SEL_BACK_HALF as BACK, SEL_FRONT_HALF as FRONT, fa4_attn
+
+    q, k, v = O.random_qkv(n, h, hkv, d, seed=7)
+    q, k, v = (rounded(x, dtype) for x in (q, k, v))
+    ks = [O.zigzag_shard(k, r, cp) for r in range(cp)]
+    vs = [O.zigzag_shard(v, r, cp) for r in range(cp)]
+    lq = O.zigzag_shard(q, rank, cp)
+    lqd = lq.to(dtype).to(DEV)
+    parts = []
+    for step in range(cp):
+        src = (rank - step) % cp
+        kd, vd = ks[src].to(dtype).to(DEV), vs[src].to(dtype).to(DEV)
+        if step == 0:
+            o, l = fa4_attn(lqd, kd, vd, causal=True)
+        elif step <= rank:
+            o, l = fa4_attn(lqd, kd, vd, causal=False, k_sel=FRONT)
+        else:
+            o = torch.zeros_like(lqd)
+            l = torch.full(lqd.shape[:2], float("-inf"), device=DEV)
+            fa4_attn(lqd, kd, vd, causal=False, q_sel=BACK, out=o, lse=l)
+        parts.append((o, l))
+    oracle_parts = [O.ring_rank(lq, ks, vs, rank, cp, scale_for(d), steps=[st]) for st in range(cp)]
+    return parts, oracle_parts
+
+
+@pytest.mark.parametrize("mode", ["incremental", "batched"])
+@pytest.mark.parametrize("rank", [0, 2, 3])
+def test_mergers_on_device_ring_partials(mode, rank):
+    """IncrementalMerger / BatchedMerger (via make_merger) fed one rank's device partials
+    step by step, as the reference's ring loop feeds them: the result equals the oracle's
+    merge of the oracle's partials, and the caller's partials are never modified."""
+    say(f"merger {mode} on device ring partials rank={rank}")
+    n, h, hkv, d, cp = 1024, 8, 2, 128, 4
+    parts, oparts = _ring_partials(n, h, hkv, d, cp, rank)
+    keep = [(o.clone(), l.clone()) for o, l in parts]
+    m = make_merger(mode)
+    for o, l in parts:
+        m.add(o, l)
+    out = m.result()
+    torch.cuda.synchronize()
+    for (o, l), (ko, kl) in zip(parts, keep):
+        assert torch.equal(o, ko) and torch.equal(l, kl), "a partial was modified"
+    if mode == "incremental":
+        eo, el = oparts[0]
+        for o, l in oparts[1:]:
+            eo, el = O.merge(eo, el, o, l)
+        assert lse_err(m.lse, el) <= TOL_LSE
+    else:
+        eo, el = O.merge_states(torch.stack([p[0] for p in oparts], 1), torch.stack([p[1] for p in oparts], 1))
+        _, lse = m.result_with_lse()
+        assert lse_err(lse, el) <= TOL_LSE
+    assert out.dtype == torch.bfloat16 and out.shape == (n // cp, h, d)
+    assert max_err(out, eo) <= TOL_BF16_OUT
+
+
+@pytest.mark.parametrize("mode", ["incremental", "batched"])
+def test_merger_single_partial(mode):
+    """One partial: the incremental merger returns a copy (later changes to the caller's
+    tensor do not reach it), the batched one the partial itself, as the reference's."""
+    say(f"merger {mode} single partial")
+    o = torch.randn(64, 2, 64, device=DEV).to(torch.bfloat16)
+    l = torch.randn(64, 2, device=DEV)
+    m = make_merger(mode)
+    m.add(o, l)
+    r = m.result()
+    assert torch.equal(r, o)
+    if mode == "incremental":
+        assert r.data_ptr() != o.data_ptr()
+    else:
+        assert r is o
 
 
 @pytest.mark.parametrize("cu", [None, [0, 8, 20, 64], [0, 8, 8, 20, 64, 64]])

@@ -14,7 +14,7 @@ from fa4_ring import Descales, LocalKVRing, PagedKVRing, RingConfig, ring_flash_
 from fa4_ring.fa4_backend import transpose_v_many
 from fa4_ring.paged import gather_kv_pages, transpose_v_paged_many
 from fa4_ring.zigzag import zigzag_shard_varlen
-from gpu_helpers import DEV, TOL_BF16_OUT, max_err, rounded, say, scale_for
+from gpu_helpers import DEV, TOL_BF16_OUT, TOL_LSE, lse_err, max_err, rounded, say, scale_for
 from oracle import ring_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -153,16 +153,19 @@ def test_paged_sweep_equals_contiguous(dtype, d, cp, full_lens, n, page_size, de
         paged = PagedKVRing.from_shards(ring.k, ring.v, page_size, local_cu, spare_pages=2,
                                         generator=torch.Generator().manual_seed(rank))
         cfg = RingConfig(cp_size=cp, cp_rank=rank)
-        want = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc,
-                               cu_seqlens=lcu, max_seqlen=mx, fused=True)
-        got = ring_flash_attn(lq, None, None, cfg, group=paged, descales=desc, cu_seqlens=lcu, max_seqlen=mx)
+        want, want_lse = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc,
+                                         cu_seqlens=lcu, max_seqlen=mx, fused=True, return_lse=True)
+        got, got_lse = ring_flash_attn(lq, None, None, cfg, group=paged, descales=desc, cu_seqlens=lcu,
+                                       max_seqlen=mx, return_lse=True)
         assert torch.equal(bits(got), bits(want)), f"rank {rank}"
+        assert torch.equal(bits(got_lse), bits(want_lse)), f"rank {rank} lse"
     if dtype == torch.bfloat16 and full_cu is None:  # the oracle, on the last rank
         qr, kr, vr = (rounded(t, dtype) for t in (q, k, v))
         ks = [O.zigzag_shard(kr, r, cp) for r in range(cp)]
         vs = [O.zigzag_shard(vr, r, cp) for r in range(cp)]
-        ref, _ = O.ring_rank(O.zigzag_shard(qr, rank, cp), ks, vs, rank, cp, scale_for(d))
+        ref, ref_lse = O.ring_rank(O.zigzag_shard(qr, rank, cp), ks, vs, rank, cp, scale_for(d))
         assert max_err(got, ref) <= TOL_BF16_OUT
+        assert lse_err(got_lse, ref_lse) <= TOL_LSE
 
 
 def test_paged_sweep_full_size_bf16_rank3():
@@ -177,9 +180,10 @@ def test_paged_sweep_full_size_bf16_rank3():
     ring = LocalKVRing(ks, vs)
     paged = PagedKVRing.from_shards(ks, vs, 256, spare_pages=5, generator=torch.Generator().manual_seed(9))
     cfg = RingConfig(cp_size=cp, cp_rank=rank)
-    want = ring_flash_attn(q, ks[rank], vs[rank], cfg, group=ring)
-    got = ring_flash_attn(q, None, None, cfg, group=paged)
+    want, want_lse = ring_flash_attn(q, ks[rank], vs[rank], cfg, group=ring, return_lse=True)
+    got, got_lse = ring_flash_attn(q, None, None, cfg, group=paged, return_lse=True)
     assert torch.equal(bits(got), bits(want))
+    assert torch.equal(bits(got_lse), bits(want_lse))
 
 
 PER_STEP_CASES = [  # (dtype, d, cp, merge mode): shapes the fused sweep does not take, and fused=False
@@ -202,6 +206,8 @@ def test_paged_per_step_equals_contiguous(dtype, d, cp, mode):
         paged = PagedKVRing.from_shards(ring.k, ring.v, 128, spare_pages=1,
                                         generator=torch.Generator().manual_seed(rank))
         cfg = RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode)
-        want = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, fused=False)
-        got = ring_flash_attn(lq, None, None, cfg, group=paged, fused=False)
+        want, want_lse = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, fused=False,
+                                         return_lse=True)
+        got, got_lse = ring_flash_attn(lq, None, None, cfg, group=paged, fused=False, return_lse=True)
         assert torch.equal(bits(got), bits(want)), f"rank {rank}"
+        assert torch.equal(bits(got_lse), bits(want_lse)), f"rank {rank} lse"

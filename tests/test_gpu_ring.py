@@ -16,7 +16,7 @@ import torch
 from fa4_ring import Descales, LocalKVRing, RingConfig, ring_flash_attn, zigzag_shard, zigzag_unshard
 from fa4_ring.reference import full_causal_reference
 from fa4_ring.zigzag import zigzag_shard_varlen, zigzag_unshard_varlen
-from gpu_helpers import DEV, TOL_BF16_OUT, TOL_FP8_OUT, max_err, rounded, say, scale_for
+from gpu_helpers import DEV, TOL_BF16_OUT, TOL_FP8_OUT, TOL_LSE, lse_err, max_err, rounded, say, scale_for
 from oracle import ring_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -57,11 +57,14 @@ def test_ring_all_ranks_small(n, h, hkv, d, cp, mode):
     outs = []
     for rank in range(cp):
         cfg, fused = _cfg_path(mode, cp, rank)
-        out = ring_flash_attn(zigzag_shard(qd, rank, cp), ring.k[rank], ring.v[rank], cfg, group=ring,
-                              fused=fused)
+        out, lse = ring_flash_attn(zigzag_shard(qd, rank, cp), ring.k[rank], ring.v[rank], cfg, group=ring,
+                                   fused=fused, return_lse=True)
         assert out.dtype == torch.bfloat16 and out.shape == (n // cp, h, d)
-        ref, _ = O.ring_rank(O.zigzag_shard(q, rank, cp), ks, vs, rank, cp, scale, merge_mode=cfg.merge_mode)
+        assert lse.dtype == torch.float32 and lse.shape == (n // cp, h)
+        ref, ref_lse = O.ring_rank(O.zigzag_shard(q, rank, cp), ks, vs, rank, cp, scale,
+                                   merge_mode=cfg.merge_mode)
         assert max_err(out, ref) <= TOL_BF16_OUT, f"rank {rank}"
+        assert lse_err(lse, ref_lse) <= TOL_LSE, f"rank {rank} lse"
         outs.append(out.float().cpu())
     dense = O.dense_causal(q, k, v, scale)
     assert max_err(O.zigzag_unshard(outs, cp), dense) <= TOL_BF16_OUT
@@ -123,6 +126,24 @@ def test_reference_gpu_test_configuration(dtype_name, mode, num_seqs):
     assert err < tol and cos > 0.999
 
 
+@pytest.mark.parametrize("dtype_name,d,h,hkv", [("bfloat16", 128, 8, 2), ("float16", 64, 4, 4),
+                                                ("bfloat16", 256, 4, 1)])
+def test_full_causal_reference_hip_matches_torch(dtype_name, d, h, hkv):
+    """full_causal_reference's two backends agree: the library's causal kernel over the whole
+    sequence against the fp32 blocked reference (and both against the oracle)."""
+    dtype = getattr(torch, dtype_name)
+    say(f"full_causal_reference hip vs torch {dtype_name} d={d} h={h}/{hkv}")
+    q, k, v = O.random_qkv(1536, h, hkv, d, seed=13)
+    q, k, v = (rounded(x, dtype) for x in (q, k, v))
+    qd, kd, vd = (x.to(dtype).to(DEV) for x in (q, k, v))
+    hip = full_causal_reference(qd, kd, vd, backend="hip")
+    ref = full_causal_reference(qd, kd, vd, backend="torch")
+    assert hip.dtype == ref.dtype == dtype
+    tol = TOL_BF16_OUT if dtype == torch.bfloat16 else 5e-3
+    assert max_err(hip, ref) <= tol
+    assert max_err(ref, O.dense_causal(q, k, v, scale_for(d))) <= tol
+
+
 def test_ring_cp1_is_causal_attention():
     say("ring cp=1")
     q, k, v = O.random_qkv(512, 8, 2, 128, seed=2)
@@ -152,11 +173,12 @@ def test_ring_varlen_all_ranks(mode):
         lq, local_cu = zigzag_shard_varlen(qd, full_cu, rank, cp)
         max_local = int((local_cu[1:] - local_cu[:-1]).max())
         cfg, fused = _cfg_path(mode, cp, rank)
-        out = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring,
-                              cu_seqlens=local_cu, max_seqlen=max_local, fused=fused)
+        out, lse = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring,
+                                   cu_seqlens=local_cu, max_seqlen=max_local, fused=fused, return_lse=True)
         oq, ocu = O.zigzag_shard_varlen(q, full_cu, rank, cp)
-        ref, _ = O.ring_rank(oq, ks, vs, rank, cp, scale, cu=ocu, merge_mode=cfg.merge_mode)
+        ref, ref_lse = O.ring_rank(oq, ks, vs, rank, cp, scale, cu=ocu, merge_mode=cfg.merge_mode)
         assert max_err(out, ref) <= TOL_BF16_OUT, f"rank {rank}"
+        assert lse_err(lse, ref_lse) <= TOL_LSE, f"rank {rank} lse"
         outs.append(out.float().cpu())
     lcu = O.local_cu_from_full(full_cu, cp)
     for j in range(len(lens)):
@@ -200,11 +222,12 @@ def test_ring_fp8_all_ranks(n, h, hkv, d, cp, mode):
                         k=[torch.tensor(s, device=DEV) for s in sk],
                         v=[torch.tensor([s] * hkv, device=DEV) for s in sv])
         cfg, fused = _cfg_path(mode, cp, rank)
-        out = ring_flash_attn(q8.to(DEV), ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc,
-                              fused=fused)
+        out, lse = ring_flash_attn(q8.to(DEV), ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc,
+                                   fused=fused, return_lse=True)
         assert out.dtype == torch.bfloat16
-        ref, _ = O.ring_rank(dq, dk, dv, rank, cp, scale, merge_mode=cfg.merge_mode)
+        ref, ref_lse = O.ring_rank(dq, dk, dv, rank, cp, scale, merge_mode=cfg.merge_mode)
         assert max_err(out, ref) <= TOL_FP8_OUT, f"rank {rank}"
+        assert lse_err(lse, ref_lse) <= TOL_LSE, f"rank {rank} lse"
 
 
 @pytest.mark.parametrize("mode", PATHS)
@@ -225,11 +248,13 @@ def test_ring_fp8_varlen_all_ranks(mode):
         local_cu = torch.tensor(O.local_cu_from_full(full_cu, cp), dtype=torch.int32)
         max_local = int((local_cu[1:] - local_cu[:-1]).max())
         cfg, fused = _cfg_path(mode, cp, rank)
-        out = ring_flash_attn(q8.to(DEV), ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc,
-                              cu_seqlens=local_cu.to(DEV), max_seqlen=max_local, fused=fused)
+        out, lse = ring_flash_attn(q8.to(DEV), ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc,
+                                   cu_seqlens=local_cu.to(DEV), max_seqlen=max_local, fused=fused,
+                                   return_lse=True)
         assert out.dtype == torch.bfloat16
-        ref, _ = O.ring_rank(dq, dk, dv, rank, cp, scale, cu=local_cu.tolist(), merge_mode=cfg.merge_mode)
+        ref, ref_lse = O.ring_rank(dq, dk, dv, rank, cp, scale, cu=local_cu.tolist(), merge_mode=cfg.merge_mode)
         assert max_err(out, ref) <= TOL_FP8_OUT, f"rank {rank}"
+        assert lse_err(lse, ref_lse) <= TOL_LSE, f"rank {rank} lse"
 
 
 @pytest.mark.parametrize("mode", PATHS)
@@ -296,26 +321,58 @@ def test_ring_bf16_row_max_grows_mid_sweep(growth, mode):
 
 
 # ----------------------------------------------------------------- benchmark sizes
+#
+# At full size the oracle cannot run the whole sweep, so every rank output is checked two
+# ways: one row of every 64-row tile (a seeded random row inside the tile, plus the shard's
+# first, middle and last rows), every head, out and LSE, against exact dense causal
+# attention; and, on the device over every row, the fused sweep against the per-step form
+# (two different kernels: a mis-scheduled row tile or head group of one shows as a
+# difference there).
 
-def _sample_local_rows(t, n_random, seed):
-    h = t // 2
-    fixed = [0, 1, 31, 32, 63, 64, h - 1, h, h + 1, h + 63, h + 64, t - 1]
+
+def _tile_rows(t, seed, tile=64):
     rng = np.random.default_rng(seed)
-    return sorted(set(fixed + rng.integers(0, t, n_random).tolist()))
+    rows = {int(t0 + rng.integers(0, min(tile, t - t0))) for t0 in range(0, t, tile)}
+    rows.update([0, t // 2 - 1, t // 2, t - 1])
+    return sorted(r for r in rows if 0 <= r < t)
 
 
-def _check_sampled(out_local, rank, cp, n, qfull_f, kfull_f, vfull_f, scale, tol, seed):
-    """Compares sampled rows of one rank's output with exact dense causal attention."""
-    t, h, _ = out_local.shape
-    rows = _sample_local_rows(t, 24, seed)
-    grow = O.zigzag_rows(n, rank, cp)
-    rng = np.random.default_rng(seed + 1)
-    heads = rng.integers(0, h, len(rows)).tolist()
-    exp, _ = O.dense_causal_rows(qfull_f, kfull_f, vfull_f, [int(grow[i]) for i in rows], heads, scale)
-    got = out_local[rows, heads].float().cpu()
-    err = float((got - exp).abs().max())
-    assert err <= tol, f"rank {rank}: sampled max err {err}"
-    return err
+def _check_tiles(name, outs, lq_f, rows, positions, starts, k_full, v_full, scale, tol):
+    """Every form's out / lse (device, local rows) against dense causal attention at the
+    given rows, every head.  lq_f: the local q in fp32 on the host (the device inputs,
+    dequantised)."""
+    exp, exp_lse = O.dense_causal_rows_all_heads(lq_f[rows], positions, starts, k_full, v_full, scale)
+    idx = torch.tensor(rows, device=DEV)
+    for form, (out, lse) in outs.items():
+        got = out.index_select(0, idx).float().cpu()
+        got_lse = lse.index_select(0, idx).cpu()
+        err = float((got - exp).abs().max())
+        lerr = float((got_lse - exp_lse).abs().max())
+        say(f"  {name} {form}: {len(rows)} rows x {out.shape[1]} heads: max |out err| {err:.3e} (bar {tol}), "
+            f"max |lse err| {lerr:.3e} (bar {TOL_LSE})")
+        assert err <= tol, f"{name} {form}: out {err}"
+        assert lerr <= TOL_LSE, f"{name} {form}: lse {lerr}"
+
+
+def _check_forms_agree(name, ref_form, outs, tol):
+    """Every row of every form against the reference form, on the device."""
+    o0, l0 = outs[ref_form]
+    for form, (o, l) in outs.items():
+        if form == ref_form:
+            continue
+        e = float((o.float() - o0.float()).abs().max())
+        le = float((l - l0).abs().max())
+        say(f"  {name}: {form} vs {ref_form} over all rows: max |out diff| {e:.3e}, max |lse diff| {le:.3e}")
+        assert e <= tol and le <= TOL_LSE, f"{name}: {form} differs from {ref_form}: {e}, {le}"
+
+
+def _run_forms(lq, ring, cp, rank, forms, **kw):
+    outs = {}
+    for form in forms:
+        cfg, fused = _cfg_path(form, cp, rank)
+        outs[form] = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, fused=fused,
+                                     return_lse=True, **kw)
+    return outs
 
 
 @pytest.mark.parametrize("rank", [3, 7])
@@ -328,24 +385,23 @@ def test_ring_c2_bf16_full_size(rank):
     v = torch.randn(n, hkv, d, device=DEV, generator=gen, dtype=torch.bfloat16)
     ring = LocalKVRing.from_full(k, v, cp)
     lq = zigzag_shard(q, rank, cp)
-    outs = {}
-    for mode in PATHS:
-        cfg, fused = _cfg_path(mode, cp, rank)
-        outs[mode] = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, fused=fused)
-    for mode, fused in (("fused", True), ("incremental", False)):
+    del q
+    outs = _run_forms(lq, ring, cp, rank, PATHS)
+    for form, fused in (("fused", True), ("incremental", False)):
         again = ring_flash_attn(lq, ring.k[rank], ring.v[rank], RingConfig(cp_size=cp, cp_rank=rank),
                                 group=ring, fused=fused)
-        assert torch.equal(again, outs[mode]), f"{mode} sweep is not bit-reproducible"
-    kc, vc = k.float().cpu(), v.float().cpu()
+        assert torch.equal(again, outs[form][0]), f"{form} sweep is not bit-reproducible"
+    _check_forms_agree(f"C2 rank {rank}", "fused", outs, TOL_BF16_OUT)
+    t = lq.shape[0]
+    rows = _tile_rows(t, seed=rank)
     grow = O.zigzag_rows(n, rank, cp)
-    qc = torch.zeros(n, hq, d)
-    qc[torch.from_numpy(grow)] = lq.float().cpu()
-    for mode, out in outs.items():
-        err = _check_sampled(out, rank, cp, n, qc, kc, vc, scale_for(d), TOL_BF16_OUT, seed=rank)
-        say(f"  C2 rank {rank} {mode}: sampled max |err| {err:.3e} (bar {TOL_BF16_OUT})")
+    kc, vc = k.float().cpu(), v.float().cpu()
+    lq_f = lq.float().cpu()
+    _check_tiles(f"C2 rank {rank}", outs, lq_f, rows, [int(grow[i]) for i in rows], [0] * len(rows), kc, vc,
+                 scale_for(d), TOL_BF16_OUT)
 
 
-def _fp8_full_size(n, cp, hq, hkv, d, rank, modes, seed):
+def _fp8_full_size(n, cp, hq, hkv, d, rank, forms, seed):
     gen = torch.Generator(device=DEV).manual_seed(seed)
     q = torch.randn(n, hq, d, device=DEV, generator=gen)
     k = torch.randn(n, hkv, d, device=DEV, generator=gen)
@@ -359,23 +415,21 @@ def _fp8_full_size(n, cp, hq, hkv, d, rank, modes, seed):
     sv = [float(x.abs().max()) / 448.0 for x in vs]
     k8 = [(x / s).clamp(-448, 448).to(torch.float8_e4m3fn) for x, s in zip(ks, sk)]
     v8 = [(x / s).clamp(-448, 448).to(torch.float8_e4m3fn) for x, s in zip(vs, sv)]
-    del q, k, v, ks, vs
+    del q, k, v, ks, vs, lq
     ring = LocalKVRing(k8, v8)
     desc = Descales(q=torch.tensor(sq, device=DEV), k=[torch.tensor(s, device=DEV) for s in sk],
                     v=[torch.tensor(s, device=DEV) for s in sv])
-    outs = {}
-    for mode in modes:
-        cfg, fused = _cfg_path(mode, cp, rank)
-        outs[mode] = ring_flash_attn(q8, ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc,
-                                     fused=fused)
+    outs = _run_forms(q8, ring, cp, rank, forms, descales=desc)
+    name = f"e4m3 n={n} d={d} rank {rank}"
+    _check_forms_agree(name, "fused", outs, TOL_FP8_OUT)
     # dense reference on the dequantised tensors
     kf = O.zigzag_unshard([x.float().cpu() * s for x, s in zip(k8, sk)], cp)
     vf = O.zigzag_unshard([x.float().cpu() * s for x, s in zip(v8, sv)], cp)
-    qf = torch.zeros(n, hq, d)
-    qf[torch.from_numpy(O.zigzag_rows(n, rank, cp))] = q8.float().cpu() * sq
-    for mode, out in outs.items():
-        err = _check_sampled(out, rank, cp, n, qf, kf, vf, scale_for(d), TOL_FP8_OUT, seed=rank + 10)
-        say(f"  e4m3 n={n} d={d} rank {rank} {mode}: sampled max |err| {err:.3e} (bar {TOL_FP8_OUT})")
+    lq_f = q8.float().cpu() * sq
+    rows = _tile_rows(q8.shape[0], seed=rank + 10)
+    grow = O.zigzag_rows(n, rank, cp)
+    _check_tiles(name, outs, lq_f, rows, [int(grow[i]) for i in rows], [0] * len(rows), kf, vf, scale_for(d),
+                 TOL_FP8_OUT)
 
 
 @pytest.mark.parametrize("rank", [0, 3, 7])
@@ -404,25 +458,24 @@ def test_ring_c4_varlen_full_size(rank):
     ring = LocalKVRing.from_full(k, v, cp, full_cu)
     lq, local_cu = zigzag_shard_varlen(q, full_cu, rank, cp)
     max_local = int((local_cu[1:] - local_cu[:-1]).max())
-    qc, kc, vc = q.float().cpu(), k.float().cpu(), v.float().cpu()
+    outs = _run_forms(lq, ring, cp, rank, PATHS, cu_seqlens=local_cu, max_seqlen=max_local)
+    _check_forms_agree(f"C4 rank {rank}", "fused", outs, TOL_BF16_OUT)
+    kc, vc = k.float().cpu(), v.float().cpu()
+    lq_f = lq.float().cpu()
     grow = O.zigzag_rows_varlen(full_cu, rank, cp)
+    # one row of every 64-row tile of every local sequence, plus each sequence's halves' ends
+    lcu = local_cu.tolist()
+    rows = set()
     rng = np.random.default_rng(rank)
-    rows = sorted(set(rng.integers(0, lq.shape[0], 40).tolist() + [0, lq.shape[0] - 1]))
-    heads = rng.integers(0, hq, len(rows)).tolist()
-    for mode in PATHS:
-        cfg, fused = _cfg_path(mode, cp, rank)
-        out = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring,
-                              cu_seqlens=local_cu, max_seqlen=max_local, fused=fused)
-        got = out[rows, heads].float().cpu()
-        exp = []
-        for i, hh in zip(rows, heads):
-            g = int(grow[i])
-            j = int(np.searchsorted(full_cu, g, side="right") - 1)
-            o, _ = O.dense_causal_rows(qc, kc, vc, [g], [hh], scale_for(d), seq_start=full_cu[j])
-            exp.append(o[0])
-        err = float((got - torch.stack(exp)).abs().max())
-        say(f"  C4 rank {rank} {mode}: sampled max |err| {err:.3e} (bar {TOL_BF16_OUT})")
-        assert err <= TOL_BF16_OUT, f"{mode}: {err}"
+    for j in range(len(lens)):
+        a, b = lcu[j], lcu[j + 1]
+        for t0 in range(a, b, 64):
+            rows.add(int(t0 + rng.integers(0, min(64, b - t0))))
+        rows.update([a, (a + b) // 2 - 1, (a + b) // 2, b - 1])
+    rows = sorted(rows)
+    starts = [full_cu[int(np.searchsorted(full_cu, int(grow[i]), side="right")) - 1] for i in rows]
+    _check_tiles(f"C4 rank {rank}", outs, lq_f, rows, [int(grow[i]) for i in rows], starts, kc, vc,
+                 scale_for(d), TOL_BF16_OUT)
 
 
 EMPTY_CASES = [(torch.bfloat16, p) for p in PATHS] + [(torch.float8_e4m3fn, "fused"),

@@ -293,6 +293,53 @@ def test_fused_sweep_rejects_what_it_does_not_cover():
         ring_flash_attn(x, x, x, big, group=LocalKVRing([x] * 17, [x] * 17), fused=True)
 
 
+def test_odd_local_lengths_are_refused():
+    """A local sequence is two zig-zag chunks of equal size: an odd length (one sequence, or
+    any packed one) is refused with AssertionError before any device work, as the
+    reference's get_half_index refuses it."""
+    cfg = RingConfig(cp_size=1, cp_rank=0)
+    q = torch.zeros(15, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="odd length"):
+        ring_flash_attn(q, q, q, cfg)
+    q = torch.zeros(16, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match=r"sequences \[1, 2\] have odd length"):
+        ring_flash_attn(q, q, q, cfg, cu_seqlens=torch.tensor([0, 6, 11, 16], dtype=torch.int32), max_seqlen=6)
+    with pytest.raises(AssertionError, match="even length"):
+        get_half_index(torch.tensor([0, 6, 11], dtype=torch.int32), front=True)
+
+
+def test_kv_shards_must_be_contiguous_in_d():
+    """The sweep's arguments carry K's row and head strides only, so a K or V view whose head
+    dim is strided is refused (it would otherwise be read as contiguous)."""
+    x = torch.zeros(16, 128, 2, dtype=torch.bfloat16).transpose(1, 2)  # [16, 2, 128], stride(2) = 2
+    ok = torch.zeros(16, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="contiguous in D"):
+        LocalKVRing([ok, x], [ok, ok])
+    with pytest.raises(AssertionError, match="contiguous in D"):
+        LocalKVRing([ok, ok], [x, ok])
+
+
+def test_merge_entry_points_validate_without_gpu():
+    lib = _lib.load()
+    ptrs = (ctypes.c_void_p * 2)(1 << 20, 1 << 21)
+    for n in (0, 17):
+        assert lib.fa4cp_merge_states_list(ptrs, ptrs, n, 1 << 22, 1 << 23, 4, 2, 64, 0, None) == -1
+        assert b"num_states" in lib.fa4cp_last_error()
+    bad = (ctypes.c_void_p * 2)(1 << 20, (1 << 21) | 4)
+    assert lib.fa4cp_merge_states_list(bad, ptrs, 2, 1 << 22, 1 << 23, 4, 2, 64, 0, None) == -1
+    assert b"aligned" in lib.fa4cp_last_error()
+    assert lib.fa4cp_merge_states_list(ptrs, ptrs, 2, None, None, 4, 2, 64, 0, None) == -1
+    assert b"null" in lib.fa4cp_last_error()
+    assert lib.fa4cp_merge_state(1 << 20, 1 << 20, 1 << 21, 1 << 21, None, None, 4, 2, 64, 0, None, 0, 0,
+                                 None) == -1
+    assert b"null" in lib.fa4cp_last_error()
+    assert lib.fa4cp_merge_state(1 << 20, 1 << 20, 1 << 21, 1 << 21, 1 << 22, 1 << 23, 3, 2, 64, 0, None, 0,
+                                 2, None) == -1
+    assert b"even" in lib.fa4cp_last_error()
+    # nothing to merge: no launch, NULL accepted
+    assert lib.fa4cp_merge_states_list(ptrs, ptrs, 2, None, None, 0, 2, 64, 0, None) == 0
+
+
 def test_public_api_names():
     for name in ["RingConfig", "ring_flash_attn", "Descales", "zigzag_shard", "zigzag_unshard",
                  "IncrementalMerger", "BatchedMerger", "make_merger", "LocalKVRing", "quantize_e4m3",

@@ -277,6 +277,27 @@ def test_dense_causal_rows_matches_full():
         assert abs(float(l[i] - lse[r, hh])) < 1e-5
 
 
+@pytest.mark.parametrize("key_block", [7, 64, 1000])
+def test_dense_causal_rows_all_heads_matches_per_pair(key_block):
+    """The batched row checker equals the per-(row, head) one on every head, for packed
+    sequences (rows of the first and second sequence, the first and last row of each), with
+    key blocks that split sequences unevenly."""
+    lens = [56, 90, 34]
+    cu = [0, 56, 146, 180]
+    q, k, v = O.random_qkv(cu[-1], 6, 2, 16, seed=12)
+    scale = 0.3
+    rows = [0, 1, 55, 56, 57, 100, 145, 146, 179, 30]
+    starts = [cu[int(np.searchsorted(cu, r, side="right")) - 1] for r in rows]
+    o, l = O.dense_causal_rows_all_heads(q[rows], rows, starts, k, v, scale, key_block=key_block)
+    for i, (r, s) in enumerate(zip(rows, starts)):
+        eo, el = O.dense_causal_rows(q, k, v, [r] * 6, list(range(6)), scale, seq_start=s)
+        assert (o[i] - eo).abs().max() < 2e-5, (r, key_block)
+        assert (l[i] - el).abs().max() < 2e-5, (r, key_block)
+    # a planted off-by-one (row i also seeing key i + 1) must be caught
+    bad, _ = O.dense_causal_rows_all_heads(q[rows], [r + 1 for r in rows[:3]] + rows[3:], starts, k, v, scale)
+    assert (bad[:3] - o[:3]).abs().max() > 1e-2
+
+
 # ---------------------------------------------------------------- e4m3
 
 
