@@ -92,6 +92,7 @@ def test_merge_state_in_place(dtype, t, h, d):
     say(f"merge_state_in_place dtype={dtype} t={t} h={h} d={d}")
     va, sa = _states(t, h, d, 1, dtype, inf_frac=0.1)
     vb, sb = _states(t, h, d, 2, dtype, inf_frac=0.1)
+    sa[0, 0] = sb[0, 0] = float("-inf")  # at least one row empty on both sides
     both = torch.isinf(sa) & torch.isinf(sb)
     vd, sd = va.to(dtype).to(DEV), sa.to(DEV)
     merge_state_in_place(vd, sd, vb.to(dtype).to(DEV), sb.to(DEV))
