@@ -14,6 +14,8 @@
 // chunks, and every thread owns the same NS chunk slots of every group: slot k of thread t
 // is chunk t + 256 k of the group.  Its row, head, position and scale are fixed, so they are
 // computed once, and a thread issues the loads of all its slots before it uses any.
+#include <mutex>
+
 #include "common.h"
 
 namespace fa4cp {
@@ -22,7 +24,7 @@ namespace {
 constexpr int kQBlock = 256;
 constexpr int kQSpan = 2048;      // 16-byte chunks per row group (8 per thread)
 constexpr int kQMaxSlots = 16;    // chunk slots per thread: rows of up to 4096 chunks
-constexpr int kQMaxScales = 1024;
+constexpr int kQMaxScales = FA4CP_QUANT_MAX_SCALES;
 constexpr int kQMaxGrid = 1024;   // workgroups (4 per CU); each loops over row groups
 
 // Where the chunks of a row group lie: group g covers rows [g rb, g rb + rb).
@@ -221,38 +223,120 @@ int launch(const fa4cp_quant_args& a, int cps, hipStream_t st) {
 
 using namespace fa4cp;
 
-extern "C" int fa4cp_quantize_e4m3(const fa4cp_quant_args* a, void* stream) {
-  clear_error();
-  if (a == nullptr || a->amax == nullptr || a->descale == nullptr)
-    return set_error(FA4CP_EINVAL, "quantize_e4m3: null pointer");
-  if (a->rows < 0 || a->h < 1 || a->d < 1) return set_error(FA4CP_EINVAL, "quantize_e4m3: bad shape");
+namespace fa4cp {
+namespace {
+
+// Checks the arguments shared by both entry points; on success sets *cps (16-byte chunks per
+// scale, 0 for one scale) and *nscale.
+int quant_check(const char* what, const fa4cp_quant_args* a, bool need_amax, int* cps, int* nscale) {
+  if (a == nullptr || (need_amax && a->amax == nullptr) || a->descale == nullptr)
+    return set_error(FA4CP_EINVAL, "%s: null pointer", what);
+  if (a->rows < 0 || a->h < 1 || a->d < 1) return set_error(FA4CP_EINVAL, "%s: bad shape", what);
   if (a->rows > 0 && (a->x == nullptr || a->y == nullptr))  // x / y may be NULL when there are no rows
-    return set_error(FA4CP_EINVAL, "quantize_e4m3: null pointer");
+    return set_error(FA4CP_EINVAL, "%s: null pointer", what);
   int esz = 0;
   switch (a->dtype) {
     case FA4CP_BF16: case FA4CP_FP16: esz = 2; break;
     case FA4CP_FP32: esz = 4; break;
-    default: return set_error(FA4CP_EUNSUPPORTED, "quantize_e4m3: dtype %d (BF16 / FP16 / FP32 only)", a->dtype);
+    default: return set_error(FA4CP_EUNSUPPORTED, "%s: dtype %d (BF16 / FP16 / FP32 only)", what, a->dtype);
   }
   const int E = 16 / esz;
-  if (a->d % E != 0) return set_error(FA4CP_EINVAL, "quantize_e4m3: d must be a multiple of %d", E);
+  if (a->d % E != 0) return set_error(FA4CP_EINVAL, "%s: d must be a multiple of %d", what, E);
   if ((reinterpret_cast<uintptr_t>(a->x) % 16) != 0 || (a->row_stride * esz) % 16 != 0 ||
       (a->head_stride * esz) % 16 != 0 || (reinterpret_cast<uintptr_t>(a->y) % 8) != 0)
-    return set_error(FA4CP_EINVAL, "quantize_e4m3: x and its strides must be 16-byte aligned, y 8-byte aligned");
+    return set_error(FA4CP_EINVAL, "%s: x and its strides must be 16-byte aligned, y 8-byte aligned", what);
   const int64_t cpr = (int64_t)a->h * (a->d / E);
   if (cpr > (int64_t)kQBlock * kQMaxSlots)
-    return set_error(FA4CP_EUNSUPPORTED, "quantize_e4m3: h * d = %lld elements per row (at most %d)",
+    return set_error(FA4CP_EUNSUPPORTED, "%s: h * d = %lld elements per row (at most %d)", what,
                      (long long)a->h * a->d, kQBlock * kQMaxSlots * E);
   const int g = a->heads_per_scale;
   if (g < 0 || (g > 0 && a->h % g != 0))
-    return set_error(FA4CP_EINVAL, "quantize_e4m3: heads_per_scale %d must be 0 or divide h = %d", g, a->h);
-  if (g > 0 && a->h / g > kQMaxScales)
-    return set_error(FA4CP_EUNSUPPORTED, "quantize_e4m3: at most %d scales", kQMaxScales);
-  const int cps = g > 0 ? g * (a->d / E) : 0;  // chunks per scale
-  hipStream_t st = (hipStream_t)stream;
-  switch (a->dtype) {
-    case FA4CP_BF16: return launch<__bf16>(*a, cps, st);
-    case FA4CP_FP16: return launch<_Float16>(*a, cps, st);
-    default: return launch<float>(*a, cps, st);
+    return set_error(FA4CP_EINVAL, "%s: heads_per_scale %d must be 0 or divide h = %d", what, g, a->h);
+  *nscale = g > 0 ? a->h / g : 1;
+  if (*nscale > kQMaxScales)
+    return set_error(FA4CP_EUNSUPPORTED, "%s: %d scales, at most %d", what, *nscale, kQMaxScales);
+  *cps = g > 0 ? g * (a->d / E) : 0;
+  return FA4CP_OK;
+}
+
+int quant_launch(const fa4cp_quant_args& a, int cps, hipStream_t st) {
+  switch (a.dtype) {
+    case FA4CP_BF16: return launch<__bf16>(a, cps, st);
+    case FA4CP_FP16: return launch<_Float16>(a, cps, st);
+    default: return launch<float>(a, cps, st);
   }
+}
+
+}  // namespace
+}  // namespace fa4cp
+
+extern "C" int fa4cp_quantize_e4m3(const fa4cp_quant_args* a, void* stream) {
+  clear_error();
+  int cps = 0, nscale = 0;
+  const int rc = quant_check("quantize_e4m3", a, true, &cps, &nscale);
+  if (rc != FA4CP_OK) return rc;
+  return quant_launch(*a, cps, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------------------
+// The entry point that allocates nothing: the amax words live in `scratch`, a static device
+// array of kQMaxScales words (4 KiB) that every GPU the library runs on holds until the
+// process ends.  In host code `scratch` names a host-side stand-in, not the device array:
+// its device address is looked up once per device (hipGetSymbolAddress, with the device
+// current) and only that address is passed to the kernels.  Each call clears the words it
+// uses with a kernel (no memset) before the amax pass, so the previous call's contents do
+// not matter; calls that overlap on one GPU (different streams) share the words and race.
+
+static __device__ __align__(256) unsigned scratch[fa4cp::kQMaxScales];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};  // device address of `scratch`, per device ordinal
+
+// Device address of the current device's `scratch`, looked up on the first call there.
+int scratch_address(const char* what, hipStream_t st, unsigned** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fa4cp::set_error(FA4CP_ELAUNCH, "%s: hipGetDevice: %s", what, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fa4cp::set_error(FA4CP_EUNSUPPORTED, "%s: device %d (at most %d devices)", what, dev, kMaxDevices);
+  if (st != nullptr) {
+    int sdev = -1;
+    e = hipStreamGetDevice(st, &sdev);
+    if (e != hipSuccess)
+      return fa4cp::set_error(FA4CP_EINVAL, "%s: hipStreamGetDevice: %s", what, hipGetErrorString(e));
+    if (sdev != dev)
+      return fa4cp::set_error(FA4CP_EINVAL, "%s: the stream belongs to device %d but device %d is current", what,
+                              sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fa4cp::set_error(FA4CP_ELAUNCH, "%s: hipGetSymbolAddress(scratch) on device %d: %s", what, dev,
+                              hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *out = static_cast<unsigned*>(g_scratch_addr[dev]);
+  return FA4CP_OK;
+}
+
+}  // namespace
+
+extern "C" int fa4cp_quantize_e4m3_noalloc(const fa4cp_quant_args* a, void* stream) {
+  fa4cp::clear_error();
+  const char* what = "quantize_e4m3_noalloc";
+  int cps = 0, nscale = 0;
+  int rc = fa4cp::quant_check(what, a, false, &cps, &nscale);
+  if (rc != FA4CP_OK) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  unsigned* words = nullptr;
+  rc = scratch_address(what, st, &words);
+  if (rc != FA4CP_OK) return rc;
+  fa4cp_quant_args b = *a;
+  b.amax = reinterpret_cast<float*>(words);
+  return fa4cp::quant_launch(b, cps, st);
 }

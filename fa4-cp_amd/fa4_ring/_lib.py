@@ -219,6 +219,7 @@ SIGNATURES = {
     ),
     "fa4cp_ring_sweep_fwd": (ctypes.c_int, [ctypes.POINTER(SweepArgs), ctypes.c_void_p]),
     "fa4cp_quantize_e4m3": (ctypes.c_int, [ctypes.POINTER(QuantArgs), ctypes.c_void_p]),
+    "fa4cp_quantize_e4m3_noalloc": (ctypes.c_int, [ctypes.POINTER(QuantArgs), ctypes.c_void_p]),
     "fa4cp_last_error": (ctypes.c_char_p, []),
     "fa4cp_abi_version": (ctypes.c_int, []),
 }

@@ -49,6 +49,39 @@ def quantize_e4m3(x: torch.Tensor, *, heads_per_scale: int = 0,
     return out, (descale.reshape(()) if g == 0 else descale)
 
 
+QUANT_MAX_SCALES = 1024  # FA4CP_QUANT_MAX_SCALES
+
+
+def quantize_e4m3_into(x: torch.Tensor, out: torch.Tensor, descale: torch.Tensor, *,
+                       heads_per_scale: int = 0) -> None:
+    """quantize_e4m3 into caller-provided ``out`` ([rows, h, d] float8_e4m3fn, contiguous) and
+    ``descale`` (float32, one element per scale, contiguous), allocating nothing on the
+    device: the amax workspace is the library's static per-GPU array
+    (fa4cp_quantize_e4m3_noalloc), so this can run where allocation is not allowed.  At most
+    QUANT_MAX_SCALES scales.  Calls that overlap on one GPU (on different streams) share that
+    workspace and race."""
+    lib = _lib.load()
+    assert x.is_cuda and x.dim() == 3 and x.stride(2) == 1, "x must be a [rows, h, d] device tensor, unit stride in d"
+    rows, h, d = x.shape
+    g = int(heads_per_scale)
+    assert g == 0 or (g > 0 and h % g == 0), f"heads_per_scale {g} must be 0 or divide h = {h}"
+    nscale = 1 if g == 0 else h // g
+    assert nscale <= QUANT_MAX_SCALES, f"{nscale} scales exceed the static workspace ({QUANT_MAX_SCALES})"
+    assert out.shape == (rows, h, d) and out.dtype == torch.float8_e4m3fn and out.is_contiguous() \
+        and out.device == x.device, f"out must be a contiguous [{rows}, {h}, {d}] float8_e4m3fn tensor on {x.device}"
+    assert descale.numel() == nscale and descale.dtype == torch.float32 and descale.is_contiguous() \
+        and descale.device == x.device, f"descale must be {nscale} contiguous float32 values on {x.device}"
+    a = _lib.QuantArgs()
+    a.x, a.rows, a.h, a.d = x.data_ptr(), rows, h, d
+    a.row_stride, a.head_stride = x.stride(0), x.stride(1)
+    a.dtype = _lib.dtype_code(x.dtype)
+    a.heads_per_scale = g
+    a.amax, a.descale, a.y = None, descale.data_ptr(), out.data_ptr()
+    with torch.cuda.device(x.device):  # the library looks up the current device's workspace
+        rc = lib.fa4cp_quantize_e4m3_noalloc(ctypes.byref(a), _lib.stream_handle(x.device))
+    _lib.check(rc, "fa4cp_quantize_e4m3_noalloc")
+
+
 def quantize_ring(local_q: torch.Tensor, k_shards: Sequence[torch.Tensor], v_shards: Sequence[torch.Tensor],
                   *, per_head: bool = False
                   ) -> Tuple[torch.Tensor, List[torch.Tensor], List[torch.Tensor], Descales]:

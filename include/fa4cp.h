@@ -300,6 +300,21 @@ typedef struct fa4cp_quant_args {
 int fa4cp_quantize_e4m3(const fa4cp_quant_args* args, void* stream);
 
 /*
+ * fa4cp_quantize_e4m3 without the caller's workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  args->amax is ignored (may be NULL): the
+ * amax words live in a static device array of FA4CP_QUANT_MAX_SCALES words (4 KiB) that each
+ * GPU holds until the process ends; its address is looked up on the first call on a device.
+ * The call allocates nothing; x, y and descale are the caller's as before.  At most
+ * FA4CP_QUANT_MAX_SCALES scales (FA4CP_EUNSUPPORTED beyond).  The stream must belong to the
+ * current device.  Every call on one GPU shares that GPU's array and clears the words it
+ * uses (with a kernel) before using them: calls that overlap on one GPU, on different
+ * streams, race.
+ */
+#define FA4CP_QUANT_MAX_SCALES 1024
+int fa4cp_quantize_e4m3_noalloc(const fa4cp_quant_args* args, void* stream);
+
+/*
  * Zig-zag shard for one rank: sequence j of the full packed tensor (rows
  * [full_cu[j], full_cu[j+1]), length N_j divisible by 2*cp_size, h_j = N_j / (2*cp_size))
  * contributes chunk cp_rank followed by chunk 2*cp_size-1-cp_rank to the local tensor,
