@@ -46,6 +46,13 @@ N, CP, HQ, HKV, D = 131072, 8, 32, 8, 128
 ATTN_TRAFFIC_BYTES_RANK3 = 466593 * 1024
 # The same for the fused sweep kernel (one launch per sweep).
 SWEEP_TRAFFIC_BYTES_RANK3 = 2395694 * 1024
+# ... for the packed-sequence sweep (cp_size 4, rank 3) and the e4m3 head-dim-256 sweep
+# (N = 262144, rank 3), and for merge_states in their batched per-step forms (same factors,
+# counter passes over `bench.py --workload c4` / `--workload c5`).
+C4_SWEEP_TRAFFIC_BYTES = (2 * 144522 + 102470) * 1024
+C5_SWEEP_TRAFFIC_BYTES = (2 * 2580570 + 266252) * 1024
+C4_MERGE_STATES_TRAFFIC_BYTES = (2 * 204965 + 100913) * 1024
+C5_MERGE_STATES_TRAFFIC_BYTES = (2 * 799004 + 264223) * 1024
 
 
 def sweep_flops(t_local: int, cp: int, hq: int, d: int) -> float:
@@ -197,15 +204,55 @@ def cpu_baseline(rank: int, rows: int) -> dict:
 C4_LENGTHS = [4856, 9720, 8592, 4864, 1832, 15456, 2784, 1576]  # 8 * randint(128, 2049), seed 0
 
 
-def bench_c4(args) -> int:
+def _cpu_threads() -> int:
+    import torch
+
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = min(threads, int(os.environ.get("OMP_NUM_THREADS", threads)))
+    torch.set_num_threads(threads)
+    return threads
+
+
+def _cpu_model() -> str:
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return cpu
+
+
+def _event_ms(fn, n=10):
+    """Mean HIP-event time of `fn` on torch's current stream (where the library launches)."""
+    import torch
+
+    for _ in range(3):
+        fn()
+    evs = []
+    for _ in range(n):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        evs.append((s, e))
+    torch.cuda.synchronize()
+    return sum(s.elapsed_time(e) for s, e in evs) / n
+
+
+def c4_block(rank: int, steps: int, warmup: int, with_cpu: bool) -> dict:
     """Packed sequences: the 8 lengths above (49680 tokens), cp_size = 4, H_q = 32, H_kv = 8,
-    D = 128, bf16, one rank's fused varlen sweep (the per-step form beside it)."""
+    D = 128, bf16, one rank's sweep in the fused form and in both per-step merge modes; the
+    zig-zag shard of the packed q; and the oracle's whole fp32 sweep of the same rank on the
+    host cores (the complete job, not a sample)."""
     import torch
 
     from fa4_ring import LocalKVRing, RingConfig, ring_flash_attn
-    from fa4_ring.zigzag import zigzag_shard_varlen
+    from fa4_ring.zigzag import _shard, zigzag_shard_varlen
 
-    cp, hq, hkv, d, rank = 4, HQ, HKV, D, args.rank % 4
+    cp, hq, hkv, d = 4, HQ, HKV, D
     full_cu = [0]
     for n in C4_LENGTHS:
         full_cu.append(full_cu[-1] + n)
@@ -218,64 +265,76 @@ def bench_c4(args) -> int:
     lq, local_cu = zigzag_shard_varlen(q, full_cu, rank, cp)
     max_local = int((local_cu[1:] - local_cu[:-1]).max())
     flops = sum(cp * 8.0 * (n // (2 * cp)) ** 2 * d * hq for n in C4_LENGTHS)
-    cfg = RingConfig(cp_size=cp, cp_rank=rank)
 
-    def run(fused):
-        return ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, cu_seqlens=local_cu,
-                               max_seqlen=max_local, fused=fused)
+    def run(fused, mode="incremental"):
+        return ring_flash_attn(lq, ring.k[rank], ring.v[rank], RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode),
+                               group=ring, cu_seqlens=local_cu, max_seqlen=max_local, fused=fused)
 
     clock = KernelClock()
-    sec = timed_sweeps(lambda: run(None), args.steps, args.warmup, clock)
+    sec = timed_sweeps(lambda: run(True), steps, warmup, clock)
     sw_ms = clock.mean_ms("sweep_kernel")
-    secp = timed_sweeps(lambda: run(False), args.steps, args.warmup)
+    seci = timed_sweeps(lambda: run(False, "incremental"), steps, warmup)
+    secb = timed_sweeps(lambda: run(False, "batched"), steps, warmup)
+    clockb = KernelClock()
+    timed_sweeps(lambda: run(False, "batched"), max(3, steps // 2), 1, clockb)
+    ms_ms = clockb.mean_ms("merge_states")
+    t_local = lq.shape[0]
+    bb = merge_bytes_batched(t_local, cp, hq, d, 2)
     # zig-zag shard of the packed full q (per-sequence chunks r and 2cp-1-r), device cu
     cu_dev = torch.tensor(full_cu, dtype=torch.int32, device=dev)
-    from fa4_ring.zigzag import _shard  # the launch alone (zigzag_shard_varlen checks cu on the host)
-    for _ in range(3):
-        _shard(q, rank, cp, cu_dev, len(C4_LENGTHS))
-    zev = []
-    for _ in range(10):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        _shard(q, rank, cp, cu_dev, len(C4_LENGTHS))
-        e.record()
-        zev.append((s, e))
-    torch.cuda.synchronize()
-    zms = sum(s.elapsed_time(e) for s, e in zev) / len(zev)
-    zbytes = 2.0 * (full_cu[-1] // cp) * hq * d * 2
-    value = flops / sec / 1e12
+    zms = _event_ms(lambda: _shard(q, rank, cp, cu_dev, len(C4_LENGTHS)))
+    zbytes = 2.0 * t_local * hq * d * 2
     kt = flops / (sw_ms * 1e-3) / 1e12
-    print(json.dumps({
-        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 3), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (q/k/v ~ N(0,1) bf16, seeded on the GPU)",
-        "config": {"workload": f"bf16 causal zig-zag ring sweep over packed sequences {C4_LENGTHS} "
-                               f"({full_cu[-1]} tokens), cp_size={cp}, rank {rank}, H_q={hq}, H_kv={hkv}, D={d}, "
-                               "fused sweep kernel",
-                   "global_batch": len(C4_LENGTHS), "seq_len": max(C4_LENGTHS), "cp_size": cp, "cp_rank": rank,
-                   "h_q": hq, "h_kv": hkv, "head_dim": d, "parallelism": "cp4 (one rank's share on 1 GPU)"},
-        "frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
-        "roofline": {"bound": "mfma", "kernel": "attn_fwd_16bit_sweep<bf16,128,4>", "achieved": round(kt, 2),
+    out = {
+        "workload": f"bf16 causal zig-zag ring sweep over packed sequences {C4_LENGTHS} ({full_cu[-1]} tokens), "
+                    f"cp_size={cp}, rank {rank}, H_q={hq}, H_kv={hkv}, D={d}",
+        "flop_per_sweep": flops,
+        "fused": {"ms_per_step": round(sec * 1e3, 3), "TFLOP/s": round(flops / sec / 1e12, 2),
+                  "frac_of_peak": round(flops / sec / 1e12 / PEAK_BF16_TFLOPS, 4)},
+        "roofline": {"bound": "mfma", "kernel": "attn_fwd_16bit_sweep<bf16,128,4> (packed)", "achieved": round(kt, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(kt / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "algorithmic_per_launch": f"{flops / 1e12:.4f} TFLOP (the whole sweep)",
+                     "traffic": C4_SWEEP_TRAFFIC_BYTES if rank == 3 else None,
+                     "algorithmic_per_launch": f"{flops / 1e12:.4f} TFLOP (the whole sweep)",
                      "avg_launch_ms": round(sw_ms, 4), "launches": clock.count("sweep_kernel")},
-        "per_step": {"ms_per_step": round(secp * 1e3, 3), "TFLOP/s": round(flops / secp / 1e12, 2)},
+        "per_step_incremental": {"ms_per_step": round(seci * 1e3, 3), "TFLOP/s": round(flops / seci / 1e12, 2)},
+        "per_step_batched": {"ms_per_step": round(secb * 1e3, 3), "TFLOP/s": round(flops / secb / 1e12, 2),
+                             "merge_states_ms": round(ms_ms, 4), "merge_states_bytes": round(bb),
+                             "merge_states_GBs": round(bb / (ms_ms * 1e-3) / 1e9, 1),
+                             "merge_states_frac": round(bb / (ms_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                             "merge_states_traffic": C4_MERGE_STATES_TRAFFIC_BYTES if rank == 3 else None},
         "zigzag_varlen": {"kernel": "shard_kernel<u32x4> (packed sequences, full q)", "avg_launch_ms": round(zms, 4),
                           "bytes": round(zbytes), "achieved_GBs": round(zbytes / (zms * 1e-3) / 1e9, 1),
                           "frac": round(zbytes / (zms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
-        "cpu_baseline": None}), flush=True)
-    return 0
+    }
+    if with_cpu:
+        from oracle import ring_oracle as O
+
+        threads = _cpu_threads()
+        qc, kc, vc = q.float().cpu(), k.float().cpu(), v.float().cpu()
+        ks = [O.zigzag_shard_varlen(kc, full_cu, r, cp)[0] for r in range(cp)]
+        vs = [O.zigzag_shard_varlen(vc, full_cu, r, cp)[0] for r in range(cp)]
+        oq, ocu = O.zigzag_shard_varlen(qc, full_cu, rank, cp)
+        t0 = time.perf_counter()
+        O.ring_rank(oq, ks, vs, rank, cp, 1 / math.sqrt(d), cu=ocu)
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+                               "kind": "port",
+                               "sample": f"the whole job: the oracle's fp32 sweep of rank {rank} over the 8 packed "
+                                         f"sequences ({flops / 1e12:.4f} TFLOP) in {dt:.2f} s on {_cpu_model()}"}
+    return out
 
 
-def bench_c5(args) -> int:
+def c5_block(rank: int, steps: int, warmup: int, with_cpu: bool, cpu_rows: int = 4096) -> dict:
     """The e4m3 head-dim-256 sweep: N = 262144, cp_size = 8 (local 32768 tokens), H_q = 16,
     H_kv = 2, D = 256, q scale per local shard and k / v scales per source shard (the FP8
-    producer), bf16 out; fused sweep timed, the per-step form beside it."""
+    producer), bf16 out.  The fused sweep, the per-step form with the batched merge (8
+    stashed partials, one merge_states) and with the incremental merge; the oracle on the
+    host cores on a bounded sample (step 1 for the first `cpu_rows` local query rows)."""
     import torch
 
     from fa4_ring import LocalKVRing, RingConfig, quantize_ring, ring_flash_attn, zigzag_shard
 
-    n, cp, hq, hkv, d, rank = 262144, 8, 16, 2, 256, args.rank
+    n, cp, hq, hkv, d = 262144, 8, 16, 2, 256
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(2)
     q = torch.randn(n, hq, d, device=dev, generator=g, dtype=torch.bfloat16)
@@ -287,33 +346,159 @@ def bench_c5(args) -> int:
     vs = [zigzag_shard(v, r, cp) for r in range(cp)]
     del k, v
     q8, k8, v8, desc = quantize_ring(lq, ks, vs)
-    del ks, vs, lq
     ring = LocalKVRing(k8, v8)
-    flops = sweep_flops(n // cp, cp, hq, d)
-    cfg = RingConfig(cp_size=cp, cp_rank=rank)
+    t_local = n // cp
+    flops = sweep_flops(t_local, cp, hq, d)
+
+    def run(fused, mode="incremental"):
+        return ring_flash_attn(q8, ring.k[rank], ring.v[rank], RingConfig(cp_size=cp, cp_rank=rank, merge_mode=mode),
+                               group=ring, descales=desc, fused=fused)
+
     clock = KernelClock()
-    sec = timed_sweeps(lambda: ring_flash_attn(q8, ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc),
-                       args.steps, args.warmup, clock)
+    sec = timed_sweeps(lambda: run(True), steps, warmup, clock)
     sw_ms = clock.mean_ms("sweep_kernel")
-    secp = timed_sweeps(lambda: ring_flash_attn(q8, ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc,
-                                                fused=False), max(3, args.steps // 2), 2)
-    value = flops / sec / 1e12
+    psteps = max(3, steps // 2)
+    secb = timed_sweeps(lambda: run(False, "batched"), psteps, 2)
+    seci = timed_sweeps(lambda: run(False, "incremental"), psteps, 2)
+    clockb = KernelClock()
+    timed_sweeps(lambda: run(False, "batched"), psteps, 1, clockb)
+    ms_ms = clockb.mean_ms("merge_states")
+    a_ms = clockb.mean_ms("attn")
+    bb = merge_bytes_batched(t_local, cp, hq, d, 2)
     kt = flops / (sw_ms * 1e-3) / 1e12
-    print(json.dumps({
-        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 3), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "e4m3", "data": "synthetic (N(0,1) bf16 quantised to OCP e4m3 on the GPU)",
-        "config": {"workload": f"e4m3 causal zig-zag ring sweep, one rank's share of cp_size={cp} over N={n} "
-                               f"(local 32768 tokens), H_q={hq}, H_kv={hkv}, D={d}, rank {rank}, fused sweep kernel",
-                   "global_batch": 1, "seq_len": n, "cp_size": cp, "cp_rank": rank, "h_q": hq, "h_kv": hkv,
-                   "head_dim": d, "parallelism": "cp8 (one rank's share on 1 GPU)"},
-        "frac_of_peak": round(value / PEAK_FP8_TFLOPS, 4),
+    out = {
+        "workload": f"e4m3 causal zig-zag ring sweep, one rank's share of cp_size={cp} over N={n} (local {t_local} "
+                    f"tokens), H_q={hq}, H_kv={hkv}, D={d}, rank {rank}, per-source-rank k/v descales, bf16 out",
+        "flop_per_sweep": flops,
+        "fused": {"ms_per_step": round(sec * 1e3, 3), "TFLOP/s": round(flops / sec / 1e12, 2),
+                  "frac_of_fp8_peak": round(flops / sec / 1e12 / PEAK_FP8_TFLOPS, 4)},
         "roofline": {"bound": "mfma", "kernel": "attn_fwd_e4m3_sweep<256,4>", "achieved": round(kt, 2),
                      "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s", "frac": round(kt / PEAK_FP8_TFLOPS, 4),
-                     "traffic": None, "algorithmic_per_launch": f"{flops / 1e12:.4f} TFLOP (the whole sweep)",
+                     "traffic": C5_SWEEP_TRAFFIC_BYTES if rank == 3 else None,
+                     "algorithmic_per_launch": f"{flops / 1e12:.4f} TFLOP (the whole sweep)",
                      "avg_launch_ms": round(sw_ms, 4), "launches": clock.count("sweep_kernel")},
-        "per_step": {"ms_per_step": round(secp * 1e3, 3), "TFLOP/s": round(flops / secp / 1e12, 2)},
-        "cpu_baseline": None}), flush=True)
+        "per_step_batched": {"ms_per_step": round(secb * 1e3, 3), "TFLOP/s": round(flops / secb / 1e12, 2),
+                             "attn_avg_launch_ms": round(a_ms, 4),
+                             "merge_states_ms": round(ms_ms, 4), "merge_states_bytes": round(bb),
+                             "merge_states_GBs": round(bb / (ms_ms * 1e-3) / 1e9, 1),
+                             "merge_states_frac": round(bb / (ms_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                             "merge_states_traffic": C5_MERGE_STATES_TRAFFIC_BYTES if rank == 3 else None},
+        "per_step_incremental": {"ms_per_step": round(seci * 1e3, 3), "TFLOP/s": round(flops / seci / 1e12, 2)},
+    }
+    if with_cpu:
+        from oracle import ring_oracle as O
+
+        threads = _cpu_threads()
+        half = t_local // 2
+        src = (rank - 1) % cp
+        qf = (q8[:cpu_rows].float() * desc.q.float()).cpu()
+        kf = (ring.k[src][:half].float() * desc.k[src].float()).cpu()
+        vf = (ring.v[src][:half].float() * desc.v[src].float()).cpu()
+        O.cpu_attn(qf[:64], kf, vf, False, 1 / math.sqrt(d))  # warm the BLAS
+        t0 = time.perf_counter()
+        O.cpu_attn(qf, kf, vf, False, 1 / math.sqrt(d))
+        dt = time.perf_counter() - t0
+        sflops = 4.0 * cpu_rows * half * d * hq
+        out["cpu_baseline"] = {"value": round(sflops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+                               "kind": "port",
+                               "sample": f"oracle cpu_attn fp32 on the dequantised e4m3 inputs, ring step 1 of rank "
+                                         f"{rank} (all Q x front half of source {src}'s KV) for the first {cpu_rows} "
+                                         f"of {t_local} local query rows, {hq} heads, Tk={half}, D={d}: "
+                                         f"{sflops / 1e12:.3f} TFLOP in {dt:.2f} s on {_cpu_model()}",
+                               "full_sweep_s_extrapolated": round(flops / (sflops / dt), 1)}
+    del ring, q8, k8, v8
+    return out
+
+
+def _single_line(args, block: dict, dtype: str, peak: float, config: dict) -> dict:
+    """A stand-alone JSON line for one of the extra workloads (``--workload``)."""
+    sec = block["fused"]["ms_per_step"] * 1e-3
+    value = block["flop_per_sweep"] / sec / 1e12
+    line = {"metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": block["fused"]["ms_per_step"], "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+            "data": "synthetic (q/k/v ~ N(0,1), seeded on the GPU)", "config": config,
+            "frac_of_peak": round(value / peak, 4)}
+    line.update({k: v for k, v in block.items() if k not in ("fused", "flop_per_sweep")})
+    line.setdefault("cpu_baseline", None)
+    return line
+
+
+def c3_block(rank: int, steps: int, warmup: int) -> dict:
+    """The e4m3 sweep at the bf16 shape (N = 131072, cp_size = 8, H_q = 32, H_kv = 8, D = 128):
+    OCP e4m3 q/k/v, q scale amax/448 of the local shard, k / v scales per source shard
+    (quantised by the library's producer), bf16 out; fused (the sweep kernel clocked) and per
+    step (attention per launch, clocked in a second pass)."""
+    from fa4_ring import RingConfig, ring_flash_attn
+
+    flops = sweep_flops(N // CP, CP, HQ, D)
+    per_launch = flops / CP
+    q8, ring8, desc = make_fp8_inputs(rank)
+    cfg8 = RingConfig(cp_size=CP, cp_rank=rank)
+    clock8 = KernelClock()
+    sec8 = timed_sweeps(lambda: ring_flash_attn(q8, ring8.k[rank], ring8.v[rank], cfg8, group=ring8,
+                                                descales=desc), steps, warmup, clock8)
+    s8 = clock8.mean_ms("sweep_kernel")
+    per_step8 = lambda: ring_flash_attn(q8, ring8.k[rank], ring8.v[rank], cfg8, group=ring8,  # noqa: E731
+                                        descales=desc, fused=False)
+    sec8p = timed_sweeps(per_step8, max(3, steps // 2), 2)  # unclocked wall time
+    clock8p = KernelClock()
+    timed_sweeps(per_step8, max(3, steps // 2), 1, clock8p)
+    a8 = clock8p.mean_ms("attn")
+    return {"workload": "same shape, OCP e4m3 q/k/v, per-source-rank k/v descales, bf16 out",
+            "ms_per_step": round(sec8 * 1e3, 3), "TFLOP/s": round(flops / sec8 / 1e12, 2),
+            "frac_of_fp8_peak": round(flops / sec8 / 1e12 / PEAK_FP8_TFLOPS, 4),
+            "sweep_kernel": {"kernel": "attn_fwd_e4m3_sweep<128,4>", "avg_launch_ms": round(s8, 4),
+                             "TFLOP/s": round(flops / (s8 * 1e-3) / 1e12, 2),
+                             "frac": round(flops / (s8 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)},
+            "per_step": {"ms_per_step": round(sec8p * 1e3, 3),
+                         "TFLOP/s": round(flops / sec8p / 1e12, 2),
+                         "attn_kernel": "attn_fwd_e4m3_vt<128,4>",
+                         "attn_avg_launch_ms": round(a8, 4),
+                         "attn_TFLOP/s": round(per_launch / (a8 * 1e-3) / 1e12, 2),
+                         "attn_frac": round(per_launch / (a8 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)}}
+
+
+def bench_c3(args) -> int:
+    import torch
+
+    block = c3_block(args.rank, args.steps, args.warmup)
+    torch.cuda.synchronize()
+    if args.rank != 7:
+        b7 = c3_block(7, max(3, args.steps // 2), 2)
+        block["rank7"] = {k: b7[k] for k in ("ms_per_step", "TFLOP/s", "frac_of_fp8_peak", "sweep_kernel")}
+    block["flop_per_sweep"] = sweep_flops(N // CP, CP, HQ, D)
+    block["fused"] = {"ms_per_step": block["ms_per_step"]}
+    config = {"workload": f"e4m3 causal zig-zag ring sweep, one rank's share of cp_size={CP} over N={N} (local "
+                          f"{N // CP} tokens), H_q={HQ}, H_kv={HKV}, D={D}, rank {args.rank}, per-source-rank k/v "
+                          "descales, fused sweep kernel",
+              "global_batch": 1, "seq_len": N, "cp_size": CP, "cp_rank": args.rank, "h_q": HQ, "h_kv": HKV,
+              "head_dim": D, "parallelism": "cp8 (one rank's share on 1 GPU)"}
+    line = _single_line(args, block, "e4m3", PEAK_FP8_TFLOPS, config)
+    line["roofline"] = {"bound": "mfma", "kernel": block["sweep_kernel"]["kernel"],
+                        "achieved": block["sweep_kernel"]["TFLOP/s"], "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
+                        "frac": block["sweep_kernel"]["frac"], "traffic": None,
+                        "avg_launch_ms": block["sweep_kernel"]["avg_launch_ms"]}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def bench_c4(args) -> int:
+    rank = args.rank % 4
+    block = c4_block(rank, args.steps, args.warmup, not args.no_cpu_baseline)
+    config = {"workload": block["workload"] + ", fused sweep kernel", "global_batch": len(C4_LENGTHS),
+              "seq_len": max(C4_LENGTHS), "cp_size": 4, "cp_rank": rank, "h_q": HQ, "h_kv": HKV, "head_dim": D,
+              "parallelism": "cp4 (one rank's share on 1 GPU)"}
+    print(json.dumps(_single_line(args, block, "bf16", PEAK_BF16_TFLOPS, config)), flush=True)
+    return 0
+
+
+def bench_c5(args) -> int:
+    block = c5_block(args.rank, args.steps, args.warmup, not args.no_cpu_baseline)
+    config = {"workload": block["workload"] + ", fused sweep kernel", "global_batch": 1, "seq_len": 262144,
+              "cp_size": 8, "cp_rank": args.rank, "h_q": 16, "h_kv": 2, "head_dim": 256,
+              "parallelism": "cp8 (one rank's share on 1 GPU)"}
+    print(json.dumps(_single_line(args, block, "e4m3", PEAK_FP8_TFLOPS, config)), flush=True)
     return 0
 
 
@@ -387,9 +572,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=16384)
     ap.add_argument("--skip-extra", action="store_true", help="only the headline bf16 sweep")
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c4", "c5"],
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
                     help="c2 (default): the bf16 N=131072 sweep with its extras; c1: the reference's "
-                         "CPU case (N=2048, cp_size 4) on every rank, with the oracle's CPU time; c4: "
+                         "CPU case (N=2048, cp_size 4) on every rank, with the oracle's CPU time; c3: "
+                         "the e4m3 sweep at the c2 shape (ranks 3 and 7); c4: "
                          "packed bf16 sequences (8 lengths, cp_size 4); c5: the e4m3 N=262144, H_q=16, "
                          "H_kv=2, D=256 sweep")
     args = ap.parse_args()
@@ -399,6 +585,8 @@ def main():
         return 2
     if args.workload == "c5":
         return bench_c5(args)
+    if args.workload == "c3":
+        return bench_c3(args)
     if args.workload == "c4":
         return bench_c4(args)
     if args.workload == "c1":
@@ -546,31 +734,12 @@ def main():
                                   "merge_states_GBs": round(bb / (ms_ms * 1e-3) / 1e9, 1)}
         del lq7
         # fp8 sweep: fused (default) and per step
-        q8, ring8, desc = make_fp8_inputs(rank)
-        cfg8 = RingConfig(cp_size=CP, cp_rank=rank)
-        clock8 = KernelClock()
-        sec8 = timed_sweeps(lambda: ring_flash_attn(q8, ring8.k[rank], ring8.v[rank], cfg8, group=ring8,
-                                                    descales=desc), args.steps, args.warmup, clock8)
-        s8 = clock8.mean_ms("sweep_kernel")
-        per_step8 = lambda: ring_flash_attn(q8, ring8.k[rank], ring8.v[rank], cfg8, group=ring8,  # noqa: E731
-                                            descales=desc, fused=False)
-        sec8p = timed_sweeps(per_step8, max(3, args.steps // 2), 2)  # unclocked wall time
-        clock8p = KernelClock()
-        timed_sweeps(per_step8, max(3, args.steps // 2), 1, clock8p)
-        a8 = clock8p.mean_ms("attn")
-        result["fp8"] = {"workload": "same shape, OCP e4m3 q/k/v, per-source-rank k/v descales, bf16 out",
-                         "ms_per_step": round(sec8 * 1e3, 3), "TFLOP/s": round(flops / sec8 / 1e12, 2),
-                         "frac_of_fp8_peak": round(flops / sec8 / 1e12 / PEAK_FP8_TFLOPS, 4),
-                         "sweep_kernel": {"kernel": "attn_fwd_e4m3_sweep<4>", "avg_launch_ms": round(s8, 4),
-                                          "TFLOP/s": round(flops / (s8 * 1e-3) / 1e12, 2),
-                                          "frac": round(flops / (s8 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)},
-                         "per_step": {"ms_per_step": round(sec8p * 1e3, 3),
-                                      "TFLOP/s": round(flops / sec8p / 1e12, 2),
-                                      "attn_kernel": "attn_fwd_e4m3_vt<4>",
-                                      "attn_avg_launch_ms": round(a8, 4),
-                                      "attn_TFLOP/s": round(per_launch / (a8 * 1e-3) / 1e12, 2),
-                                      "attn_frac": round(per_launch / (a8 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)}}
-        del q8, ring8
+        result["fp8"] = c3_block(rank, args.steps, args.warmup)
+        # rank 7 (only front-half steps) in e4m3, its own inputs and descales
+        b7 = c3_block(7, max(3, args.steps // 2), 2)
+        result["fp8"]["rank7"] = {k: b7[k] for k in ("ms_per_step", "TFLOP/s", "frac_of_fp8_peak", "sweep_kernel")}
+        result["fp8"]["cpu_baseline"] = ("the oracle computes e4m3 inputs dequantised in fp32: the same CPU work "
+                                         "per FLOP as the bf16 sweep's cpu_baseline below")
         # paged K/V caches (pages of 256 rows in a random order): page gather + paged V^T + sweep
         from fa4_ring import PagedKVRing
         from fa4_ring.paged import gather_kv_pages, transpose_v_paged_many
@@ -578,21 +747,8 @@ def main():
                                         generator=torch.Generator().manual_seed(rank))
         secpg = timed_sweeps(lambda: ring_flash_attn(lq, None, None, cfg, group=paged), args.steps, 2)
 
-        def event_ms(fn, n=10):
-            for _ in range(3):
-                fn()
-            evs = []
-            for _ in range(n):
-                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                s.record()
-                fn()
-                e.record()
-                evs.append((s, e))
-            torch.cuda.synchronize()
-            return sum(s.elapsed_time(e) for s, e in evs) / n
-
-        g_ms = event_ms(lambda: gather_kv_pages(paged, "k", t_local))
-        pt_ms = event_ms(lambda: transpose_v_paged_many(paged, t_local))
+        g_ms = _event_ms(lambda: gather_kv_pages(paged, "k", t_local))
+        pt_ms = _event_ms(lambda: transpose_v_paged_many(paged, t_local))
         pbytes = CP * 2.0 * t_local * HKV * D * 2  # every source's K (or V): read once, written once
         result["paged_bf16"] = {
             "workload": "same sweep with every source's K/V in a paged cache (256-row pages, random "
@@ -608,6 +764,12 @@ def main():
         del paged
     del ring, lq, q_full
     torch.cuda.synchronize()
+    if not args.skip_extra:
+        # the packed-sequence and head-dim-256 configurations, every form they name
+        result["c4_varlen_bf16"] = c4_block(3, args.steps, args.warmup, not args.no_cpu_baseline)
+        torch.cuda.synchronize()
+        result["c5_fp8_d256"] = c5_block(3, max(3, args.steps // 2), 2, not args.no_cpu_baseline)
+        torch.cuda.synchronize()
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(rank, args.cpu_rows)

@@ -1521,8 +1521,21 @@ __device__ __forceinline__ i32x8 cat8(i32x4 a, i32x4 b) {
   return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// A register whose contents do not matter: the empty statement defines it with no
+// instruction, so the register allocator places it wherever its user needs it.  Volatile so
+// that two of them are never merged into one value.
+__device__ __forceinline__ int any_bits() {
+  int x;
+  asm volatile("" : "=v"(x));
+  return x;
+}
+
 // Packs probabilities of S^T registers into e4m3 P^T fragments: slot j of k-step u is
-// register j % 16 of tile 2u + j / 16.
+// register j % 16 of tile 2u + j / 16.  A conversion writes one 16-bit half of its
+// destination and keeps the other, and the second of each pair overwrites the half the first
+// keeps.  So the first keeps whatever its destination held (any_bits): with a defined old
+// value such as 0 the compiler would first write it into each slot of the 8-register MFMA
+// operand, 16 VALU moves per tile in the phase that bounds the kernel.
 template <int NPS, int NMT>
 __device__ __forceinline__ void pack_e4m3(const f32x16 (&s)[NMT], i32x8 (&pf)[NPS]) {
 #pragma unroll
@@ -1531,7 +1544,7 @@ __device__ __forceinline__ void pack_e4m3(const f32x16 (&s)[NMT], i32x8 (&pf)[NP
     for (int w = 0; w < 8; ++w) {
       const f32x16& t = s[2 * u + (w >> 2)];
       const int i = 4 * (w & 3);
-      int x = __builtin_amdgcn_cvt_pk_fp8_f32(t[i], t[i + 1], 0, false);
+      int x = __builtin_amdgcn_cvt_pk_fp8_f32(t[i], t[i + 1], any_bits(), false);
       x = __builtin_amdgcn_cvt_pk_fp8_f32(t[i + 2], t[i + 3], x, true);
       pf[u][w] = x;
     }
@@ -1549,7 +1562,7 @@ __device__ __forceinline__ void pack_e4m3_residual(const f32x16 (&s)[NMT], const
       const int i = 4 * (w & 3);
       const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(hi[u][w], false);
       const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8(hi[u][w], true);
-      int x = __builtin_amdgcn_cvt_pk_fp8_f32(t[i] - a[0], t[i + 1] - a[1], 0, false);
+      int x = __builtin_amdgcn_cvt_pk_fp8_f32(t[i] - a[0], t[i + 1] - a[1], any_bits(), false);
       x = __builtin_amdgcn_cvt_pk_fp8_f32(t[i + 2] - b[0], t[i + 3] - b[1], x, true);
       lo[u][w] = x;
     }
