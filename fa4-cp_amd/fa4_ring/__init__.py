@@ -10,8 +10,11 @@ and, for the single-GPU ring:
     LocalKVRing         every source rank's KV shard resident in HBM
     PagedKVRing         every source rank's paged K/V cache (fused sweep)
     quantize_e4m3 / quantize_ring   the FP8 producer (e4m3 shards and their descales)
+    ring_flash_attn_backward / ring_flash_attn_func   the sweep's backward (the reference is
+                        forward-only): functional, and as a torch.autograd function
 """
 
+from .backward import ring_flash_attn_backward, ring_flash_attn_func
 from .config import RingConfig
 from .fp8 import quantize_e4m3, quantize_ring
 from .merge import BatchedMerger, IncrementalMerger, make_merger
@@ -32,4 +35,6 @@ __all__ = [
     "make_merger",
     "quantize_e4m3",
     "quantize_ring",
+    "ring_flash_attn_backward",
+    "ring_flash_attn_func",
 ]

@@ -147,6 +147,46 @@ class SweepArgs(ctypes.Structure):
     ]
 
 
+class SweepBwdArgs(ctypes.Structure):
+    """Mirror of fa4cp_sweep_bwd_args."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("dout", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("delta", ctypes.c_void_p),
+        ("dq", ctypes.c_void_p),
+        ("q_row_stride", ctypes.c_int64),
+        ("q_head_stride", ctypes.c_int64),
+        ("do_row_stride", ctypes.c_int64),
+        ("do_head_stride", ctypes.c_int64),
+        ("o_row_stride", ctypes.c_int64),
+        ("o_head_stride", ctypes.c_int64),
+        ("lse_row_stride", ctypes.c_int64),
+        ("k", ctypes.c_void_p * MAX_CP),
+        ("v", ctypes.c_void_p * MAX_CP),
+        ("dk", ctypes.c_void_p * MAX_CP),
+        ("dv", ctypes.c_void_p * MAX_CP),
+        ("k_row_stride", ctypes.c_int64),
+        ("k_head_stride", ctypes.c_int64),
+        ("v_row_stride", ctypes.c_int64),
+        ("v_head_stride", ctypes.c_int64),
+        ("cu", ctypes.c_void_p),
+        ("nseq", ctypes.c_int32),
+        ("max_seqlen", ctypes.c_int32),
+        ("total", ctypes.c_int32),
+        ("h_q", ctypes.c_int32),
+        ("h_kv", ctypes.c_int32),
+        ("d", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("cp_rank", ctypes.c_int32),
+        ("cp_size", ctypes.c_int32),
+        ("softmax_scale", ctypes.c_float),
+        ("accumulate", ctypes.c_int32),
+    ]
+
+
 class PagedArgs(ctypes.Structure):
     """Mirror of fa4cp_paged_args."""
     _fields_ = [
@@ -218,6 +258,7 @@ SIGNATURES = {
          ctypes.c_int32, ctypes.c_void_p],
     ),
     "fa4cp_ring_sweep_fwd": (ctypes.c_int, [ctypes.POINTER(SweepArgs), ctypes.c_void_p]),
+    "fa4cp_ring_sweep_bwd": (ctypes.c_int, [ctypes.POINTER(SweepBwdArgs), ctypes.c_void_p]),
     "fa4cp_quantize_e4m3": (ctypes.c_int, [ctypes.POINTER(QuantArgs), ctypes.c_void_p]),
     "fa4cp_quantize_e4m3_noalloc": (ctypes.c_int, [ctypes.POINTER(QuantArgs), ctypes.c_void_p]),
     "fa4cp_last_error": (ctypes.c_char_p, []),

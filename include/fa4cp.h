@@ -232,6 +232,44 @@ typedef struct fa4cp_sweep_args {
 int fa4cp_ring_sweep_fwd(const fa4cp_sweep_args* args, void* stream);
 
 /*
+ * Backward of fa4cp_ring_sweep_fwd (BF16 / FP16, d = 64 or 128).  No counterpart in the
+ * reference, which is forward-only (README.md: "forward only"); this is the training side of
+ * the same sweep.  Given the forward's out and natural-log lse and the gradient dout of out:
+ *   dq            = the gradient of the local q                       [total][h_q][d] float32
+ *   dk[i], dv[i]  = this rank's contribution to source rank i's K / V gradient
+ *                   (keys this rank does not attend get 0)            [total][h_kv][d] float32
+ * Every (query row, key) pair of the forward's three step patterns contributes, with the
+ * probability exp(scale q.k - lse) taken against the final lse.  delta is a caller-owned
+ * [total][h_q] float32 workspace (rowsum(dout * out), written here).  With accumulate != 0 the
+ * results are added to dq / dk / dv instead of stored (summing the contributions of several
+ * ranks, as a ring's backward does).  q, dout and out may have any row and head stride; k / v
+ * shards share strides and the cu layout of fa4cp_ring_sweep_fwd.  Three launches on `stream`.
+ */
+typedef struct fa4cp_sweep_bwd_args {
+  const void* q;    /* [total] x h_q x d */
+  const void* dout; /* [total] x h_q x d, gradient of the forward's out */
+  const void* out;  /* [total] x h_q x d, the forward's out */
+  const float* lse; /* lse[row * lse_row_stride + head], the forward's natural-log lse */
+  float* delta;     /* [total][h_q] workspace */
+  float* dq;        /* [total][h_q][d] */
+  int64_t q_row_stride, q_head_stride, do_row_stride, do_head_stride, o_row_stride, o_head_stride;
+  int64_t lse_row_stride;
+  const void* k[FA4CP_MAX_CP];
+  const void* v[FA4CP_MAX_CP];
+  float* dk[FA4CP_MAX_CP]; /* [total][h_kv][d] per source rank */
+  float* dv[FA4CP_MAX_CP];
+  int64_t k_row_stride, k_head_stride, v_row_stride, v_head_stride;
+  const int32_t* cu; /* local cu_seqlens [nseq + 1] or NULL (one sequence of `total` rows) */
+  int32_t nseq, max_seqlen, total;
+  int32_t h_q, h_kv, d, dtype;
+  int32_t cp_rank, cp_size;
+  float softmax_scale;
+  int32_t accumulate;
+} fa4cp_sweep_bwd_args;
+
+int fa4cp_ring_sweep_bwd(const fa4cp_sweep_bwd_args* args, void* stream);
+
+/*
  * In-place online-softmax merge (flashinfer.cascade.merge_state_in_place semantics, natural
  * log LSE):
  *     m = max(s, s_o);  w = e^(s-m);  w_o = e^(s_o-m)

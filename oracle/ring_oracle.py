@@ -267,6 +267,57 @@ def ring_rank(lq: torch.Tensor, k_shards: Sequence[torch.Tensor], v_shards: Sequ
     return acc_o, acc_l
 
 
+def ring_rank_backward(lq: torch.Tensor, k_shards: Sequence[torch.Tensor], v_shards: Sequence[torch.Tensor],
+                       dout: torch.Tensor, out: torch.Tensor, lse: torch.Tensor, rank: int, cp_size: int,
+                       scale: float, cu: Optional[Sequence[int]] = None, drop_delta: bool = False):
+    """One rank's gradients in fp32, given its ring output ``out`` and natural-log ``lse``
+    (from ring_rank) and the gradient ``dout`` of ``out``: (dq [T,H,D], dk per source rank,
+    dv per source rank), the dk / dv entries being this rank's contributions to that
+    source's K / V gradient.  The reference has no backward; this restates the gradient of
+    its forward schedule (ring_rank above): every (row, key) pair of a step contributes with
+    P = exp(scale q.k - lse) against the final lse, dS = P (dO.v - delta) with
+    delta = rowsum(dO * out), dq += scale dS k, dk += scale dS^T q, dv += P^T dO.
+    ``drop_delta`` plants a mistake (delta taken as 0) for the oracle's own negative test."""
+    t, h, d = lq.shape
+    cu = [0, t] if cu is None else [int(c) for c in cu]
+    hkv = k_shards[0].shape[1]
+    g = h // hkv
+    qf, dof = lq.float(), dout.float()
+    delta = torch.zeros(t, h) if drop_delta else (dof * out.float()).sum(-1)
+    dq = torch.zeros(t, h, d)
+    dks = [torch.zeros(t, hkv, d) for _ in range(cp_size)]
+    dvs = [torch.zeros(t, hkv, v_shards[0].shape[2]) for _ in range(cp_size)]
+    for step in range(cp_size):
+        src = (rank - step) % cp_size
+        k, v = k_shards[src].float(), v_shards[src].float()
+        for j in range(len(cu) - 1):
+            s0, e0 = cu[j], cu[j + 1]
+            n = e0 - s0
+            if n == 0:
+                continue
+            half = n // 2
+            if step == 0:
+                rows, keys = torch.arange(s0, e0), torch.arange(s0, e0)
+            elif step <= rank:
+                rows, keys = torch.arange(s0, e0), torch.arange(s0, s0 + half)
+            else:
+                rows, keys = torch.arange(s0 + half, e0), torch.arange(s0, e0)
+            if rows.numel() == 0 or keys.numel() == 0:
+                continue
+            for hh in range(h):
+                kvh = hh // g
+                qh, kh, vh, dh = qf[rows, hh], k[keys, kvh], v[keys, kvh], dof[rows, hh]
+                sc = (qh @ kh.T) * scale
+                if step == 0:
+                    sc = sc.masked_fill(keys.unsqueeze(0) > rows.unsqueeze(1), float("-inf"))
+                p = torch.exp(sc - lse[rows, hh].unsqueeze(1))
+                ds = p * (dh @ vh.T - delta[rows, hh].unsqueeze(1))
+                dq[rows, hh] += scale * (ds @ kh)
+                dks[src][keys, kvh] += scale * (ds.T @ qh)
+                dvs[src][keys, kvh] += p.T @ dh
+    return dq, dks, dvs
+
+
 def dense_causal(q, k, v, scale):
     """test_algorithm_cpu.py:93-95."""
     return cpu_attn(q, k, v, causal=True, scale=scale)[0]

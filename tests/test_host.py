@@ -182,6 +182,7 @@ def test_sweep_entry_point_validates_before_launching():
 @pytest.mark.parametrize("struct,cname", [(_lib.AttnArgs, "fa4cp_attn_args"),
                                            (_lib.TransposeArgs, "fa4cp_transpose_args"),
                                            (_lib.SweepArgs, "fa4cp_sweep_args"),
+                                           (_lib.SweepBwdArgs, "fa4cp_sweep_bwd_args"),
                                            (_lib.QuantArgs, "fa4cp_quant_args"),
                                            (_lib.PagedArgs, "fa4cp_paged_args")])
 def test_args_layout_matches_c_header(struct, cname):

@@ -298,6 +298,69 @@ def test_dense_causal_rows_all_heads_matches_per_pair(key_block):
     assert (bad[:3] - o[:3]).abs().max() > 1e-2
 
 
+def _dense_grads_fp64(q, k, v, dout, scale, full_cu):
+    """torch autograd of block-diagonal causal attention in float64 (GQA by repetition)."""
+    q64, k64, v64 = (x.double().requires_grad_(True) for x in (q, k, v))
+    h = q.shape[1]
+    g = h // k.shape[1]
+    outs = []
+    for j in range(len(full_cu) - 1):
+        s, e = full_cu[j], full_cu[j + 1]
+        kq = k64[s:e].repeat_interleave(g, dim=1)
+        vq = v64[s:e].repeat_interleave(g, dim=1)
+        sc = torch.einsum("qhd,khd->hqk", q64[s:e], kq) * scale
+        n = e - s
+        sc = sc.masked_fill(torch.triu(torch.ones(n, n, dtype=torch.bool), 1), float("-inf"))
+        outs.append(torch.einsum("hqk,khd->qhd", torch.softmax(sc, -1), vq))
+    torch.cat(outs).backward(dout.double())
+    return q64.grad, k64.grad, v64.grad
+
+
+def _ring_grads(q, k, v, dout, cp, scale, full_cu, drop_delta=False):
+    """Every rank's oracle backward; dK / dV contributions summed per source shard and all
+    shards stitched back to the full sequence."""
+    ks = [O.zigzag_shard_varlen(k, full_cu, r, cp)[0] for r in range(cp)]
+    vs = [O.zigzag_shard_varlen(v, full_cu, r, cp)[0] for r in range(cp)]
+    dqs, dk_sum, dv_sum = [], [torch.zeros_like(x) for x in ks], [torch.zeros_like(x) for x in vs]
+    for rank in range(cp):
+        lq, lcu = O.zigzag_shard_varlen(q, full_cu, rank, cp)
+        ldo = O.zigzag_shard_varlen(dout, full_cu, rank, cp)[0]
+        out, lse = O.ring_rank(lq, ks, vs, rank, cp, scale, cu=lcu)
+        dq, dk, dv = O.ring_rank_backward(lq, ks, vs, ldo, out, lse, rank, cp, scale, cu=lcu, drop_delta=drop_delta)
+        dqs.append(dq)
+        for i in range(cp):
+            dk_sum[i] += dk[i]
+            dv_sum[i] += dv[i]
+
+    def stitch(parts):
+        full = torch.zeros(q.shape[0], *parts[0].shape[1:])
+        for r in range(cp):
+            full[torch.from_numpy(O.zigzag_rows_varlen(full_cu, r, cp))] = parts[r]
+        return full
+
+    return stitch(dqs), stitch(dk_sum), stitch(dv_sum)
+
+
+@pytest.mark.parametrize("lens,h,hkv,d,cp", [([64], 4, 2, 16, 4), ([96], 2, 1, 8, 2), ([32, 48, 16], 4, 2, 8, 2),
+                                             ([128], 4, 4, 16, 8), ([64, 128], 8, 2, 8, 4)])
+def test_ring_backward_equals_dense_autograd(lens, h, hkv, d, cp):
+    """Summed over every rank (dq stitched, each source's dK / dV contributions added), the
+    oracle's ring backward equals torch autograd of dense causal attention in float64, per
+    packed sequence; the same with delta dropped (a plausible mistake) does not."""
+    full_cu = [0]
+    for n in lens:
+        full_cu.append(full_cu[-1] + n)
+    q, k, v = O.random_qkv(full_cu[-1], h, hkv, d, seed=21)
+    dout = torch.randn(full_cu[-1], h, d, generator=torch.Generator().manual_seed(22))
+    scale = 1 / math.sqrt(d)
+    gq, gk, gv = _dense_grads_fp64(q, k, v, dout, scale, full_cu)
+    dq, dk, dv = _ring_grads(q, k, v, dout, cp, scale, full_cu)
+    for got, want in ((dq, gq), (dk, gk), (dv, gv)):
+        assert (got.double() - want).abs().max() < 1e-4 * max(1.0, float(want.abs().max()))
+    bq, bk, _ = _ring_grads(q, k, v, dout, cp, scale, full_cu, drop_delta=True)
+    assert (bq.double() - gq).abs().max() > 1e-2 and (bk.double() - gk).abs().max() > 1e-2
+
+
 # ---------------------------------------------------------------- e4m3
 
 
