@@ -483,6 +483,54 @@ def bench_c3(args) -> int:
     return 0
 
 
+def bwd_block(rank: int, steps: int, warmup: int) -> dict:
+    """The backward of the bf16 sweep at the headline shape (N = 131072, cp_size = 8, H_q = 32,
+    H_kv = 8, D = 128): dq and every source's dk / dv contribution for one rank, from the
+    forward's out and LSE.  FLOPs counted as 2.5 x the forward's (the usual five products of
+    a flash-attention backward against the forward's two: 43.98 TFLOP); the kernels compute
+    seven (dq recomputes the scores and dP)."""
+    import torch
+
+    from fa4_ring import RingConfig, ring_flash_attn
+    from fa4_ring.backward import ring_flash_attn_backward
+
+    _, lq, ring = make_bf16_inputs(rank)
+    cfg = RingConfig(cp_size=CP, cp_rank=rank)
+    out, lse = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, return_lse=True)
+    g = torch.Generator(device=lq.device).manual_seed(7)
+    dout = torch.randn(lq.shape, device=lq.device, generator=g, dtype=torch.bfloat16)
+    t = lq.shape[0]
+    dq = torch.empty(lq.shape, dtype=torch.float32, device=lq.device)
+    dk = [torch.empty((t, HKV, D), dtype=torch.float32, device=lq.device) for _ in range(CP)]
+    dv = [torch.empty((t, HKV, D), dtype=torch.float32, device=lq.device) for _ in range(CP)]
+
+    def bwd():
+        return ring_flash_attn_backward(dout, lq, ring.k[rank], ring.v[rank], out, lse, cfg, group=ring, dq=dq, dk=dk,
+                                        dv=dv)
+
+    ms = _event_ms(bwd, n=max(3, steps // 2))
+    flops = 2.5 * sweep_flops(t, CP, HQ, D)
+    return {"workload": f"backward of the bf16 sweep (rank {rank}): dq and the dk / dv contributions to all {CP} "
+                        "source shards, fp32 gradients",
+            "ms_per_step": round(ms, 3), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2),
+            "frac_of_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "flop_per_step": flops, "kernels": "bwd_delta_kernel + bwd_dq_kernel<bf16,128,4> + bwd_dkdv_kernel<bf16,128>"}
+
+
+def bench_bwd(args) -> int:
+    block = bwd_block(args.rank, args.steps, args.warmup)
+    value = block["TFLOP/s"]
+    print(json.dumps({
+        "metric": METRIC, "value": value, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": block["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (q/k/v/dout ~ N(0,1) bf16, seeded on the GPU)",
+        "config": {"workload": block["workload"] + f", N={N}, cp_size={CP}, H_q={HQ}, H_kv={HKV}, D={D}",
+                   "global_batch": 1, "seq_len": N, "cp_size": CP, "cp_rank": args.rank, "h_q": HQ, "h_kv": HKV,
+                   "head_dim": D, "parallelism": "cp8 (one rank's share on 1 GPU)"},
+        "frac_of_peak": block["frac_of_peak"], "cpu_baseline": None}), flush=True)
+    return 0
+
+
 def bench_c4(args) -> int:
     rank = args.rank % 4
     block = c4_block(rank, args.steps, args.warmup, not args.no_cpu_baseline)
@@ -572,7 +620,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=16384)
     ap.add_argument("--skip-extra", action="store_true", help="only the headline bf16 sweep")
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "bwd"],
                     help="c2 (default): the bf16 N=131072 sweep with its extras; c1: the reference's "
                          "CPU case (N=2048, cp_size 4) on every rank, with the oracle's CPU time; c3: "
                          "the e4m3 sweep at the c2 shape (ranks 3 and 7); c4: "
@@ -587,6 +635,8 @@ def main():
         return bench_c5(args)
     if args.workload == "c3":
         return bench_c3(args)
+    if args.workload == "bwd":
+        return bench_bwd(args)
     if args.workload == "c4":
         return bench_c4(args)
     if args.workload == "c1":
@@ -769,6 +819,8 @@ def main():
         result["c4_varlen_bf16"] = c4_block(3, args.steps, args.warmup, not args.no_cpu_baseline)
         torch.cuda.synchronize()
         result["c5_fp8_d256"] = c5_block(3, max(3, args.steps // 2), 2, not args.no_cpu_baseline)
+        torch.cuda.synchronize()
+        result["backward_bf16"] = bwd_block(rank, args.steps, args.warmup)
         torch.cuda.synchronize()
 
     if not args.no_cpu_baseline:

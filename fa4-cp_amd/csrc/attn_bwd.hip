@@ -98,19 +98,6 @@ __device__ __forceinline__ StepPairs step_pairs(int rank, int S, int src, int L)
   return sp;
 }
 
-// A 32-row tile of rows [row0, row0 + 32) x D of a [rows][heads][D] tensor into LDS at row
-// stride RS elements; rows at or past `lim` are zero (so a product never sees stale data).
-template <typename T, int D, int RS, int NT>
-__device__ __forceinline__ void stage_rows(T* lds, const T* src, int64_t rs, int row0, int lim, int rows) {
-  constexpr int CPR = D / 8;  // 16-byte chunks per row
-  for (int c = threadIdx.x; c < rows * CPR; c += NT) {
-    const int r = c / CPR, ch = c % CPR;
-    u32x4 x = {0u, 0u, 0u, 0u};
-    if (row0 + r < lim) x = *reinterpret_cast<const u32x4*>(src + (int64_t)(row0 + r) * rs + 8 * ch);
-    *reinterpret_cast<u32x4*>(lds + r * RS + 8 * ch) = x;
-  }
-}
-
 // 8 elements (16 bytes) of LDS row `row`, starting at element 8 * chunk.
 template <typename T, int RS>
 __device__ __forceinline__ typename BwdMfma<T>::frag lds_frag(const T* lds, int row, int chunk) {
@@ -131,6 +118,15 @@ __device__ __forceinline__ typename BwdMfma<T>::frag lds_frag_tr(const T* lds, i
   const bs16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_bs16x4*)(p + 4 * RS));
   const bs16x4 ab[2] = {a, b};
   return __builtin_bit_cast(typename BwdMfma<T>::frag, ab);
+}
+
+// Workgroup barrier after this wavefront's LDS writes have completed, leaving its global
+// loads in flight: __syncthreads() would also wait for those (its fence waits for every
+// outstanding memory operation), which would serialise the prefetch of the next tile with
+// the barrier.
+__device__ __forceinline__ void lds_written_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt unconstrained
+  wg_barrier();
 }
 
 template <typename T>
@@ -167,14 +163,43 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(const T* __restrict__ do
   if (g < n && lane == 0) delta[g] = acc;
 }
 
+// A 32-row x D tile in flight to LDS: thread t loads 16-byte chunks t + NT i (row-major over
+// the tile) into registers, so the next tile's loads overlap the current tile's products;
+// rows at or past `lim` read as zeros (a product must never see stale or non-finite data).
+template <typename T, int D, int NT>
+struct TileFetch {
+  static constexpr int CPR = D / 8;
+  static constexpr int N = kBwdRows * CPR / NT;
+  static_assert(N * NT == kBwdRows * CPR, "threads must split the tile evenly");
+  u32x4 x[N];
+  __device__ __forceinline__ void fetch(const T* src, int64_t rs, int row0, int lim) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int c = (int)threadIdx.x + NT * i, r = c / CPR, ch = c % CPR;
+      x[i] = u32x4{0u, 0u, 0u, 0u};
+      if (row0 + r < lim) x[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)(row0 + r) * rs + 8 * ch);
+    }
+  }
+  template <int RS>
+  __device__ __forceinline__ void store(T* lds) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int c = (int)threadIdx.x + NT * i, r = c / CPR, ch = c % CPR;
+      *reinterpret_cast<u32x4*>(lds + r * RS + 8 * ch) = x[i];
+    }
+  }
+};
+
 // dQ: one workgroup per 32 query rows x HP query heads of one kv head (one wavefront per
-// head), walking every ring step's keys in tiles of 32 (the forward sweep's schedule).
+// head), walking every ring step's keys in tiles of 32 (the forward sweep's schedule).  The
+// tiles go through LDS; the next tile's loads are in flight while the current one is used.
 template <typename T, int D, int HP>
 __global__ __launch_bounds__(64 * HP) void bwd_dq_kernel(BwdParams p) {
   using M = BwdMfma<T>;
   constexpr int RS = D + 8;     // LDS row stride (elements): rows shift by 16 bytes
   constexpr int NKS = D / 16;   // k-steps over the head dim
   constexpr int NDT = D / 32;   // output tiles over the head dim
+  constexpr int NT = 64 * HP;
   __shared__ __align__(16) T ks[kBwdRows * RS];
   __shared__ __align__(16) T vs[kBwdRows * RS];
 
@@ -213,38 +238,69 @@ __global__ __launch_bounds__(64 * HP) void bwd_dq_kernel(BwdParams p) {
 #pragma unroll
   for (int i = 0; i < NDT; ++i) acc[i] = f32x16{};
 
-  for (int s = 0; s < p.S; ++s) {
-    const int src = p.rank - s < 0 ? p.rank - s + p.S : p.rank - s;
-    const StepPairs sp = step_pairs(p.rank, p.S, src, L);
-    if (r0 + kBwdRows <= sp.row_min) continue;  // no row of the tile attends this step
-    const int key_end = sp.causal ? min(sp.key_lim, r0 + kBwdRows) : sp.key_lim;
-    const T* kb = reinterpret_cast<const T*>(p.k[src]) + (int64_t)qs * p.k_rs + (int64_t)kvh * p.k_hs;
-    const T* vb = reinterpret_cast<const T*>(p.v[src]) + (int64_t)qs * p.v_rs + (int64_t)kvh * p.v_hs;
-    for (int k0 = 0; k0 < key_end; k0 += kBwdRows) {
-      __syncthreads();  // the previous tile's readers are done
-      stage_rows<T, D, RS, 64 * HP>(ks, kb, p.k_rs, k0, sp.key_lim, kBwdRows);
-      stage_rows<T, D, RS, 64 * HP>(vs, vb, p.v_rs, k0, sp.key_lim, kBwdRows);
-      __syncthreads();
-      f32x16 st = {}, dpt = {};
-#pragma unroll
-      for (int t = 0; t < NKS; ++t) st = M::mma(lds_frag<T, RS>(ks, sig(lq), 2 * t + h), qf[t], st);
-#pragma unroll
-      for (int t = 0; t < NKS; ++t) dpt = M::mma(lds_frag<T, RS>(vs, sig(lq), 2 * t + h), df[t], dpt);
-      float dsv[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kp = k0 + acc_pos(r, h);
-        const bool ok = row_ok && qpos >= sp.row_min && kp < sp.key_lim && (!sp.causal || kp <= qpos);
-        const float pr = ok ? __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2)) : 0.f;
-        dsv[r] = pr * (dpt[r] - dl);
-      }
-      const typename M::frag ds0 = to_frag<T>(dsv), ds1 = to_frag<T>(dsv + 8);
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        acc[dt] = M::mma(ds0, lds_frag_tr<T, RS>(ks, 0, 32 * dt), acc[dt]);
-        acc[dt] = M::mma(ds1, lds_frag_tr<T, RS>(ks, 16, 32 * dt), acc[dt]);
-      }
+  // the key tiles of every step the row tile attends, in order: (step, first key)
+  auto src_of = [&](int s) { return p.rank - s < 0 ? p.rank - s + p.S : p.rank - s; };
+  auto key_end_of = [&](int s) {  // keys of step s the tile sees (0: no row attends it)
+    const StepPairs sp = step_pairs(p.rank, p.S, src_of(s), L);
+    if (r0 + kBwdRows <= sp.row_min) return 0;
+    return sp.causal ? min(sp.key_lim, r0 + kBwdRows) : sp.key_lim;
+  };
+  auto next_tile = [&](int& s, int& k0, int& kend) {
+    k0 += kBwdRows;
+    while (s < p.S && k0 >= kend) {
+      ++s;
+      k0 = 0;
+      if (s < p.S) kend = key_end_of(s);
     }
+  };
+  auto kv_base = [&](int s, bool isk) {
+    const int src = src_of(s);
+    return isk ? reinterpret_cast<const T*>(p.k[src]) + (int64_t)qs * p.k_rs + (int64_t)kvh * p.k_hs
+               : reinterpret_cast<const T*>(p.v[src]) + (int64_t)qs * p.v_rs + (int64_t)kvh * p.v_hs;
+  };
+  int cs = 0, ck0 = -kBwdRows, ckend = key_end_of(0);
+  next_tile(cs, ck0, ckend);  // the first tile (step 0 always has one: r0 < L)
+  TileFetch<T, D, NT> fk, fv;
+  if (cs < p.S) {
+    const int lim = step_pairs(p.rank, p.S, src_of(cs), L).key_lim;
+    fk.fetch(kv_base(cs, true), p.k_rs, ck0, lim);
+    fv.fetch(kv_base(cs, false), p.v_rs, ck0, lim);
+  }
+  while (cs < p.S) {
+    const StepPairs sp = step_pairs(p.rank, p.S, src_of(cs), L);
+    __syncthreads();  // the previous tile's readers are done
+    fk.template store<RS>(ks);
+    fv.template store<RS>(vs);
+    int ns = cs, nk0 = ck0, nkend = ckend;
+    next_tile(ns, nk0, nkend);
+    if (ns < p.S) {
+      const int lim = step_pairs(p.rank, p.S, src_of(ns), L).key_lim;
+      fk.fetch(kv_base(ns, true), p.k_rs, nk0, lim);
+      fv.fetch(kv_base(ns, false), p.v_rs, nk0, lim);
+    }
+    lds_written_barrier();
+    f32x16 st = {}, dpt = {};
+#pragma unroll
+    for (int t = 0; t < NKS; ++t) st = M::mma(lds_frag<T, RS>(ks, sig(lq), 2 * t + h), qf[t], st);
+#pragma unroll
+    for (int t = 0; t < NKS; ++t) dpt = M::mma(lds_frag<T, RS>(vs, sig(lq), 2 * t + h), df[t], dpt);
+    float dsv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kp = ck0 + acc_pos(r, h);
+      const bool ok = row_ok && qpos >= sp.row_min && kp < sp.key_lim && (!sp.causal || kp <= qpos);
+      const float pr = ok ? __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2)) : 0.f;
+      dsv[r] = pr * (dpt[r] - dl);
+    }
+    const typename M::frag ds0 = to_frag<T>(dsv), ds1 = to_frag<T>(dsv + 8);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      acc[dt] = M::mma(ds0, lds_frag_tr<T, RS>(ks, 0, 32 * dt), acc[dt]);
+      acc[dt] = M::mma(ds1, lds_frag_tr<T, RS>(ks, 16, 32 * dt), acc[dt]);
+    }
+    cs = ns;
+    ck0 = nk0;
+    ckend = nkend;
   }
   // accumulator register r of lane l: query row 8 (r / 4) + 4h + r % 4, column 32 dt + lq
 #pragma unroll
@@ -261,7 +317,9 @@ __global__ __launch_bounds__(64 * HP) void bwd_dq_kernel(BwdParams p) {
 }
 
 // dK / dV: one workgroup per 128 keys of one source rank's sequence and kv head (32 keys per
-// wavefront), walking the query rows that attend them for every query head of the kv head.
+// wavefront, K and V of those keys held in registers as operands), walking the query rows
+// that attend them for every query head of the kv head; the next 32-row block of Q / dO is
+// in flight while the current one is used.
 template <typename T, int D>
 __global__ __launch_bounds__(64 * kDkdvWaves) void bwd_dkdv_kernel(BwdParams p) {
   using M = BwdMfma<T>;
@@ -269,8 +327,6 @@ __global__ __launch_bounds__(64 * kDkdvWaves) void bwd_dkdv_kernel(BwdParams p) 
   constexpr int NKS = D / 16;
   constexpr int NDT = D / 32;
   constexpr int NT = 64 * kDkdvWaves;
-  __shared__ __align__(16) T ks[kDkdvKeys * RS];
-  __shared__ __align__(16) T vs[kDkdvKeys * RS];
   __shared__ __align__(16) T qt[kBwdRows * RS];
   __shared__ __align__(16) T dot[kBwdRows * RS];
   __shared__ float lse2s[kBwdRows], dls[kBwdRows];
@@ -295,54 +351,77 @@ __global__ __launch_bounds__(64 * kDkdvWaves) void bwd_dkdv_kernel(BwdParams p) 
   for (int i = 0; i < NDT; ++i) dk[i] = dv[i] = f32x16{};
 
   if (kb0 < sp.key_lim) {
-    const T* kb = reinterpret_cast<const T*>(p.k[src]) + (int64_t)qs * p.k_rs + (int64_t)kvh * p.k_hs;
-    const T* vb = reinterpret_cast<const T*>(p.v[src]) + (int64_t)qs * p.v_rs + (int64_t)kvh * p.v_hs;
-    stage_rows<T, D, RS, NT>(ks, kb, p.k_rs, kb0, sp.key_lim, kDkdvKeys);
-    stage_rows<T, D, RS, NT>(vs, vb, p.v_rs, kb0, sp.key_lim, kDkdvKeys);
-    const T* kw = ks + w * kBwdRows * RS;
-    const T* vw = vs + w * kBwdRows * RS;
+    // K and V of the lane's key: B operands of S = Q K^T and dP = dO V^T
+    typename M::frag kf[NKS], vf[NKS];
+    {
+      const bool ok = key < sp.key_lim;
+      const T* kr = reinterpret_cast<const T*>(p.k[src]) + (int64_t)(qs + key) * p.k_rs + (int64_t)kvh * p.k_hs;
+      const T* vr = reinterpret_cast<const T*>(p.v[src]) + (int64_t)(qs + key) * p.v_rs + (int64_t)kvh * p.v_hs;
+#pragma unroll
+      for (int t = 0; t < NKS; ++t) {
+        typename M::frag z = {};
+        kf[t] = ok ? *reinterpret_cast<const typename M::frag*>(kr + 8 * h + 16 * t) : z;
+        vf[t] = ok ? *reinterpret_cast<const typename M::frag*>(vr + 8 * h + 16 * t) : z;
+      }
+    }
     const float c = p.scale * kLog2e;
     // query rows that can see a key of this workgroup: from the first key on when causal
     const int row_begin = max(sp.row_min, sp.causal ? kb0 : 0) / kBwdRows * kBwdRows;
-    for (int hq = kvh * p.group; hq < (kvh + 1) * p.group; ++hq) {
-      const T* qb = reinterpret_cast<const T*>(p.q) + (int64_t)qs * p.q_rs + (int64_t)hq * p.q_hs;
-      const T* db = reinterpret_cast<const T*>(p.dout) + (int64_t)qs * p.do_rs + (int64_t)hq * p.do_hs;
-      for (int r0 = row_begin; r0 < L; r0 += kBwdRows) {
-        __syncthreads();  // the previous block's readers are done (and K / V are staged)
-        stage_rows<T, D, RS, NT>(qt, qb, p.q_rs, r0, L, kBwdRows);
-        stage_rows<T, D, RS, NT>(dot, db, p.do_rs, r0, L, kBwdRows);
-        if (threadIdx.x < kBwdRows) {
-          const int row = r0 + threadIdx.x;
-          lse2s[threadIdx.x] = row < L ? p.lse[(int64_t)(qs + row) * p.lse_rs + hq] * kLog2e : 0.f;
-          dls[threadIdx.x] = row < L ? p.delta[(int64_t)(qs + row) * p.h_q + hq] : 0.f;
-        }
-        __syncthreads();
-        f32x16 st = {}, dpt = {};
+    const int n_rb = (L - row_begin + kBwdRows - 1) / kBwdRows;
+    const int n_blk = n_rb * p.group;  // (query head, 32-row block) pairs, head-major
+    auto qbase = [&](int bi, bool isq) {
+      const int hq = kvh * p.group + bi / n_rb;
+      return isq ? reinterpret_cast<const T*>(p.q) + (int64_t)qs * p.q_rs + (int64_t)hq * p.q_hs
+                 : reinterpret_cast<const T*>(p.dout) + (int64_t)qs * p.do_rs + (int64_t)hq * p.do_hs;
+    };
+    auto row0_of = [&](int bi) { return row_begin + (bi % n_rb) * kBwdRows; };
+    TileFetch<T, D, NT> fq, fd;
+    float flse = 0.f, fdl = 0.f;
+    auto fetch = [&](int bi) {
+      const int r0 = row0_of(bi), hq = kvh * p.group + bi / n_rb;
+      fq.fetch(qbase(bi, true), p.q_rs, r0, L);
+      fd.fetch(qbase(bi, false), p.do_rs, r0, L);
+      if (threadIdx.x < kBwdRows) {
+        const int row = r0 + threadIdx.x;
+        flse = row < L ? p.lse[(int64_t)(qs + row) * p.lse_rs + hq] : 0.f;  // scaled at the store: no wait here
+        fdl = row < L ? p.delta[(int64_t)(qs + row) * p.h_q + hq] : 0.f;
+      }
+    };
+    if (n_blk > 0) fetch(0);
+    for (int bi = 0; bi < n_blk; ++bi) {
+      const int r0 = row0_of(bi);
+      __syncthreads();  // the previous block's readers are done
+      fq.template store<RS>(qt);
+      fd.template store<RS>(dot);
+      if (threadIdx.x < kBwdRows) {
+        lse2s[threadIdx.x] = flse * kLog2e;
+        dls[threadIdx.x] = fdl;
+      }
+      if (bi + 1 < n_blk) fetch(bi + 1);
+      lds_written_barrier();
+      f32x16 st = {}, dpt = {};
 #pragma unroll
-        for (int t = 0; t < NKS; ++t)
-          st = M::mma(lds_frag<T, RS>(qt, sig(lk), 2 * t + h), lds_frag<T, RS>(kw, lk, 2 * t + h), st);
+      for (int t = 0; t < NKS; ++t) st = M::mma(lds_frag<T, RS>(qt, sig(lk), 2 * t + h), kf[t], st);
 #pragma unroll
-        for (int t = 0; t < NKS; ++t)
-          dpt = M::mma(lds_frag<T, RS>(dot, sig(lk), 2 * t + h), lds_frag<T, RS>(vw, lk, 2 * t + h), dpt);
-        // accumulator register r: query row r0 + acc_pos(r, h), key `key`
-        float pv[16], dsv[16];
+      for (int t = 0; t < NKS; ++t) dpt = M::mma(lds_frag<T, RS>(dot, sig(lk), 2 * t + h), vf[t], dpt);
+      // accumulator register r: query row r0 + acc_pos(r, h), key `key`
+      float pv[16], dsv[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int qi = acc_pos(r, h);
-          const int row = r0 + qi;
-          const bool ok = row < L && row >= sp.row_min && key < sp.key_lim && (!sp.causal || key <= row);
-          pv[r] = ok ? __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2s[qi])) : 0.f;
-          dsv[r] = pv[r] * (dpt[r] - dls[qi]);
-        }
-        const typename M::frag p0 = to_frag<T>(pv), p1 = to_frag<T>(pv + 8);
-        const typename M::frag s0 = to_frag<T>(dsv), s1 = to_frag<T>(dsv + 8);
+      for (int r = 0; r < 16; ++r) {
+        const int qi = acc_pos(r, h);
+        const int row = r0 + qi;
+        const bool ok = row < L && row >= sp.row_min && key < sp.key_lim && (!sp.causal || key <= row);
+        pv[r] = ok ? __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2s[qi])) : 0.f;
+        dsv[r] = pv[r] * (dpt[r] - dls[qi]);
+      }
+      const typename M::frag p0 = to_frag<T>(pv), p1 = to_frag<T>(pv + 8);
+      const typename M::frag s0 = to_frag<T>(dsv), s1 = to_frag<T>(dsv + 8);
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          dv[dt] = M::mma(lds_frag_tr<T, RS>(dot, 0, 32 * dt), p0, dv[dt]);
-          dv[dt] = M::mma(lds_frag_tr<T, RS>(dot, 16, 32 * dt), p1, dv[dt]);
-          dk[dt] = M::mma(lds_frag_tr<T, RS>(qt, 0, 32 * dt), s0, dk[dt]);
-          dk[dt] = M::mma(lds_frag_tr<T, RS>(qt, 16, 32 * dt), s1, dk[dt]);
-        }
+      for (int dt = 0; dt < NDT; ++dt) {
+        dv[dt] = M::mma(lds_frag_tr<T, RS>(dot, 0, 32 * dt), p0, dv[dt]);
+        dv[dt] = M::mma(lds_frag_tr<T, RS>(dot, 16, 32 * dt), p1, dv[dt]);
+        dk[dt] = M::mma(lds_frag_tr<T, RS>(qt, 0, 32 * dt), s0, dk[dt]);
+        dk[dt] = M::mma(lds_frag_tr<T, RS>(qt, 16, 32 * dt), s1, dk[dt]);
       }
     }
   }
