@@ -424,11 +424,12 @@ def _single_line(args, block: dict, dtype: str, peak: float, config: dict) -> di
     return line
 
 
-def c3_block(rank: int, steps: int, warmup: int) -> dict:
+def c3_block(rank: int, steps: int, warmup: int, paged: bool = False) -> dict:
     """The e4m3 sweep at the bf16 shape (N = 131072, cp_size = 8, H_q = 32, H_kv = 8, D = 128):
     OCP e4m3 q/k/v, q scale amax/448 of the local shard, k / v scales per source shard
     (quantised by the library's producer), bf16 out; fused (the sweep kernel clocked) and per
-    step (attention per launch, clocked in a second pass)."""
+    step (attention per launch, clocked in a second pass).  `paged`: also the fused sweep
+    over paged caches of the same K/V (256-row pages), K read through the page tables."""
     from fa4_ring import RingConfig, ring_flash_attn
 
     flops = sweep_flops(N // CP, CP, HQ, D)
@@ -445,7 +446,26 @@ def c3_block(rank: int, steps: int, warmup: int) -> dict:
     clock8p = KernelClock()
     timed_sweeps(per_step8, max(3, steps // 2), 1, clock8p)
     a8 = clock8p.mean_ms("attn")
-    return {"workload": "same shape, OCP e4m3 q/k/v, per-source-rank k/v descales, bf16 out",
+    extra = {}
+    if paged:
+        import torch
+
+        from fa4_ring import PagedKVRing
+        pring = PagedKVRing.from_shards(ring8.k, ring8.v, 256, spare_pages=8,
+                                        generator=torch.Generator().manual_seed(rank))
+        clockpg = KernelClock()
+        secpg = timed_sweeps(lambda: ring_flash_attn(q8, None, None, cfg8, group=pring, descales=desc),
+                             max(3, steps // 2), 2, clockpg)
+        spg = clockpg.mean_ms("sweep_kernel")
+        extra["paged"] = {"workload": "the fused sweep over paged caches (256-row pages, random order), K read in "
+                                      "place through the page tables",
+                          "ms_per_step": round(secpg * 1e3, 3), "TFLOP/s": round(flops / secpg / 1e12, 2),
+                          "sweep_kernel": {"kernel": "attn_fwd_e4m3_sweep<128,4,paged K>",
+                                           "avg_launch_ms": round(spg, 4),
+                                           "TFLOP/s": round(flops / (spg * 1e-3) / 1e12, 2),
+                                           "frac": round(flops / (spg * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)}}
+        del pring
+    return {**extra, "workload": "same shape, OCP e4m3 q/k/v, per-source-rank k/v descales, bf16 out",
             "ms_per_step": round(sec8 * 1e3, 3), "TFLOP/s": round(flops / sec8 / 1e12, 2),
             "frac_of_fp8_peak": round(flops / sec8 / 1e12 / PEAK_FP8_TFLOPS, 4),
             "sweep_kernel": {"kernel": "attn_fwd_e4m3_sweep<128,4>", "avg_launch_ms": round(s8, 4),
@@ -784,29 +804,31 @@ def main():
                                   "merge_states_GBs": round(bb / (ms_ms * 1e-3) / 1e9, 1)}
         del lq7
         # fp8 sweep: fused (default) and per step
-        result["fp8"] = c3_block(rank, args.steps, args.warmup)
+        result["fp8"] = c3_block(rank, args.steps, args.warmup, paged=True)
         # rank 7 (only front-half steps) in e4m3, its own inputs and descales
         b7 = c3_block(7, max(3, args.steps // 2), 2)
         result["fp8"]["rank7"] = {k: b7[k] for k in ("ms_per_step", "TFLOP/s", "frac_of_fp8_peak", "sweep_kernel")}
         result["fp8"]["cpu_baseline"] = ("the oracle computes e4m3 inputs dequantised in fp32: the same CPU work "
                                          "per FLOP as the bf16 sweep's cpu_baseline below")
-        # paged K/V caches (pages of 256 rows in a random order): page gather + paged V^T + sweep
+        # paged K/V caches (pages of 256 rows in a random order): paged V^T, then the sweep
+        # kernel reading K through the page tables
         from fa4_ring import PagedKVRing
-        from fa4_ring.paged import gather_kv_pages, transpose_v_paged_many
+        from fa4_ring.paged import transpose_v_paged_many
         paged = PagedKVRing.from_shards(ring.k, ring.v, 256, spare_pages=8,
                                         generator=torch.Generator().manual_seed(rank))
-        secpg = timed_sweeps(lambda: ring_flash_attn(lq, None, None, cfg, group=paged), args.steps, 2)
-
-        g_ms = _event_ms(lambda: gather_kv_pages(paged, "k", t_local))
+        clockpg = KernelClock()
+        secpg = timed_sweeps(lambda: ring_flash_attn(lq, None, None, cfg, group=paged), args.steps, 2, clockpg)
+        pk_ms = clockpg.mean_ms("sweep_kernel")
         pt_ms = _event_ms(lambda: transpose_v_paged_many(paged, t_local))
-        pbytes = CP * 2.0 * t_local * HKV * D * 2  # every source's K (or V): read once, written once
+        pbytes = CP * 2.0 * t_local * HKV * D * 2  # every source's V: read once, written once (as V^T)
         result["paged_bf16"] = {
             "workload": "same sweep with every source's K/V in a paged cache (256-row pages, random "
-                        "page order): one K page gather, one paged V^T launch, the same sweep kernel",
+                        "page order): one paged V^T launch, then the sweep kernel reading K in place "
+                        "through the page tables (no K copy)",
             "ms_per_step": round(secpg * 1e3, 3), "TFLOP/s": round(flops / secpg / 1e12, 2),
-            "gather_kv_pages": {"kernel": "gather_pages_kernel (8 caches per launch)", "avg_launch_ms": round(g_ms, 4),
-                                "bytes": round(pbytes), "achieved_GBs": round(pbytes / (g_ms * 1e-3) / 1e9, 1),
-                                "frac": round(pbytes / (g_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+            "sweep_kernel": {"kernel": "attn_fwd_16bit_sweep<bf16,128,4,paged K>", "avg_launch_ms": round(pk_ms, 4),
+                             "TFLOP/s": round(flops / (pk_ms * 1e-3) / 1e12, 2),
+                             "frac": round(flops / (pk_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
             "transpose_v_paged": {"kernel": "transpose_v_kernel<u16,128>, paged (8 caches per launch)",
                                   "avg_launch_ms": round(pt_ms, 4), "bytes": round(pbytes),
                                   "achieved_GBs": round(pbytes / (pt_ms * 1e-3) / 1e9, 1),

@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libfa4cp.so"
 # FA4CP_LIB selects another build of the library (the in-tree one by default)
 LIB_PATH = os.environ.get("FA4CP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # element types (FA4CP_*)
 BF16, FP16, E4M3, FP32 = 0, 1, 2, 3
@@ -147,6 +147,17 @@ class SweepArgs(ctypes.Structure):
     ]
 
 
+class SweepKPages(ctypes.Structure):
+    """Mirror of fa4cp_sweep_kpages."""
+
+    _fields_ = [
+        ("page_table", ctypes.c_void_p * MAX_CP),
+        ("pt_stride", ctypes.c_int64),
+        ("page_size", ctypes.c_int32),
+        ("num_pages", ctypes.c_int32),
+    ]
+
+
 class SweepBwdArgs(ctypes.Structure):
     """Mirror of fa4cp_sweep_bwd_args."""
 
@@ -258,6 +269,8 @@ SIGNATURES = {
          ctypes.c_int32, ctypes.c_void_p],
     ),
     "fa4cp_ring_sweep_fwd": (ctypes.c_int, [ctypes.POINTER(SweepArgs), ctypes.c_void_p]),
+    "fa4cp_ring_sweep_fwd_paged": (
+        ctypes.c_int, [ctypes.POINTER(SweepArgs), ctypes.POINTER(SweepKPages), ctypes.c_void_p]),
     "fa4cp_ring_sweep_bwd": (ctypes.c_int, [ctypes.POINTER(SweepBwdArgs), ctypes.c_void_p]),
     "fa4cp_quantize_e4m3": (ctypes.c_int, [ctypes.POINTER(QuantArgs), ctypes.c_void_p]),
     "fa4cp_quantize_e4m3_noalloc": (ctypes.c_int, [ctypes.POINTER(QuantArgs), ctypes.c_void_p]),

@@ -6,12 +6,13 @@ The reference keeps every rotated K/V shard contiguous and lists paged KV as not
 entry ``[j, k]`` names the page holding rows ``[k * page_size, (k + 1) * page_size)`` of local
 sequence ``j`` (the zig-zag local layout of ``cu_seqlens``).  ``page_size`` is a multiple of 128.
 
-The sweep kernel itself stays the contiguous one.  Before it, one launch gathers each source's
-K pages into contiguous rows, and one writes each source's V^T straight from its V pages.
-Both are HBM-bound copies: about 0.5 GB for the 131072-token, cp=8, 8-kv-head, D=128 bf16
-sweep, under 1 % of its compute time.  Table entries that name no page of the cache read as
-zero rows, and V^T positions past a sequence's end are zeros, so unused cache rows (stale or
-NaN) never reach the attention.
+The fused sweep reads K in place: its K loads walk the page tables (one table entry per
+page, fa4cp_ring_sweep_fwd_paged), so no contiguous K copy is made.  V is read once anyway
+to write the V^T layout the sweep loads, and that launch reads it from the V pages.  Table
+entries that name no page of the cache read as zero rows, and rows past a sequence's end
+are never read, so unused cache rows (stale or NaN) never reach the attention.  The per-step
+form (``fused=False``, and the shapes the fused sweep does not take) gathers the K and V
+pages into contiguous shards first (``gather_kv_pages``).
 """
 
 from __future__ import annotations

@@ -287,16 +287,18 @@ def ring_sweep(local_q: torch.Tensor, local_k: torch.Tensor, local_v: torch.Tens
         assert k.stride(2) == 1 and v.stride(2) == 1, "K and V shards must be contiguous in D"
     assert all(v.stride() == vs[0].stride() for v in vs), "all V shards must share strides"
     vts, stride = transpose_v_many(vs, cu_seqlens_k=cu_seqlens, max_seqlen_k=max_seqlen)
-    return _sweep_launch(local_q, ks, vts, stride, cfg, cu_seqlens, max_seqlen, out, lse, descales)
+    return _sweep_launch(local_q, [k.data_ptr() for k in ks], (ks[0].stride(0), ks[0].stride(1)), h_kv, vts,
+                         stride, cfg, cu_seqlens, max_seqlen, out, lse, descales)
 
 
 def ring_sweep_paged(local_q: torch.Tensor, cfg: RingConfig, ring: "PagedKVRing",
                      cu_seqlens: Optional[torch.Tensor] = None, max_seqlen: Optional[int] = None,
                      out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
                      descales: Optional[Descales] = None) -> torch.Tensor:
-    """ring_sweep over paged K/V caches: one launch gathers every source's K pages into
-    contiguous rows, one writes every source's V^T from its V pages, then the same sweep
-    kernel runs.  The result is bit-identical to ring_sweep on the contiguous shards."""
+    """ring_sweep over paged K/V caches: one launch writes every source's V^T from its V
+    pages, then the sweep kernel reads K straight from the caches through the page tables
+    (fa4cp_ring_sweep_fwd_paged: one table entry per page, no contiguous K copy).  The result
+    is bit-identical to ring_sweep on the contiguous shards."""
     _lib.load()  # fails here, before any allocation, without the library
     total, _, d = local_q.shape
     assert local_q.is_cuda and local_q.stride(2) == 1, "local_q must be a device tensor, contiguous in D"
@@ -305,20 +307,27 @@ def ring_sweep_paged(local_q: torch.Tensor, cfg: RingConfig, ring: "PagedKVRing"
         "caches must match local_q's dtype, head dim and device"
     nseq = 1 if cu_seqlens is None else cu_seqlens.shape[0] - 1
     assert ring.page_tables[0].shape[0] == nseq, "page tables need one row per local sequence"
-    ks = gather_kv_pages(ring, "k", total, cu_seqlens, max_seqlen)
     vts, stride = transpose_v_paged_many(ring, total, cu_seqlens, max_seqlen)
-    return _sweep_launch(local_q, ks, vts, stride, cfg, cu_seqlens, max_seqlen, out, lse, descales)
+    kp = _lib.SweepKPages()
+    for i, pt in enumerate(ring.page_tables):
+        kp.page_table[i] = pt.data_ptr()
+    kp.pt_stride = ring.page_tables[0].shape[1]
+    kp.page_size = ring.page_size
+    kp.num_pages = kc.shape[0]
+    # a cache is [num_pages, page_size, H_kv, D]: rows at stride(1), heads at stride(2)
+    return _sweep_launch(local_q, [k.data_ptr() for k in ring.k], (kc.stride(1), kc.stride(2)), kc.shape[2],
+                         vts, stride, cfg, cu_seqlens, max_seqlen, out, lse, descales, kpages=kp)
 
 
-def _sweep_launch(local_q: torch.Tensor, ks: List[torch.Tensor], vts: List[torch.Tensor], stride: int,
-                  cfg: RingConfig, cu_seqlens: Optional[torch.Tensor], max_seqlen: Optional[int],
-                  out: Optional[torch.Tensor], lse: Optional[torch.Tensor],
-                  descales: Optional[Descales]) -> torch.Tensor:
-    """Queues fa4cp_ring_sweep_fwd over K shards `ks` and V^T buffers `vts` (row stride
-    `stride`) of every source rank."""
+def _sweep_launch(local_q: torch.Tensor, k_ptrs: List[int], k_strides: Tuple[int, int], h_kv: int,
+                  vts: List[torch.Tensor], stride: int, cfg: RingConfig, cu_seqlens: Optional[torch.Tensor],
+                  max_seqlen: Optional[int], out: Optional[torch.Tensor], lse: Optional[torch.Tensor],
+                  descales: Optional[Descales], kpages: Optional["_lib.SweepKPages"] = None) -> torch.Tensor:
+    """Queues fa4cp_ring_sweep_fwd over every source rank's K (device addresses `k_ptrs`, row
+    and head strides `k_strides`) and V^T buffers `vts` (row stride `stride`); with `kpages`,
+    fa4cp_ring_sweep_fwd_paged, the K addresses being the sources' paged caches."""
     S, rank = cfg.cp_size, cfg.cp_rank
     total, h_q, d = local_q.shape
-    h_kv = ks[0].shape[1]
     dev = local_q.device
     nseq = 1 if cu_seqlens is None else cu_seqlens.shape[0] - 1
     e4m3 = local_q.dtype == torch.float8_e4m3fn
@@ -338,8 +347,8 @@ def _sweep_launch(local_q: torch.Tensor, ks: List[torch.Tensor], vts: List[torch
         f"out must be [{total}, {h_q}, {d}] {odt} on {dev}, contiguous in D"
     assert lse.shape == (total, h_q) and lse.dtype == torch.float32 and lse.device == dev and lse.stride(1) == 1, \
         f"lse must be [{total}, {h_q}] float32 on {dev} with unit head stride"
-    for i, (k, vt) in enumerate(zip(ks, vts)):
-        assert k.device == dev and vt.device == dev, f"source {i}'s K / V^T must be on {dev}"
+    for i, vt in enumerate(vts):
+        assert vt.device == dev, f"source {i}'s V^T must be on {dev}"
     if cu_seqlens is not None:
         assert cu_seqlens.dtype == torch.int32 and cu_seqlens.device == dev and cu_seqlens.is_contiguous(), \
             "cu_seqlens must be contiguous int32 on the device"
@@ -350,9 +359,9 @@ def _sweep_launch(local_q: torch.Tensor, ks: List[torch.Tensor], vts: List[torch
     a.o_row_stride, a.o_head_stride = out.stride(0), out.stride(1)
     a.lse_row_stride = lse.stride(0)
     for i in range(S):
-        a.k[i] = ks[i].data_ptr()
+        a.k[i] = k_ptrs[i]
         a.v_t[i] = vts[i].data_ptr()
-    a.k_row_stride, a.k_head_stride = ks[0].stride(0), ks[0].stride(1)
+    a.k_row_stride, a.k_head_stride = k_strides
     a.vt_d_stride = stride
     a.cu = _lib.ptr(cu_seqlens)
     a.nseq = nseq
@@ -363,12 +372,18 @@ def _sweep_launch(local_q: torch.Tensor, ks: List[torch.Tensor], vts: List[torch
     a.cp_rank, a.cp_size = rank, S
     a.softmax_scale = float(cfg.softmax_scale if cfg.softmax_scale is not None else 1.0 / math.sqrt(d))
     a.q_descale, a.k_descale, a.v_descale = _lib.ptr(qd), _lib.ptr(kd), _lib.ptr(vd)
-    launch_sweep(a, dev)
+    launch_sweep(a, dev, kpages)
     return out
 
 
-def launch_sweep(args: "_lib.SweepArgs", device: torch.device) -> None:
-    """Queues the fused sweep kernel on the current stream of `device`."""
+def launch_sweep(args: "_lib.SweepArgs", device: torch.device,
+                 kpages: Optional["_lib.SweepKPages"] = None) -> None:
+    """Queues the fused sweep kernel on the current stream of `device` (with `kpages`: the
+    paged-K sweep)."""
     lib = _lib.load()
-    _lib.check(lib.fa4cp_ring_sweep_fwd(ctypes.byref(args), _lib.stream_handle(device)),
-               "fa4cp_ring_sweep_fwd")
+    if kpages is None:
+        _lib.check(lib.fa4cp_ring_sweep_fwd(ctypes.byref(args), _lib.stream_handle(device)),
+                   "fa4cp_ring_sweep_fwd")
+    else:
+        _lib.check(lib.fa4cp_ring_sweep_fwd_paged(ctypes.byref(args), ctypes.byref(kpages),
+                                                  _lib.stream_handle(device)), "fa4cp_ring_sweep_fwd_paged")

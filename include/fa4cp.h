@@ -36,6 +36,8 @@
  *                                  shards plus their descales, Descales ring_attention.py:43-52)
  *   fa4cp_gather_kv_pages,      <- no counterpart: paged K/V caches in front of the sweep
  *   fa4cp_transpose_v_paged_many   (README.md:139-140 lists paged KV as not supported)
+ *   fa4cp_ring_sweep_fwd_paged  <- ring_attention.py:61-174 as fa4cp_ring_sweep_fwd, K read from
+ *                                  paged caches in place (README.md:139-140: no paged KV)
  */
 #ifndef FA4CP_H_
 #define FA4CP_H_
@@ -46,7 +48,7 @@
 extern "C" {
 #endif
 
-#define FA4CP_ABI_VERSION 5
+#define FA4CP_ABI_VERSION 6
 
 /* status codes */
 #define FA4CP_OK 0
@@ -230,6 +232,26 @@ typedef struct fa4cp_sweep_args {
 } fa4cp_sweep_args;
 
 int fa4cp_ring_sweep_fwd(const fa4cp_sweep_args* args, void* stream);
+
+/*
+ * fa4cp_ring_sweep_fwd with every source rank's K read in place from a paged cache, with no
+ * contiguous copy (the reference keeps K contiguous and has no paged KV, README.md:139-140).
+ * args->k[i] is then source i's cache: num_pages pages of page_size rows, page p starting at
+ * row p * page_size, rows at args->k_row_stride / k_head_stride.  page_table[i][j * pt_stride
+ * + n] (device int32) names the page that holds rows [n * page_size, (n + 1) * page_size) of
+ * local sequence j of cu.  An entry outside [0, num_pages), and rows past a sequence's end,
+ * read as zeros, so unused cache rows never reach the attention.  page_size is a multiple
+ * of 128 (a key tile never straddles two pages).  V^T is given as for fa4cp_ring_sweep_fwd
+ * (fa4cp_transpose_v_paged_many writes it from paged V caches).  The result is bit-identical
+ * to fa4cp_ring_sweep_fwd over the contiguous K the table describes.
+ */
+typedef struct fa4cp_sweep_kpages {
+  const int32_t* page_table[FA4CP_MAX_CP]; /* per source rank: [nseq][pt_stride] */
+  int64_t pt_stride;                        /* entries per row (>= pages of the longest sequence) */
+  int32_t page_size, num_pages;
+} fa4cp_sweep_kpages;
+
+int fa4cp_ring_sweep_fwd_paged(const fa4cp_sweep_args* args, const fa4cp_sweep_kpages* k_pages, void* stream);
 
 /*
  * Backward of fa4cp_ring_sweep_fwd (BF16 / FP16, d = 64 or 128).  No counterpart in the

@@ -26,8 +26,9 @@ def bits(t: torch.Tensor) -> torch.Tensor:
     return t.detach().contiguous().cpu().view(torch.uint8)
 
 
-def host_pages(shards, cu, page_size, spare, seed):
-    """(caches, tables) on the host: sequence j's rows [k P, (k+1) P) go to a random page."""
+def host_pages(shards, cu, page_size, spare, seed, extra_cols=0):
+    """(caches, tables) on the host: sequence j's rows [k P, (k+1) P) go to a random page;
+    `extra_cols` more table columns than the longest sequence needs, holding -1."""
     gen = torch.Generator().manual_seed(seed)
     lens = [cu[j + 1] - cu[j] for j in range(len(cu) - 1)]
     npg = [(n + page_size - 1) // page_size for n in lens]
@@ -35,7 +36,7 @@ def host_pages(shards, cu, page_size, spare, seed):
     caches, tables = [], []
     for x in shards:
         perm = torch.randperm(num_pages, generator=gen)
-        table = torch.full((len(lens), max(1, max(npg))), -1, dtype=torch.int32)
+        table = torch.full((len(lens), max(1, max(npg)) + extra_cols), -1, dtype=torch.int32)
         cache = torch.full((num_pages, page_size) + tuple(x.shape[1:]), NAN).to(x.dtype)
         i = 0
         for j in range(len(lens)):
@@ -211,3 +212,90 @@ def test_paged_per_step_equals_contiguous(dtype, d, cp, mode):
         got, got_lse = ring_flash_attn(lq, None, None, cfg, group=paged, fused=False, return_lse=True)
         assert torch.equal(bits(got), bits(want)), f"rank {rank}"
         assert torch.equal(bits(got_lse), bits(want_lse)), f"rank {rank} lse"
+
+
+WALK_CASES = [  # (dtype, d, cp, rank, page_size, local sequence lengths, extra table columns)
+    (torch.bfloat16, 128, 4, 2, 384, [1536], 0),             # six 64-key tiles per page
+    (torch.bfloat16, 64, 3, 1, 384, [770, 2, 1150], 3),      # ragged packed sequences, wider table
+    (torch.float16, 128, 2, 1, 128, [640, 0, 256], 1),       # two tiles per page, an empty sequence
+    (torch.float8_e4m3fn, 128, 4, 3, 384, [1152, 514], 2),   # three 128-key tiles per page
+    (torch.float8_e4m3fn, 128, 2, 0, 128, [1024], 0),        # one tile per page: every step a new page
+    (torch.float8_e4m3fn, 256, 3, 2, 128, [896], 0),         # two 64-key tiles per page
+]
+
+
+@pytest.mark.parametrize("dtype,d,cp,rank,page_size,lens,extra", WALK_CASES)
+@pytest.mark.parametrize("bad_entries", [False, True])
+def test_in_kernel_page_walk_equals_contiguous(dtype, d, cp, rank, page_size, lens, extra, bad_entries):
+    """The fused sweep reading K through the page tables (fa4cp_ring_sweep_fwd_paged) against
+    the contiguous sweep over the same rows, bit for bit: caches built on the host with pages
+    in a random order and NaN in every unused row.  bad_entries: a few table entries name no
+    page of the cache (negative, or past num_pages); those rows read as zeros, so the
+    reference is the contiguous sweep with the same K and V rows zeroed."""
+    say(f"paged K walk {dtype} d={d} cp={cp} rank={rank} page={page_size} lens={lens} extra={extra} "
+        f"bad={bad_entries}")
+    h, h_kv = 8, 2
+    gen = torch.Generator().manual_seed(31)
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    total = cu[-1]
+    ks = [_rand(total, h_kv, d, dtype, gen) for _ in range(cp)]
+    vs = [_rand(total, h_kv, d, dtype, gen) for _ in range(cp)]
+    q = _rand(total, h, d, dtype, gen)
+    kc, pt = host_pages(ks, cu, page_size, spare=2, seed=3, extra_cols=extra)
+    vc, _ = host_pages(vs, cu, page_size, spare=2, seed=3, extra_cols=extra)  # the same tables
+    if bad_entries:
+        num_pages = kc[0].shape[0]
+        j = max(range(len(lens)), key=lambda i: lens[i])  # the longest sequence
+        npg = (lens[j] + page_size - 1) // page_size
+        for src in range(cp):
+            col = (src + 1) % npg
+            pt[src][j, col] = -7 if src % 2 else num_pages + src
+            r0 = cu[j] + col * page_size
+            r1 = min(r0 + page_size, cu[j + 1])
+            ks[src] = ks[src].clone()
+            vs[src] = vs[src].clone()
+            ks[src][r0:r1] = 0
+            vs[src][r0:r1] = 0
+    paged = PagedKVRing([c.to(DEV) for c in kc], [c.to(DEV) for c in vc], [t.to(DEV) for t in pt])
+    ring = LocalKVRing([x.to(DEV) for x in ks], [x.to(DEV) for x in vs])
+    packed = len(lens) > 1
+    cu_dev = torch.tensor(cu, dtype=torch.int32, device=DEV) if packed else None
+    mx = max(lens) if packed else None
+    desc = None
+    if dtype == torch.float8_e4m3fn:
+        desc = Descales(q=torch.tensor(0.8, device=DEV),
+                        k=[torch.full((h_kv,), 0.4 + 0.1 * r, device=DEV) for r in range(cp)],
+                        v=[torch.full((h_kv,), 1.3 - 0.1 * r, device=DEV) for r in range(cp)])
+    cfg = RingConfig(cp_size=cp, cp_rank=rank)
+    qd = q.to(DEV)
+    want, want_lse = ring_flash_attn(qd, ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc,
+                                     cu_seqlens=cu_dev, max_seqlen=mx, fused=True, return_lse=True)
+    got, got_lse = ring_flash_attn(qd, None, None, cfg, group=paged, descales=desc, cu_seqlens=cu_dev,
+                                   max_seqlen=mx, fused=True, return_lse=True)
+    assert torch.isfinite(want.float()).all()
+    assert torch.equal(bits(got), bits(want))
+    assert torch.equal(bits(got_lse), bits(want_lse))
+
+
+def test_paged_sweep_full_size_e4m3_rank3():
+    """N=131072, cp=8, H 32/8, D=128 in OCP e4m3 with per-source descales, rank 3, pages of
+    256 rows in a random order: the in-kernel page walk is bit-identical to the contiguous
+    sweep."""
+    say("paged sweep e4m3 N=131072 cp=8 rank 3 page 256")
+    n, cp, rank, d = 131072, 8, 3, 128
+    gen = torch.Generator(device=DEV).manual_seed(6)
+    e4 = torch.float8_e4m3fn
+    q = (torch.randn(n // cp, 32, d, generator=gen, device=DEV) * 2).to(e4)
+    ks = [(torch.randn(n // cp, 8, d, generator=gen, device=DEV) * 2).to(e4) for _ in range(cp)]
+    vs = [(torch.randn(n // cp, 8, d, generator=gen, device=DEV) * 2).to(e4) for _ in range(cp)]
+    desc = Descales(q=torch.tensor(0.02, device=DEV), k=[torch.tensor(0.01 + 0.002 * r, device=DEV) for r in range(cp)],
+                    v=[torch.tensor(0.03 - 0.001 * r, device=DEV) for r in range(cp)])
+    ring = LocalKVRing(ks, vs)
+    paged = PagedKVRing.from_shards(ks, vs, 256, spare_pages=5, generator=torch.Generator().manual_seed(4))
+    cfg = RingConfig(cp_size=cp, cp_rank=rank)
+    want, want_lse = ring_flash_attn(q, ks[rank], vs[rank], cfg, group=ring, descales=desc, return_lse=True)
+    got, got_lse = ring_flash_attn(q, None, None, cfg, group=paged, descales=desc, return_lse=True)
+    assert torch.equal(bits(got), bits(want))
+    assert torch.equal(bits(got_lse), bits(want_lse))

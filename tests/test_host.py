@@ -178,13 +178,41 @@ def test_sweep_entry_point_validates_before_launching():
     a.k[1] = 0
     assert lib.fa4cp_ring_sweep_fwd(ctypes.byref(a), None) != 0 and b"source 1" in lib.fa4cp_last_error()
 
+    # the paged-K form: the same checks, plus its page geometry and tables
+    def kpages(**kw):
+        kp = _lib.SweepKPages()
+        kp.pt_stride, kp.page_size, kp.num_pages = 2, 128, 4
+        for i in range(2):
+            kp.page_table[i] = fake
+        for key, val in kw.items():
+            setattr(kp, key, val)
+        return kp
+
+    assert lib.fa4cp_ring_sweep_fwd_paged(ctypes.byref(args()), None, None) != 0
+    assert b"null k_pages" in lib.fa4cp_last_error()
+    for kw, msg in [(dict(page_size=96), b"page_size"), (dict(page_size=0), b"page_size"),
+                    (dict(num_pages=-1), b"num_pages"), (dict(pt_stride=1), b"pt_stride"),
+                    (dict(pt_stride=1 << 31), b"pt_stride")]:
+        rc = lib.fa4cp_ring_sweep_fwd_paged(ctypes.byref(args()), ctypes.byref(kpages(**kw)), None)
+        assert rc != 0 and msg in lib.fa4cp_last_error(), (kw, lib.fa4cp_last_error())
+    kp = kpages()
+    kp.page_table[1] = 0
+    rc = lib.fa4cp_ring_sweep_fwd_paged(ctypes.byref(args()), ctypes.byref(kp), None)
+    assert rc != 0 and b"page table of source 1" in lib.fa4cp_last_error()
+    rc = lib.fa4cp_ring_sweep_fwd_paged(ctypes.byref(args(cp_rank=3)), ctypes.byref(kpages()), None)
+    assert rc != 0 and b"out of range" in lib.fa4cp_last_error()
+    kp = kpages()
+    kp.page_table[0] = kp.page_table[1] = 0
+    assert lib.fa4cp_ring_sweep_fwd_paged(ctypes.byref(args(total=0)), ctypes.byref(kp), None) == 0
+
 
 @pytest.mark.parametrize("struct,cname", [(_lib.AttnArgs, "fa4cp_attn_args"),
                                            (_lib.TransposeArgs, "fa4cp_transpose_args"),
                                            (_lib.SweepArgs, "fa4cp_sweep_args"),
                                            (_lib.SweepBwdArgs, "fa4cp_sweep_bwd_args"),
                                            (_lib.QuantArgs, "fa4cp_quant_args"),
-                                           (_lib.PagedArgs, "fa4cp_paged_args")])
+                                           (_lib.PagedArgs, "fa4cp_paged_args"),
+                                           (_lib.SweepKPages, "fa4cp_sweep_kpages")])
 def test_args_layout_matches_c_header(struct, cname):
     fields = [f for f, _ in struct._fields_]
     prog = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",
