@@ -1165,12 +1165,11 @@ __device__ __forceinline__ void vt_pipeline(const Geo& geo, const T* q, int64_t 
   __syncthreads();
   if (grp == 1) __syncthreads();  // group 1 runs one phase behind group 0
 
-  // The tile loop.  From here on group 0 loads the K tiles and group 1 the V^T tiles; isk_c
-  // is the group as a type (one copy of the loop per group, neither carrying the other's
-  // cursor: 0.7 % faster) or as a bool (one loop: the paged walk's scalar registers do not
-  // fit two copies).
-  auto run = [&](auto isk_c) __attribute__((always_inline)) {
-    const bool ISK = isk_c;
+  // The tile loop.  From here on group 0 loads the K tiles and group 1 the V^T tiles, in one
+  // loop for both groups.  (A copy per group measured no faster, and with the LDS slot of its
+  // loads known the compiler waits for every LDS-DMA in flight before the first V^T read of
+  // each MFMA phase; the paged walk's scalar registers do not fit two copies either.)
+  auto run = [&](bool ISK) __attribute__((always_inline)) {
     LoadCursor lc = ISK ? kc : vc;
     int pend = -1;  // paged K: the page entry lc's next page event takes
     int ld_voff[NLD / 4];
@@ -1239,9 +1238,7 @@ __device__ __forceinline__ void vt_pipeline(const Geo& geo, const T* q, int64_t 
       __builtin_amdgcn_s_setprio(0);
     }
   };
-  if constexpr (Geo::kPagedK) run(grp == 0);
-  else if (grp == 0) run(std::true_type{});
-  else run(std::false_type{});
+  run(grp == 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (grp == 0) __syncthreads();  // both groups pass the same number of barriers
