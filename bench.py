@@ -631,6 +631,62 @@ def bench_c1(args) -> int:
     return 0
 
 
+def bench_paged(args) -> int:
+    """The fused sweep over paged K/V caches (256-row pages in a random order, 8 spare pages)
+    against the same sweep over contiguous shards, bf16 and e4m3, at the headline shape
+    (N = 131072, cp_size = 8, H_q = 32, H_kv = 8, D = 128, rank ``--rank``).  The two forms
+    alternate in one process; the sweep kernels are clocked with HIP events."""
+    import torch
+
+    from fa4_ring import PagedKVRing, RingConfig, ring_flash_attn
+
+    rank = args.rank
+    flops = sweep_flops(N // CP, CP, HQ, D)
+    cfg = RingConfig(cp_size=CP, cp_rank=rank)
+
+    def kernel_ms(fn):
+        clock = KernelClock()
+        timed_sweeps(fn, args.steps, args.warmup, clock)
+        return clock.mean_ms("sweep_kernel")
+
+    def pair(lq, ring, desc, peak, name):
+        paged = PagedKVRing.from_shards(ring.k, ring.v, 256, spare_pages=8,
+                                        generator=torch.Generator().manual_seed(rank))
+        cont = lambda: ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc)  # noqa: E731
+        pg = lambda: ring_flash_attn(lq, None, None, cfg, group=paged, descales=desc)  # noqa: E731
+        c_ms, p_ms = [], []
+        for _ in range(2):
+            c_ms.append(kernel_ms(cont))
+            p_ms.append(kernel_ms(pg))
+        c, p = sum(c_ms) / 2, sum(p_ms) / 2
+        del paged
+        return {"contiguous": {"kernel": name, "avg_launch_ms": round(c, 4),
+                               "frac": round(flops / (c * 1e-3) / 1e12 / peak, 4)},
+                "paged": {"kernel": name.replace(">", ",paged K>"), "avg_launch_ms": round(p, 4),
+                          "frac": round(flops / (p * 1e-3) / 1e12 / peak, 4)},
+                "paged_over_contiguous": round(p / c - 1, 4)}
+
+    q, lq, ring = make_bf16_inputs(rank)
+    del q
+    bf = pair(lq, ring, None, PEAK_BF16_TFLOPS, "attn_fwd_16bit_sweep<bf16,128,4>")
+    del lq, ring
+    torch.cuda.synchronize()
+    q8, ring8, desc = make_fp8_inputs(rank)
+    e8 = pair(q8, ring8, desc, PEAK_FP8_TFLOPS, "attn_fwd_e4m3_sweep<128,4>")
+    sec = bf["paged"]["avg_launch_ms"] * 1e-3
+    line = {"metric": METRIC, "value": round(flops / sec / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": bf["paged"]["avg_launch_ms"],
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (q/k/v ~ N(0,1), seeded on the GPU)",
+            "config": {"workload": f"bf16 causal zig-zag ring sweep (N={N}, cp_size={CP}, H_q={HQ}, H_kv={HKV}, "
+                                   f"D={D}, rank {rank}) with every source's K/V in a paged cache (256-row pages, "
+                                   "random order), K read in place; ms_per_step is the sweep kernel alone",
+                       "seq_len": N, "cp_size": CP, "cp_rank": rank},
+            "frac_of_peak": bf["paged"]["frac"], "bf16": bf, "e4m3": e8, "cpu_baseline": None}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -640,12 +696,13 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=16384)
     ap.add_argument("--skip-extra", action="store_true", help="only the headline bf16 sweep")
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "bwd"],
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "bwd", "paged"],
                     help="c2 (default): the bf16 N=131072 sweep with its extras; c1: the reference's "
                          "CPU case (N=2048, cp_size 4) on every rank, with the oracle's CPU time; c3: "
                          "the e4m3 sweep at the c2 shape (ranks 3 and 7); c4: "
                          "packed bf16 sequences (8 lengths, cp_size 4); c5: the e4m3 N=262144, H_q=16, "
-                         "H_kv=2, D=256 sweep")
+                         "H_kv=2, D=256 sweep; paged: the c2 and c3 sweeps over paged K/V caches against "
+                         "contiguous shards")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: measures one GPU only (one rank's sweep with every source "
@@ -661,6 +718,8 @@ def main():
         return bench_c4(args)
     if args.workload == "c1":
         return bench_c1(args)
+    if args.workload == "paged":
+        return bench_paged(args)
 
     import torch
 
