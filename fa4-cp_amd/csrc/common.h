@@ -175,16 +175,29 @@ constexpr int kVtPad = 128;
 
 // First V^T position of sequence j: the padded lengths of the sequences before it (ranges
 // clamped as seq_bounds, so the positions stay inside fa4cp_vt_min_d_stride(total, nseq)).
+// The wavefront's lanes take one sequence each and sum with a butterfly, so a kernel's
+// prologue makes one round trip to cu per 64 earlier sequences instead of a chain of
+// dependent scalar loads, one per sequence.  Every lane of the wavefront must be active; the
+// result is wave-uniform.
 __device__ __forceinline__ int64_t vt_seq_start(const int32_t* cu, int j, int total, int sel) {
+  const int lane = (int)(threadIdx.x & 63);
   int64_t p = 0;
-  for (int i = 0; i < j; ++i) {
-    int s, e;
-    seq_bounds(cu, i, total, s, e);
-    const int mid = (s + e) >> 1;
-    const int len = sel == FA4CP_SEL_FRONT_HALF ? mid - s : sel == FA4CP_SEL_BACK_HALF ? e - mid : e - s;
-    p += (len + kVtPad - 1) / kVtPad * kVtPad;
+  for (int b = 0; b < j; b += 64) {
+    const int i = b + lane;
+    if (i < j) {
+      int s, e;
+      seq_bounds(cu, i, total, s, e);
+      const int mid = (s + e) >> 1;
+      const int len = sel == FA4CP_SEL_FRONT_HALF ? mid - s : sel == FA4CP_SEL_BACK_HALF ? e - mid : e - s;
+      p += (len + kVtPad - 1) / kVtPad * kVtPad;
+    }
   }
-  return p;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) p += __shfl_xor(p, m);
+  const uint64_t u = (uint64_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
 // Index of the packed sequence that contains `row`: the largest j with cu[j] <= row

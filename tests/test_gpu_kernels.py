@@ -297,6 +297,42 @@ def test_transpose_v_layout_bit_exact(dtype, d, cu, sel):
         pos += pad
 
 
+def _many_seq_cu(nseq, seed):
+    """cu of nseq packed sequences with even lengths in [0, 300], some empty, some 2 rows."""
+    g = torch.Generator().manual_seed(seed)
+    lens = (torch.randint(0, 151, (nseq,), generator=g) * 2).tolist()
+    lens[3] = 0
+    lens[70 % nseq] = 2
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    return cu
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float8_e4m3fn, 128)])
+@pytest.mark.parametrize("sel", [SEL_ALL, SEL_FRONT_HALF, SEL_BACK_HALF])
+def test_transpose_v_layout_many_sequences(dtype, d, sel):
+    """150 packed sequences: the V^T start of sequence j sums more than 64 earlier padded
+    lengths (the kernels sum them 64 at a time across a wavefront)."""
+    from fa4_ring.fa4_backend import transpose_v
+    cu = _many_seq_cu(150, 9)
+    say(f"transpose_v {dtype} d={d} 150 sequences sel={sel}")
+    total, hkv = cu[-1], 2
+    v = torch.randn(total, hkv, d, generator=torch.Generator().manual_seed(6)).to(dtype)
+    cud = torch.tensor(cu, dtype=torch.int32, device=DEV)
+    mx = max(b - a for a, b in zip(cu[:-1], cu[1:]))
+    vt, stride = transpose_v(v.to(DEV), cu_seqlens_k=cud, max_seqlen_k=mx, k_sel=sel)
+    got = vt.cpu().view(torch.uint8 if dtype == torch.float8_e4m3fn else torch.int16).reshape(hkv, d, stride)
+    raw = v.view(torch.uint8 if dtype == torch.float8_e4m3fn else torch.int16)
+    pos = 0
+    for (s0, e0) in seq_bounds(cu, total, sel):
+        n = e0 - s0
+        pad = (n + 127) // 128 * 128
+        assert torch.equal(got[:, :, pos:pos + n], raw[s0:e0].permute(1, 2, 0))
+        assert (got[:, :, pos + n:pos + pad] == 0).all()
+        pos += pad
+
+
 @pytest.mark.parametrize("dtype,d,count", [(torch.bfloat16, 128, 8), (torch.float8_e4m3fn, 256, 3),
                                            (torch.float16, 64, 16), (torch.bfloat16, 128, 1)])
 @pytest.mark.parametrize("cu", [None, [0, 200, 200, 713]])

@@ -187,6 +187,38 @@ def test_ring_varlen_all_ranks(mode):
         assert max_err(seq, O.dense_causal(q[s:e], k[s:e], v[s:e], scale)) <= TOL_BF16_OUT
 
 
+@pytest.mark.parametrize("mode", ["fused", "incremental"])
+def test_ring_varlen_many_sequences(mode):
+    """80 packed sequences (some empty, some of 4 rows): every kernel finds a sequence's V^T
+    start by summing the padded lengths of up to 79 earlier ones, 64 per wavefront pass."""
+    cp, h, hkv, d = 2, 4, 2, 64
+    g = torch.Generator().manual_seed(12)
+    lens = (torch.randint(0, 33, (80,), generator=g) * 4).tolist()
+    lens[5] = 0
+    lens[66] = 4
+    say(f"ring varlen {len(lens)} sequences cp={cp} path={mode}")
+    full_cu = [0]
+    for n in lens:
+        full_cu.append(full_cu[-1] + n)
+    q, k, v = O.random_qkv(full_cu[-1], h, hkv, d, seed=4)
+    q, k, v = (rounded(t, torch.bfloat16) for t in (q, k, v))
+    scale = scale_for(d)
+    qd, kd, vd = (t.to(torch.bfloat16).to(DEV) for t in (q, k, v))
+    ring = LocalKVRing.from_full(kd, vd, cp, full_cu)
+    ks = [O.zigzag_shard_varlen(k, full_cu, r, cp)[0] for r in range(cp)]
+    vs = [O.zigzag_shard_varlen(v, full_cu, r, cp)[0] for r in range(cp)]
+    for rank in range(cp):
+        lq, local_cu = zigzag_shard_varlen(qd, full_cu, rank, cp)
+        max_local = int((local_cu[1:] - local_cu[:-1]).max())
+        cfg, fused = _cfg_path(mode, cp, rank)
+        out, lse = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring,
+                                   cu_seqlens=local_cu, max_seqlen=max_local, fused=fused, return_lse=True)
+        oq, ocu = O.zigzag_shard_varlen(q, full_cu, rank, cp)
+        ref, ref_lse = O.ring_rank(oq, ks, vs, rank, cp, scale, cu=ocu, merge_mode=cfg.merge_mode)
+        assert max_err(out, ref) <= TOL_BF16_OUT, f"rank {rank}"
+        assert lse_err(lse, ref_lse) <= TOL_LSE, f"rank {rank} lse"
+
+
 def _fp8_ring_inputs(q, k, v, cp, rank, full_cu=None):
     """Per-tensor q scale (local shard amax / 448), per-source-rank k / v scales."""
     if full_cu is None:
