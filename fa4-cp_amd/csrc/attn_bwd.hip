@@ -190,6 +190,38 @@ struct TileFetch {
   }
 };
 
+// The same tile through a buffer resource that starts at the tile's first row and ends at the
+// sequence's last: rows past the end read as zeros in hardware, and a lane keeps one 32-bit
+// offset per chunk (fixed for the kernel) instead of a 64-bit address and a row test.  The
+// offsets go in the vector offset, which the resource's range check covers.
+template <typename T, int D, int NT>
+struct TileFetchBuf {
+  static constexpr int CPR = D / 8;
+  static constexpr int N = kBwdRows * CPR / NT;
+  static_assert(N * NT == kBwdRows * CPR, "threads must split the tile evenly");
+  u32x4 x[N];
+  int voff[N];
+  __device__ __forceinline__ explicit TileFetchBuf(int rsb) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int c = (int)threadIdx.x + NT * i;
+      voff[i] = (c / CPR) * rsb + 16 * (c % CPR);
+    }
+  }
+  __device__ __forceinline__ void fetch(__amdgpu_buffer_rsrc_t r) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] = bload128(r, voff[i]);
+  }
+  template <int RS>
+  __device__ __forceinline__ void store(T* lds) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int c = (int)threadIdx.x + NT * i, r = c / CPR, ch = c % CPR;
+      *reinterpret_cast<u32x4*>(lds + r * RS + 8 * ch) = x[i];
+    }
+  }
+};
+
 // dQ: one workgroup per 32 query rows x HP query heads of one kv head (one wavefront per
 // head), walking every ring step's keys in tiles of 32 (the forward sweep's schedule).  The
 // tiles go through LDS; the next tile's loads are in flight while the current one is used.
@@ -317,11 +349,12 @@ __global__ __launch_bounds__(64 * HP) void bwd_dq_kernel(BwdParams p) {
 }
 
 // dK / dV: one workgroup per 128 keys of one source rank's sequence and kv head (32 keys per
-// wavefront, K and V of those keys held in registers as operands), walking the query rows
-// that attend them for every query head of the kv head; the next 32-row block of Q / dO is
-// in flight while the current one is used.
+// wavefront, K of those keys held in registers and V in the wavefront's LDS rows as
+// operands), walking the query rows that attend them for every query head of the kv head;
+// the next 32-row block of Q / dO is in flight while the current one is used.  At most 256
+// registers, so two workgroups share each SIMD and hide each other's barrier and memory waits.
 template <typename T, int D>
-__global__ __launch_bounds__(64 * kDkdvWaves) void bwd_dkdv_kernel(BwdParams p) {
+__global__ __launch_bounds__(64 * kDkdvWaves, 2) void bwd_dkdv_kernel(BwdParams p) {
   using M = BwdMfma<T>;
   constexpr int RS = D + 8;
   constexpr int NKS = D / 16;
@@ -330,6 +363,9 @@ __global__ __launch_bounds__(64 * kDkdvWaves) void bwd_dkdv_kernel(BwdParams p) 
   __shared__ __align__(16) T qt[kBwdRows * RS];
   __shared__ __align__(16) T dot[kBwdRows * RS];
   __shared__ float lse2s[kBwdRows], dls[kBwdRows];
+  // V of each wavefront's 32 keys (written and read by that wavefront only): the B operands of
+  // dP come from here, which keeps the registers of two workgroups on a SIMD
+  __shared__ __align__(16) T vsm[kDkdvWaves * kBwdRows * RS];
 
   int b = blockIdx.x;
   const int kt = b % p.n_tiles;
@@ -352,7 +388,8 @@ __global__ __launch_bounds__(64 * kDkdvWaves) void bwd_dkdv_kernel(BwdParams p) 
 
   if (kb0 < sp.key_lim) {
     // K and V of the lane's key: B operands of S = Q K^T and dP = dO V^T
-    typename M::frag kf[NKS], vf[NKS];
+    typename M::frag kf[NKS];
+    T* const vw = vsm + w * kBwdRows * RS;  // this wavefront's V rows, one per key
     {
       const bool ok = key < sp.key_lim;
       const T* kr = reinterpret_cast<const T*>(p.k[src]) + (int64_t)(qs + key) * p.k_rs + (int64_t)kvh * p.k_hs;
@@ -361,7 +398,8 @@ __global__ __launch_bounds__(64 * kDkdvWaves) void bwd_dkdv_kernel(BwdParams p) 
       for (int t = 0; t < NKS; ++t) {
         typename M::frag z = {};
         kf[t] = ok ? *reinterpret_cast<const typename M::frag*>(kr + 8 * h + 16 * t) : z;
-        vf[t] = ok ? *reinterpret_cast<const typename M::frag*>(vr + 8 * h + 16 * t) : z;
+        *reinterpret_cast<typename M::frag*>(vw + lk * RS + 8 * h + 16 * t) =
+            ok ? *reinterpret_cast<const typename M::frag*>(vr + 8 * h + 16 * t) : z;
       }
     }
     const float c = p.scale * kLog2e;
@@ -375,12 +413,13 @@ __global__ __launch_bounds__(64 * kDkdvWaves) void bwd_dkdv_kernel(BwdParams p) 
                  : reinterpret_cast<const T*>(p.dout) + (int64_t)qs * p.do_rs + (int64_t)hq * p.do_hs;
     };
     auto row0_of = [&](int bi) { return row_begin + (bi % n_rb) * kBwdRows; };
-    TileFetch<T, D, NT> fq, fd;
+    const int q_rsb = (int)(p.q_rs * (int64_t)sizeof(T)), do_rsb = (int)(p.do_rs * (int64_t)sizeof(T));
+    TileFetchBuf<T, D, NT> fq(q_rsb), fd(do_rsb);
     float flse = 0.f, fdl = 0.f;
     auto fetch = [&](int bi) {
       const int r0 = row0_of(bi), hq = kvh * p.group + bi / n_rb;
-      fq.fetch(qbase(bi, true), p.q_rs, r0, L);
-      fd.fetch(qbase(bi, false), p.do_rs, r0, L);
+      fq.fetch(make_rsrc(qbase(bi, true) + (int64_t)r0 * p.q_rs, (int64_t)(L - r0) * q_rsb));
+      fd.fetch(make_rsrc(qbase(bi, false) + (int64_t)r0 * p.do_rs, (int64_t)(L - r0) * do_rsb));
       if (threadIdx.x < kBwdRows) {
         const int row = r0 + threadIdx.x;
         flse = row < L ? p.lse[(int64_t)(qs + row) * p.lse_rs + hq] : 0.f;  // scaled at the store: no wait here
@@ -403,25 +442,29 @@ __global__ __launch_bounds__(64 * kDkdvWaves) void bwd_dkdv_kernel(BwdParams p) 
 #pragma unroll
       for (int t = 0; t < NKS; ++t) st = M::mma(lds_frag<T, RS>(qt, sig(lk), 2 * t + h), kf[t], st);
 #pragma unroll
-      for (int t = 0; t < NKS; ++t) dpt = M::mma(lds_frag<T, RS>(dot, sig(lk), 2 * t + h), vf[t], dpt);
-      // accumulator register r: query row r0 + acc_pos(r, h), key `key`
-      float pv[16], dsv[16];
+      for (int t = 0; t < NKS; ++t)
+        dpt = M::mma(lds_frag<T, RS>(dot, sig(lk), 2 * t + h), lds_frag<T, RS>(vw, lk, 2 * t + h), dpt);
+      // accumulator register r: query row r0 + acc_pos(r, h), key `key`.  Registers 8 kk ..
+      // 8 kk + 7 hold the block's rows 16 kk .. 16 kk + 15 (the k-step kk of dV and dK): one
+      // k-step's P and dS at a time keeps two workgroups' registers on a SIMD
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int qi = acc_pos(r, h);
-        const int row = r0 + qi;
-        const bool ok = row < L && row >= sp.row_min && key < sp.key_lim && (!sp.causal || key <= row);
-        pv[r] = ok ? __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2s[qi])) : 0.f;
-        dsv[r] = pv[r] * (dpt[r] - dls[qi]);
-      }
-      const typename M::frag p0 = to_frag<T>(pv), p1 = to_frag<T>(pv + 8);
-      const typename M::frag s0 = to_frag<T>(dsv), s1 = to_frag<T>(dsv + 8);
+      for (int kk = 0; kk < 2; ++kk) {
+        float pv[8], dsv[8];
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        dv[dt] = M::mma(lds_frag_tr<T, RS>(dot, 0, 32 * dt), p0, dv[dt]);
-        dv[dt] = M::mma(lds_frag_tr<T, RS>(dot, 16, 32 * dt), p1, dv[dt]);
-        dk[dt] = M::mma(lds_frag_tr<T, RS>(qt, 0, 32 * dt), s0, dk[dt]);
-        dk[dt] = M::mma(lds_frag_tr<T, RS>(qt, 16, 32 * dt), s1, dk[dt]);
+        for (int j = 0; j < 8; ++j) {
+          const int r = 8 * kk + j;
+          const int qi = acc_pos(r, h);
+          const int row = r0 + qi;
+          const bool ok = row < L && row >= sp.row_min && key < sp.key_lim && (!sp.causal || key <= row);
+          pv[j] = ok ? __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2s[qi])) : 0.f;
+          dsv[j] = pv[j] * (dpt[r] - dls[qi]);
+        }
+        const typename M::frag pk = to_frag<T>(pv), sk = to_frag<T>(dsv);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          dv[dt] = M::mma(lds_frag_tr<T, RS>(dot, 16 * kk, 32 * dt), pk, dv[dt]);
+          dk[dt] = M::mma(lds_frag_tr<T, RS>(qt, 16 * kk, 32 * dt), sk, dk[dt]);
+        }
       }
     }
   }
