@@ -362,7 +362,8 @@ __global__ __launch_bounds__(64 * kDkdvWaves, 2) void bwd_dkdv_kernel(BwdParams 
   constexpr int NT = 64 * kDkdvWaves;
   __shared__ __align__(16) T qt[kBwdRows * RS];
   __shared__ __align__(16) T dot[kBwdRows * RS];
-  __shared__ float lse2s[kBwdRows], dls[kBwdRows];
+  __shared__ __align__(16) float lse2s[kBwdRows];
+  __shared__ __align__(16) float dls[kBwdRows];
   // V of each wavefront's 32 keys (written and read by that wavefront only): the B operands of
   // dP come from here, which keeps the registers of two workgroups on a SIMD
   __shared__ __align__(16) T vsm[kDkdvWaves * kBwdRows * RS];
@@ -449,15 +450,20 @@ __global__ __launch_bounds__(64 * kDkdvWaves, 2) void bwd_dkdv_kernel(BwdParams 
       // k-step's P and dS at a time keeps two workgroups' registers on a SIMD
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
+        // rows acc_pos(8 kk + j, h) = 16 kk + 8h + j: consecutive, read four at a time
         float pv[8], dsv[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int r = 8 * kk + j;
-          const int qi = acc_pos(r, h);
-          const int row = r0 + qi;
-          const bool ok = row < L && row >= sp.row_min && key < sp.key_lim && (!sp.causal || key <= row);
-          pv[j] = ok ? __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2s[qi])) : 0.f;
-          dsv[j] = pv[j] * (dpt[r] - dls[qi]);
+        for (int q = 0; q < 2; ++q) {
+          const f32x4 lq4 = *reinterpret_cast<const f32x4*>(lse2s + 16 * kk + 8 * h + 4 * q);
+          const f32x4 dq4 = *reinterpret_cast<const f32x4*>(dls + 16 * kk + 8 * h + 4 * q);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int j = 4 * q + e, r = 8 * kk + j;
+            const int row = r0 + 16 * kk + 8 * h + j;
+            const bool ok = row < L && row >= sp.row_min && key < sp.key_lim && (!sp.causal || key <= row);
+            pv[j] = ok ? __builtin_amdgcn_exp2f(fmaf(st[r], c, -lq4[e])) : 0.f;
+            dsv[j] = pv[j] * (dpt[r] - dq4[e]);
+          }
         }
         const typename M::frag pk = to_frag<T>(pv), sk = to_frag<T>(dsv);
 #pragma unroll
