@@ -317,12 +317,20 @@ __global__ __launch_bounds__(64 * HP) void bwd_dq_kernel(BwdParams p) {
 #pragma unroll
     for (int t = 0; t < NKS; ++t) dpt = M::mma(lds_frag<T, RS>(vs, sig(lq), 2 * t + h), df[t], dpt);
     float dsv[16];
+    // no pair of the tile masked (the usual case): no per-element test
+    const bool full = r0 + kBwdRows <= L && r0 >= sp.row_min && ck0 + kBwdRows <= sp.key_lim &&
+                      (!sp.causal || ck0 + kBwdRows - 1 <= r0);
+    if (__builtin_expect(full, 1)) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int kp = ck0 + acc_pos(r, h);
-      const bool ok = row_ok && qpos >= sp.row_min && kp < sp.key_lim && (!sp.causal || kp <= qpos);
-      const float pr = ok ? __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2)) : 0.f;
-      dsv[r] = pr * (dpt[r] - dl);
+      for (int r = 0; r < 16; ++r) dsv[r] = __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2)) * (dpt[r] - dl);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kp = ck0 + acc_pos(r, h);
+        const bool ok = row_ok & (qpos >= sp.row_min) & (kp < sp.key_lim) & (!sp.causal | (kp <= qpos));
+        const float pr = __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2));
+        dsv[r] = (ok ? pr : 0.f) * (dpt[r] - dl);
+      }
     }
     const typename M::frag ds0 = to_frag<T>(dsv), ds1 = to_frag<T>(dsv + 8);
 #pragma unroll
@@ -445,6 +453,10 @@ __global__ __launch_bounds__(64 * kDkdvWaves, 2) void bwd_dkdv_kernel(BwdParams 
 #pragma unroll
       for (int t = 0; t < NKS; ++t)
         dpt = M::mma(lds_frag<T, RS>(dot, sig(lk), 2 * t + h), lds_frag<T, RS>(vw, lk, 2 * t + h), dpt);
+      // no pair of the block masked for this wavefront's keys (the usual case)
+      const int kw0 = kb0 + w * kBwdRows;
+      const bool full = r0 + kBwdRows <= L && r0 >= sp.row_min && kw0 + kBwdRows <= sp.key_lim &&
+                        (!sp.causal || kw0 + kBwdRows - 1 <= r0);
       // accumulator register r: query row r0 + acc_pos(r, h), key `key`.  Registers 8 kk ..
       // 8 kk + 7 hold the block's rows 16 kk .. 16 kk + 15 (the k-step kk of dV and dK): one
       // k-step's P and dS at a time keeps two workgroups' registers on a SIMD
@@ -460,8 +472,13 @@ __global__ __launch_bounds__(64 * kDkdvWaves, 2) void bwd_dkdv_kernel(BwdParams 
           for (int e = 0; e < 4; ++e) {
             const int j = 4 * q + e, r = 8 * kk + j;
             const int row = r0 + 16 * kk + 8 * h + j;
-            const bool ok = row < L && row >= sp.row_min && key < sp.key_lim && (!sp.causal || key <= row);
-            pv[j] = ok ? __builtin_amdgcn_exp2f(fmaf(st[r], c, -lq4[e])) : 0.f;
+            const float pr = __builtin_amdgcn_exp2f(fmaf(st[r], c, -lq4[e]));
+            if (full) {
+              pv[j] = pr;
+            } else {
+              const bool ok = (row < L) & (row >= sp.row_min) & (key < sp.key_lim) & (!sp.causal | (key <= row));
+              pv[j] = ok ? pr : 0.f;
+            }
             dsv[j] = pv[j] * (dpt[r] - dq4[e]);
           }
         }
