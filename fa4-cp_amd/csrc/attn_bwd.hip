@@ -312,10 +312,12 @@ __global__ __launch_bounds__(64 * HP) void bwd_dq_kernel(BwdParams p) {
     }
     lds_written_barrier();
     f32x16 st = {}, dpt = {};
+    // the two chains interleaved: each one's operand reads run under the other's MFMA
 #pragma unroll
-    for (int t = 0; t < NKS; ++t) st = M::mma(lds_frag<T, RS>(ks, sig(lq), 2 * t + h), qf[t], st);
-#pragma unroll
-    for (int t = 0; t < NKS; ++t) dpt = M::mma(lds_frag<T, RS>(vs, sig(lq), 2 * t + h), df[t], dpt);
+    for (int t = 0; t < NKS; ++t) {
+      st = M::mma(lds_frag<T, RS>(ks, sig(lq), 2 * t + h), qf[t], st);
+      dpt = M::mma(lds_frag<T, RS>(vs, sig(lq), 2 * t + h), df[t], dpt);
+    }
     float dsv[16];
     // no pair of the tile masked (the usual case): no per-element test
     const bool full = r0 + kBwdRows <= L && r0 >= sp.row_min && ck0 + kBwdRows <= sp.key_lim &&
