@@ -17,10 +17,12 @@
 // of src's keys.  dK / dV go to one buffer per source rank: this rank's contribution to that
 // source's gradient (a multi-GPU ring sends them back to their owners).
 //
-// Three launches: bwd_delta_kernel (HBM-bound), bwd_dq_kernel (one workgroup per 32 query
-// rows x HP heads of one kv head, walking the same key segments as the forward sweep), and
-// bwd_dkdv_kernel (one workgroup per 128 keys of one source and kv head, walking the query
-// rows that attend them, for every query head of the group).
+// Three launches: bwd_pack_kernel (HBM-bound: delta, and every 32-row block of Q and dO
+// copied into the operand order of the dK / dV products, in rows and transposed), bwd_dq_kernel
+// (one workgroup per 32 query rows x HP heads of one kv head, walking the same key segments as
+// the forward sweep), and bwd_dkdv_kernel (one workgroup per 128 keys of one source and kv
+// head, eight wavefronts in pairs, walking the packed blocks of the query rows that attend
+// them, for every query head of the group).
 //
 // Products run on v_mfma_f32_32x32x16_{bf16,f16}.  Operand layouts (lane l, h = l / 32):
 // A lane l holds row l % 32, k = 8h + 0..7; B lane l holds column l % 32, the same k; the
@@ -29,14 +31,27 @@
 // lane l the entry 16 (r / 8) + 8h + r % 8 along the A side, which is exactly the k slot
 // layout of an A or B operand of the next product: the scores of one product feed the next
 // without leaving the registers.  Transposed operands come from ds_read_b64_tr_b16.
+#include <type_traits>
+
 #include "common.h"
 
 namespace fa4cp {
 namespace {
 
 constexpr int kBwdRows = 32;  // query rows (dq) or keys (dk/dv) per wavefront
-constexpr int kDkdvWaves = 4;
-constexpr int kDkdvKeys = kDkdvWaves * kBwdRows;
+constexpr int kDkdvKeys = 4 * kBwdRows;  // keys per dk/dv workgroup
+
+// A packed block: rows [32 b, 32 b + 32) of one sequence and one query head in four regions of
+// D / 16 MFMA operand fragments of 1 KB (lane l's 16 bytes at 16 l), then 256 bytes of
+// per-row values.  Regions: 0 Q rows, 1 dO transposed, 2 dO rows, 3 Q transposed.  Fragment t
+// of a row region gives lane l the elements 16 t + 8 (l / 32) + 0..7 of row sig(l % 32);
+// fragment 2 dt + kk of a transposed region gives lane l the elements of column
+// 32 dt + l % 32 in rows 16 kk + 8 (l / 32) + 0..7.  Per-row values: lse * log2(e) (+inf
+// past the sequence's end, which zeroes every probability of such a row), then delta.
+template <int D>
+constexpr int pack_region_bytes() { return 64 * D; }
+template <int D>
+constexpr int pack_block_bytes() { return 4 * pack_region_bytes<D>() + 256; }
 
 typedef short bs16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) bs16x4 lds_bs16x4;
@@ -67,13 +82,16 @@ struct BwdParams {
   const void* q;
   const void* dout;
   const float* lse;    // natural log
-  const float* delta;  // [total][h_q], from bwd_delta_kernel
+  float* delta;        // [total][h_q], written by bwd_pack_kernel
+  const void* out;
+  char* pk;            // packed blocks [h_q][n_pb][pack_block_bytes]
+  int64_t n_pb;
   float* dq;           // [total][h_q][d]
   const void* k[FA4CP_MAX_CP];
   const void* v[FA4CP_MAX_CP];
   float* dk[FA4CP_MAX_CP];  // [total][h_kv][d] per source
   float* dv[FA4CP_MAX_CP];
-  int64_t q_rs, q_hs, do_rs, do_hs, lse_rs, k_rs, k_hs, v_rs, v_hs;
+  int64_t q_rs, q_hs, do_rs, do_hs, o_rs, o_hs, lse_rs, k_rs, k_hs, v_rs, v_hs;
   const int32_t* cu;
   int nseq, total, max_seqlen;
   int h_q, h_kv, group;
@@ -137,30 +155,88 @@ __device__ __forceinline__ typename BwdMfma<T>::frag to_frag(const float* x) {
   return f;
 }
 
-// delta[row, h] = sum_d dO[row, h, d] * O[row, h, d] (fp32); 16 lanes per (row, head).
-template <typename T>
-__global__ __launch_bounds__(256) void bwd_delta_kernel(const T* __restrict__ dout, int64_t do_rs, int64_t do_hs,
-                                                        const T* __restrict__ out, int64_t o_rs, int64_t o_hs,
-                                                        float* __restrict__ delta, int64_t n, int h, int d) {
-  const int64_t g = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int lane = threadIdx.x & 15;
-  float acc = 0.f;
-  if (g < n) {
-    const int64_t row = g / h;
-    const int head = (int)(g - row * h);
-    const T* a = dout + row * do_rs + (int64_t)head * do_hs;
-    const T* b = out + row * o_rs + (int64_t)head * o_hs;
-    for (int c = lane * 8; c < d; c += 128) {
-      float x[8], y[8];
-      load8_f32<T>(a + c, x);
-      load8_f32<T>(b + c, y);
+// One packed block (see pack_block_bytes) per workgroup: rows [32 rb, 32 rb + 32) of sequence
+// `seq` and query head hq, rows past the sequence's end zero.  Also writes delta[row, hq] =
+// sum_d dO[row, hq, d] O[row, hq, d] (fp32) for the dq kernel.  The packed blocks of sequence j
+// start at block fa4cp_vt_min_d_stride's padded position of j / 32.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void bwd_pack_kernel(BwdParams p) {
+  typedef T t8 __attribute__((ext_vector_type(8)));
+  constexpr int RS = D + 8;
+  constexpr int NKS = D / 16;
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+  __shared__ __align__(16) T ql[kBwdRows * RS];
+  __shared__ __align__(16) T dl[kBwdRows * RS];
+  __shared__ float dsum[kBwdRows];
+  int b = blockIdx.x;
+  const int hq = b % p.h_q;
+  b /= p.h_q;
+  const int rb = b % p.n_tiles;
+  const int seq = b / p.n_tiles;
+  const int64_t pstart = vt_seq_start(p.cu, seq, p.total, FA4CP_SEL_ALL) / kBwdRows;
+  int qs, L;
+  seq_range(p.cu, seq, p.total, FA4CP_SEL_ALL, qs, L);
+  const int r0 = rb * kBwdRows;
+  if (r0 >= L) return;
+  const int t = threadIdx.x;
+  {  // thread t: row t / 8, chunks t % 8 + 8 j
+    const int row = t >> 3;
+    const bool ok = r0 + row < L;
+    const int64_t grow = (int64_t)qs + r0 + row;
+    const T* qr = reinterpret_cast<const T*>(p.q) + grow * p.q_rs + (int64_t)hq * p.q_hs;
+    const T* dr = reinterpret_cast<const T*>(p.dout) + grow * p.do_rs + (int64_t)hq * p.do_hs;
+    const T* orow = reinterpret_cast<const T*>(p.out) + grow * p.o_rs + (int64_t)hq * p.o_hs;
+    float acc = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc = fmaf(x[i], y[i], acc);
+    for (int j = 0; j < CPR / 8; ++j) {
+      const int ch = (t & 7) + 8 * j;
+      u32x4 xq = {0u, 0u, 0u, 0u}, xd = {0u, 0u, 0u, 0u};
+      if (ok) {
+        xq = *reinterpret_cast<const u32x4*>(qr + 8 * ch);
+        xd = *reinterpret_cast<const u32x4*>(dr + 8 * ch);
+        float o[8];
+        load8_f32<T>(orow + 8 * ch, o);
+        const t8 dv = __builtin_bit_cast(t8, xd);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = fmaf((float)dv[e], o[e], acc);
+      }
+      *reinterpret_cast<u32x4*>(ql + row * RS + 8 * ch) = xq;
+      *reinterpret_cast<u32x4*>(dl + row * RS + 8 * ch) = xd;
+    }
+#pragma unroll
+    for (int o = 4; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 8);
+    if ((t & 7) == 0) {
+      dsum[row] = acc;
+      if (ok) p.delta[grow * p.h_q + hq] = acc;
     }
   }
+  __syncthreads();
+  char* dst = p.pk + ((int64_t)hq * p.n_pb + pstart + rb) * pack_block_bytes<D>();
+  constexpr int NCH = 4 * NKS * 64;  // 16-byte chunks of the four regions
 #pragma unroll
-  for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 16);
-  if (g < n && lane == 0) delta[g] = acc;
+  for (int g = t; g < NCH; g += 256) {
+    const int region = g / (NKS * 64), f = (g >> 6) % NKS, lane = g & 63, lh = lane >> 5, lm = lane & 31;
+    const T* src = (region == 0 || region == 3) ? ql : dl;
+    u32x4 x;
+    if (region == 0 || region == 2) {
+      x = *reinterpret_cast<const u32x4*>(src + sig(lm) * RS + 16 * f + 8 * lh);
+    } else {
+      const int dt = f >> 1, kk = f & 1;
+      t8 e8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) e8[e] = src[(16 * kk + 8 * lh + e) * RS + 32 * dt + lm];
+      x = __builtin_bit_cast(u32x4, e8);
+    }
+    *reinterpret_cast<u32x4*>(dst + (int64_t)g * 16) = x;
+  }
+  if (t < 2 * kBwdRows) {
+    float v;
+    if (t < kBwdRows)
+      v = r0 + t < L ? p.lse[(int64_t)(qs + r0 + t) * p.lse_rs + hq] * kLog2e : INFINITY;
+    else
+      v = dsum[t - kBwdRows];
+    *reinterpret_cast<float*>(dst + 4 * pack_region_bytes<D>() + 4 * t) = v;
+  }
 }
 
 // A 32-row x D tile in flight to LDS: thread t loads 16-byte chunks t + NT i (row-major over
@@ -179,38 +255,6 @@ struct TileFetch {
       x[i] = u32x4{0u, 0u, 0u, 0u};
       if (row0 + r < lim) x[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)(row0 + r) * rs + 8 * ch);
     }
-  }
-  template <int RS>
-  __device__ __forceinline__ void store(T* lds) const {
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const int c = (int)threadIdx.x + NT * i, r = c / CPR, ch = c % CPR;
-      *reinterpret_cast<u32x4*>(lds + r * RS + 8 * ch) = x[i];
-    }
-  }
-};
-
-// The same tile through a buffer resource that starts at the tile's first row and ends at the
-// sequence's last: rows past the end read as zeros in hardware, and a lane keeps one 32-bit
-// offset per chunk (fixed for the kernel) instead of a 64-bit address and a row test.  The
-// offsets go in the vector offset, which the resource's range check covers.
-template <typename T, int D, int NT>
-struct TileFetchBuf {
-  static constexpr int CPR = D / 8;
-  static constexpr int N = kBwdRows * CPR / NT;
-  static_assert(N * NT == kBwdRows * CPR, "threads must split the tile evenly");
-  u32x4 x[N];
-  int voff[N];
-  __device__ __forceinline__ explicit TileFetchBuf(int rsb) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const int c = (int)threadIdx.x + NT * i;
-      voff[i] = (c / CPR) * rsb + 16 * (c % CPR);
-    }
-  }
-  __device__ __forceinline__ void fetch(__amdgpu_buffer_rsrc_t r) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) x[i] = bload128(r, voff[i]);
   }
   template <int RS>
   __device__ __forceinline__ void store(T* lds) const {
@@ -358,25 +402,39 @@ __global__ __launch_bounds__(64 * HP) void bwd_dq_kernel(BwdParams p) {
   }
 }
 
-// dK / dV: one workgroup per 128 keys of one source rank's sequence and kv head (32 keys per
-// wavefront, K of those keys held in registers and V in the wavefront's LDS rows as
-// operands), walking the query rows that attend them for every query head of the kv head;
-// the next 32-row block of Q / dO is in flight while the current one is used.  At most 256
-// registers, so two workgroups share each SIMD and hide each other's barrier and memory waits.
+// dK / dV: one workgroup per 128 keys of one source rank's sequence and kv head, eight
+// wavefronts in four pairs; pair g owns keys 32 g .. 32 g + 31 of the workgroup.  The first
+// wavefront of a pair (waves 0-3) holds K of its keys as the B operand of S = Q K^T, turns S
+// into P and accumulates dV += P^T dO; the second (waves 4-7) holds V as the B operand of
+// dP = dO V^T, takes P from its partner through LDS (fp16), forms dS = P (dP - delta) and
+// accumulates dK += dS^T Q.  The workgroup walks the packed blocks of the query rows that
+// attend its keys (every query head of the kv head): block i arrives by LDS-DMA into stage
+// i % 3 one iteration ahead, and iteration i runs the products of block i that need only
+// the block (S, dP) and those of block i - 1 that need the other wavefront's result (dV,
+// dK), so the two wavefronts of a pair never wait on each other within an iteration.  One
+// barrier per iteration: block i + 1 has landed, P of block i is in LDS, and the stage of
+// block i - 1 is free for block i + 2.
 template <typename T, int D>
-__global__ __launch_bounds__(64 * kDkdvWaves, 2) void bwd_dkdv_kernel(BwdParams p) {
+__global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
   using M = BwdMfma<T>;
-  constexpr int RS = D + 8;
+  typedef typename M::frag frag;
   constexpr int NKS = D / 16;
   constexpr int NDT = D / 32;
-  constexpr int NT = 64 * kDkdvWaves;
-  __shared__ __align__(16) T qt[kBwdRows * RS];
-  __shared__ __align__(16) T dot[kBwdRows * RS];
-  __shared__ __align__(16) float lse2s[kBwdRows];
-  __shared__ __align__(16) float dls[kBwdRows];
-  // V of each wavefront's 32 keys (written and read by that wavefront only): the B operands of
-  // dP come from here, which keeps the registers of two workgroups on a SIMD
-  __shared__ __align__(16) T vsm[kDkdvWaves * kBwdRows * RS];
+  constexpr int R = pack_region_bytes<D>();
+  constexpr int BB = pack_block_bytes<D>();
+  constexpr int CPW = 4 * NKS / 8;  // 1 KB fragments each wavefront loads per block
+  constexpr int kWaitAll = 7 << 4;  // vmcnt(0), lgkmcnt(0)
+  static_assert(CPW * 8 == 4 * NKS, "fragments must split evenly over the wavefronts");
+  // Three stages in separate arrays: the LDS-DMA destination is chosen at run time, so the
+  // compiler does not make the first LDS read of an iteration wait for every load in flight.
+  __shared__ __align__(16) char stage0[BB];
+  __shared__ __align__(16) char stage1[BB];
+  __shared__ __align__(16) char stage2[BB];
+  __shared__ __align__(16) char xch[2 * 4 * 2048];  // P of a block per pair, two blocks
+  auto stage_of = [&](int bi) {
+    const int m = bi % 3;
+    return m == 0 ? stage0 : m == 1 ? stage1 : stage2;
+  };
 
   int b = blockIdx.x;
   const int kt = b % p.n_tiles;
@@ -385,32 +443,33 @@ __global__ __launch_bounds__(64 * kDkdvWaves, 2) void bwd_dkdv_kernel(BwdParams 
   b /= p.nseq;
   const int kvh = b % p.h_kv;
   const int src = b / p.h_kv;
+  const int64_t pstart = vt_seq_start(p.cu, seq, p.total, FA4CP_SEL_ALL) / kBwdRows;
   int qs, L;
   seq_range(p.cu, seq, p.total, FA4CP_SEL_ALL, qs, L);
   const int kb0 = kt * kDkdvKeys;
   if (kb0 >= L) return;
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, h = l >> 5, lk = l & 31;
-  const int key = kb0 + w * kBwdRows + lk;  // this lane's key in the sequence
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int l = threadIdx.x & 63, h = l >> 5, lk = l & 31;
+  const bool pwave = w < 4;
+  const int kg0 = kb0 + kBwdRows * (w & 3);  // first key of the pair's group
+  const int key = kg0 + lk;                  // this lane's key in the sequence
   const StepPairs sp = step_pairs(p.rank, p.S, src, L);
 
-  f32x16 dk[NDT], dv[NDT];
+  f32x16 acc[NDT];  // dV (first wavefront of a pair) or dK (second)
 #pragma unroll
-  for (int i = 0; i < NDT; ++i) dk[i] = dv[i] = f32x16{};
+  for (int i = 0; i < NDT; ++i) acc[i] = f32x16{};
 
   if (kb0 < sp.key_lim) {
-    // K and V of the lane's key: B operands of S = Q K^T and dP = dO V^T
-    typename M::frag kf[NKS];
-    T* const vw = vsm + w * kBwdRows * RS;  // this wavefront's V rows, one per key
+    // K (first wavefront) or V (second) of the lane's key: B operands of S and dP
+    frag kv[NKS];
     {
       const bool ok = key < sp.key_lim;
-      const T* kr = reinterpret_cast<const T*>(p.k[src]) + (int64_t)(qs + key) * p.k_rs + (int64_t)kvh * p.k_hs;
-      const T* vr = reinterpret_cast<const T*>(p.v[src]) + (int64_t)(qs + key) * p.v_rs + (int64_t)kvh * p.v_hs;
+      const T* r = pwave ? reinterpret_cast<const T*>(p.k[src]) + (int64_t)(qs + key) * p.k_rs + (int64_t)kvh * p.k_hs
+                         : reinterpret_cast<const T*>(p.v[src]) + (int64_t)(qs + key) * p.v_rs + (int64_t)kvh * p.v_hs;
 #pragma unroll
       for (int t = 0; t < NKS; ++t) {
-        typename M::frag z = {};
-        kf[t] = ok ? *reinterpret_cast<const typename M::frag*>(kr + 8 * h + 16 * t) : z;
-        *reinterpret_cast<typename M::frag*>(vw + lk * RS + 8 * h + 16 * t) =
-            ok ? *reinterpret_cast<const typename M::frag*>(vr + 8 * h + 16 * t) : z;
+        frag z = {};
+        kv[t] = ok ? *reinterpret_cast<const frag*>(r + 8 * h + 16 * t) : z;
       }
     }
     const float c = p.scale * kLog2e;
@@ -418,114 +477,146 @@ __global__ __launch_bounds__(64 * kDkdvWaves, 2) void bwd_dkdv_kernel(BwdParams 
     const int row_begin = max(sp.row_min, sp.causal ? kb0 : 0) / kBwdRows * kBwdRows;
     const int n_rb = (L - row_begin + kBwdRows - 1) / kBwdRows;
     const int n_blk = n_rb * p.group;  // (query head, 32-row block) pairs, head-major
-    auto qbase = [&](int bi, bool isq) {
-      const int hq = kvh * p.group + bi / n_rb;
-      return isq ? reinterpret_cast<const T*>(p.q) + (int64_t)qs * p.q_rs + (int64_t)hq * p.q_hs
-                 : reinterpret_cast<const T*>(p.dout) + (int64_t)qs * p.do_rs + (int64_t)hq * p.do_hs;
-    };
-    auto row0_of = [&](int bi) { return row_begin + (bi % n_rb) * kBwdRows; };
-    const int q_rsb = (int)(p.q_rs * (int64_t)sizeof(T)), do_rsb = (int)(p.do_rs * (int64_t)sizeof(T));
-    TileFetchBuf<T, D, NT> fq(q_rsb), fd(do_rsb);
-    float flse = 0.f, fdl = 0.f;
-    auto fetch = [&](int bi) {
-      const int r0 = row0_of(bi), hq = kvh * p.group + bi / n_rb;
-      fq.fetch(make_rsrc(qbase(bi, true) + (int64_t)r0 * p.q_rs, (int64_t)(L - r0) * q_rsb));
-      fd.fetch(make_rsrc(qbase(bi, false) + (int64_t)r0 * p.do_rs, (int64_t)(L - r0) * do_rsb));
-      if (threadIdx.x < kBwdRows) {
-        const int row = r0 + threadIdx.x;
-        flse = row < L ? p.lse[(int64_t)(qs + row) * p.lse_rs + hq] : 0.f;  // scaled at the store: no wait here
-        fdl = row < L ? p.delta[(int64_t)(qs + row) * p.h_q + hq] : 0.f;
+    const int64_t blk0 = pstart + row_begin / kBwdRows;
+    int lh = 0, lr = 0;  // query head (within the group) and row block of the next load
+    auto load = [&](int bi) {
+      const char* g = p.pk + ((int64_t)(kvh * p.group + lh) * p.n_pb + blk0 + lr) * BB;
+      const __amdgpu_buffer_rsrc_t rs = make_rsrc32(uniform_ptr(g), BB);
+      char* st = stage_of(bi);
+#pragma unroll
+      for (int j = 0; j < CPW; ++j) {
+        const int f = w + 8 * j;
+        dma16(rs, st + 1024 * f, 1024 * f + 16 * l);
+      }
+      dma4(rs, st + 4 * R, 4 * R + 4 * l);  // every wavefront writes the same per-row values
+      if (++lr == n_rb) {
+        lr = 0;
+        ++lh;
       }
     };
-    if (n_blk > 0) fetch(0);
-    for (int bi = 0; bi < n_blk; ++bi) {
-      const int r0 = row0_of(bi);
-      __syncthreads();  // the previous block's readers are done
-      fq.template store<RS>(qt);
-      fd.template store<RS>(dot);
-      if (threadIdx.x < kBwdRows) {
-        lse2s[threadIdx.x] = flse * kLog2e;
-        dls[threadIdx.x] = fdl;
+    // lse * log2(e) (off 0) or delta (off 128) of the rows of accumulator registers 0..15
+    auto row_vals = [&](const char* st, int off, float (&v)[16]) {
+      const f32x4* s4 = reinterpret_cast<const f32x4*>(st + 4 * R + off);
+      const f32x4 a = s4[2 * h], bq = s4[2 * h + 1], cq = s4[4 + 2 * h], dq = s4[5 + 2 * h];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[j] = a[j];
+        v[4 + j] = bq[j];
+        v[8 + j] = cq[j];
+        v[12 + j] = dq[j];
       }
-      if (bi + 1 < n_blk) fetch(bi + 1);
-      lds_written_barrier();
-      f32x16 st = {}, dpt = {};
+    };
+    auto frag_at = [&](const char* st, int off) { return *reinterpret_cast<const frag*>(st + off + 16 * l); };
+    auto run = [&](auto role) {
+      constexpr bool PW = decltype(role)::value;
+      frag pb0, pb1;  // first wavefront: P of the previous block (operands of dV)
+      f32x16 dpt;     // second wavefront: dP of the previous block
+      int cr = 0;     // row block (within the head) of block i
+      load(0);
+      __builtin_amdgcn_s_waitcnt(kWaitAll);
+      wg_barrier();
+      for (int i = 0; i <= n_blk; ++i) {
+        if (i + 1 < n_blk) load(i + 1);
+        const char* cur = stage_of(i);
+        const char* prev = stage_of(i + 2);
+        if constexpr (PW) {
+          if (i > 0) {
 #pragma unroll
-      for (int t = 0; t < NKS; ++t) st = M::mma(lds_frag<T, RS>(qt, sig(lk), 2 * t + h), kf[t], st);
-#pragma unroll
-      for (int t = 0; t < NKS; ++t)
-        dpt = M::mma(lds_frag<T, RS>(dot, sig(lk), 2 * t + h), lds_frag<T, RS>(vw, lk, 2 * t + h), dpt);
-      // no pair of the block masked for this wavefront's keys (the usual case)
-      const int kw0 = kb0 + w * kBwdRows;
-      const bool full = r0 + kBwdRows <= L && r0 >= sp.row_min && kw0 + kBwdRows <= sp.key_lim &&
-                        (!sp.causal || kw0 + kBwdRows - 1 <= r0);
-      // accumulator register r: query row r0 + acc_pos(r, h), key `key`.  Registers 8 kk ..
-      // 8 kk + 7 hold the block's rows 16 kk .. 16 kk + 15 (the k-step kk of dV and dK): one
-      // k-step's P and dS at a time keeps two workgroups' registers on a SIMD
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        // rows acc_pos(8 kk + j, h) = 16 kk + 8h + j: consecutive, read four at a time
-        float pv[8], dsv[8];
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const f32x4 lq4 = *reinterpret_cast<const f32x4*>(lse2s + 16 * kk + 8 * h + 4 * q);
-          const f32x4 dq4 = *reinterpret_cast<const f32x4*>(dls + 16 * kk + 8 * h + 4 * q);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int j = 4 * q + e, r = 8 * kk + j;
-            const int row = r0 + 16 * kk + 8 * h + j;
-            const float pr = __builtin_amdgcn_exp2f(fmaf(st[r], c, -lq4[e]));
-            if (full) {
-              pv[j] = pr;
-            } else {
-              const bool ok = (row < L) & (row >= sp.row_min) & (key < sp.key_lim) & (!sp.causal | (key <= row));
-              pv[j] = ok ? pr : 0.f;
+            for (int dt = 0; dt < NDT; ++dt) {
+              acc[dt] = M::mma(frag_at(prev, R + 1024 * (2 * dt)), pb0, acc[dt]);
+              acc[dt] = M::mma(frag_at(prev, R + 1024 * (2 * dt + 1)), pb1, acc[dt]);
             }
-            dsv[j] = pv[j] * (dpt[r] - dq4[e]);
+          }
+          if (i < n_blk) {
+            f32x16 st = {};
+#pragma unroll
+            for (int t = 0; t < NKS; ++t) st = M::mma(frag_at(cur, 1024 * t), kv[t], st);
+            float lse[16], pv[16];
+            row_vals(cur, 0, lse);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse[r]));
+            const int row0 = row_begin + cr * kBwdRows;
+            const bool full = row0 >= sp.row_min && kg0 + kBwdRows <= sp.key_lim &&
+                              (!sp.causal || row0 >= kg0 + kBwdRows - 1);
+            if (!full) {
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const int row = row0 + acc_pos(r, h);
+                const bool ok = row >= sp.row_min && key < sp.key_lim && (!sp.causal || key <= row);
+                pv[r] = ok ? pv[r] : 0.f;
+              }
+            }
+            pb0 = to_frag<T>(pv);
+            pb1 = to_frag<T>(pv + 8);
+            char* xb = xch + ((i & 1) * 4 + (w & 3)) * 2048;
+            *reinterpret_cast<f16x8*>(xb + 16 * l) = to_frag<_Float16>(pv);
+            *reinterpret_cast<f16x8*>(xb + 1024 + 16 * l) = to_frag<_Float16>(pv + 8);
+          }
+        } else {
+          if (i > 0) {
+            const char* xb = xch + (((i - 1) & 1) * 4 + (w & 3)) * 2048;
+            const f16x8 e0 = *reinterpret_cast<const f16x8*>(xb + 16 * l);
+            const f16x8 e1 = *reinterpret_cast<const f16x8*>(xb + 1024 + 16 * l);
+            float dl[16], dsv[16];
+            row_vals(prev, 128, dl);
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+              dsv[r] = (float)e0[r] * (dpt[r] - dl[r]);
+              dsv[8 + r] = (float)e1[r] * (dpt[8 + r] - dl[8 + r]);
+            }
+            const frag s0 = to_frag<T>(dsv), s1 = to_frag<T>(dsv + 8);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+              acc[dt] = M::mma(frag_at(prev, 3 * R + 1024 * (2 * dt)), s0, acc[dt]);
+              acc[dt] = M::mma(frag_at(prev, 3 * R + 1024 * (2 * dt + 1)), s1, acc[dt]);
+            }
+          }
+          if (i < n_blk) {
+            dpt = f32x16{};
+#pragma unroll
+            for (int t = 0; t < NKS; ++t) dpt = M::mma(frag_at(cur, 2 * R + 1024 * t), kv[t], dpt);
           }
         }
-        const typename M::frag pk = to_frag<T>(pv), sk = to_frag<T>(dsv);
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          dv[dt] = M::mma(lds_frag_tr<T, RS>(dot, 16 * kk, 32 * dt), pk, dv[dt]);
-          dk[dt] = M::mma(lds_frag_tr<T, RS>(qt, 16 * kk, 32 * dt), sk, dk[dt]);
+        if (i < n_blk) {  // block i + 1 has landed (each wavefront's own loads), P of block i written
+          __builtin_amdgcn_s_waitcnt(kWaitAll);
+          wg_barrier();
         }
+        if (++cr == n_rb) cr = 0;
       }
+    };
+    if (n_blk > 0) {
+      if (pwave) run(std::true_type{});
+      else run(std::false_type{});
     }
   }
   // accumulator register r of lane l: head-dim element 32 dt + 8 (r / 4) + 4h + r % 4 of key
   // `key`; keys no query of this rank attends (past key_lim) get zeros
   if (key >= L) return;
-  float* dko = p.dk[src] + ((int64_t)(qs + key) * p.h_kv + kvh) * D;
-  float* dvo = p.dv[src] + ((int64_t)(qs + key) * p.h_kv + kvh) * D;
+  float* o = pwave ? p.dv[src] + ((int64_t)(qs + key) * p.h_kv + kvh) * D
+                   : p.dk[src] + ((int64_t)(qs + key) * p.h_kv + kvh) * D;
+  const float sc = pwave ? 1.f : p.scale;
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d = 32 * dt + 8 * g + 4 * h;
-      f32x4 a = {dk[dt][4 * g] * p.scale, dk[dt][4 * g + 1] * p.scale, dk[dt][4 * g + 2] * p.scale,
-                 dk[dt][4 * g + 3] * p.scale};
-      f32x4 bb = {dv[dt][4 * g], dv[dt][4 * g + 1], dv[dt][4 * g + 2], dv[dt][4 * g + 3]};
-      if (p.accumulate) {
-        a += *reinterpret_cast<const f32x4*>(dko + d);
-        bb += *reinterpret_cast<const f32x4*>(dvo + d);
-      }
-      *reinterpret_cast<f32x4*>(dko + d) = a;
-      *reinterpret_cast<f32x4*>(dvo + d) = bb;
+      f32x4 a = {acc[dt][4 * g] * sc, acc[dt][4 * g + 1] * sc, acc[dt][4 * g + 2] * sc, acc[dt][4 * g + 3] * sc};
+      if (p.accumulate) a += *reinterpret_cast<const f32x4*>(o + d);
+      *reinterpret_cast<f32x4*>(o + d) = a;
     }
 }
+
 
 template <typename T, int D>
 int launch_bwd(const BwdParams& base, const fa4cp_sweep_bwd_args& a, hipStream_t st) {
   BwdParams p = base;
-  // delta = rowsum(dO * O)
-  const int64_t n = (int64_t)a.total * a.h_q;
-  hipLaunchKernelGGL(bwd_delta_kernel<T>, dim3((unsigned)((n + 15) / 16)), dim3(256), 0, st,
-                     reinterpret_cast<const T*>(a.dout), a.do_row_stride, a.do_head_stride,
-                     reinterpret_cast<const T*>(a.out), a.o_row_stride, a.o_head_stride, a.delta, n, a.h_q, D);
+  // delta and the packed Q / dO blocks
+  p.n_tiles = (p.max_seqlen + kBwdRows - 1) / kBwdRows;
+  const int64_t pack_blocks = (int64_t)p.nseq * p.n_tiles * p.h_q;
+  if (pack_blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "ring_sweep_bwd: too many row tiles");
+  hipLaunchKernelGGL((bwd_pack_kernel<T, D>), dim3((unsigned)pack_blocks), dim3(256), 0, st, p);
   // dq
   const int hp = p.group % 4 == 0 ? 4 : p.group % 2 == 0 ? 2 : 1;
-  p.n_tiles = (p.max_seqlen + kBwdRows - 1) / kBwdRows;
   const int64_t dq_blocks = (int64_t)p.nseq * p.n_tiles * (p.h_q / hp);
   if (dq_blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "ring_sweep_bwd: too many row tiles");
   switch (hp) {
@@ -537,14 +628,30 @@ int launch_bwd(const BwdParams& base, const fa4cp_sweep_bwd_args& a, hipStream_t
   p.n_tiles = (p.max_seqlen + kDkdvKeys - 1) / kDkdvKeys;
   const int64_t kv_blocks = (int64_t)p.S * p.h_kv * p.nseq * p.n_tiles;
   if (kv_blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "ring_sweep_bwd: too many key tiles");
-  hipLaunchKernelGGL((bwd_dkdv_kernel<T, D>), dim3((unsigned)kv_blocks), dim3(64 * kDkdvWaves), 0, st, p);
+  hipLaunchKernelGGL((bwd_dkdv_kernel<T, D>), dim3((unsigned)kv_blocks), dim3(512), 0, st, p);
   return check_launch("ring_sweep_bwd");
 }
+
+// Workspace: delta [total][h_q] float32 (rounded up to 256 bytes), then the packed blocks
+// [h_q][n_pb][pack_block_bytes], n_pb = fa4cp_vt_min_d_stride(total, nseq) / 32.
+int64_t delta_bytes(int total, int h_q) { return ((int64_t)total * h_q * 4 + 255) / 256 * 256; }
+int64_t packed_blocks(int total, int nseq) { return fa4cp_vt_min_d_stride(total, nseq) / kBwdRows; }
+int64_t block_bytes(int d) { return d == 128 ? pack_block_bytes<128>() : pack_block_bytes<64>(); }
 
 }  // namespace
 }  // namespace fa4cp
 
 using namespace fa4cp;
+
+extern "C" int64_t fa4cp_ring_sweep_bwd_workspace_bytes(const fa4cp_sweep_bwd_args* a) {
+  clear_error();
+  if (a == nullptr) return set_error(FA4CP_EINVAL, "ring_sweep_bwd_workspace_bytes: null args");
+  if (a->total < 0 || a->h_q <= 0 || (a->d != 64 && a->d != 128) || (a->cu != nullptr && a->nseq <= 0))
+    return set_error(FA4CP_EINVAL, "ring_sweep_bwd_workspace_bytes: bad shape total=%d h_q=%d d=%d nseq=%d", a->total,
+                     a->h_q, a->d, a->nseq);
+  const int nseq = a->cu ? a->nseq : 1;
+  return delta_bytes(a->total, a->h_q) + (int64_t)a->h_q * packed_blocks(a->total, nseq) * block_bytes(a->d);
+}
 
 extern "C" int fa4cp_ring_sweep_bwd(const fa4cp_sweep_bwd_args* a, void* stream) {
   clear_error();
@@ -560,8 +667,13 @@ extern "C" int fa4cp_ring_sweep_bwd(const fa4cp_sweep_bwd_args* a, void* stream)
   if (a->cu != nullptr && a->nseq <= 0) return set_error(FA4CP_EINVAL, "ring_sweep_bwd: nseq must be >= 1 with cu");
   if (a->cu != nullptr && a->max_seqlen < 0) return set_error(FA4CP_EINVAL, "ring_sweep_bwd: negative max_seqlen");
   if (a->total == 0) return FA4CP_OK;
-  if (!a->q || !a->dout || !a->out || !a->lse || !a->delta || !a->dq)
-    return set_error(FA4CP_EINVAL, "ring_sweep_bwd: null tensor");
+  if (!a->q || !a->dout || !a->out || !a->lse || !a->workspace || !a->dq)
+    return set_error(FA4CP_EINVAL, "ring_sweep_bwd: null tensor or workspace");
+  const int64_t need = fa4cp_ring_sweep_bwd_workspace_bytes(a);
+  if (need < 0) return (int)need;
+  if (a->workspace_bytes < need || reinterpret_cast<uintptr_t>(a->workspace) % 256 != 0)
+    return set_error(FA4CP_EINVAL, "ring_sweep_bwd: workspace of %lld bytes at %p; %lld bytes, 256-byte aligned, needed",
+                     (long long)a->workspace_bytes, a->workspace, (long long)need);
   for (int i = 0; i < a->cp_size; ++i)
     if (!a->k[i] || !a->v[i] || !a->dk[i] || !a->dv[i])
       return set_error(FA4CP_EINVAL, "ring_sweep_bwd: null K / V / dK / dV of source %d", i);
@@ -578,7 +690,10 @@ extern "C" int fa4cp_ring_sweep_bwd(const fa4cp_sweep_bwd_args* a, void* stream)
   p.q = a->q;
   p.dout = a->dout;
   p.lse = a->lse;
-  p.delta = a->delta;
+  p.out = a->out;
+  p.delta = reinterpret_cast<float*>(a->workspace);
+  p.pk = reinterpret_cast<char*>(a->workspace) + delta_bytes(a->total, a->h_q);
+  p.n_pb = packed_blocks(a->total, a->cu ? a->nseq : 1);
   p.dq = a->dq;
   for (int i = 0; i < a->cp_size; ++i) {
     p.k[i] = a->k[i];
@@ -590,6 +705,8 @@ extern "C" int fa4cp_ring_sweep_bwd(const fa4cp_sweep_bwd_args* a, void* stream)
   p.q_hs = a->q_head_stride;
   p.do_rs = a->do_row_stride;
   p.do_hs = a->do_head_stride;
+  p.o_rs = a->o_row_stride;
+  p.o_hs = a->o_head_stride;
   p.lse_rs = a->lse_row_stride;
   p.k_rs = a->k_row_stride;
   p.k_hs = a->k_head_stride;

@@ -103,18 +103,6 @@ __device__ __forceinline__ i32x2 lds_tr8(const void* p) {
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)p);
 }
 
-// 16-byte LDS-DMA load: lane L's 16 bytes from `r` at byte offset voff land at lds + 16 L
-// (lanes past the end of `r` write zeros).  `lds` must be wave-uniform.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff,
-                                           0, 0, 0);
-}
-// The same with a wave-uniform byte offset `soff` added in the scalar offset field.
-__device__ __forceinline__ void dma16s(__amdgpu_buffer_rsrc_t r, void* lds, int voff, int soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff,
-                                           soff, 0, 0);
-}
-
 // Instruction-scheduling groups for __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedValu = 0x002 | 0x400;  // VALU including transcendentals
 constexpr int kSchedMfma = 0x008;

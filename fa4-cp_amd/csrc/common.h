@@ -96,6 +96,34 @@ __device__ __forceinline__ u32x4 bload128(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
 
+// 16-byte LDS-DMA load: lane L's 16 bytes from `r` at byte offset voff land at lds + 16 L
+// (lanes past the end of `r` write zeros).  `lds` must be wave-uniform.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff,
+                                           0, 0, 0);
+}
+// The same with a wave-uniform byte offset `soff` added in the scalar offset field.
+__device__ __forceinline__ void dma16s(__amdgpu_buffer_rsrc_t r, void* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff,
+                                           soff, 0, 0);
+}
+// 4-byte LDS-DMA load: lane L's 4 bytes from `r` at byte offset voff land at lds + 4 L.
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, voff,
+                                           0, 0, 0);
+}
+
+// A wave-uniform pointer moved to scalar registers (readfirstlane of both 32-bit halves).
+// readfirstlane returns a signed int: each half is taken as uint32_t before the two are
+// joined, so a low half with bit 31 set is not sign-extended over the high half (which would
+// turn an address such as 0x00007f3a9abcdef0 into 0xffffffff9abcdef0).
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t u = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  return reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo);
+}
+
 // Eight elements at byte offset `off` of buffer `r`, widened to fp32 (zeros past the end).
 template <typename T>
 __device__ __forceinline__ void bload8_f32(__amdgpu_buffer_rsrc_t r, int off, float (&out)[8]) {

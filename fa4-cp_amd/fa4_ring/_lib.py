@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libfa4cp.so"
 # FA4CP_LIB selects another build of the library (the in-tree one by default)
 LIB_PATH = os.environ.get("FA4CP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # element types (FA4CP_*)
 BF16, FP16, E4M3, FP32 = 0, 1, 2, 3
@@ -166,7 +166,8 @@ class SweepBwdArgs(ctypes.Structure):
         ("dout", ctypes.c_void_p),
         ("out", ctypes.c_void_p),
         ("lse", ctypes.c_void_p),
-        ("delta", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_int64),
         ("dq", ctypes.c_void_p),
         ("q_row_stride", ctypes.c_int64),
         ("q_head_stride", ctypes.c_int64),
@@ -272,6 +273,7 @@ SIGNATURES = {
     "fa4cp_ring_sweep_fwd_paged": (
         ctypes.c_int, [ctypes.POINTER(SweepArgs), ctypes.POINTER(SweepKPages), ctypes.c_void_p]),
     "fa4cp_ring_sweep_bwd": (ctypes.c_int, [ctypes.POINTER(SweepBwdArgs), ctypes.c_void_p]),
+    "fa4cp_ring_sweep_bwd_workspace_bytes": (ctypes.c_int64, [ctypes.POINTER(SweepBwdArgs)]),
     "fa4cp_quantize_e4m3": (ctypes.c_int, [ctypes.POINTER(QuantArgs), ctypes.c_void_p]),
     "fa4cp_quantize_e4m3_noalloc": (ctypes.c_int, [ctypes.POINTER(QuantArgs), ctypes.c_void_p]),
     "fa4cp_last_error": (ctypes.c_char_p, []),

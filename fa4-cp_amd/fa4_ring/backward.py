@@ -90,10 +90,9 @@ def ring_flash_attn_backward(dout: torch.Tensor, local_q: torch.Tensor, local_k:
     dq = buf(dq, (total, h_q, d), "dq")
     dk = [buf(None if dk is None else dk[i], (total, h_kv, d), f"dk[{i}]") for i in range(S)]
     dv = [buf(None if dv is None else dv[i], (total, h_kv, d), f"dv[{i}]") for i in range(S)]
-    delta = torch.empty((total, h_q), dtype=torch.float32, device=dev)
     a = _lib.SweepBwdArgs()
-    a.q, a.dout, a.out, a.lse, a.delta, a.dq = (local_q.data_ptr(), dout.data_ptr(), out.data_ptr(), lse.data_ptr(),
-                                                delta.data_ptr(), dq.data_ptr())
+    a.q, a.dout, a.out, a.lse, a.dq = (local_q.data_ptr(), dout.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                                       dq.data_ptr())
     a.q_row_stride, a.q_head_stride = local_q.stride(0), local_q.stride(1)
     a.do_row_stride, a.do_head_stride = dout.stride(0), dout.stride(1)
     a.o_row_stride, a.o_head_stride = out.stride(0), out.stride(1)
@@ -111,6 +110,11 @@ def ring_flash_attn_backward(dout: torch.Tensor, local_q: torch.Tensor, local_k:
     a.cp_rank, a.cp_size = rank, S
     a.softmax_scale = float(cfg.softmax_scale if cfg.softmax_scale is not None else 1.0 / math.sqrt(d))
     a.accumulate = 1 if accumulate else 0
+    ws_bytes = lib.fa4cp_ring_sweep_bwd_workspace_bytes(ctypes.byref(a))
+    _lib.check(int(min(ws_bytes, 0)), "fa4cp_ring_sweep_bwd_workspace_bytes")
+    # delta and the packed q / dout blocks (caching allocator blocks are 512-byte aligned)
+    ws = torch.empty((max(int(ws_bytes), 1),), dtype=torch.uint8, device=dev)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes
     _lib.check(lib.fa4cp_ring_sweep_bwd(ctypes.byref(a), _lib.stream_handle(dev)), "fa4cp_ring_sweep_bwd")
     return dq, dk, dv
 

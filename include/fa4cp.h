@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define FA4CP_ABI_VERSION 6
+#define FA4CP_ABI_VERSION 7
 
 /* status codes */
 #define FA4CP_OK 0
@@ -261,18 +261,22 @@ int fa4cp_ring_sweep_fwd_paged(const fa4cp_sweep_args* args, const fa4cp_sweep_k
  *   dk[i], dv[i]  = this rank's contribution to source rank i's K / V gradient
  *                   (keys this rank does not attend get 0)            [total][h_kv][d] float32
  * Every (query row, key) pair of the forward's three step patterns contributes, with the
- * probability exp(scale q.k - lse) taken against the final lse.  delta is a caller-owned
- * [total][h_q] float32 workspace (rowsum(dout * out), written here).  With accumulate != 0 the
- * results are added to dq / dk / dv instead of stored (summing the contributions of several
- * ranks, as a ring's backward does).  q, dout and out may have any row and head stride; k / v
- * shards share strides and the cu layout of fa4cp_ring_sweep_fwd.  Three launches on `stream`.
+ * probability exp(scale q.k - lse) taken against the final lse.  workspace is caller-owned
+ * device memory of at least fa4cp_ring_sweep_bwd_workspace_bytes(args) bytes, 256-byte
+ * aligned: the first launch writes rowsum(dout * out) and a copy of q and dout in the operand
+ * order of the dk / dv products there (about 4 x the bytes of q for d = 128); it holds nothing
+ * across calls.  With accumulate != 0 the results are added to dq / dk / dv instead of stored
+ * (summing the contributions of several ranks, as a ring's backward does).  q, dout and out
+ * may have any row and head stride; k / v shards share strides and the cu layout of
+ * fa4cp_ring_sweep_fwd.  Three launches on `stream`.
  */
 typedef struct fa4cp_sweep_bwd_args {
   const void* q;    /* [total] x h_q x d */
   const void* dout; /* [total] x h_q x d, gradient of the forward's out */
   const void* out;  /* [total] x h_q x d, the forward's out */
   const float* lse; /* lse[row * lse_row_stride + head], the forward's natural-log lse */
-  float* delta;     /* [total][h_q] workspace */
+  void* workspace;  /* fa4cp_ring_sweep_bwd_workspace_bytes(args) bytes, 256-byte aligned */
+  int64_t workspace_bytes;
   float* dq;        /* [total][h_q][d] */
   int64_t q_row_stride, q_head_stride, do_row_stride, do_head_stride, o_row_stride, o_head_stride;
   int64_t lse_row_stride;
@@ -290,6 +294,9 @@ typedef struct fa4cp_sweep_bwd_args {
 } fa4cp_sweep_bwd_args;
 
 int fa4cp_ring_sweep_bwd(const fa4cp_sweep_bwd_args* args, void* stream);
+/* Workspace bytes fa4cp_ring_sweep_bwd needs for args' total, nseq (with cu), h_q and d (the
+ * other fields are not read); a negative FA4CP_E* code for a bad shape. */
+int64_t fa4cp_ring_sweep_bwd_workspace_bytes(const fa4cp_sweep_bwd_args* args);
 
 /*
  * In-place online-softmax merge (flashinfer.cascade.merge_state_in_place semantics, natural

@@ -206,6 +206,64 @@ def test_sweep_entry_point_validates_before_launching():
     assert lib.fa4cp_ring_sweep_fwd_paged(ctypes.byref(args(total=0)), ctypes.byref(kp), None) == 0
 
 
+def test_backward_workspace_size_and_checks():
+    """fa4cp_ring_sweep_bwd_workspace_bytes: delta (total x h_q float32, rounded up to 256
+    bytes) plus h_q x (padded rows / 32) packed blocks of 4 x 64 x d + 256 bytes each; the
+    backward refuses a workspace that is small or not 256-byte aligned before any HIP call.
+    The pointers are fake, so this never runs where a device is visible."""
+    if torch.cuda.device_count() > 0:
+        pytest.skip("fake device pointers: host-only test")
+    lib = _lib.load()
+    fake = 1 << 20
+
+    def args(**kw):
+        a = _lib.SweepBwdArgs()
+        a.q = a.dout = a.out = a.lse = a.dq = a.workspace = fake
+        a.q_row_stride = a.do_row_stride = a.o_row_stride = 8 * 128
+        a.q_head_stride = a.do_head_stride = a.o_head_stride = 128
+        a.lse_row_stride = 8
+        a.k_row_stride = a.v_row_stride = 2 * 128
+        a.k_head_stride = a.v_head_stride = 128
+        a.total, a.h_q, a.h_kv, a.d = 256, 8, 2, 128
+        a.dtype = _lib.dtype_code(torch.bfloat16)
+        a.cp_rank, a.cp_size = 0, 2
+        a.softmax_scale = 0.1
+        for i in range(2):
+            a.k[i] = a.v[i] = a.dk[i] = a.dv[i] = fake
+        for key, val in kw.items():
+            setattr(a, key, val)
+        return a
+
+    def expect(total, nseq, h_q, d):
+        delta = -(-total * h_q * 4 // 256) * 256
+        # rows of the padded layout: every sequence padded to a multiple of 128 rows fits in
+        # total + 128 nseq, rounded up to 128 (fa4cp_vt_min_d_stride)
+        rows = -(-(total + 128 * nseq) // 128) * 128
+        assert rows == lib.fa4cp_vt_min_d_stride(total, nseq)
+        return delta + h_q * (rows // 32) * (4 * 64 * d + 256)
+
+    # one sequence of 256 rows: 384 padded rows, so 8 heads x 12 blocks of 33024 bytes + 8 KB
+    assert lib.fa4cp_ring_sweep_bwd_workspace_bytes(ctypes.byref(args())) == 8192 + 8 * 12 * 33024
+    for total, nseq, h_q, d in [(256, 1, 8, 128), (100, 1, 3, 64), (16384, 1, 32, 128), (1000, 7, 4, 64)]:
+        a = args(total=total, h_q=h_q, d=d, nseq=nseq, cu=fake if nseq > 1 else None)
+        assert lib.fa4cp_ring_sweep_bwd_workspace_bytes(ctypes.byref(a)) == expect(total, nseq, h_q, d)
+    for kw, msg in [(dict(d=96), b"bad shape"), (dict(h_q=0), b"bad shape"), (dict(total=-1), b"bad shape"),
+                    (dict(cu=fake, nseq=0), b"bad shape")]:
+        assert lib.fa4cp_ring_sweep_bwd_workspace_bytes(ctypes.byref(args(**kw))) < 0
+        assert msg in lib.fa4cp_last_error(), kw
+    assert lib.fa4cp_ring_sweep_bwd_workspace_bytes(None) < 0
+
+    need = lib.fa4cp_ring_sweep_bwd_workspace_bytes(ctypes.byref(args()))
+    for kw, msg in [(dict(workspace_bytes=need - 1), b"workspace"), (dict(workspace_bytes=need, workspace=fake + 16),
+                                                                     b"workspace"),
+                    (dict(workspace=None, workspace_bytes=need), b"workspace"), (dict(d=96), b"head dim"),
+                    (dict(cp_rank=2), b"cp_rank")]:
+        rc = lib.fa4cp_ring_sweep_bwd(ctypes.byref(args(**kw)), None)
+        assert rc != 0 and msg in lib.fa4cp_last_error(), (kw, lib.fa4cp_last_error())
+    # nothing to do: no workspace needed
+    assert lib.fa4cp_ring_sweep_bwd(ctypes.byref(args(total=0, workspace=None)), None) == 0
+
+
 @pytest.mark.parametrize("struct,cname", [(_lib.AttnArgs, "fa4cp_attn_args"),
                                            (_lib.TransposeArgs, "fa4cp_transpose_args"),
                                            (_lib.SweepArgs, "fa4cp_sweep_args"),
