@@ -561,8 +561,52 @@ def bench_c4(args) -> int:
     return 0
 
 
+def c5_bf16_block(rank: int, steps: int, warmup: int) -> dict:
+    """The head-dim-256 shape of c5_block in bf16 (no quantisation): the fused sweep
+    (attn_fwd_16bit_sweep<bf16,256,4>, 32-key tiles) with its kernel clocked, and the per-step
+    form with the incremental merge."""
+    import torch
+
+    from fa4_ring import LocalKVRing, RingConfig, ring_flash_attn, zigzag_shard
+
+    n, cp, hq, hkv, d = 262144, 8, 16, 2, 256
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(2)
+    q = torch.randn(n, hq, d, device=dev, generator=g, dtype=torch.bfloat16)
+    k = torch.randn(n, hkv, d, device=dev, generator=g, dtype=torch.bfloat16)
+    v = torch.randn(n, hkv, d, device=dev, generator=g, dtype=torch.bfloat16)
+    lq = zigzag_shard(q, rank, cp)
+    del q
+    ring = LocalKVRing.from_full(k, v, cp)
+    del k, v
+    t_local = n // cp
+    flops = sweep_flops(t_local, cp, hq, d)
+
+    def run(fused):
+        return ring_flash_attn(lq, ring.k[rank], ring.v[rank], RingConfig(cp_size=cp, cp_rank=rank),
+                               group=ring, fused=fused)
+
+    clock = KernelClock()
+    sec = timed_sweeps(lambda: run(True), steps, warmup, clock)
+    sw_ms = clock.mean_ms("sweep_kernel")
+    seci = timed_sweeps(lambda: run(False), max(3, steps // 2), 2)
+    kt = flops / (sw_ms * 1e-3) / 1e12
+    out = {
+        "workload": f"bf16 causal zig-zag ring sweep, one rank's share of cp_size={cp} over N={n} (local {t_local} "
+                    f"tokens), H_q={hq}, H_kv={hkv}, D={d}, rank {rank}",
+        "ms_per_step": round(sec * 1e3, 3), "TFLOP/s": round(flops / sec / 1e12, 2),
+        "frac_of_peak": round(flops / sec / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "sweep_kernel": {"kernel": "attn_fwd_16bit_sweep<bf16,256,4>", "avg_launch_ms": round(sw_ms, 4),
+                         "TFLOP/s": round(kt, 2), "frac": round(kt / PEAK_BF16_TFLOPS, 4)},
+        "per_step_incremental": {"ms_per_step": round(seci * 1e3, 3), "TFLOP/s": round(flops / seci / 1e12, 2)},
+    }
+    del ring, lq
+    return out
+
+
 def bench_c5(args) -> int:
     block = c5_block(args.rank, args.steps, args.warmup, not args.no_cpu_baseline)
+    block["bf16_d256"] = c5_bf16_block(args.rank, max(3, args.steps // 2), 2)
     config = {"workload": block["workload"] + ", fused sweep kernel", "global_batch": 1, "seq_len": 262144,
               "cp_size": 8, "cp_rank": args.rank, "h_q": 16, "h_kv": 2, "head_dim": 256,
               "parallelism": "cp8 (one rank's share on 1 GPU)"}
@@ -701,7 +745,7 @@ def main():
                          "CPU case (N=2048, cp_size 4) on every rank, with the oracle's CPU time; c3: "
                          "the e4m3 sweep at the c2 shape (ranks 3 and 7); c4: "
                          "packed bf16 sequences (8 lengths, cp_size 4); c5: the e4m3 N=262144, H_q=16, "
-                         "H_kv=2, D=256 sweep; paged: the c2 and c3 sweeps over paged K/V caches against "
+                         "H_kv=2, D=256 sweep (and the same shape in bf16); paged: the c2 and c3 sweeps over paged K/V caches against "
                          "contiguous shards")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -900,6 +944,8 @@ def main():
         result["c4_varlen_bf16"] = c4_block(3, args.steps, args.warmup, not args.no_cpu_baseline)
         torch.cuda.synchronize()
         result["c5_fp8_d256"] = c5_block(3, max(3, args.steps // 2), 2, not args.no_cpu_baseline)
+        torch.cuda.synchronize()
+        result["c5_bf16_d256"] = c5_bf16_block(3, max(3, args.steps // 2), 2)
         torch.cuda.synchronize()
         result["backward_bf16"] = bwd_block(rank, args.steps, args.warmup)
         torch.cuda.synchronize()

@@ -49,6 +49,10 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kBN = 64;  // keys per tile
+// Keys per tile of the V^T ping-pong pipeline: 64, or 32 at head dim 256, where a wavefront's
+// 32 x 256 fp32 output already takes 128 VGPRs and its Q fragments 64.
+template <int D>
+constexpr int vt_bn() { return D > 128 ? 32 : kBN; }
 
 struct AttnParams {
   const void* q;
@@ -1012,8 +1016,10 @@ __device__ __forceinline__ void vt_pipeline(const Geo& geo, const T* q, int64_t 
                                             int k_rsb, int vt_rsb, float scale) {
   using Ops = MfmaOps<T>;
   using frag = typename Ops::frag;
-  constexpr int BN = kBN;
+  constexpr int BN = vt_bn<D>();
   constexpr int CH = D / 8;
+  constexpr int VCH = BN * (int)sizeof(T) / 16;  // 16-byte chunks of a V^T tile row
+  constexpr int VRPB = 16 / VCH;                 // V^T tile rows per 256 bytes (the LDS banks' width)
   constexpr int NLD = BN * CH / 64;  // wave-wide LDS-DMA loads per K (or V^T) tile
   constexpr int NMT = BN / 32;
   constexpr int NDT = D / 32;
@@ -1021,8 +1027,8 @@ __device__ __forceinline__ void vt_pipeline(const Geo& geo, const T* q, int64_t 
   constexpr int NPS = BN / 16;
   constexpr int KS = 4, VS = 3;      // LDS slots of K and V^T tiles
   constexpr int TILE = BN * D;       // elements of one K or V^T tile
-  static_assert(D <= 128, "ping-pong kernel holds one 32 x D output tile per wavefront");
-  static_assert(BN * (int)sizeof(T) == 128, "V^T rows are 8 chunks");
+  static_assert(D <= 256 && BN * D <= 64 * 128, "ping-pong kernel holds one 32 x D output tile per wavefront");
+  static_assert(VCH == 4 || VCH == 8, "V^T tile rows of 4 or 8 chunks");
   static_assert(NLD % 4 == 0 && NLD % kPPWaves == 0, "tile loads must split over the wavefronts");
   // s_waitcnt: LDS reads done; this wavefront's loads of its latest VALU phase may remain
   constexpr int kWaitOlder = (NLD / 4) | (7 << 4);
@@ -1061,9 +1067,11 @@ __device__ __forceinline__ void vt_pipeline(const Geo& geo, const T* q, int64_t 
     const int row = P / CH, c = (P % CH) ^ ksw16<CH>(row);
     return row * k_rsb + 16 * c;
   };
+  // V^T tile row d holds its chunk c at slot c ^ ((d / VRPB) % VCH): the VCH rows that share
+  // a 256-byte bank span (and the 16 lanes reading them together) then hit distinct banks
   auto v_voff = [&](int w, int nw, int n) __attribute__((always_inline)) {
     const int P = 64 * (w + nw * n) + lane;
-    const int d = P >> 3, c = (P & 7) ^ ((d >> 1) & 7);
+    const int d = P / VCH, c = (P % VCH) ^ ((d / VRPB) % VCH);
     return d * vt_rsb + 16 * c;
   };
 
@@ -1091,7 +1099,7 @@ __device__ __forceinline__ void vt_pipeline(const Geo& geo, const T* q, int64_t 
   for (int t = 0; t < NKS; ++t) k_off[t] = kr * D + 8 * ((2 * t + lh) ^ ksw16<CH>(kr));
   int v_off[NPS];
 #pragma unroll
-  for (int t = 0; t < NPS; ++t) v_off[t] = lq * BN + 8 * ((2 * t + lh) ^ ((lq >> 1) & 7));
+  for (int t = 0; t < NPS; ++t) v_off[t] = lq * BN + 8 * ((2 * t + lh) ^ ((lq / VRPB) % VCH));
 
   const float c_log2 = scale * kLog2e;
   f32x16 o[NDT];
@@ -1261,7 +1269,7 @@ struct OneSegment {
 
 template <typename T, int D, int HP>
 __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_vt(AttnParams p) {
-  constexpr int BN = kBN;
+  constexpr int BN = vt_bn<D>();
   constexpr int RB = kPPWaves / HP;  // 32-row blocks per workgroup
   int hg, seq, rt;
   decode_block(p, hg, seq, rt);
@@ -1286,7 +1294,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_vt(AttnParams p)
     const int kmax = min(row_tile0 + RB * 32, Lq) - 1 + off;
     geo.g.tiles = kmax < 0 ? 0 : min(geo.g.tiles, kmax / BN + 1);
   }
-  geo.g.first_mask = mask_free_tiles(geo.g.tiles, Lk, p.causal, row_tile0, off);
+  geo.g.first_mask = mask_free_tiles<BN>(geo.g.tiles, Lk, p.causal, row_tile0, off);
   geo.g.off = p.causal ? off : kNoCausal;
   geo.g.qmin = 0;
   geo.g.kd = geo.g.vd = 1.f;
@@ -1397,7 +1405,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_sweep(SweepParam
   const int head = kvh * p.group + (hg - kvh * groups_per_kv) * HP + (wave % HP);
   const int r0 = row_tile0 + (wave / HP) * 32;
 
-  RingSegments<kBN, PAGED> geo;
+  RingSegments<vt_bn<D>(), PAGED> geo;
   geo.p = &p;
   geo.L = L;
   geo.row_tile0 = row_tile0;
@@ -2567,7 +2575,7 @@ struct KernelChoice {
 template <typename T>
 KernelChoice pick16(int d, int hp, bool vt) {
   KernelChoice k;
-  if (vt && (d == 64 || d == 128)) {
+  if (vt && (d == 64 || d == 128 || d == 256)) {
     k.threads = kPPThreads;
     k.rows = 32 * kPPWaves / hp;
 #define FA4CP_PICK(DD)                                  \
@@ -2578,6 +2586,7 @@ KernelChoice pick16(int d, int hp, bool vt) {
   }
     FA4CP_PICK(64)
     FA4CP_PICK(128)
+    FA4CP_PICK(256)
 #undef FA4CP_PICK
   } else if (d == 64 || d == 128) {
     k.threads = kPPThreads;
@@ -2756,8 +2765,8 @@ static int ring_sweep_launch(const fa4cp_sweep_args* a, const fa4cp_sweep_kpages
   const bool fp8 = a->dtype == FA4CP_E4M3;
   if (a->dtype != FA4CP_BF16 && a->dtype != FA4CP_FP16 && !fp8)
     return set_error(FA4CP_EUNSUPPORTED, "ring_sweep_fwd: dtype %d (BF16 / FP16 / E4M3 only)", a->dtype);
-  if (fp8 ? (d != 128 && d != 256) : (d != 64 && d != 128))
-    return set_error(FA4CP_EUNSUPPORTED, "ring_sweep_fwd: head dim %d (64 / 128 for BF16 / FP16, 128 / 256 for E4M3)", d);
+  if (fp8 ? (d != 128 && d != 256) : (d != 64 && d != 128 && d != 256))
+    return set_error(FA4CP_EUNSUPPORTED, "ring_sweep_fwd: head dim %d (64 / 128 / 256 for BF16 / FP16, 128 / 256 for E4M3)", d);
   {
     // element sizes: q / k 1 (e4m3) or 2; out 2 (bf16 for e4m3)
     const int esz = fp8 ? 1 : 2;
@@ -2827,10 +2836,12 @@ static int ring_sweep_launch(const fa4cp_sweep_args* a, const fa4cp_sweep_kpages
     else FA4CP_PICK_HP(attn_fwd_e4m3_sweep, 256)
   } else if (a->dtype == FA4CP_BF16) {
     if (d == 64) FA4CP_PICK_HP(attn_fwd_16bit_sweep, __bf16, 64)
-    else FA4CP_PICK_HP(attn_fwd_16bit_sweep, __bf16, 128)
+    else if (d == 128) FA4CP_PICK_HP(attn_fwd_16bit_sweep, __bf16, 128)
+    else FA4CP_PICK_HP(attn_fwd_16bit_sweep, __bf16, 256)
   } else {
     if (d == 64) FA4CP_PICK_HP(attn_fwd_16bit_sweep, _Float16, 64)
-    else FA4CP_PICK_HP(attn_fwd_16bit_sweep, _Float16, 128)
+    else if (d == 128) FA4CP_PICK_HP(attn_fwd_16bit_sweep, _Float16, 128)
+    else FA4CP_PICK_HP(attn_fwd_16bit_sweep, _Float16, 256)
   }
 #undef FA4CP_PICK_HP
   hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kPPThreads), 0, (hipStream_t)stream, p);

@@ -26,7 +26,7 @@ from ._lib import SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF
 SUPPORTED_HEAD_DIMS = {torch.bfloat16: (64, 128, 256), torch.float16: (64, 128, 256),
                        torch.float8_e4m3fn: (128, 256)}
 # (dtype, head dim) pairs whose kernels read a pre-transposed V^T (fa4cp_transpose_v)
-VT_HEAD_DIMS = {torch.bfloat16: (64, 128), torch.float16: (64, 128), torch.float8_e4m3fn: (128, 256)}
+VT_HEAD_DIMS = {torch.bfloat16: (64, 128, 256), torch.float16: (64, 128, 256), torch.float8_e4m3fn: (128, 256)}
 
 
 def has_fa4() -> bool:

@@ -132,7 +132,7 @@ def ring_flash_attn(
 
     ``fused`` (default: whenever supported) runs the whole sweep as one kernel over every
     source's K / V^T (``ring_sweep``): no per-step partials, no merges.  It needs
-    cp_size in [2, 16] with a LocalKVRing and either bf16 / fp16 with head dim 64 or 128 and
+    cp_size in [2, 16] with a LocalKVRing and either bf16 / fp16 with head dim 64, 128 or 256 and
     no descales, or e4m3 with head dim 128 or 256 (any descales); ``fused=False`` runs the
     per-step path of the reference (attention + LSE merge per step), which covers every
     case.  ``cfg.merge_mode`` chooses how the per-step path merges its partials
@@ -169,7 +169,7 @@ def ring_flash_attn(
     d = local_q.shape[2]
     e4m3 = local_q.dtype == torch.float8_e4m3fn
     can_fuse = 1 < S <= _lib.MAX_CP and (
-        (descales is None and local_q.dtype in (torch.bfloat16, torch.float16) and d in (64, 128))
+        (descales is None and local_q.dtype in (torch.bfloat16, torch.float16) and d in (64, 128, 256))
         or (e4m3 and d in (128, 256)))
     def finish(out, lse):
         return (out, lse) if return_lse else out
@@ -181,7 +181,7 @@ def ring_flash_attn(
                                            descales=descales), lse)
         if fused:
             raise AssertionError("fused ring sweep needs cp_size in [2, 16] and bf16/fp16 with head dim "
-                                 "64/128 and no descales, or e4m3 with head dim 128/256")
+                                 "64/128/256 and no descales, or e4m3 with head dim 128/256")
         # the per-step form reads contiguous shards: gather every source's K and V pages first
         group = LocalKVRing(gather_kv_pages(group, "k", total, cu_seqlens, max_seqlen),
                             gather_kv_pages(group, "v", total, cu_seqlens, max_seqlen))
@@ -189,7 +189,7 @@ def ring_flash_attn(
         fused = False
     if fused and not can_fuse:
         raise AssertionError("fused ring sweep needs cp_size in [2, 16] and bf16/fp16 with head dim "
-                             "64/128 and no descales, or e4m3 with head dim 128/256")
+                             "64/128/256 and no descales, or e4m3 with head dim 128/256")
     if fused is None:
         fused = can_fuse
     if fused:

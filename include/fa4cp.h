@@ -208,7 +208,7 @@ int fa4cp_transpose_v_paged_many(const fa4cp_paged_args* args, const void* const
  * partial results and no merges: every workgroup carries its online softmax across the
  * sources.  k[i] is source rank i's local K shard and v_t[i] its V^T (fa4cp_transpose_v with
  * k_sel = ALL over the same cu); all shards share strides and the local sequence layout cu.
- * BF16 / FP16 with d = 64 or 128, or E4M3 with d = 128 (bf16 out; q_descale [h_kv] and the
+ * BF16 / FP16 with d = 64, 128 or 256, or E4M3 with d = 128 or 256 (bf16 out; q_descale [h_kv] and the
  * per-source k_descale / v_descale [cp_size][h_kv], any of them NULL for 1, as the
  * reference's Descales: ring_attention.py:43-52, fa4_backend.py:45-55); cp_size <=
  * FA4CP_MAX_CP.

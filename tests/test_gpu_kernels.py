@@ -385,6 +385,11 @@ ATTN_CASES = [
     (None, None, 8, 2, 128, True, SEL_ALL, SEL_ALL, [0, 64, 64, 200, 200]),         # empty seqs
     (None, None, 8, 2, 64, False, SEL_BACK_HALF, SEL_ALL, [0, 0, 130, 131, 260]),   # 1-row seq
     (None, None, 4, 1, 128, False, SEL_ALL, SEL_FRONT_HALF, [0, 1, 1, 67]),         # no keys
+    # head dim 256 (32-key tiles when V^T is given)
+    (512, 512, 8, 2, 256, False, SEL_ALL, SEL_FRONT_HALF, None),
+    (72, 100, 4, 2, 256, True, SEL_ALL, SEL_ALL, None),           # bottom-right causal, tails
+    (None, None, 4, 2, 256, True, SEL_ALL, SEL_ALL, [0, 64, 200, 202, 460]),
+    (None, None, 8, 1, 256, False, SEL_BACK_HALF, SEL_ALL, [0, 0, 130, 131, 260]),
 ]
 
 

@@ -121,6 +121,7 @@ RING_CASES = [  # (dtype, d, cp, full lengths (None: one sequence of n), n, page
     (torch.float16, 128, 8, None, 4096, 128, False),
     (torch.float8_e4m3fn, 128, 4, [1024, 520, 2048], 0, 128, True),
     (torch.float8_e4m3fn, 256, 2, None, 1024, 256, True),
+    (torch.bfloat16, 256, 4, [768, 1280], 0, 128, False),
 ]
 
 
@@ -221,6 +222,7 @@ WALK_CASES = [  # (dtype, d, cp, rank, page_size, local sequence lengths, extra 
     (torch.float8_e4m3fn, 128, 4, 3, 384, [1152, 514], 2),   # three 128-key tiles per page
     (torch.float8_e4m3fn, 128, 2, 0, 128, [1024], 0),        # one tile per page: every step a new page
     (torch.float8_e4m3fn, 256, 3, 2, 128, [896], 0),         # two 64-key tiles per page
+    (torch.bfloat16, 256, 4, 1, 128, [640, 386], 1),         # four 32-key tiles per page
 ]
 
 

@@ -27,6 +27,7 @@ SMALL_CASES = [  # (N, H, H_kv, D, cp): the reference's CPU cases' structure at 
     (2048, 8, 2, 128, 4),  # the CPU benchmark configuration's shape
     (1024, 16, 2, 128, 4), (1024, 16, 1, 64, 2),  # GQA 8 and 16 query heads per kv head
     (2048, 4, 2, 128, 16),  # the largest ring the fused sweep takes
+    (1024, 8, 2, 256, 4), (512, 4, 4, 256, 2), (2048, 16, 2, 256, 8),  # head dim 256 (32-key tiles)
 ]
 
 
@@ -153,11 +154,12 @@ def test_ring_cp1_is_causal_attention():
     assert max_err(out, O.dense_causal(q, k, v, scale_for(128))) <= TOL_BF16_OUT
 
 
+@pytest.mark.parametrize("d", [128, 256])
 @pytest.mark.parametrize("mode", PATHS)
-def test_ring_varlen_all_ranks(mode):
+def test_ring_varlen_all_ranks(mode, d):
     lens = [608, 1216, 1072, 608, 232, 1928, 344, 200]  # the packed benchmark lengths / 8
-    cp, h, hkv, d = 4, 8, 2, 128
-    say(f"ring varlen lens={lens} cp={cp} path={mode}")
+    cp, h, hkv = 4, 8, 2
+    say(f"ring varlen lens={lens} cp={cp} d={d} path={mode}")
     full_cu = [0]
     for n in lens:
         full_cu.append(full_cu[-1] + n)
@@ -322,13 +324,15 @@ def test_ring_fp8_row_max_grows_inside_a_later_source(growth, mode):
     assert max_err(out, ref) <= TOL_FP8_OUT
 
 
+@pytest.mark.parametrize("d", [128, 256])
 @pytest.mark.parametrize("mode", PATHS)
 @pytest.mark.parametrize("growth", [5.0, 8.8, 150.0])
-def test_ring_bf16_row_max_grows_mid_sweep(growth, mode):
-    """As the e4m3 case above in bf16 (64-key tiles): the row max jumps by `growth` (log2
-    units) on key 300 of source 0, the fifth tile of rank 1's second step."""
-    n, h, hkv, d, cp, rank = 2048, 2, 1, 128, 2, 1
-    say(f"ring bf16 late max growth={growth} path={mode}")
+def test_ring_bf16_row_max_grows_mid_sweep(growth, mode, d):
+    """As the e4m3 case above in bf16: the row max jumps by `growth` (log2 units) on key 300 of
+    source 0, inside rank 1's second step (its fifth 64-key tile at head dim 128, its tenth
+    32-key tile at 256)."""
+    n, h, hkv, cp, rank = 2048, 2, 1, 2, 1
+    say(f"ring bf16 late max growth={growth} d={d} path={mode}")
     g = torch.Generator().manual_seed(9)
     u = torch.randn(d, generator=g)
     u = u / u.norm()
@@ -468,6 +472,27 @@ def _fp8_full_size(n, cp, hq, hkv, d, rank, forms, seed):
 def test_ring_c3_fp8_full_size(rank):
     say(f"ring C3 e4m3 n=131072 rank={rank}")
     _fp8_full_size(131072, 8, 32, 8, 128, rank, ("fused", "incremental"), seed=1)
+
+
+def test_ring_c5_bf16_d256_full_size():
+    """The C5 shape (N=262144, cp 8, H 16/2, D 256) in bf16, rank 3: the fused sweep (32-key
+    tiles) against the per-step form on every row, and sampled rows of every 64-row tile
+    against dense causal attention."""
+    n, cp, hq, hkv, d, rank = 262144, 8, 16, 2, 256, 3
+    say(f"ring C5-shape bf16 d={d} n={n} rank={rank}")
+    gen = torch.Generator(device=DEV).manual_seed(4)
+    q = torch.randn(n, hq, d, device=DEV, generator=gen, dtype=torch.bfloat16)
+    k = torch.randn(n, hkv, d, device=DEV, generator=gen, dtype=torch.bfloat16)
+    v = torch.randn(n, hkv, d, device=DEV, generator=gen, dtype=torch.bfloat16)
+    ring = LocalKVRing.from_full(k, v, cp)
+    lq = zigzag_shard(q, rank, cp)
+    del q
+    outs = _run_forms(lq, ring, cp, rank, ("fused", "incremental"))
+    _check_forms_agree(f"C5-shape bf16 rank {rank}", "fused", outs, TOL_BF16_OUT)
+    rows = _tile_rows(lq.shape[0], seed=rank + 20)
+    grow = O.zigzag_rows(n, rank, cp)
+    _check_tiles(f"C5-shape bf16 rank {rank}", outs, lq.float().cpu(), rows, [int(grow[i]) for i in rows],
+                 [0] * len(rows), k.float().cpu(), v.float().cpu(), scale_for(d), TOL_BF16_OUT)
 
 
 def test_ring_c5_fp8_d256_full_size():

@@ -359,14 +359,14 @@ def test_ring_without_local_kv_source_raises():
 
 def test_fused_sweep_rejects_what_it_does_not_cover():
     """fused=True is refused (AssertionError, before any device work) outside the fused
-    kernel's cases: fp32, a head dim other than 64/128 (bf16) or 128/256 (e4m3), cp_size 1 or
-    above 16, bf16 with descales."""
+    kernel's cases: fp32, a head dim other than 64/128/256 (bf16) or 128/256 (e4m3), cp_size 1
+    or above 16, bf16 with descales."""
     cfg = RingConfig(cp_size=2, cp_rank=0)
 
     def ring_of(x):
         return LocalKVRing([x, x], [x, x])
 
-    for dt, d in [(torch.float32, 128), (torch.bfloat16, 256), (torch.float8_e4m3fn, 64)]:
+    for dt, d in [(torch.float32, 128), (torch.bfloat16, 96), (torch.float8_e4m3fn, 64)]:
         x = torch.zeros(16, 2, d, dtype=dt)
         with pytest.raises(AssertionError, match="fused ring sweep"):
             ring_flash_attn(x, x, x, cfg, group=ring_of(x), fused=True)
