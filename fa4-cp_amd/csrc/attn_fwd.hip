@@ -1026,15 +1026,30 @@ __device__ __forceinline__ void vt_pipeline(const Geo& geo, const T* q, int64_t 
   constexpr int NKS = D / 16;
   constexpr int NPS = BN / 16;
   constexpr int KS = 4, VS = 3;      // LDS slots of K and V^T tiles
-  constexpr int TILE = BN * D;       // elements of one K or V^T tile
+  constexpr int TILE = BN * D;       // elements of one V^T tile (and of a K tile unpadded)
+  // K tile rows in LDS.  Up to head dim 128: D elements, chunk c of row r at slot c ^ ksw16(r).
+  // At 256 (KPAD): rows of D elements + 16 bytes, unswizzled, so that row r starts r slots
+  // into the bank span and a fragment's 16 lanes still hit distinct banks, while the
+  // fragments of a lane differ by constant offsets: one address register instead of one per
+  // fragment (the 256-VGPR kernel has none to spare).  The slot is rounded up to whole 4 KB
+  // (one LDS-DMA per wavefront of a group); its pad and tail slots receive copies of real
+  // chunks and are never read.
+  constexpr bool KPAD = D > 128;  // (and LDS fragment reads 2 MFMAs ahead instead of 4: at 256
+                                  // VGPRs the compiler holds no more, and gives up on any deeper)
+  constexpr int KRB = D * (int)sizeof(T) + (KPAD ? 16 : 0);                // bytes per K row in LDS
+  constexpr int KSLOT = KPAD ? (BN * KRB + 4095) / 4096 * 4096 : TILE * (int)sizeof(T);  // bytes
+  constexpr int NLDK = KSLOT / 1024;  // wave-wide LDS-DMA loads per K tile
   static_assert(D <= 256 && BN * D <= 64 * 128, "ping-pong kernel holds one 32 x D output tile per wavefront");
   static_assert(VCH == 4 || VCH == 8, "V^T tile rows of 4 or 8 chunks");
-  static_assert(NLD % 4 == 0 && NLD % kPPWaves == 0, "tile loads must split over the wavefronts");
-  // s_waitcnt: LDS reads done; this wavefront's loads of its latest VALU phase may remain
-  constexpr int kWaitOlder = (NLD / 4) | (7 << 4);
-  static_assert(NLD / 4 < 16, "vmcnt field");
+  static_assert(NLD % 4 == 0 && NLD % kPPWaves == 0 && NLDK % 4 == 0, "tile loads must split over the wavefronts");
+  static_assert(KS * KSLOT + VS * TILE * (int)sizeof(T) <= 160 * 1024, "LDS");
+  // s_waitcnt: LDS reads done; this wavefront's loads of its latest VALU phase may remain (a
+  // K-loading wavefront issues NLDK / 4 per phase, a V^T-loading one NLD / 4; the smaller
+  // count is the safe wait for both)
+  constexpr int kWaitOlder = ((NLD < NLDK ? NLD : NLDK) / 4) | (7 << 4);
+  static_assert(NLDK / 4 < 16, "vmcnt field");
 
-  __shared__ __attribute__((aligned(1024))) T kl[KS][TILE];
+  __shared__ __attribute__((aligned(1024))) T kl[KS][KSLOT / sizeof(T)];
   __shared__ __attribute__((aligned(1024))) T vtl[VS][TILE];
 
   const int tid = threadIdx.x;
@@ -1064,8 +1079,17 @@ __device__ __forceinline__ void vt_pipeline(const Geo& geo, const T* q, int64_t 
   // LDS chunks [64 (w + nw n), +64) of the tile)
   auto k_voff = [&](int w, int nw, int n) __attribute__((always_inline)) {
     const int P = 64 * (w + nw * n) + lane;
-    const int row = P / CH, c = (P % CH) ^ ksw16<CH>(row);
-    return row * k_rsb + 16 * c;
+    if constexpr (KPAD) {
+      int row = 16 * P / KRB, cb = 16 * P % KRB;
+      if (row >= BN || cb >= D * (int)sizeof(T)) {  // a pad or tail slot: any chunk of the tile
+        row = min(row, BN - 1);
+        cb = 0;
+      }
+      return row * k_rsb + cb;
+    } else {
+      const int row = P / CH, c = (P % CH) ^ ksw16<CH>(row);
+      return row * k_rsb + 16 * c;
+    }
   };
   // V^T tile row d holds its chunk c at slot c ^ ((d / VRPB) % VCH): the VCH rows that share
   // a 256-byte bank span (and the 16 lanes reading them together) then hit distinct banks
@@ -1080,9 +1104,15 @@ __device__ __forceinline__ void vt_pipeline(const Geo& geo, const T* q, int64_t 
 #pragma unroll
   for (int i = 0; i < KS - 1; ++i) {
     const auto r = walk.rsrc(kc, true);
+    if constexpr (KPAD) {
 #pragma unroll
-    for (int n = 0; n < NLD / kPPWaves; ++n)
-      dma16(r, kl[i] + 512 * (wave + kPPWaves * n), k_voff(wave, kPPWaves, n));
+      for (int n = 0; n < (NLDK + kPPWaves - 1) / kPPWaves; ++n)
+        if (wave + kPPWaves * n < NLDK) dma16(r, kl[i] + 512 * (wave + kPPWaves * n), k_voff(wave, kPPWaves, n));
+    } else {
+#pragma unroll
+      for (int n = 0; n < NLD / kPPWaves; ++n)
+        dma16(r, kl[i] + 512 * (wave + kPPWaves * n), k_voff(wave, kPPWaves, n));
+    }
     walk.template step<true>(kc, true, 0);
   }
 #pragma unroll
@@ -1094,9 +1124,13 @@ __device__ __forceinline__ void vt_pipeline(const Geo& geo, const T* q, int64_t 
     walk.template step<true>(vc, false, 0);
   }
   const int kr = swap_bits23(lq);
-  int k_off[NKS];
+  int k_off[KPAD ? 1 : NKS];  // elements from the slot start to fragment t's 16 bytes
+  if constexpr (KPAD) {
+    k_off[0] = (kr * KRB + 16 * lh) / (int)sizeof(T);  // fragment t: + 16 t
+  } else {
 #pragma unroll
-  for (int t = 0; t < NKS; ++t) k_off[t] = kr * D + 8 * ((2 * t + lh) ^ ksw16<CH>(kr));
+    for (int t = 0; t < NKS; ++t) k_off[t] = kr * D + 8 * ((2 * t + lh) ^ ksw16<CH>(kr));
+  }
   int v_off[NPS];
 #pragma unroll
   for (int t = 0; t < NPS; ++t) v_off[t] = lq * BN + 8 * ((2 * t + lh) ^ ((lq / VRPB) % VCH));
@@ -1121,7 +1155,7 @@ __device__ __forceinline__ void vt_pipeline(const Geo& geo, const T* q, int64_t 
     for (int t = 0; t < NKS; ++t)
 #pragma unroll
       for (int mt = 0; mt < NMT; ++mt) {
-        const frag a = *reinterpret_cast<const frag*>(ksrc + k_off[t] + 32 * mt * D);
+        const frag a = *reinterpret_cast<const frag*>(ksrc + (KPAD ? k_off[0] + 16 * t : k_off[t] + 32 * mt * D));
         s[mt] = Ops::mma(a, qf[t], s[mt]);
       }
   };
@@ -1168,9 +1202,10 @@ __device__ __forceinline__ void vt_pipeline(const Geo& geo, const T* q, int64_t 
   auto run = [&](bool ISK) __attribute__((always_inline)) {
     LoadCursor lc = ISK ? kc : vc;
     int pend = -1;  // paged K: the page entry lc's next page event takes
-    int ld_voff[NLD / 4];
+    constexpr int NLDX = (NLD > NLDK ? NLD : NLDK) / 4;  // loads per phase of either role
+    int ld_voff[NLDX];
 #pragma unroll
-    for (int n = 0; n < NLD / 4; ++n) ld_voff[n] = ISK ? k_voff(wi, 4, n) : v_voff(wi, 4, n);
+    for (int n = 0; n < NLDX; ++n) ld_voff[n] = ISK ? k_voff(wi, 4, n) : v_voff(wi, 4, n);
     T* const ld_base = ISK ? kl[0] : vtl[0];
     const int ld_slots = ISK ? KS : VS;
     int ld_slot = ld_slots - 1;
@@ -1184,7 +1219,7 @@ __device__ __forceinline__ void vt_pipeline(const Geo& geo, const T* q, int64_t 
       qk(kl[j & (KS - 1)]);
       if constexpr (decltype(with_pv)::value) {
         pv(vtl[vr]);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kPPReadAhead, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, KPAD ? 2 : kPPReadAhead, 0);
 #pragma unroll
         for (int i = 0; i < NMT * NKS + NDT * NPS; ++i) {
           __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
@@ -1205,9 +1240,16 @@ __device__ __forceinline__ void vt_pipeline(const Geo& geo, const T* q, int64_t 
         if (ISK) pend = walk.prefetch(lc);  // in flight through the VALU phase
       }
       wg_barrier();
-      T* const dst = ld_base + ld_slot * TILE;
+      if constexpr (KPAD) {
+        T* const dst = ld_base + ld_slot * (ISK ? KSLOT / (int)sizeof(T) : TILE);
 #pragma unroll
-      for (int n = 0; n < NLD / 4; ++n) dma16(r, dst + 512 * (wi + 4 * n), ld_voff[n]);
+        for (int n = 0; n < NLDX; ++n)
+          if (n < (ISK ? NLDK : NLD) / 4) dma16(r, dst + 512 * (wi + 4 * n), ld_voff[n]);
+      } else {
+        T* const dst = ld_base + ld_slot * TILE;
+#pragma unroll
+        for (int n = 0; n < NLD / 4; ++n) dma16(r, dst + 512 * (wi + 4 * n), ld_voff[n]);
+      }
       ld_slot = ld_slot + 1 == ld_slots ? 0 : ld_slot + 1;
       if (__builtin_expect(masked, 0)) mask();
       tile_max_rescale<NMT, NDT>(s, o, m, lsum, c_log2);
