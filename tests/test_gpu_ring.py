@@ -28,6 +28,7 @@ SMALL_CASES = [  # (N, H, H_kv, D, cp): the reference's CPU cases' structure at 
     (1024, 16, 2, 128, 4), (1024, 16, 1, 64, 2),  # GQA 8 and 16 query heads per kv head
     (2048, 4, 2, 128, 16),  # the largest ring the fused sweep takes
     (1024, 8, 2, 256, 4), (512, 4, 4, 256, 2), (2048, 16, 2, 256, 8),  # head dim 256 (32-key tiles)
+    (1024, 4, 2, 256, 4),  # head dim 256, two query heads per kv head
 ]
 
 
@@ -69,6 +70,32 @@ def test_ring_all_ranks_small(n, h, hkv, d, cp, mode):
         outs.append(out.float().cpu())
     dense = O.dense_causal(q, k, v, scale)
     assert max_err(O.zigzag_unshard(outs, cp), dense) <= TOL_BF16_OUT
+
+
+@pytest.mark.parametrize("mode", PATHS)
+@pytest.mark.parametrize("d", [128, 256])
+def test_ring_fp16_all_ranks(d, mode):
+    """fp16 inputs and out on every rank of a cp 4 ring, at both 64-key (D 128) and 32-key
+    (D 256) tiles, against the oracle at the fp16 bar (5e-3) and dense causal attention."""
+    n, h, hkv, cp = 1024, 8, 2, 4
+    say(f"ring fp16 n={n} h={h}/{hkv} d={d} cp={cp} path={mode}")
+    q, k, v = O.random_qkv(n, h, hkv, d, seed=6)
+    q, k, v = (rounded(t, torch.float16) for t in (q, k, v))
+    scale = scale_for(d)
+    qd, ring = _device_ring(q, k, v, cp, torch.float16)
+    ks = [O.zigzag_shard(k, r, cp) for r in range(cp)]
+    vs = [O.zigzag_shard(v, r, cp) for r in range(cp)]
+    outs = []
+    for rank in range(cp):
+        cfg, fused = _cfg_path(mode, cp, rank)
+        out, lse = ring_flash_attn(zigzag_shard(qd, rank, cp), ring.k[rank], ring.v[rank], cfg, group=ring,
+                                   fused=fused, return_lse=True)
+        assert out.dtype == torch.float16
+        ref, ref_lse = O.ring_rank(O.zigzag_shard(q, rank, cp), ks, vs, rank, cp, scale, merge_mode=cfg.merge_mode)
+        assert max_err(out, ref) <= 5e-3, f"rank {rank}"
+        assert lse_err(lse, ref_lse) <= TOL_LSE, f"rank {rank} lse"
+        outs.append(out.float().cpu())
+    assert max_err(O.zigzag_unshard(outs, cp), O.dense_causal(q, k, v, scale)) <= 5e-3
 
 
 @functools.lru_cache(maxsize=4)
