@@ -563,8 +563,8 @@ def bench_c4(args) -> int:
 
 def c5_bf16_block(rank: int, steps: int, warmup: int) -> dict:
     """The head-dim-256 shape of c5_block in bf16 (no quantisation): the fused sweep
-    (attn_fwd_16bit_sweep<bf16,256,4>, 32-key tiles) with its kernel clocked, and the per-step
-    form with the incremental merge."""
+    (attn_fwd_16bit_sweep<bf16,256,4>, 32-key tiles) with its kernel clocked, the per-step
+    form with the incremental merge, and the backward (FLOPs counted as 2.5 x the forward's)."""
     import torch
 
     from fa4_ring import LocalKVRing, RingConfig, ring_flash_attn, zigzag_shard
@@ -591,6 +591,19 @@ def c5_bf16_block(rank: int, steps: int, warmup: int) -> dict:
     sw_ms = clock.mean_ms("sweep_kernel")
     seci = timed_sweeps(lambda: run(False), max(3, steps // 2), 2)
     kt = flops / (sw_ms * 1e-3) / 1e12
+    # the backward of the same sweep (dq and every source's dk / dv contribution, fp32)
+    from fa4_ring.backward import ring_flash_attn_backward
+
+    cfg = RingConfig(cp_size=cp, cp_rank=rank)
+    o, lse = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, return_lse=True)
+    dout = torch.randn(lq.shape, device=dev, generator=g, dtype=torch.bfloat16)
+    dq = torch.empty(lq.shape, dtype=torch.float32, device=dev)
+    dk = [torch.empty((t_local, hkv, d), dtype=torch.float32, device=dev) for _ in range(cp)]
+    dv = [torch.empty((t_local, hkv, d), dtype=torch.float32, device=dev) for _ in range(cp)]
+    bms = _event_ms(lambda: ring_flash_attn_backward(dout, lq, ring.k[rank], ring.v[rank], o, lse, cfg, group=ring,
+                                                     dq=dq, dk=dk, dv=dv), n=max(3, steps // 2))
+    bflops = 2.5 * flops
+    del o, lse, dout, dq, dk, dv
     out = {
         "workload": f"bf16 causal zig-zag ring sweep, one rank's share of cp_size={cp} over N={n} (local {t_local} "
                     f"tokens), H_q={hq}, H_kv={hkv}, D={d}, rank {rank}",
@@ -599,6 +612,10 @@ def c5_bf16_block(rank: int, steps: int, warmup: int) -> dict:
         "sweep_kernel": {"kernel": "attn_fwd_16bit_sweep<bf16,256,4>", "avg_launch_ms": round(sw_ms, 4),
                          "TFLOP/s": round(kt, 2), "frac": round(kt / PEAK_BF16_TFLOPS, 4)},
         "per_step_incremental": {"ms_per_step": round(seci * 1e3, 3), "TFLOP/s": round(flops / seci / 1e12, 2)},
+        "backward": {"ms_per_step": round(bms, 3), "TFLOP/s": round(bflops / (bms * 1e-3) / 1e12, 2),
+                     "frac_of_peak": round(bflops / (bms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                     "flop_per_step": bflops,
+                     "kernels": "bwd_pack_kernel + bwd_dq_kernel<bf16,256,4> + bwd_dkdv_kernel<bf16,256>"},
     }
     del ring, lq
     return out

@@ -408,12 +408,18 @@ __global__ __launch_bounds__(64 * HP) void bwd_dq_kernel(BwdParams p) {
 // into P and accumulates dV += P^T dO; the second (waves 4-7) holds V as the B operand of
 // dP = dO V^T, takes P from its partner through LDS (fp16), forms dS = P (dP - delta) and
 // accumulates dK += dS^T Q.  The workgroup walks the packed blocks of the query rows that
-// attend its keys (every query head of the kv head): block i arrives by LDS-DMA into stage
-// i % 3 one iteration ahead, and iteration i runs the products of block i that need only
-// the block (S, dP) and those of block i - 1 that need the other wavefront's result (dV,
-// dK), so the two wavefronts of a pair never wait on each other within an iteration.  One
-// barrier per iteration: block i + 1 has landed, P of block i is in LDS, and the stage of
-// block i - 1 is free for block i + 2.
+// attend its keys (every query head of the kv head).  Iteration i runs the products of block
+// i that need only the block (S, dP: its Q and dO rows) and those of block i - 1 that need
+// the other wavefront's result (dV, dK: its transposed dO and Q), so the two wavefronts of a
+// pair never wait on each other within an iteration.  One barrier per iteration: the loads
+// have landed, P of block i is in LDS, and what the iteration read is free.
+//
+// Staging.  Up to head dim 128 a whole block arrives by LDS-DMA into stage i % 3 one
+// iteration ahead (3 x 33 KB at 128).  At 256 three whole blocks do not fit the LDS, so a
+// block's row regions and transposed regions go to different half-stages, each kind
+// double-buffered by block parity: iteration i reads rows(i) and transposed(i - 1) and
+// loads rows(i + 1) and transposed(i) over those of blocks i - 1 and i - 2 (4 x 64.25 KB).
+// (The halves measured 7 % slower at 128, where whole stages fit.)
 template <typename T, int D>
 __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
   using M = BwdMfma<T>;
@@ -422,19 +428,32 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
   constexpr int NDT = D / 32;
   constexpr int R = pack_region_bytes<D>();
   constexpr int BB = pack_block_bytes<D>();
-  constexpr int CPW = 4 * NKS / 8;  // 1 KB fragments each wavefront loads per block
+  constexpr bool HALVES = D > 128;
+  constexpr int HB = 2 * R + 256;   // a half-stage: two regions and the per-row values
+  constexpr int CPW = (HALVES ? 2 : 4) * NKS / 8;  // 1 KB fragments each wavefront loads per (half-)stage
   constexpr int kWaitAll = 7 << 4;  // vmcnt(0), lgkmcnt(0)
-  static_assert(CPW * 8 == 4 * NKS, "fragments must split evenly over the wavefronts");
-  // Three stages in separate arrays: the LDS-DMA destination is chosen at run time, so the
+  static_assert(CPW * 8 == (HALVES ? 2 : 4) * NKS, "fragments must split evenly over the wavefronts");
+  // Stages in separate arrays: the LDS-DMA destination is chosen at run time, so the
   // compiler does not make the first LDS read of an iteration wait for every load in flight.
-  __shared__ __align__(16) char stage0[BB];
-  __shared__ __align__(16) char stage1[BB];
-  __shared__ __align__(16) char stage2[BB];
+  // A whole stage holds regions 0-3 then the per-row values.  Row halves: region 0 (Q rows)
+  // at 0, region 2 (dO rows) at R; transposed halves: region 1 (dO transposed) at 0, region 3
+  // (Q transposed) at R; both then the per-row values.
+  __shared__ __align__(16) char stage0[HALVES ? HB : BB];
+  __shared__ __align__(16) char stage1[HALVES ? HB : BB];
+  __shared__ __align__(16) char stage2[HALVES ? HB : BB];
+  __shared__ __align__(16) char stage3[HALVES ? HB : 16];
   __shared__ __align__(16) char xch[2 * 4 * 2048];  // P of a block per pair, two blocks
+  // whole stages
   auto stage_of = [&](int bi) {
     const int m = bi % 3;
     return m == 0 ? stage0 : m == 1 ? stage1 : stage2;
   };
+  // half-stages
+  auto rows_of = [&](int bi) { return (bi & 1) ? stage1 : stage0; };
+  auto trans_of = [&](int bi) { return (bi & 1) ? stage3 : stage2; };
+  // offsets in a stage: the row regions (S, dP), the transposed ones (dV, dK), the values
+  constexpr int OQ = 0, ODO = HALVES ? R : 2 * R, ODOT = HALVES ? 0 : R, OQT = HALVES ? R : 3 * R;
+  constexpr int OVAL = HALVES ? 2 * R : 4 * R;
 
   int b = blockIdx.x;
   const int kt = b % p.n_tiles;
@@ -478,25 +497,31 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
     const int n_rb = (L - row_begin + kBwdRows - 1) / kBwdRows;
     const int n_blk = n_rb * p.group;  // (query head, 32-row block) pairs, head-major
     const int64_t blk0 = pstart + row_begin / kBwdRows;
-    int lh = 0, lr = 0;  // query head (within the group) and row block of the next load
-    auto load = [&](int bi) {
-      const char* g = p.pk + ((int64_t)(kvh * p.group + lh) * p.n_pb + blk0 + lr) * BB;
+    // query head (within the group) and row block of the next block a load takes
+    struct Cursor {
+      int lh, lr;
+    };
+    Cursor rc{0, 0}, tc{0, 0};
+    // the block at cursor cu into stage st: whole (r0 < 0), or its half of regions r0 and
+    // r0 + 2; then the per-row values
+    auto load = [&](Cursor& cu, char* st, int r0) {
+      const char* g = p.pk + ((int64_t)(kvh * p.group + cu.lh) * p.n_pb + blk0 + cu.lr) * BB;
       const __amdgpu_buffer_rsrc_t rs = make_rsrc32(uniform_ptr(g), BB);
-      char* st = stage_of(bi);
 #pragma unroll
       for (int j = 0; j < CPW; ++j) {
-        const int f = w + 8 * j;
-        dma16(rs, st + 1024 * f, 1024 * f + 16 * l);
+        const int f = w + 8 * j;  // of a half: region r0 + 2 (f / NKS), fragment f % NKS
+        const int src = r0 < 0 ? 1024 * f : (r0 + 2 * (f / NKS)) * R + 1024 * (f % NKS);
+        dma16(rs, st + 1024 * f, src + 16 * l);
       }
-      dma4(rs, st + 4 * R, 4 * R + 4 * l);  // every wavefront writes the same per-row values
-      if (++lr == n_rb) {
-        lr = 0;
-        ++lh;
+      dma4(rs, st + OVAL, 4 * R + 4 * l);  // every wavefront writes the same per-row values
+      if (++cu.lr == n_rb) {
+        cu.lr = 0;
+        ++cu.lh;
       }
     };
     // lse * log2(e) (off 0) or delta (off 128) of the rows of accumulator registers 0..15
     auto row_vals = [&](const char* st, int off, float (&v)[16]) {
-      const f32x4* s4 = reinterpret_cast<const f32x4*>(st + 4 * R + off);
+      const f32x4* s4 = reinterpret_cast<const f32x4*>(st + OVAL + off);
       const f32x4 a = s4[2 * h], bq = s4[2 * h + 1], cq = s4[4 + 2 * h], dq = s4[5 + 2 * h];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -512,25 +537,35 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
       frag pb0, pb1;  // first wavefront: P of the previous block (operands of dV)
       f32x16 dpt;     // second wavefront: dP of the previous block
       int cr = 0;     // row block (within the head) of block i
-      load(0);
+      if constexpr (HALVES) load(rc, rows_of(0), 0);
+      else load(rc, stage_of(0), -1);
       __builtin_amdgcn_s_waitcnt(kWaitAll);
       wg_barrier();
       for (int i = 0; i <= n_blk; ++i) {
-        if (i + 1 < n_blk) load(i + 1);
-        const char* cur = stage_of(i);
-        const char* prev = stage_of(i + 2);
+        const char* cur;   // block i: its row regions
+        const char* prev;  // block i - 1: its transposed regions and the values
+        if constexpr (HALVES) {
+          if (i + 1 < n_blk) load(rc, rows_of(i + 1), 0);
+          if (i < n_blk) load(tc, trans_of(i), 1);
+          cur = rows_of(i);
+          prev = trans_of(i + 1);
+        } else {
+          if (i + 1 < n_blk) load(rc, stage_of(i + 1), -1);
+          cur = stage_of(i);
+          prev = stage_of(i + 2);
+        }
         if constexpr (PW) {
           if (i > 0) {
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) {
-              acc[dt] = M::mma(frag_at(prev, R + 1024 * (2 * dt)), pb0, acc[dt]);
-              acc[dt] = M::mma(frag_at(prev, R + 1024 * (2 * dt + 1)), pb1, acc[dt]);
+              acc[dt] = M::mma(frag_at(prev, ODOT + 1024 * (2 * dt)), pb0, acc[dt]);
+              acc[dt] = M::mma(frag_at(prev, ODOT + 1024 * (2 * dt + 1)), pb1, acc[dt]);
             }
           }
           if (i < n_blk) {
             f32x16 st = {};
 #pragma unroll
-            for (int t = 0; t < NKS; ++t) st = M::mma(frag_at(cur, 1024 * t), kv[t], st);
+            for (int t = 0; t < NKS; ++t) st = M::mma(frag_at(cur, OQ + 1024 * t), kv[t], st);
             float lse[16], pv[16];
             row_vals(cur, 0, lse);
 #pragma unroll
@@ -567,17 +602,17 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
             const frag s0 = to_frag<T>(dsv), s1 = to_frag<T>(dsv + 8);
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) {
-              acc[dt] = M::mma(frag_at(prev, 3 * R + 1024 * (2 * dt)), s0, acc[dt]);
-              acc[dt] = M::mma(frag_at(prev, 3 * R + 1024 * (2 * dt + 1)), s1, acc[dt]);
+              acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt)), s0, acc[dt]);
+              acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt + 1)), s1, acc[dt]);
             }
           }
           if (i < n_blk) {
             dpt = f32x16{};
 #pragma unroll
-            for (int t = 0; t < NKS; ++t) dpt = M::mma(frag_at(cur, 2 * R + 1024 * t), kv[t], dpt);
+            for (int t = 0; t < NKS; ++t) dpt = M::mma(frag_at(cur, ODO + 1024 * t), kv[t], dpt);
           }
         }
-        if (i < n_blk) {  // block i + 1 has landed (each wavefront's own loads), P of block i written
+        if (i < n_blk) {  // the loads landed (each wavefront's own), P of block i written
           __builtin_amdgcn_s_waitcnt(kWaitAll);
           wg_barrier();
         }
@@ -636,7 +671,9 @@ int launch_bwd(const BwdParams& base, const fa4cp_sweep_bwd_args& a, hipStream_t
 // [h_q][n_pb][pack_block_bytes], n_pb = fa4cp_vt_min_d_stride(total, nseq) / 32.
 int64_t delta_bytes(int total, int h_q) { return ((int64_t)total * h_q * 4 + 255) / 256 * 256; }
 int64_t packed_blocks(int total, int nseq) { return fa4cp_vt_min_d_stride(total, nseq) / kBwdRows; }
-int64_t block_bytes(int d) { return d == 128 ? pack_block_bytes<128>() : pack_block_bytes<64>(); }
+int64_t block_bytes(int d) {
+  return d == 256 ? pack_block_bytes<256>() : d == 128 ? pack_block_bytes<128>() : pack_block_bytes<64>();
+}
 
 }  // namespace
 }  // namespace fa4cp
@@ -646,7 +683,7 @@ using namespace fa4cp;
 extern "C" int64_t fa4cp_ring_sweep_bwd_workspace_bytes(const fa4cp_sweep_bwd_args* a) {
   clear_error();
   if (a == nullptr) return set_error(FA4CP_EINVAL, "ring_sweep_bwd_workspace_bytes: null args");
-  if (a->total < 0 || a->h_q <= 0 || (a->d != 64 && a->d != 128) || (a->cu != nullptr && a->nseq <= 0))
+  if (a->total < 0 || a->h_q <= 0 || (a->d != 64 && a->d != 128 && a->d != 256) || (a->cu != nullptr && a->nseq <= 0))
     return set_error(FA4CP_EINVAL, "ring_sweep_bwd_workspace_bytes: bad shape total=%d h_q=%d d=%d nseq=%d", a->total,
                      a->h_q, a->d, a->nseq);
   const int nseq = a->cu ? a->nseq : 1;
@@ -663,7 +700,8 @@ extern "C" int fa4cp_ring_sweep_bwd(const fa4cp_sweep_bwd_args* a, void* stream)
                      a->cp_size, FA4CP_MAX_CP);
   if (a->dtype != FA4CP_BF16 && a->dtype != FA4CP_FP16)
     return set_error(FA4CP_EUNSUPPORTED, "ring_sweep_bwd: dtype %d (BF16 / FP16 only)", a->dtype);
-  if (a->d != 64 && a->d != 128) return set_error(FA4CP_EUNSUPPORTED, "ring_sweep_bwd: head dim %d (64 / 128)", a->d);
+  if (a->d != 64 && a->d != 128 && a->d != 256)
+    return set_error(FA4CP_EUNSUPPORTED, "ring_sweep_bwd: head dim %d (64 / 128 / 256)", a->d);
   if (a->cu != nullptr && a->nseq <= 0) return set_error(FA4CP_EINVAL, "ring_sweep_bwd: nseq must be >= 1 with cu");
   if (a->cu != nullptr && a->max_seqlen < 0) return set_error(FA4CP_EINVAL, "ring_sweep_bwd: negative max_seqlen");
   if (a->total == 0) return FA4CP_OK;
@@ -725,6 +763,8 @@ extern "C" int fa4cp_ring_sweep_bwd(const fa4cp_sweep_bwd_args* a, void* stream)
   p.accumulate = a->accumulate != 0;
   hipStream_t st = (hipStream_t)stream;
   if (a->dtype == FA4CP_BF16)
-    return a->d == 128 ? launch_bwd<__bf16, 128>(p, *a, st) : launch_bwd<__bf16, 64>(p, *a, st);
-  return a->d == 128 ? launch_bwd<_Float16, 128>(p, *a, st) : launch_bwd<_Float16, 64>(p, *a, st);
+    return a->d == 256 ? launch_bwd<__bf16, 256>(p, *a, st)
+           : a->d == 128 ? launch_bwd<__bf16, 128>(p, *a, st) : launch_bwd<__bf16, 64>(p, *a, st);
+  return a->d == 256 ? launch_bwd<_Float16, 256>(p, *a, st)
+         : a->d == 128 ? launch_bwd<_Float16, 128>(p, *a, st) : launch_bwd<_Float16, 64>(p, *a, st);
 }

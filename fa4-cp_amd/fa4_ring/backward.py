@@ -14,7 +14,7 @@ computation on one GPU, every source rank's K / V resident in HBM (LocalKVRing):
 
 Both run fa4cp_ring_sweep_bwd: the probabilities come from the forward's final natural-log
 LSE, so every step's pairs contribute independently (no merge in reverse).  bf16 / fp16
-with head dim 64 or 128.
+with head dim 64, 128 or 256.
 """
 
 from __future__ import annotations
@@ -52,7 +52,7 @@ def ring_flash_attn_backward(dout: torch.Tensor, local_q: torch.Tensor, local_k:
     dev = local_q.device
     _require(local_q.is_cuda, "ring_flash_attn_backward runs on the GPU: local_q must be a device tensor")
     _require(local_q.dtype in (torch.bfloat16, torch.float16), "backward takes bf16 / fp16 inputs")
-    _require(d in (64, 128), f"backward head dim must be 64 or 128, got {d}")
+    _require(d in (64, 128, 256), f"backward head dim must be 64, 128 or 256, got {d}")
     if S > 1:
         _require(isinstance(group, LocalKVRing) and group.cp_size == S,
                  "cp_size > 1 needs group=LocalKVRing holding every source rank's K / V")

@@ -254,7 +254,7 @@ typedef struct fa4cp_sweep_kpages {
 int fa4cp_ring_sweep_fwd_paged(const fa4cp_sweep_args* args, const fa4cp_sweep_kpages* k_pages, void* stream);
 
 /*
- * Backward of fa4cp_ring_sweep_fwd (BF16 / FP16, d = 64 or 128).  No counterpart in the
+ * Backward of fa4cp_ring_sweep_fwd (BF16 / FP16, d = 64, 128 or 256).  No counterpart in the
  * reference, which is forward-only (README.md: "forward only"); this is the training side of
  * the same sweep.  Given the forward's out and natural-log lse and the gradient dout of out:
  *   dq            = the gradient of the local q                       [total][h_q][d] float32

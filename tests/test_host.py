@@ -244,7 +244,8 @@ def test_backward_workspace_size_and_checks():
 
     # one sequence of 256 rows: 384 padded rows, so 8 heads x 12 blocks of 33024 bytes + 8 KB
     assert lib.fa4cp_ring_sweep_bwd_workspace_bytes(ctypes.byref(args())) == 8192 + 8 * 12 * 33024
-    for total, nseq, h_q, d in [(256, 1, 8, 128), (100, 1, 3, 64), (16384, 1, 32, 128), (1000, 7, 4, 64)]:
+    for total, nseq, h_q, d in [(256, 1, 8, 128), (100, 1, 3, 64), (16384, 1, 32, 128), (1000, 7, 4, 64),
+                                (512, 1, 4, 256)]:
         a = args(total=total, h_q=h_q, d=d, nseq=nseq, cu=fake if nseq > 1 else None)
         assert lib.fa4cp_ring_sweep_bwd_workspace_bytes(ctypes.byref(a)) == expect(total, nseq, h_q, d)
     for kw, msg in [(dict(d=96), b"bad shape"), (dict(h_q=0), b"bad shape"), (dict(total=-1), b"bad shape"),
