@@ -615,7 +615,7 @@ def c5_bf16_block(rank: int, steps: int, warmup: int) -> dict:
         "backward": {"ms_per_step": round(bms, 3), "TFLOP/s": round(bflops / (bms * 1e-3) / 1e12, 2),
                      "frac_of_peak": round(bflops / (bms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                      "flop_per_step": bflops,
-                     "kernels": "bwd_pack_kernel + bwd_dq_kernel<bf16,256,4> + bwd_dkdv_kernel<bf16,256>"},
+                     "kernels": "bwd_pack_kernel + bwd_pack_kv_kernel + bwd_dq_pair_kernel<bf16,256,4> + bwd_dkdv_kernel<bf16,256>"},
     }
     del ring, lq
     return out

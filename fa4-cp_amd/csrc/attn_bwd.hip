@@ -17,12 +17,16 @@
 // of src's keys.  dK / dV go to one buffer per source rank: this rank's contribution to that
 // source's gradient (a multi-GPU ring sends them back to their owners).
 //
-// Three launches: bwd_pack_kernel (HBM-bound: delta, and every 32-row block of Q and dO
-// copied into the operand order of the dK / dV products, in rows and transposed), bwd_dq_kernel
-// (one workgroup per 32 query rows x HP heads of one kv head, walking the same key segments as
-// the forward sweep), and bwd_dkdv_kernel (one workgroup per 128 keys of one source and kv
-// head, eight wavefronts in pairs, walking the packed blocks of the query rows that attend
-// them, for every query head of the group).
+// Three launches:
+// * bwd_pack_kernel (HBM-bound): delta, and every 32-row block of Q and dO copied into the
+//   operand order of the dK / dV products, in rows and transposed;
+// * bwd_dq_kernel: one workgroup per 32 query rows x HP heads of one kv head, walking the same
+//   key segments as the forward sweep;
+// * bwd_dkdv_kernel: one workgroup per 128 keys of one source and kv head, eight wavefronts
+//   in pairs, walking the packed blocks of the query rows that attend them, for every query
+//   head of the group.
+// At head dim 256 dq runs as two launches instead: bwd_pack_kv_kernel packs every source's K
+// and V blocks, and bwd_dq_pair_kernel runs its wavefronts in pairs as dK / dV does.
 //
 // Products run on v_mfma_f32_32x32x16_{bf16,f16}.  Operand layouts (lane l, h = l / 32):
 // A lane l holds row l % 32, k = 8h + 0..7; B lane l holds column l % 32, the same k; the
@@ -52,6 +56,10 @@ template <int D>
 constexpr int pack_region_bytes() { return 64 * D; }
 template <int D>
 constexpr int pack_block_bytes() { return 4 * pack_region_bytes<D>() + 256; }
+// A packed key block (head dim 256 only): keys [32 b, 32 b + 32) of one source's sequence and
+// kv head in three regions of the same formats: 0 K rows, 1 V rows, 2 K transposed.
+template <int D>
+constexpr int kv_block_bytes() { return 3 * pack_region_bytes<D>(); }
 
 typedef short bs16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) bs16x4 lds_bs16x4;
@@ -84,7 +92,8 @@ struct BwdParams {
   const float* lse;    // natural log
   float* delta;        // [total][h_q], written by bwd_pack_kernel
   const void* out;
-  char* pk;            // packed blocks [h_q][n_pb][pack_block_bytes]
+  char* pk;            // packed Q / dO blocks [h_q][n_pb][pack_block_bytes]
+  char* pkv;           // packed K / V blocks [S][h_kv][n_pb][kv_block_bytes] (head dim 256)
   int64_t n_pb;
   float* dq;           // [total][h_q][d]
   const void* k[FA4CP_MAX_CP];
@@ -155,6 +164,20 @@ __device__ __forceinline__ typename BwdMfma<T>::frag to_frag(const float* x) {
   return f;
 }
 
+// 16-byte chunk (fragment f, lane `lane`) of a packed region from a row-major 32-row LDS tile
+// of row stride RS: the row format (transposed false) or the transposed one.
+template <typename T, int RS>
+__device__ __forceinline__ u32x4 pack_chunk(const T* tile, bool transposed, int f, int lane) {
+  typedef T t8 __attribute__((ext_vector_type(8)));
+  const int lh = lane >> 5, lm = lane & 31;
+  if (!transposed) return *reinterpret_cast<const u32x4*>(tile + sig(lm) * RS + 16 * f + 8 * lh);
+  const int dt = f >> 1, kk = f & 1;
+  t8 e8;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) e8[e] = tile[(16 * kk + 8 * lh + e) * RS + 32 * dt + lm];
+  return __builtin_bit_cast(u32x4, e8);
+}
+
 // One packed block (see pack_block_bytes) per workgroup: rows [32 rb, 32 rb + 32) of sequence
 // `seq` and query head hq, rows past the sequence's end zero.  Also writes delta[row, hq] =
 // sum_d dO[row, hq, d] O[row, hq, d] (fp32) for the dq kernel.  The packed blocks of sequence j
@@ -215,18 +238,8 @@ __global__ __launch_bounds__(256) void bwd_pack_kernel(BwdParams p) {
   constexpr int NCH = 4 * NKS * 64;  // 16-byte chunks of the four regions
 #pragma unroll
   for (int g = t; g < NCH; g += 256) {
-    const int region = g / (NKS * 64), f = (g >> 6) % NKS, lane = g & 63, lh = lane >> 5, lm = lane & 31;
-    const T* src = (region == 0 || region == 3) ? ql : dl;
-    u32x4 x;
-    if (region == 0 || region == 2) {
-      x = *reinterpret_cast<const u32x4*>(src + sig(lm) * RS + 16 * f + 8 * lh);
-    } else {
-      const int dt = f >> 1, kk = f & 1;
-      t8 e8;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) e8[e] = src[(16 * kk + 8 * lh + e) * RS + 32 * dt + lm];
-      x = __builtin_bit_cast(u32x4, e8);
-    }
+    const int region = g / (NKS * 64), f = (g >> 6) % NKS;
+    const u32x4 x = pack_chunk<T, RS>((region == 0 || region == 3) ? ql : dl, region & 1, f, g & 63);
     *reinterpret_cast<u32x4*>(dst + (int64_t)g * 16) = x;
   }
   if (t < 2 * kBwdRows) {
@@ -236,6 +249,245 @@ __global__ __launch_bounds__(256) void bwd_pack_kernel(BwdParams p) {
     else
       v = dsum[t - kBwdRows];
     *reinterpret_cast<float*>(dst + 4 * pack_region_bytes<D>() + 4 * t) = v;
+  }
+}
+
+// One packed key block (see kv_block_bytes) per workgroup: keys [32 kb, 32 kb + 32) of source
+// src's sequence `seq` and kv head kvh, keys past the sequence's end zero.  Blocks that no
+// query row of this rank attends (from the step's key limit on) are not written.  The blocks
+// of sequence j start at fa4cp_vt_min_d_stride's padded position of j / 32.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void bwd_pack_kv_kernel(BwdParams p) {
+  constexpr int RS = D + 8;
+  constexpr int NKS = D / 16;
+  constexpr int CPR = D / 8;
+  __shared__ __align__(16) T kl[kBwdRows * RS];
+  __shared__ __align__(16) T vl[kBwdRows * RS];
+  int b = blockIdx.x;
+  const int kb = b % p.n_tiles;
+  b /= p.n_tiles;
+  const int seq = b % p.nseq;
+  b /= p.nseq;
+  const int kvh = b % p.h_kv;
+  const int src = b / p.h_kv;
+  const int64_t pstart = vt_seq_start(p.cu, seq, p.total, FA4CP_SEL_ALL) / kBwdRows;
+  int qs, L;
+  seq_range(p.cu, seq, p.total, FA4CP_SEL_ALL, qs, L);
+  const int k0 = kb * kBwdRows;
+  if (k0 >= step_pairs(p.rank, p.S, src, L).key_lim) return;  // (the key limit is at most L)
+  const int t = threadIdx.x;
+  const T* kbase = reinterpret_cast<const T*>(p.k[src]) + (int64_t)kvh * p.k_hs;
+  const T* vbase = reinterpret_cast<const T*>(p.v[src]) + (int64_t)kvh * p.v_hs;
+#pragma unroll
+  for (int c = t; c < kBwdRows * CPR; c += 256) {
+    const int row = c / CPR, ch = c % CPR;
+    u32x4 xk = {0u, 0u, 0u, 0u}, xv = {0u, 0u, 0u, 0u};
+    if (k0 + row < L) {
+      const int64_t key = (int64_t)qs + k0 + row;
+      xk = *reinterpret_cast<const u32x4*>(kbase + key * p.k_rs + 8 * ch);
+      xv = *reinterpret_cast<const u32x4*>(vbase + key * p.v_rs + 8 * ch);
+    }
+    *reinterpret_cast<u32x4*>(kl + row * RS + 8 * ch) = xk;
+    *reinterpret_cast<u32x4*>(vl + row * RS + 8 * ch) = xv;
+  }
+  __syncthreads();
+  char* dst = p.pkv + (((int64_t)src * p.h_kv + kvh) * p.n_pb + pstart + kb) * kv_block_bytes<D>();
+  constexpr int NCH = 3 * NKS * 64;
+#pragma unroll
+  for (int g = t; g < NCH; g += 256) {
+    const int region = g / (NKS * 64), f = (g >> 6) % NKS;
+    const u32x4 x = pack_chunk<T, RS>(region == 1 ? vl : kl, region == 2, f, g & 63);
+    *reinterpret_cast<u32x4*>(dst + (int64_t)g * 16) = x;
+  }
+}
+
+// dQ at head dim 256, where the single-wavefront kernel below holds 404 registers and runs
+// one wavefront per SIMD: one workgroup per 32 query rows x HP query heads of one kv head,
+// 2 HP wavefronts in HP pairs (pair g: query head g of the workgroup).  The first wavefront
+// of a pair holds Q of its rows as the B operand of S^T = K Q^T, turns S^T into P^T and writes it to LDS (fp16); the
+// second holds dO as the B operand of dP^T = V dO^T, takes P^T from its partner, forms
+// dS^T = P^T (dP^T - delta) and accumulates dQ^T += K^T dS^T.  The workgroup walks the key
+// blocks of every step its rows attend (the forward sweep's segments, in 32-key blocks):
+// block i arrives by LDS-DMA into stage i % 3 one iteration ahead, and iteration i runs S / dP
+// of block i and dQ of block i - 1, so neither wavefront of a pair waits for the other within
+// an iteration.  One barrier per iteration: block i + 1 has landed, P^T of block i is in LDS,
+// and the stage of block i - 1 is free for block i + 2.
+template <typename T, int D, int HP>
+__global__ __launch_bounds__(128 * HP) void bwd_dq_pair_kernel(BwdParams p) {
+  using M = BwdMfma<T>;
+  typedef typename M::frag frag;
+  constexpr int NKS = D / 16;
+  constexpr int NDT = D / 32;
+  constexpr int R = pack_region_bytes<D>();
+  constexpr int KB = kv_block_bytes<D>();
+  constexpr int NW = 2 * HP;   // wavefronts
+  constexpr int NF = 3 * NKS;  // 1 KB fragments per key block
+  constexpr int kWaitAll = 7 << 4;  // vmcnt(0), lgkmcnt(0)
+  // Three stages in separate arrays: the LDS-DMA destination is chosen at run time, so the
+  // compiler does not make the first LDS read of an iteration wait for every load in flight.
+  __shared__ __align__(16) char stage0[KB];
+  __shared__ __align__(16) char stage1[KB];
+  __shared__ __align__(16) char stage2[KB];
+  __shared__ __align__(16) char xch[2 * HP * 2048];  // P^T of a block per pair, two blocks
+  auto stage_of = [&](int bi) {
+    const int m = bi % 3;
+    return m == 0 ? stage0 : m == 1 ? stage1 : stage2;
+  };
+
+  const int n_hg = p.h_q / HP;
+  int b = blockIdx.x;
+  const int hg = b % n_hg;
+  b /= n_hg;
+  const int rt = b % p.n_tiles;
+  const int seq = b / p.n_tiles;
+  const int64_t pstart = vt_seq_start(p.cu, seq, p.total, FA4CP_SEL_ALL) / kBwdRows;
+  int qs, L;
+  seq_range(p.cu, seq, p.total, FA4CP_SEL_ALL, qs, L);
+  const int r0 = rt * kBwdRows;
+  if (r0 >= L) return;
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int l = threadIdx.x & 63, h = l >> 5, lq = l & 31;
+  const bool swave = w < HP;
+  const int head = hg * HP + w % HP;
+  const int kvh = head / p.group;  // the same for the workgroup's HP heads (group % HP == 0)
+  const int qpos = r0 + lq;        // this lane's query row in the sequence
+  const bool row_ok = qpos < L;
+
+  // Q (first wavefront) or dO (second) of the lane's row: B operands of S^T and dP^T
+  frag xf[NKS];
+  {
+    const T* r = swave ? reinterpret_cast<const T*>(p.q) + (int64_t)(qs + qpos) * p.q_rs + (int64_t)head * p.q_hs
+                       : reinterpret_cast<const T*>(p.dout) + (int64_t)(qs + qpos) * p.do_rs + (int64_t)head * p.do_hs;
+#pragma unroll
+    for (int t = 0; t < NKS; ++t) {
+      frag z = {};
+      xf[t] = row_ok ? *reinterpret_cast<const frag*>(r + 8 * h + 16 * t) : z;
+    }
+  }
+  const float c = p.scale * kLog2e;
+  // lse * log2(e) (first wavefront) or delta (second) of the lane's row
+  const float rv = !row_ok ? 0.f
+                   : swave ? p.lse[(int64_t)(qs + qpos) * p.lse_rs + head] * kLog2e
+                           : p.delta[(int64_t)(qs + qpos) * p.h_q + head];
+  f32x16 acc[NDT];  // dQ^T (second wavefront)
+#pragma unroll
+  for (int i = 0; i < NDT; ++i) acc[i] = f32x16{};
+
+  // the key blocks of every step the row block attends, in order: (step, first key)
+  auto src_of = [&](int s) { return p.rank - s < 0 ? p.rank - s + p.S : p.rank - s; };
+  auto key_end_of = [&](int s) {  // keys of step s the rows see (0: no row attends it)
+    const StepPairs sp = step_pairs(p.rank, p.S, src_of(s), L);
+    if (r0 + kBwdRows <= sp.row_min) return 0;
+    return sp.causal ? min(sp.key_lim, r0 + kBwdRows) : sp.key_lim;
+  };
+  int n_blk = 0;
+  for (int s = 0; s < p.S; ++s) n_blk += (key_end_of(s) + kBwdRows - 1) / kBwdRows;
+  struct Cursor {
+    int s, k0, kend;
+  };
+  auto settle = [&](Cursor& cu) {
+    while (cu.s < p.S && cu.k0 >= cu.kend) {
+      ++cu.s;
+      cu.k0 = 0;
+      if (cu.s < p.S) cu.kend = key_end_of(cu.s);
+    }
+  };
+  Cursor lc{0, 0, key_end_of(0)};  // the next block to load
+  settle(lc);
+  auto load = [&](int bi) {
+    const char* g = p.pkv + (((int64_t)src_of(lc.s) * p.h_kv + kvh) * p.n_pb + pstart + lc.k0 / kBwdRows) * KB;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc32(uniform_ptr(g), KB);
+    char* st = stage_of(bi);
+    for (int f = w; f < NF; f += NW) dma16(rs, st + 1024 * f, 1024 * f + 16 * l);
+    lc.k0 += kBwdRows;
+    settle(lc);
+  };
+  auto frag_at = [&](const char* st, int off) { return *reinterpret_cast<const frag*>(st + off + 16 * l); };
+
+  auto run = [&](auto role) {
+    constexpr bool SW = decltype(role)::value;
+    f32x16 dpt;                       // second wavefront: dP^T of the previous block
+    Cursor cc{0, 0, key_end_of(0)};  // first wavefront: the block of the MFMA phase
+    settle(cc);
+    load(0);
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
+    wg_barrier();
+    for (int i = 0; i <= n_blk; ++i) {
+      if (i + 1 < n_blk) load(i + 1);
+      const char* cur = stage_of(i);
+      const char* prev = stage_of(i + 2);
+      if constexpr (SW) {
+        if (i < n_blk) {
+          f32x16 st = {};
+#pragma unroll
+          for (int t = 0; t < NKS; ++t) st = M::mma(frag_at(cur, 1024 * t), xf[t], st);
+          const StepPairs sp = step_pairs(p.rank, p.S, src_of(cc.s), L);
+          // no pair of the block masked (the usual case): no per-element test
+          const bool full = r0 + kBwdRows <= L && r0 >= sp.row_min && cc.k0 + kBwdRows <= sp.key_lim &&
+                            (!sp.causal || cc.k0 + kBwdRows - 1 <= r0);
+          float pv[16];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(fmaf(st[r], c, -rv));
+          if (!full) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int kp = cc.k0 + acc_pos(r, h);
+              const bool ok = row_ok & (qpos >= sp.row_min) & (kp < sp.key_lim) & (!sp.causal | (kp <= qpos));
+              pv[r] = ok ? pv[r] : 0.f;
+            }
+          }
+          char* xb = xch + ((i & 1) * HP + w % HP) * 2048;
+          *reinterpret_cast<f16x8*>(xb + 16 * l) = to_frag<_Float16>(pv);
+          *reinterpret_cast<f16x8*>(xb + 1024 + 16 * l) = to_frag<_Float16>(pv + 8);
+          cc.k0 += kBwdRows;
+          settle(cc);
+        }
+      } else {
+        if (i > 0) {
+          const char* xb = xch + (((i - 1) & 1) * HP + w % HP) * 2048;
+          const f16x8 e0 = *reinterpret_cast<const f16x8*>(xb + 16 * l);
+          const f16x8 e1 = *reinterpret_cast<const f16x8*>(xb + 1024 + 16 * l);
+          float dsv[16];
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            dsv[r] = (float)e0[r] * (dpt[r] - rv);
+            dsv[8 + r] = (float)e1[r] * (dpt[8 + r] - rv);
+          }
+          const frag s0 = to_frag<T>(dsv), s1 = to_frag<T>(dsv + 8);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            acc[dt] = M::mma(s0, frag_at(prev, 2 * R + 1024 * (2 * dt)), acc[dt]);
+            acc[dt] = M::mma(s1, frag_at(prev, 2 * R + 1024 * (2 * dt + 1)), acc[dt]);
+          }
+        }
+        if (i < n_blk) {
+          dpt = f32x16{};
+#pragma unroll
+          for (int t = 0; t < NKS; ++t) dpt = M::mma(frag_at(cur, R + 1024 * t), xf[t], dpt);
+        }
+      }
+      if (i < n_blk) {  // block i + 1 has landed (each wavefront's own loads), P^T of block i written
+        __builtin_amdgcn_s_waitcnt(kWaitAll);
+        wg_barrier();
+      }
+    }
+  };
+  if (n_blk > 0) {
+    if (swave) run(std::true_type{});
+    else run(std::false_type{});
+  }
+  if (swave) return;
+  // accumulator register r of lane l: query row 8 (r / 4) + 4h + r % 4, column 32 dt + lq
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = r0 + 8 * (r >> 2) + 4 * h + (r & 3);
+    if (row >= L) continue;
+    float* o = p.dq + ((int64_t)(qs + row) * p.h_q + head) * D + lq;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const float x = acc[dt][r] * p.scale;
+      o[32 * dt] = p.accumulate ? o[32 * dt] + x : x;
+    }
   }
 }
 
@@ -654,10 +906,21 @@ int launch_bwd(const BwdParams& base, const fa4cp_sweep_bwd_args& a, hipStream_t
   const int hp = p.group % 4 == 0 ? 4 : p.group % 2 == 0 ? 2 : 1;
   const int64_t dq_blocks = (int64_t)p.nseq * p.n_tiles * (p.h_q / hp);
   if (dq_blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "ring_sweep_bwd: too many row tiles");
-  switch (hp) {
-    case 4: hipLaunchKernelGGL((bwd_dq_kernel<T, D, 4>), dim3((unsigned)dq_blocks), dim3(256), 0, st, p); break;
-    case 2: hipLaunchKernelGGL((bwd_dq_kernel<T, D, 2>), dim3((unsigned)dq_blocks), dim3(128), 0, st, p); break;
-    default: hipLaunchKernelGGL((bwd_dq_kernel<T, D, 1>), dim3((unsigned)dq_blocks), dim3(64), 0, st, p); break;
+  if constexpr (D == 256) {  // the packed K / V blocks, then the paired kernel
+    const int64_t kv_pack_blocks = (int64_t)p.S * p.h_kv * p.nseq * p.n_tiles;
+    if (kv_pack_blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "ring_sweep_bwd: too many key blocks");
+    hipLaunchKernelGGL((bwd_pack_kv_kernel<T, D>), dim3((unsigned)kv_pack_blocks), dim3(256), 0, st, p);
+    switch (hp) {
+      case 4: hipLaunchKernelGGL((bwd_dq_pair_kernel<T, D, 4>), dim3((unsigned)dq_blocks), dim3(512), 0, st, p); break;
+      case 2: hipLaunchKernelGGL((bwd_dq_pair_kernel<T, D, 2>), dim3((unsigned)dq_blocks), dim3(256), 0, st, p); break;
+      default: hipLaunchKernelGGL((bwd_dq_pair_kernel<T, D, 1>), dim3((unsigned)dq_blocks), dim3(128), 0, st, p); break;
+    }
+  } else {
+    switch (hp) {
+      case 4: hipLaunchKernelGGL((bwd_dq_kernel<T, D, 4>), dim3((unsigned)dq_blocks), dim3(256), 0, st, p); break;
+      case 2: hipLaunchKernelGGL((bwd_dq_kernel<T, D, 2>), dim3((unsigned)dq_blocks), dim3(128), 0, st, p); break;
+      default: hipLaunchKernelGGL((bwd_dq_kernel<T, D, 1>), dim3((unsigned)dq_blocks), dim3(64), 0, st, p); break;
+    }
   }
   // dk / dv
   p.n_tiles = (p.max_seqlen + kDkdvKeys - 1) / kDkdvKeys;
@@ -667,8 +930,9 @@ int launch_bwd(const BwdParams& base, const fa4cp_sweep_bwd_args& a, hipStream_t
   return check_launch("ring_sweep_bwd");
 }
 
-// Workspace: delta [total][h_q] float32 (rounded up to 256 bytes), then the packed blocks
-// [h_q][n_pb][pack_block_bytes], n_pb = fa4cp_vt_min_d_stride(total, nseq) / 32.
+// Workspace: delta [total][h_q] float32 (rounded up to 256 bytes), the packed Q / dO blocks
+// [h_q][n_pb][pack_block_bytes], and at head dim 256 the packed K / V blocks
+// [S][h_kv][n_pb][kv_block_bytes]; n_pb = fa4cp_vt_min_d_stride(total, nseq) / 32.
 int64_t delta_bytes(int total, int h_q) { return ((int64_t)total * h_q * 4 + 255) / 256 * 256; }
 int64_t packed_blocks(int total, int nseq) { return fa4cp_vt_min_d_stride(total, nseq) / kBwdRows; }
 int64_t block_bytes(int d) {
@@ -686,8 +950,12 @@ extern "C" int64_t fa4cp_ring_sweep_bwd_workspace_bytes(const fa4cp_sweep_bwd_ar
   if (a->total < 0 || a->h_q <= 0 || (a->d != 64 && a->d != 128 && a->d != 256) || (a->cu != nullptr && a->nseq <= 0))
     return set_error(FA4CP_EINVAL, "ring_sweep_bwd_workspace_bytes: bad shape total=%d h_q=%d d=%d nseq=%d", a->total,
                      a->h_q, a->d, a->nseq);
-  const int nseq = a->cu ? a->nseq : 1;
-  return delta_bytes(a->total, a->h_q) + (int64_t)a->h_q * packed_blocks(a->total, nseq) * block_bytes(a->d);
+  if (a->d == 256 && (a->h_kv <= 0 || a->cp_size < 1 || a->cp_size > FA4CP_MAX_CP))
+    return set_error(FA4CP_EINVAL, "ring_sweep_bwd_workspace_bytes: bad shape h_kv=%d cp_size=%d", a->h_kv,
+                     a->cp_size);
+  const int64_t n_pb = packed_blocks(a->total, a->cu ? a->nseq : 1);
+  const int64_t kv = a->d == 256 ? (int64_t)a->cp_size * a->h_kv * n_pb * kv_block_bytes<256>() : 0;
+  return delta_bytes(a->total, a->h_q) + (int64_t)a->h_q * n_pb * block_bytes(a->d) + kv;
 }
 
 extern "C" int fa4cp_ring_sweep_bwd(const fa4cp_sweep_bwd_args* a, void* stream) {
@@ -732,6 +1000,7 @@ extern "C" int fa4cp_ring_sweep_bwd(const fa4cp_sweep_bwd_args* a, void* stream)
   p.delta = reinterpret_cast<float*>(a->workspace);
   p.pk = reinterpret_cast<char*>(a->workspace) + delta_bytes(a->total, a->h_q);
   p.n_pb = packed_blocks(a->total, a->cu ? a->nseq : 1);
+  p.pkv = p.pk + (int64_t)a->h_q * p.n_pb * block_bytes(a->d);  // read at head dim 256 only
   p.dq = a->dq;
   for (int i = 0; i < a->cp_size; ++i) {
     p.k[i] = a->k[i];
