@@ -264,11 +264,12 @@ int fa4cp_ring_sweep_fwd_paged(const fa4cp_sweep_args* args, const fa4cp_sweep_k
  * probability exp(scale q.k - lse) taken against the final lse.  workspace is caller-owned
  * device memory of at least fa4cp_ring_sweep_bwd_workspace_bytes(args) bytes, 256-byte
  * aligned: the first launch writes rowsum(dout * out) and a copy of q and dout in the operand
- * order of the dk / dv products there (about 4 x the bytes of q for d = 128); it holds nothing
+ * order of the dk / dv products there (about 4 x the bytes of q), at d = 256 also a copy of
+ * every source's k and v (3 x the bytes of one source's k, per source); it holds nothing
  * across calls.  With accumulate != 0 the results are added to dq / dk / dv instead of stored
  * (summing the contributions of several ranks, as a ring's backward does).  q, dout and out
  * may have any row and head stride; k / v shards share strides and the cu layout of
- * fa4cp_ring_sweep_fwd.  Three launches on `stream`.
+ * fa4cp_ring_sweep_fwd.  Three launches on `stream` (four at d = 256).
  */
 typedef struct fa4cp_sweep_bwd_args {
   const void* q;    /* [total] x h_q x d */
