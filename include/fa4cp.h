@@ -295,8 +295,9 @@ typedef struct fa4cp_sweep_bwd_args {
 } fa4cp_sweep_bwd_args;
 
 int fa4cp_ring_sweep_bwd(const fa4cp_sweep_bwd_args* args, void* stream);
-/* Workspace bytes fa4cp_ring_sweep_bwd needs for args' total, nseq (with cu), h_q and d (the
- * other fields are not read); a negative FA4CP_E* code for a bad shape. */
+/* Workspace bytes fa4cp_ring_sweep_bwd needs for args' total, nseq (with cu), h_q and d, and
+ * at d = 256 h_kv and cp_size (the other fields are not read); a negative FA4CP_E* code for a
+ * bad shape. */
 int64_t fa4cp_ring_sweep_bwd_workspace_bytes(const fa4cp_sweep_bwd_args* args);
 
 /*
