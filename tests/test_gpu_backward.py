@@ -182,3 +182,79 @@ def test_backward_is_deterministic():
     assert torch.equal(a[0], b[0])
     assert all(torch.equal(x, y) for x, y in zip(a[1], b[1]))
     assert all(torch.equal(x, y) for x, y in zip(a[2], b[2]))
+
+
+def test_backward_full_size_sampled_rows_and_keys():
+    """The headline shape (N=131072, cp 8, rank 3, H 32/8, D 128, bf16), where the oracle's
+    whole ring backward is out of reach: dq of sampled rows (every 1024th local row and the
+    last, every head) and the rank's dk / dv contributions for sampled keys of its own source,
+    an earlier one and a later one, against float64 sums on the host over every key (row)
+    each attends in the dense causal sequence, from the same inputs and the forward's out and
+    LSE.  Keys of an earlier source that no row of the rank attends (its back half) must get
+    exact zeros."""
+    n, cp, rank, hq, hkv, d = 131072, 8, 3, 32, 8, 128
+    group = hq // hkv
+    say(f"ring backward full size n={n} cp={cp} rank={rank} h={hq}/{hkv} d={d}")
+    gen = torch.Generator(device=DEV).manual_seed(8)
+    q = torch.randn(n, hq, d, device=DEV, generator=gen, dtype=torch.bfloat16)
+    k = torch.randn(n, hkv, d, device=DEV, generator=gen, dtype=torch.bfloat16)
+    v = torch.randn(n, hkv, d, device=DEV, generator=gen, dtype=torch.bfloat16)
+    ring = LocalKVRing.from_full(k, v, cp)
+    lq = zigzag_shard(q, rank, cp)
+    del q
+    ldo = torch.randn(lq.shape, device=DEV, generator=gen, dtype=torch.bfloat16)
+    cfg = RingConfig(cp_size=cp, cp_rank=rank)
+    out, lse = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, return_lse=True)
+    dq, dk, dv = ring_flash_attn_backward(ldo, lq, ring.k[rank], ring.v[rank], out, lse, cfg, group=ring)
+    scale = scale_for(d)
+    t = lq.shape[0]
+    grow = torch.from_numpy(O.zigzag_rows(n, rank, cp))  # global position of each local row
+    kf, vf = k.float().cpu(), v.float().cpu()
+    qf, dof, of = lq.double().cpu(), ldo.double().cpu(), out.double().cpu()
+    lsef = lse.double().cpu()
+    delta = (dof * of).sum(-1)  # [t, hq]
+
+    # dq of sampled rows: dq[r, h] = scale sum_j P_j (dO.v_j - delta) k_j over keys j <= row
+    rows = sorted(set(range(0, t, 1024)) | {t // 2 - 1, t - 1})
+    got = dq[torch.tensor(rows, device=DEV)].double().cpu()
+    exp = torch.empty_like(got)
+    for i, r in enumerate(rows):
+        g = int(grow[r])
+        for kh in range(hkv):
+            hs = slice(kh * group, (kh + 1) * group)
+            kk, vv = kf[:g + 1, kh].double(), vf[:g + 1, kh].double()
+            p = torch.exp(qf[r, hs] @ kk.T * scale - lsef[r, hs, None])  # [group, g + 1]
+            ds = p * (dof[r, hs] @ vv.T - delta[r, hs, None])
+            exp[i, hs] = scale * (ds @ kk)
+    err = float((got - exp).abs().max()) / max(1.0, float(exp.abs().max()))
+    say(f"  dq: {len(rows)} rows x {hq} heads: max relative |err| {err:.2e} (bar 2e-2)")
+    assert err <= 2e-2, err
+
+    # dk / dv of sampled keys: this rank's rows r with position >= the key's, every head of
+    # the key's group: dv_j = sum P dO_r, dk_j = scale sum dS q_r
+    half = t // 2
+    for src in (rank, (rank - 1) % cp, (rank + 2) % cp):
+        kpos = torch.from_numpy(O.zigzag_rows(n, src, cp))
+        keys = [0, half // 3, half - 1, half, half + half // 2, t - 1]
+        gk_, gv_ = dk[src][torch.tensor(keys, device=DEV)].double().cpu(), dv[src][torch.tensor(keys, device=DEV)].double().cpu()
+        ek, ev = torch.zeros_like(gk_), torch.zeros_like(gv_)
+        kcpu, vcpu = ring.k[src][torch.tensor(keys, device=DEV)].double().cpu(), \
+            ring.v[src][torch.tensor(keys, device=DEV)].double().cpu()
+        for kh in range(hkv):
+            hs = slice(kh * group, (kh + 1) * group)
+            qh, doh, lh, dh = qf[:, hs], dof[:, hs], lsef[:, hs], delta[:, hs]
+            for i, kj in enumerate(keys):
+                m = grow >= int(kpos[kj])  # the rank's rows that attend this key
+                if not bool(m.any()):
+                    continue
+                qm, dom = qh[m], doh[m]  # [rows, group, d]
+                p = torch.exp(qm @ kcpu[i, kh] * scale - lh[m])  # [rows, group]
+                ds = p * (dom @ vcpu[i, kh] - dh[m])
+                ev[i, kh] = (p[..., None] * dom).sum((0, 1))
+                ek[i, kh] = scale * (ds[..., None] * qm).sum((0, 1))
+        for name, gt, ex in (("dk", gk_, ek), ("dv", gv_, ev)):
+            e = float((gt - ex).abs().max()) / max(1.0, float(ex.abs().max()))
+            say(f"  {name}[{src}]: {len(keys)} keys x {hkv} heads: max relative |err| {e:.2e} (bar 2e-2)")
+            assert e <= 2e-2, (name, src, e)
+        if src == (rank - 1) % cp:  # an earlier source: only its front half is attended
+            assert float(gk_[3:].abs().max()) == 0.0 and float(gv_[3:].abs().max()) == 0.0
