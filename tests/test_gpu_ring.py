@@ -216,16 +216,18 @@ def test_ring_varlen_all_ranks(mode, d):
         assert max_err(seq, O.dense_causal(q[s:e], k[s:e], v[s:e], scale)) <= TOL_BF16_OUT
 
 
+@pytest.mark.parametrize("d", [64, 256])
 @pytest.mark.parametrize("mode", ["fused", "incremental"])
-def test_ring_varlen_many_sequences(mode):
+def test_ring_varlen_many_sequences(mode, d):
     """80 packed sequences (some empty, some of 4 rows): every kernel finds a sequence's V^T
-    start by summing the padded lengths of up to 79 earlier ones, 64 per wavefront pass."""
-    cp, h, hkv, d = 2, 4, 2, 64
+    start by summing the padded lengths of up to 79 earlier ones, 64 per wavefront pass; at
+    head dim 256 with 32-key tiles, most segments end in a partial tile."""
+    cp, h, hkv = 2, 4, 2
     g = torch.Generator().manual_seed(12)
     lens = (torch.randint(0, 33, (80,), generator=g) * 4).tolist()
     lens[5] = 0
     lens[66] = 4
-    say(f"ring varlen {len(lens)} sequences cp={cp} path={mode}")
+    say(f"ring varlen {len(lens)} sequences cp={cp} d={d} path={mode}")
     full_cu = [0]
     for n in lens:
         full_cu.append(full_cu[-1] + n)
