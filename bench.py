@@ -50,7 +50,7 @@ SWEEP_TRAFFIC_BYTES_RANK3 = 2395694 * 1024
 # (N = 262144, rank 3), and for merge_states in their batched per-step forms (same factors,
 # counter passes over `bench.py --workload c4` / `--workload c5`).
 C4_SWEEP_TRAFFIC_BYTES = (2 * 144522 + 102470) * 1024
-C5_SWEEP_TRAFFIC_BYTES = (2 * 2580570 + 266252) * 1024
+C5_SWEEP_TRAFFIC_BYTES = (2 * 2793692 + 266244) * 1024
 C4_MERGE_STATES_TRAFFIC_BYTES = (2 * 204965 + 100913) * 1024
 C5_MERGE_STATES_TRAFFIC_BYTES = (2 * 799004 + 264223) * 1024
 

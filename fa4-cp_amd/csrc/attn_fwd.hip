@@ -126,6 +126,31 @@ __device__ __forceinline__ void sched_interleave() {
   }
 }
 
+// Orders the MFMA phase of e8_pipeline with Q^T read beside K: NPV groups of PREV MFMAs
+// (P V) then NMF - NPV single MFMAs (S^T = K Q^T, NMT per k-step), each group's LDS reads
+// (2 fragment halves, plus 2 of Q^T on a k-step's first MFMA) issued RA groups ahead.
+template <int NPV, int NMT, int NMF, int RA, int PREV>
+struct E8Sched {
+  static constexpr int rd(int k) { return k >= NMF ? 0 : (k < NPV || (k - NPV) % NMT) ? 2 : 4; }
+  static constexpr int pre() {
+    int p = 0;
+    for (int k = 0; k < RA; ++k) p += rd(k);
+    return p;
+  }
+  template <int K>
+  static __device__ __forceinline__ void step() {
+    if constexpr (K < NMF) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, K < NPV ? PREV : 1, 0);
+      if constexpr (rd(K + RA) > 0) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, rd(K + RA), 0);
+      step<K + 1>();
+    }
+  }
+  static __device__ __forceinline__ void run() {
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, pre(), 0);
+    step<0>();
+  }
+};
+
 // True when any lane of the wavefront has `p` set (wave-uniform result).
 __device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 
@@ -2085,7 +2110,8 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_pp(AttnParams p) 
 //   Q    per wavefront, lane-contiguous 16-byte halves of the Q^T fragments
 // The load schedule, the constant wait and the fence-free barriers are those of
 // vt_pipeline: K in four slots three tiles ahead (group 0), V^T in three slots two tiles
-// ahead (group 1), the segment walk a few scalar instructions per tile.
+// ahead (group 1), the segment walk a few scalar instructions per tile.  Head dim 256 (64-key
+// tiles) keeps K in three slots two tiles ahead and V^T in two slots one tile ahead.
 //
 // Segments may come from sources with different descales.  The running max is kept in
 // log2 units of the scaled scores (m2 = max of s * scale * qd * kd * log2 e), so each
@@ -2116,9 +2142,10 @@ struct E8Layout<128, 128> {
   __device__ static int kpos(int r, int c) { return c ^ kswz(r); }
   __device__ static int vpos(int d, int c) { return c ^ ((d >> 1) & 7); }
 };
-// D = 256, 64-key tiles: 256-byte K rows (a 16-lane read touches rows {0-7, 32-39} + 8 g +
-// 16 mt, told apart by bits 0-2 and 5), 64-byte V^T rows (four to a 256-byte window: rows
-// d .. d + 15 need bits 2-3 of d in the slot), two S^T tiles.
+// D = 256, 64-key tiles: 256-byte K rows held in LDS as 272-byte rows (one 16-byte slot
+// further into the 256-byte bank window per row), so a 16-lane read -- rows {0-3, 32-35} +
+// 4 g + 16 mt -- needs only bit 5 of the row in the slot; 64-byte V^T rows (four to a
+// 256-byte window: rows d .. d + 15 need bits 2-3 of d in the slot), two S^T tiles.
 template <>
 struct E8Layout<256, 64> {
   static constexpr int KCH = 16, VCH = 4;
@@ -2126,22 +2153,28 @@ struct E8Layout<256, 64> {
     return 16 * mt + 32 * ((rho >> 2) & 1) + 4 * (rho >> 3) + (rho & 3);
   }
   __device__ static int key(int mt, int i, int h) { return 16 * mt + 32 * h + i; }
-  __device__ static int kpos(int r, int c) { return c ^ ((r & 7) | (((r >> 5) & 1) << 3)); }
+  __device__ static int kpos(int r, int c) { return c ^ (((r >> 5) & 1) << 3); }
   __device__ static int vpos(int d, int c) { return c ^ ((d >> 2) & 3); }
 };
 template <int D>
 constexpr int e8_bn() { return D == 256 ? 64 : 128; }
 
-// LDS of e8_pipeline: K tiles in four slots and V^T tiles in VS (16 KB each in both
-// layouts), and every wavefront's Q^T fragments (16 bytes per lane per half k-step), kept
-// in LDS instead of registers: they are read once per tile, and the registers hold the
-// scores (D = 128: 64 per lane) or O (D = 256: 128 registers) instead.  D = 256 keeps two
-// V^T slots so that the 64 KB of Q^T fit: 64 + 32 + 64 KB.
+// LDS of e8_pipeline: K tiles in KS slots and V^T tiles in VS (16 KB tiles in both layouts),
+// and every wavefront's Q^T fragments (16 bytes per lane per half k-step), kept in LDS
+// instead of registers: they are read once per tile, and the registers hold the scores
+// (D = 128: 64 per lane) or O (D = 256: 128 registers) instead.  D = 256 keeps three K slots
+// of padded rows and two V^T slots so that the 64 KB of Q^T fit: 60 + 32 + 64 KB.
 template <int D>
 struct E8Lds {
   static constexpr int TILE = 16384;
   static constexpr int VS = D == 256 ? 2 : 3;
-  __attribute__((aligned(1024))) uint8_t kl[4][TILE];
+  // K slots.  Head dim 256: three slots of 64 rows padded to 272 bytes (17 KB, rounded up
+  // to 20 KB: five LDS-DMA loads for each of the four loading wavefronts; 17 loads, with the
+  // pad slots' lanes reading past the tile's buffer, measured 0.6 % slower); otherwise four
+  // slots of unpadded rows.
+  static constexpr int KS = D == 256 ? 3 : 4;
+  static constexpr int KSLOT = D == 256 ? 20480 : TILE;
+  __attribute__((aligned(1024))) uint8_t kl[KS][KSLOT];
   __attribute__((aligned(1024))) uint8_t vt[VS][TILE];
   __attribute__((aligned(1024))) uint8_t qsm[kPPWaves][D / 64][2][64 * 16];
 };
@@ -2162,16 +2195,28 @@ __device__ __forceinline__ void e8_pipeline(E8Lds<D>& lds, const Geo& geo,
   constexpr int NKS = D / 64;            // S^T k-steps (64 d each)
   constexpr int NDT = D / 32;            // O^T tiles
   constexpr int NPS = BN / 64;           // O^T k-steps (64 keys each)
-  constexpr int KS = 4, VS = E8Lds<D>::VS;  // LDS slots of K and V^T tiles
+  constexpr int KS = E8Lds<D>::KS, VS = E8Lds<D>::VS;  // LDS slots of K and V^T tiles
   constexpr int TILE = BN * D;           // bytes of one K or V^T tile
-  constexpr int KRB = Lay::KCH * 16, VRB = Lay::VCH * 16;  // LDS bytes per K / V^T row
+  constexpr int KRB = Lay::KCH * 16, VRB = Lay::VCH * 16;  // bytes per K / V^T row
   static_assert(KRB == D && VRB == BN, "tile rows");
   static_assert(NLD % 4 == 0 && NLD % kPPWaves == 0, "tile loads must split over the wavefronts");
   static_assert(E8Lds<D>::TILE == TILE, "E8Lds layout");
+  // KPAD (head dim 256): K rows of KRB + 16 bytes in LDS, so a lane's fragments differ by
+  // constant offsets (two address registers instead of eight: the kernel's 256 VGPRs then
+  // leave room for reading fragments ahead of their MFMAs).  Row r starts r slots into the
+  // 256-byte bank window and kpos flips chunk bit 3 by row bit 5, so the 16 lanes of a read
+  // (rows krow(mt, 0..15): 0-3, 32-35, 4-7, 36-39 and the like) hit distinct banks.  Pad and
+  // tail slots of a K slot receive copies of real chunks and are never read.
+  constexpr bool KPAD = E8Lds<D>::KSLOT != TILE;
+  constexpr int KRBL = KPAD ? KRB + 16 : KRB;  // LDS bytes per K row
+  constexpr int NLDK = E8Lds<D>::KSLOT / 1024;  // wave-wide LDS-DMA loads per K tile
+  constexpr int NGK = NLDK / 4;
+  static_assert(NLDK % 4 == 0 && NGK < 16, "K tile loads must split over a group's wavefronts");
+  static_assert(KS * E8Lds<D>::KSLOT + VS * TILE + kPPWaves * D * 32 <= 160 * 1024, "LDS");
   constexpr int kWaitOlder = NG | (7 << 4);
   static_assert(NG < 16, "vmcnt field");
   // MFMAs whose fragments are read ahead (D = 256 keeps 128 registers of O and 32 of Q^T)
-  constexpr int RA = D == 256 ? 1 : kPPReadAhead;
+  constexpr int RA = D == 256 ? (KPAD ? 2 : 1) : kPPReadAhead;
   auto& kl = lds.kl;
   auto& vt = lds.vt;
 
@@ -2206,8 +2251,17 @@ __device__ __forceinline__ void e8_pipeline(E8Lds<D>& lds, const Geo& geo,
   // tile; slot P is row P / CH, position P % CH, which holds chunk kpos / vpos(row, P % CH).
   auto k_voff = [&](int w, int nw, int n) __attribute__((always_inline)) {
     const int P = 64 * (w + nw * n) + lane;
-    const int r = P / Lay::KCH;
-    return r * k_rsb + 16 * Lay::kpos(r, P % Lay::KCH);
+    if constexpr (KPAD) {
+      int r = 16 * P / KRBL, c = 16 * P % KRBL / 16;
+      if (r >= BN || c >= Lay::KCH) {  // a pad or tail slot: any chunk of the tile
+        r = min(r, BN - 1);
+        c = 0;
+      }
+      return r * k_rsb + 16 * Lay::kpos(r, c);
+    } else {
+      const int r = P / Lay::KCH;
+      return r * k_rsb + 16 * Lay::kpos(r, P % Lay::KCH);
+    }
   };
   auto v_voff = [&](int w, int nw, int n) __attribute__((always_inline)) {
     const int P = 64 * (w + nw * n) + lane;
@@ -2220,9 +2274,15 @@ __device__ __forceinline__ void e8_pipeline(E8Lds<D>& lds, const Geo& geo,
 #pragma unroll
   for (int i = 0; i < KS - 1; ++i) {
     const auto r = walk.rsrc(kc, true);
+    if constexpr (KPAD) {
 #pragma unroll
-    for (int n = 0; n < NLD / kPPWaves; ++n)
-      dma16(r, kl[i] + 1024 * (wave + kPPWaves * n), k_voff(wave, kPPWaves, n));
+      for (int n = 0; n < (NLDK + kPPWaves - 1) / kPPWaves; ++n)
+        if (wave + kPPWaves * n < NLDK) dma16(r, kl[i] + 1024 * (wave + kPPWaves * n), k_voff(wave, kPPWaves, n));
+    } else {
+#pragma unroll
+      for (int n = 0; n < NLD / kPPWaves; ++n)
+        dma16(r, kl[i] + 1024 * (wave + kPPWaves * n), k_voff(wave, kPPWaves, n));
+    }
     walk.template step<true>(kc, true, 0);
   }
 #pragma unroll
@@ -2235,13 +2295,21 @@ __device__ __forceinline__ void e8_pipeline(E8Lds<D>& lds, const Geo& geo,
   }
   // fragment addresses (bytes): K row krow(0, lq), chunks 4t + 2h + e; V^T row lq, chunks
   // 4u + 2h + e; tiles mt and dt add compile-time offsets (krow(mt, .) - krow(0, .) and
-  // 32 dt rows change no swizzle bit)
+  // 32 dt rows change no swizzle bit).  KPAD: chunk 4t + 2h + e sits at 4t + 2h + e plus 8
+  // (t < 2) or minus 8 (t >= 2) when bit 5 of the row is set, so two bases serve every (t, e).
   const int k_row = Lay::krow(0, lq);
-  int k_off[NKS][2], v_off[NPS][2];
+  int k_off[KPAD ? 1 : NKS][2], v_off[NPS][2];
+  int k_base[2] = {0, 0};
+  if constexpr (KPAD) {
+    const int b5 = (k_row >> 5) & 1;
+    k_base[0] = k_row * KRBL + 32 * lh + 128 * b5;
+    k_base[1] = k_row * KRBL + 32 * lh - 128 * b5;
+  } else {
 #pragma unroll
-  for (int t = 0; t < NKS; ++t)
+    for (int t = 0; t < NKS; ++t)
 #pragma unroll
-    for (int e = 0; e < 2; ++e) k_off[t][e] = k_row * KRB + 16 * Lay::kpos(k_row, 4 * t + 2 * lh + e);
+      for (int e = 0; e < 2; ++e) k_off[t][e] = k_row * KRB + 16 * Lay::kpos(k_row, 4 * t + 2 * lh + e);
+  }
 #pragma unroll
   for (int u = 0; u < NPS; ++u)
 #pragma unroll
@@ -2257,20 +2325,31 @@ __device__ __forceinline__ void e8_pipeline(E8Lds<D>& lds, const Geo& geo,
 
   // MFMA order: consecutive MFMAs share their register operand (as in vt_pipeline)
   auto qk = [&](const uint8_t* ksrc) __attribute__((always_inline)) {
+    // KPAD reads each Q^T k-step beside the K fragments of its first MFMA (the read-ahead
+    // then holds one or two k-steps, not all four)
     i32x8 qf[NKS];
-#pragma unroll
-    for (int t = 0; t < NKS; ++t)
+    auto read_q = [&](int t) __attribute__((always_inline)) {
       qf[t] = cat8(*reinterpret_cast<const i32x4*>(&lds.qsm[wave][t][0][16 * lane]),
                    *reinterpret_cast<const i32x4*>(&lds.qsm[wave][t][1][16 * lane]));
+    };
+    if constexpr (!KPAD) {
+#pragma unroll
+      for (int t = 0; t < NKS; ++t) read_q(t);
+    }
 #pragma unroll
     for (int mt = 0; mt < NMT; ++mt) s[mt] = f32x16{};
 #pragma unroll
     for (int t = 0; t < NKS; ++t)
 #pragma unroll
       for (int mt = 0; mt < NMT; ++mt) {
-        const int mo = (Lay::krow(mt, 0) - Lay::krow(0, 0)) * KRB;
-        const i32x4 a0 = *reinterpret_cast<const i32x4*>(ksrc + mo + k_off[t][0]);
-        const i32x4 a1 = *reinterpret_cast<const i32x4*>(ksrc + mo + k_off[t][1]);
+        if constexpr (KPAD) {
+          if (mt == 0) read_q(t);
+        }
+        const int mo = (Lay::krow(mt, 0) - Lay::krow(0, 0)) * KRBL;
+        const int o0 = KPAD ? k_base[t >= 2] + 64 * t : k_off[KPAD ? 0 : t][0];
+        const int o1 = KPAD ? k_base[t >= 2] + 64 * t + 16 : k_off[KPAD ? 0 : t][1];
+        const i32x4 a0 = *reinterpret_cast<const i32x4*>(ksrc + mo + o0);
+        const i32x4 a1 = *reinterpret_cast<const i32x4*>(ksrc + mo + o1);
         s[mt] = mma_fp8(cat8(a0, a1), qf[t], s[mt]);
       }
   };
@@ -2357,13 +2436,17 @@ __device__ __forceinline__ void e8_pipeline(E8Lds<D>& lds, const Geo& geo,
   const bool isk = grp == 0;
   LoadCursor lc = isk ? kc : vc;
   int pend = -1;  // paged K: the page entry lc's next page event takes
-  int ld_voff[NG];
+  constexpr int NGL = KPAD ? NGK : NG;  // loads per wavefront and tile (K's, when more)
+  static_assert(NGL >= NG, "K loads");
+  int ld_voff[NGL];
 #pragma unroll
-  for (int n = 0; n < NG; ++n) ld_voff[n] = isk ? k_voff(wi, 4, n) : v_voff(wi, 4, n);
+  for (int n = 0; n < NGL; ++n) ld_voff[n] = isk ? k_voff(wi, 4, n) : v_voff(wi, 4, n);
   uint8_t* const ld_base = isk ? kl[0] : vt[0];
   const int ld_slots = isk ? KS : VS;
+  const int ld_stride = isk ? E8Lds<D>::KSLOT : TILE;
   int ld_slot = ld_slots - 1;
   int vr = VS - 1;  // V^T slot of the tile before the one in the MFMA phase
+  int kr = 0;       // K slot of the tile in the MFMA phase (three slots; four use j & 3)
   // One tile j.  MFMA phase: PV of tile j - 1 (PREV = 1: one e4m3 term, 2: with the
   // residual term, 0: none), then S^T of tile j -- PV first, since it consumes P before QK
   // defines the new scores, so the two never hold registers at the same time -- then the
@@ -2376,20 +2459,24 @@ __device__ __forceinline__ void e8_pipeline(E8Lds<D>& lds, const Geo& geo,
     __builtin_amdgcn_s_setprio(1);
     if constexpr (Geo::kPagedK) __builtin_amdgcn_s_waitcnt(kWaitLgkm);  // the page entry, before any LDS read
     if constexpr (PREV == 0) {
-      qk(kl[j & (KS - 1)]);
+      qk(kl[KPAD ? kr : (j & (KS - 1))]);
     } else {
       pv(vt[vr], std::integral_constant<bool, PREV == 2>{});
-      qk(kl[j & (KS - 1)]);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * RA, 0);
+      qk(kl[KPAD ? kr : (j & (KS - 1))]);
+      if constexpr (KPAD) {
+        E8Sched<NDT * NPS, NMT, NDT * NPS + NMT * NKS, RA, PREV>::run();
+      } else {
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * RA, 0);
 #pragma unroll
-      for (int i = 0; i < NDT * NPS; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, PREV, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
-      }
+        for (int i = 0; i < NDT * NPS; ++i) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, PREV, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+        }
 #pragma unroll
-      for (int i = 0; i < NMT * NKS; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+        for (int i = 0; i < NMT * NKS; ++i) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+        }
       }
       walk.template step<false>(lc, isk, pend);
       ++mc.t;
@@ -2405,18 +2492,20 @@ __device__ __forceinline__ void e8_pipeline(E8Lds<D>& lds, const Geo& geo,
     if (__builtin_expect(mc.t >= mc.g.first_mask, 0)) mask();
     max_rescale(c);
     // K_{j+1} / V^T_j, loaded two VALU phases ago, are read in the next phase; with two
-    // V^T slots V^T_j is group 1's latest load
-    if (VS == 2 && !isk) __builtin_amdgcn_s_waitcnt(0);
+    // V^T slots V^T_j is group 1's latest load, with three K slots K_{j+1} group 0's
+    if ((VS == 2 && !isk) || (KS == 3 && isk)) __builtin_amdgcn_s_waitcnt(0);
     else __builtin_amdgcn_s_waitcnt(kWaitOlder);
     if constexpr (Geo::kPagedK) {
       __builtin_amdgcn_sched_barrier(0);
       if (isk) pend = walk.prefetch(lc);  // in flight through the VALU phase
     }
     wg_barrier();
-    uint8_t* const dst = ld_base + ld_slot * TILE;
+    uint8_t* const dst = ld_base + ld_slot * (KPAD ? ld_stride : TILE);
 #pragma unroll
-    for (int n = 0; n < NG; ++n) dma16(r, dst + 1024 * (wi + 4 * n), ld_voff[n]);
+    for (int n = 0; n < NGL; ++n)
+      if (n < NG || isk) dma16(r, dst + 1024 * (wi + 4 * n), ld_voff[n]);
     ld_slot = ld_slot + 1 == ld_slots ? 0 : ld_slot + 1;
+    if constexpr (KPAD) kr = kr + 1 == KS ? 0 : kr + 1;
     exp_tile(c);
     pack_e4m3<NPS, NMT>(s, pf);
     if constexpr (decltype(split)::value) pack_e4m3_residual<NPS, NMT>(s, pf, pl);
