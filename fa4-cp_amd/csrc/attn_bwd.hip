@@ -808,10 +808,21 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
         }
         if constexpr (PW) {
           if (i > 0) {
+            // head dim 256: the two 16-row halves in turn over the d tiles, so that consecutive
+            // MFMAs update different accumulators (each still sums its terms in the same
+            // order): 1.5-2 % off this kernel there, where the same order made the head-dim-128
+            // backward 1.2 % slower
+            if constexpr (HALVES) {
 #pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) {
-              acc[dt] = M::mma(frag_at(prev, ODOT + 1024 * (2 * dt)), pb0, acc[dt]);
-              acc[dt] = M::mma(frag_at(prev, ODOT + 1024 * (2 * dt + 1)), pb1, acc[dt]);
+              for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(frag_at(prev, ODOT + 1024 * (2 * dt)), pb0, acc[dt]);
+#pragma unroll
+              for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(frag_at(prev, ODOT + 1024 * (2 * dt + 1)), pb1, acc[dt]);
+            } else {
+#pragma unroll
+              for (int dt = 0; dt < NDT; ++dt) {
+                acc[dt] = M::mma(frag_at(prev, ODOT + 1024 * (2 * dt)), pb0, acc[dt]);
+                acc[dt] = M::mma(frag_at(prev, ODOT + 1024 * (2 * dt + 1)), pb1, acc[dt]);
+              }
             }
           }
           if (i < n_blk) {
@@ -852,10 +863,17 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
               dsv[8 + r] = (float)e1[r] * (dpt[8 + r] - dl[8 + r]);
             }
             const frag s0 = to_frag<T>(dsv), s1 = to_frag<T>(dsv + 8);
+            if constexpr (HALVES) {  // as for dV above
 #pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) {
-              acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt)), s0, acc[dt]);
-              acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt + 1)), s1, acc[dt]);
+              for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt)), s0, acc[dt]);
+#pragma unroll
+              for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt + 1)), s1, acc[dt]);
+            } else {
+#pragma unroll
+              for (int dt = 0; dt < NDT; ++dt) {
+                acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt)), s0, acc[dt]);
+                acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt + 1)), s1, acc[dt]);
+              }
             }
           }
           if (i < n_blk) {
