@@ -917,6 +917,7 @@ int launch_bwd(const BwdParams& base, const fa4cp_sweep_bwd_args& a, hipStream_t
   BwdParams p = base;
   // delta and the packed Q / dO blocks
   p.n_tiles = (p.max_seqlen + kBwdRows - 1) / kBwdRows;
+  if (p.n_tiles == 0) return FA4CP_OK;  // every sequence empty: nothing to launch
   const int64_t pack_blocks = (int64_t)p.nseq * p.n_tiles * p.h_q;
   if (pack_blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "ring_sweep_bwd: too many row tiles");
   hipLaunchKernelGGL((bwd_pack_kernel<T, D>), dim3((unsigned)pack_blocks), dim3(256), 0, st, p);

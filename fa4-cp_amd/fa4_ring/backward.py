@@ -65,7 +65,7 @@ def ring_flash_attn_backward(dout: torch.Tensor, local_q: torch.Tensor, local_k:
         _require(max_seqlen is not None, "max_seqlen required when cu_seqlens is given")
         _require(cu_seqlens.dtype == torch.int32 and cu_seqlens.device == dev and cu_seqlens.is_contiguous(),
                  "cu_seqlens must be contiguous int32 on the device")
-    _check_even_lengths(cu_seqlens, total)
+    _check_even_lengths(cu_seqlens, total, max_seqlen)
     h_kv = ks[0].shape[1]
     _require(h_q % h_kv == 0, f"{h_q} query heads cannot share {h_kv} kv heads evenly")
     for name, x in (("dout", dout), ("out", out)):

@@ -40,6 +40,28 @@ def _require(cond: bool, msg: str) -> None:
         raise AssertionError(msg)
 
 
+def kernel_head_dim(dtype: torch.dtype, d: int) -> int:
+    """The head dim the kernels run a head dim ``d`` at: ``d`` itself where a kernel exists,
+    else the smallest supported one above it (q, k and v are then zero-padded in D: the
+    padded columns add nothing to any score, and the output's padded columns are dropped).
+    Raises for ``d`` above the largest supported head dim."""
+    dims = SUPPORTED_HEAD_DIMS.get(dtype)
+    _require(dims is not None, f"unsupported dtype {dtype}")
+    _require(1 <= d <= max(dims), f"head dim {d} above {max(dims)} is not supported for {dtype}")
+    return min(x for x in dims if x >= d)
+
+
+def pad_head_dim(x: torch.Tensor, dp: int) -> torch.Tensor:
+    """x [..., d] -> a new contiguous [..., dp] tensor, zeros in columns d..dp-1 (x itself
+    when d == dp and x is contiguous in D)."""
+    d = x.shape[-1]
+    if d == dp:
+        return x if x.stride(-1) == 1 else x.contiguous()
+    y = torch.zeros((*x.shape[:-1], dp), dtype=x.dtype, device=x.device)
+    y[..., :d] = x
+    return y
+
+
 def _norm_descale(d: Optional[torch.Tensor], h_kv: int, device) -> Optional[torch.Tensor]:
     """Descale -> float32 contiguous [h_kv] on `device` (a scalar broadcasts to every kv
     head, [h_kv] and (1, h_kv) are taken as is; fa4_backend.py:45-55)."""
@@ -188,13 +210,30 @@ def fa4_attn(
     t_k, h_kv, dk = k.shape
     _require(v.shape == k.shape, f"k {tuple(k.shape)} and v {tuple(v.shape)} must match")
     _require(dk == d, f"q head dim {d} != k head dim {dk}")
-    _require(d in SUPPORTED_HEAD_DIMS[dt], f"head dim {d} not supported for {dt} "
-             f"(supported: {SUPPORTED_HEAD_DIMS[dt]})")
     _require(h_q % h_kv == 0, f"H_q={h_q} not a multiple of H_kv={h_kv}")
-    for name, t in (("q", q), ("k", k), ("v", v)):
-        _require(t.stride(2) == 1, f"{name} must be contiguous in the head dim")
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(d)
+    # the kernels read rows contiguous in D; other layouts are copied (as the reference's
+    # .contiguous() before FA4, fa4_backend.py:106-109)
+    q, k, v = (t if t.stride(2) == 1 else t.contiguous() for t in (q, k, v))
+    dp = kernel_head_dim(dt, d)
+    if dp != d:
+        # no kernel at this head dim: run the next one up on zero-padded copies
+        _require(v_t is None, f"v_t cannot be given at head dim {d} (the kernels run at {dp})")
+        odt = out_dtype_for(dt)
+        if out is not None:
+            _require(out.shape == (t_q, h_q, d) and out.dtype == odt and out.device == dev,
+                     f"out must be [{t_q}, {h_q}, {d}] {odt}")
+        # (a given out is padded too, so the rows outside a q selection keep what it held)
+        o_p, lse = fa4_attn(pad_head_dim(q, dp), pad_head_dim(k, dp), pad_head_dim(v, dp), causal=causal,
+                            softmax_scale=softmax_scale, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k,
+                            max_seqlen_q=max_seqlen_q, max_seqlen_k=max_seqlen_k, q_descale=q_descale,
+                            k_descale=k_descale, v_descale=v_descale, q_sel=q_sel, k_sel=k_sel,
+                            out=None if out is None else pad_head_dim(out, dp), lse=lse, use_vt=use_vt)
+        if out is None:
+            return o_p[..., :d].contiguous(), lse
+        out.copy_(o_p[..., :d])
+        return out, lse
 
     if (cu_seqlens_q is None) != (cu_seqlens_k is None):
         # one side packed, the other a single sequence: describe the latter explicitly
@@ -261,5 +300,5 @@ def fa4_attn(
     return out, lse
 
 
-__all__ = ["fa4_attn", "transpose_v", "uses_vt", "has_fa4", "out_dtype_for", "SEL_ALL", "SEL_BACK_HALF",
+__all__ = ["fa4_attn", "kernel_head_dim", "pad_head_dim", "transpose_v", "uses_vt", "has_fa4", "out_dtype_for", "SEL_ALL", "SEL_BACK_HALF",
            "SEL_FRONT_HALF"]

@@ -6,9 +6,9 @@ HBM-bound HIP kernels of libfa4cp.so.  LSEs are float32 natural log on both side
 
 ``IncrementalMerger`` / ``BatchedMerger`` / ``make_merger`` keep the reference classes'
 interface (fa4_ring/merge.py:45-94): ``add(out, lse)`` per ring step, ``result()`` at the
-end.  They move less data than a clone-then-merge / stack-then-merge would: the incremental
-merger's first merge is out of place (``merge_state``), and the batched one merges its
-partials through a pointer list (``merge_states_list``).  The first partial added must cover
+end.  The incremental merger copies its first partial and merges every later one into that
+copy in place; the batched one merges its partials through a pointer list
+(``merge_states_list``) instead of stacking them.  The first partial added must cover
 every row with a finite LSE (step 0 of the ring); a -inf row of a later partial is the
 identity, and a row that is -inf in both gets NaN, as the reference's formula does.
 """
@@ -155,44 +155,24 @@ def merge_states_list(vs: Sequence[torch.Tensor], ss: Sequence[torch.Tensor],
 class IncrementalMerger:
     """Folds ring partials into one (out, lse) state as they arrive (fa4_ring/merge.py:45-64).
 
-    The first partial is held by reference, not copied.  The second is merged with it into
-    buffers the merger owns (one out-of-place merge: reads both, writes one), and every later
-    partial is merged into those in place.  The caller's tensors are never written.  The
-    first partial must give every row a finite LSE (ring step 0); a -inf row of a later
-    partial leaves the row unchanged."""
+    The first partial is copied into buffers the merger owns (as the reference's clone at the
+    first add, fa4_ring/merge.py:53-57), so a caller may write the next step into the same
+    buffer before the next add.  Every later partial is merged into those buffers in place
+    (merge_state_in_place); the caller's tensors are never written.  The first partial must
+    give every row a finite LSE (ring step 0); a -inf row of a later partial leaves the row
+    unchanged."""
 
     def __init__(self):
-        self._v: Optional[torch.Tensor] = None
-        self._s: Optional[torch.Tensor] = None
-        self._owned = False  # whether (_v, _s) are the merger's own buffers
+        self.out: Optional[torch.Tensor] = None  # [T, H, D]
+        self.lse: Optional[torch.Tensor] = None  # [T, H] float32
         self.count = 0
 
     def add(self, out: torch.Tensor, lse: torch.Tensor) -> None:
-        if self._v is None:
-            self._v, self._s = out, lse
-        elif not self._owned:
-            self._v, self._s = merge_state(self._v, self._s, out, lse)
-            self._owned = True
+        if self.out is None:
+            self.out, self.lse = out.clone(), lse.clone()
         else:
-            merge_state_in_place(self._v, self._s, out, lse)
+            merge_state_in_place(self.out, self.lse, out, lse)
         self.count += 1
-
-    def _own(self) -> None:
-        """Copies a lone first partial, so the caller gets a tensor of its own (as the
-        reference's clone at the first add)."""
-        if self._v is not None and not self._owned:
-            self._v, self._s = self._v.clone(), self._s.clone()
-            self._owned = True
-
-    @property
-    def out(self) -> Optional[torch.Tensor]:
-        self._own()
-        return self._v
-
-    @property
-    def lse(self) -> Optional[torch.Tensor]:
-        self._own()
-        return self._s
 
     def result(self) -> torch.Tensor:
         assert self.count > 0, "result() called before any partial was added"

@@ -26,6 +26,7 @@ and every launch goes to torch's current stream.
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 import math
 import weakref
 from dataclasses import dataclass
@@ -35,8 +36,8 @@ import torch
 
 from . import _lib
 from .config import RingConfig
-from .fa4_backend import (SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, _norm_descale, fa4_attn, out_dtype_for,
-                          transpose_v, transpose_v_many, uses_vt)
+from .fa4_backend import (SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, SUPPORTED_HEAD_DIMS, _norm_descale, fa4_attn,
+                          kernel_head_dim, out_dtype_for, pad_head_dim, transpose_v, transpose_v_many, uses_vt)
 from .merge import merge_state_in_place, merge_states
 from .paged import PagedKVRing, gather_kv_pages, transpose_v_paged_many
 from .zigzag import zigzag_shard, zigzag_shard_varlen
@@ -61,10 +62,13 @@ class LocalKVRing:
         for k, v in zip(k_shards, v_shards):
             assert k.shape == v.shape == k_shards[0].shape, "every shard must have one shape"
             assert k.dtype == v.dtype == k_shards[0].dtype
-            assert k.dim() == 3 and k.stride(2) == 1 and v.stride(2) == 1, \
-                "K and V shards must be [T, H_kv, D] and contiguous in D"
-        self.k = list(k_shards)
-        self.v = list(v_shards)
+            assert k.dim() == 3, "K and V shards must be [T, H_kv, D]"
+        # the kernels read rows contiguous in D: shards laid out otherwise are copied once
+        self.k = [k if k.stride(2) == 1 else k.contiguous() for k in k_shards]
+        self.v = [v if v.stride(2) == 1 else v.contiguous() for v in v_shards]
+        if len({x.stride() for x in self.k}) > 1 or len({x.stride() for x in self.v}) > 1:
+            self.k = [x.contiguous() for x in self.k]
+            self.v = [x.contiguous() for x in self.v]
 
     @property
     def cp_size(self) -> int:
@@ -85,15 +89,21 @@ class LocalKVRing:
         return cls(ks, vs)
 
 
-_checked_cu = {}  # id(cu tensor) -> (weak reference, tensor version) of cu tables found even
+_checked_cu = {}  # id(cu tensor) -> (weak reference, tensor version, longest sequence) of cu tables found even
 
 
-def _check_even_lengths(cu_seqlens: Optional[torch.Tensor], total: int) -> None:
+def _check_even_lengths(cu_seqlens: Optional[torch.Tensor], total: int,
+                        max_seqlen: Optional[int] = None) -> None:
     """Every local sequence is two zig-zag chunks of equal size, so its length must be even
     (the reference asserts it through get_half_index, fa4_ring/zigzag.py:75, on every call).
     The kernels split a sequence at (start + end) / 2 and the half-row merges at cu / 2,
-    which agree only for even lengths.  A device cu table is read once (one host
-    synchronisation) and remembered until it is modified or freed."""
+    which agree only for even lengths.  ``max_seqlen``, when given, must cover the longest
+    sequence: the kernels size their grids by it, and rows past it would be left unwritten.
+
+    A device cu table is read once (one host synchronisation, which must therefore happen
+    outside any graph capture: make one call with the table before capturing) and
+    remembered until it is modified through torch or freed.  A table refilled by writes
+    torch does not see (a raw pointer, a foreign kernel) is not checked again."""
     if cu_seqlens is None:
         if total % 2:
             raise AssertionError(f"the local sequence has odd length {total}: a zig-zag shard is two "
@@ -102,15 +112,20 @@ def _check_even_lengths(cu_seqlens: Optional[torch.Tensor], total: int) -> None:
     key = id(cu_seqlens)
     seen = _checked_cu.get(key)
     if seen is not None and seen[0]() is cu_seqlens and seen[1] == cu_seqlens._version:
-        return
-    cu = cu_seqlens.to("cpu", torch.int64)
-    odd = ((cu[1:] - cu[:-1]) % 2 != 0).nonzero().flatten().tolist()
-    if odd:
-        raise AssertionError(f"local sequences {odd[:8]} have odd length: a zig-zag shard is two chunks of "
-                             "equal size")
-    if len(_checked_cu) > 256:
-        _checked_cu.clear()
-    _checked_cu[key] = (weakref.ref(cu_seqlens), cu_seqlens._version)
+        longest = seen[2]
+    else:
+        cu = cu_seqlens.to("cpu", torch.int64)
+        lens = cu[1:] - cu[:-1]
+        odd = (lens % 2 != 0).nonzero().flatten().tolist()
+        if odd:
+            raise AssertionError(f"local sequences {odd[:8]} have odd length: a zig-zag shard is two chunks of "
+                                 "equal size")
+        longest = int(lens.max()) if lens.numel() else 0
+        if len(_checked_cu) > 256:
+            _checked_cu.clear()
+        _checked_cu[key] = (weakref.ref(cu_seqlens), cu_seqlens._version, longest)
+    if max_seqlen is not None and max_seqlen < longest:
+        raise AssertionError(f"max_seqlen {max_seqlen} is below the longest local sequence ({longest})")
 
 
 def ring_flash_attn(
@@ -138,7 +153,8 @@ def ring_flash_attn(
     case.  ``cfg.merge_mode`` chooses how the per-step path merges its partials
     (incremental: in place after every step; batched: one merge_states at the end).  The
     fused sweep has no partials to merge, so it runs for either mode; pass
-    ``fused=False`` to get the merge the mode names.
+    ``fused=False`` to get the merge the mode names.  Other head dims up to 256 run at the
+    next supported one, on copies of Q and every K / V shard zero-padded in D.
 
     One sequence per rank: leave ``cu_seqlens=None``.  Packed sequences: pass the LOCAL
     ``cu_seqlens`` (each entry a zig-zag ``2*h_j`` shard length) on the device and
@@ -149,13 +165,41 @@ def ring_flash_attn(
     pages into contiguous shards first)."""
     S = cfg.cp_size
     rank = cfg.cp_rank
+    d = local_q.shape[2]
+    dp = kernel_head_dim(local_q.dtype, d) if local_q.dtype in SUPPORTED_HEAD_DIMS else d
+    if dp != d:
+        # no kernel at this head dim: pad Q and every source's K / V with zero columns once
+        # and run the sweep at the next supported head dim (scores are unchanged; the output's
+        # padded columns are dropped)
+        cfg_p = dataclasses.replace(cfg, softmax_scale=cfg.softmax_scale if cfg.softmax_scale is not None
+                                    else 1.0 / math.sqrt(d))
+        if isinstance(group, PagedKVRing):
+            group_p = PagedKVRing([pad_head_dim(x, dp) for x in group.k], [pad_head_dim(x, dp) for x in group.v],
+                                  group.page_tables)
+            lk = lv = None
+        else:
+            group_p = None if group is None else LocalKVRing([pad_head_dim(x, dp) for x in group.k],
+                                                             [pad_head_dim(x, dp) for x in group.v])
+            same = group is not None and S > 1 and local_k is group.k[rank] and local_v is group.v[rank]
+            lk, lv = group_p.kv(rank) if same else (pad_head_dim(local_k, dp), pad_head_dim(local_v, dp))
+        res = ring_flash_attn(pad_head_dim(local_q, dp), lk, lv, cfg_p, group=group_p, descales=descales,
+                              cu_seqlens=cu_seqlens, max_seqlen=max_seqlen, fused=fused, return_lse=return_lse)
+        if return_lse:
+            return res[0][..., :d].contiguous(), res[1]
+        return res[..., :d].contiguous()
+    # the kernels read rows contiguous in D (the reference copies with .contiguous() too)
+    local_q = local_q if local_q.stride(2) == 1 else local_q.contiguous()
+    if local_k is not None and local_k.stride(2) != 1:
+        local_k = local_k.contiguous()
+    if local_v is not None and local_v.stride(2) != 1:
+        local_v = local_v.contiguous()
     scale = cfg.softmax_scale
     total = local_q.shape[0]
     if cu_seqlens is not None:
         assert max_seqlen is not None, "max_seqlen required when cu_seqlens is given"
     else:
         max_seqlen = total
-    _check_even_lengths(cu_seqlens, total)
+    _check_even_lengths(cu_seqlens, total, max_seqlen)
     paged = isinstance(group, PagedKVRing)
     if paged:
         assert group.cp_size == S, f"PagedKVRing holds {group.cp_size} caches, cp_size is {S}"

@@ -15,14 +15,20 @@
  *     clamps the sequence ranges it derives from them, so no access leaves the tensors;
  *   - the return value is 0 on success and a negative FA4CP_E* code otherwise; the
  *     message for the last failure on the calling thread is in fa4cp_last_error();
- *   - the library keeps no state besides that thread-local message, so every entry point
- *     is reentrant.  Two calls that write the same memory on different streams race.
+ *   - max_seqlen arguments must be at least the longest sequence their cu table describes:
+ *     the kernels size their grids by them, and rows past a too-small bound are not written;
+ *   - the library's state is that thread-local message and, for
+ *     fa4cp_quantize_e4m3_noalloc only, a static 4 KiB device array per GPU (its amax words)
+ *     with a per-device cache of that array's address (filled once per device under a
+ *     mutex).  Every other entry point is reentrant; two calls that write the same memory
+ *     on different streams race, and so do two fa4cp_quantize_e4m3_noalloc calls that
+ *     overlap on one GPU.
  *
  * Reference interfaces replaced (paths are in hxy0118/fa4-cp):
  *   fa4cp_attn_fwd              <- fa4_ring/fa4_backend.py:58-123 (fa4_attn -> FA4 _flash_attn_fwd)
  *   fa4cp_merge_state_inplace   <- fa4_ring/merge.py:31-36 (flashinfer.cascade.merge_state_in_place)
- *   fa4cp_merge_state           <- fa4_ring/merge.py:45-64 (IncrementalMerger.add's first merge, which
- *                                  the reference does as clone() + merge_state_in_place)
+ *   fa4cp_merge_state           <- no direct counterpart: merge_state_in_place (fa4_ring/merge.py:31-36)
+ *                                  writing to other buffers, inputs left unmodified
  *   fa4cp_merge_states          <- fa4_ring/merge.py:39-42 (flashinfer.cascade.merge_states)
  *   fa4cp_merge_states_list     <- fa4_ring/merge.py:67-86 (BatchedMerger.result: torch.stack of the
  *                                  partials, then merge_states)
@@ -117,9 +123,9 @@ typedef struct fa4cp_attn_args {
   const float* k_descale; /* [h_kv] or NULL */
   const float* v_descale; /* [h_kv] or NULL */
   /* Optional V^T of the selected keys, written by fa4cp_transpose_v with the same v, cu_k,
-   * nseq, total_k, max_seqlen_k, k_sel, h_kv, d and dtype.  When set (head dims 64 and 128
-   * for BF16 / FP16, 128 for E4M3), the kernels load V^T tiles directly instead of
-   * transposing V in LDS, which is markedly faster.  NULL: V alone is read. */
+   * nseq, total_k, max_seqlen_k, k_sel, h_kv, d and dtype.  When set (head dims 64, 128 and
+   * 256 for BF16 / FP16, 128 and 256 for E4M3), the kernels load V^T tiles directly instead
+   * of transposing V in LDS, which is markedly faster.  NULL: V alone is read. */
   const void* v_t;
   int64_t vt_d_stride;
 } fa4cp_attn_args;

@@ -27,7 +27,9 @@ chunking does not change the arithmetic of a row.
 How each function is pinned (tests/test_oracle.py):
   zig-zag / half index / local_cu  the reference's known-answer lists (tests/golden/zigzag_kat.json,
                                    copied from tests/test_zigzag.py:21-78) and closed forms
-  cpu_attn / lse                   torch SDPA, brute-force float64 loops, softmax invariants
+  cpu_attn / lse                   torch SDPA, brute-force float64 loops (square and bottom-right
+                                   causal, with a planted alignment error that must fail),
+                                   softmax invariants
   merge / merge_states             attention over K1 u K2 == merge(attention over K1, over K2)
   ring sweep                       unshard(all ranks) == dense causal attention for the eleven
                                    cases of tests/test_algorithm_cpu.py:202-223, plus a planted
@@ -142,13 +144,14 @@ def expand_kv(k: torch.Tensor, n_q_heads: int) -> torch.Tensor:
 def cpu_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: float,
              row_chunk: int = 2048, heads: Optional[Sequence[int]] = None):
     """q [Tq,H,D], k/v [Tk,Hkv,D] -> out [Tq,H,D] fp32, lse [Tq,H] fp32 natural log
-    (test_algorithm_cpu.py:36-48).  The causal mask is the square one the ring uses
-    (query i sees key j <= i; only used with Tq == Tk).  ``heads`` restricts the
-    computation to those query heads (the other rows are left NaN)."""
+    (test_algorithm_cpu.py:36-48).  The causal mask is the one the ring uses (query i sees
+    key j <= i) when Tq == Tk, and bottom-right aligned otherwise, as FA4's varlen causal
+    mask (the call of fa4_ring/fa4_backend.py:106-120): query i sees key j <= i + Tk - Tq.
+    A row that sees no key gets out 0 and lse -inf.  ``heads`` restricts the computation
+    to those query heads (the other rows are left NaN)."""
     tq, h, d = q.shape
     tk = k.shape[0]
-    if causal:
-        assert tq == tk, "the oracle's causal mask is square"
+    off = tk - tq  # bottom-right alignment (0 for the ring's square causal step)
     kq = expand_kv(k.float(), h)
     vq = expand_kv(v.float(), h)
     out = torch.full((tq, h, v.shape[2]), float("nan"), dtype=torch.float32)
@@ -162,11 +165,12 @@ def cpu_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, sc
             r1 = min(tq, r0 + row_chunk)
             sc = (qf[r0:r1, hh, :] @ kh.T) * scale  # [rows, Tk]
             if causal:
-                qi = torch.arange(r0, r1).unsqueeze(1)
+                qi = torch.arange(r0, r1).unsqueeze(1) + off
                 kj = torch.arange(tk).unsqueeze(0)
                 sc = sc.masked_fill(kj > qi, float("-inf"))
             l = torch.logsumexp(sc, dim=-1)
-            p = torch.softmax(sc, dim=-1)
+            # a row without keys (all -inf) has a NaN softmax: it gets out 0, lse -inf
+            p = torch.nan_to_num(torch.softmax(sc, dim=-1), nan=0.0)
             out[r0:r1, hh, :] = p @ vh
             lse[r0:r1, hh] = l
     return out, lse

@@ -44,8 +44,9 @@ def seq_bounds(cu, total, sel):
 
 
 def oracle_attn(q, k, v, causal, scale, cu_q=None, cu_k=None, q_sel=0, k_sel=0):
-    """Oracle attention over the same packed layout and selections as the kernel: rows not
-    selected are NaN (out) / NaN (lse).  Causal is bottom-right aligned per sequence."""
+    """Oracle attention (O.cpu_attn per sequence) over the same packed layout and selections
+    as the kernel: rows not selected are NaN (out) / NaN (lse).  Causal is bottom-right
+    aligned per sequence."""
     tq, h, d = q.shape
     out = torch.full((tq, h, v.shape[2]), float("nan"))
     lse = torch.full((tq, h), float("nan"))
@@ -59,33 +60,9 @@ def oracle_attn(q, k, v, causal, scale, cu_q=None, cu_k=None, q_sel=0, k_sel=0):
             out[qs:qe] = 0
             lse[qs:qe] = float("-inf")
             continue
-        if causal and lq == lk:
-            o, l = O.cpu_attn(q[qs:qe], k[ks:ke], v[ks:ke], causal=True, scale=scale)
-            out[qs:qe] = o
-            lse[qs:qe] = l
-        elif causal:
-            off = lk - lq
-            # square causal on the aligned suffix; rows with no key get (0, -inf)
-            o = torch.zeros(lq, h, v.shape[2])
-            l = torch.full((lq, h), float("-inf"))
-            kq = O.expand_kv(k[ks:ke].float(), h)
-            vq = O.expand_kv(v[ks:ke].float(), h)
-            for hh in range(h):
-                sc = (q[qs:qe, hh].float() @ kq[:, hh].T) * scale
-                qi = torch.arange(lq).unsqueeze(1) + off
-                kj = torch.arange(lk).unsqueeze(0)
-                sc = sc.masked_fill(kj > qi, float("-inf"))
-                ll = torch.logsumexp(sc, -1)
-                p = torch.softmax(sc, -1)
-                p = torch.nan_to_num(p, nan=0.0)
-                o[:, hh] = p @ vq[:, hh]
-                l[:, hh] = ll
-            out[qs:qe] = o
-            lse[qs:qe] = l
-        else:
-            o, l = O.cpu_attn(q[qs:qe], k[ks:ke], v[ks:ke], causal=False, scale=scale)
-            out[qs:qe] = o
-            lse[qs:qe] = l
+        o, l = O.cpu_attn(q[qs:qe], k[ks:ke], v[ks:ke], causal=causal, scale=scale)
+        out[qs:qe] = o
+        lse[qs:qe] = l
     return out, lse
 
 

@@ -215,6 +215,29 @@ def test_mergers_on_device_ring_partials(mode, rank):
     assert max_err(out, eo) <= TOL_BF16_OUT
 
 
+def test_incremental_merger_reused_buffer():
+    """A caller that writes every step's partial into one preallocated buffer (as
+    fa4_attn(..., out=part) invites) gets the same merge as with separate buffers: the
+    first add copies the partial before the buffer is overwritten."""
+    say("incremental merger, one partial buffer reused across add() calls")
+    n, h, hkv, d, cp, rank = 1024, 8, 2, 128, 4, 3
+    parts, oparts = _ring_partials(n, h, hkv, d, cp, rank)
+    buf_o, buf_l = torch.empty_like(parts[0][0]), torch.empty_like(parts[0][1])
+    m = make_merger("incremental")
+    for o, l in parts:
+        buf_o.copy_(o)
+        buf_l.copy_(l)
+        m.add(buf_o, buf_l)
+    buf_o.fill_(float("nan"))  # the merger must hold nothing of the caller's buffer
+    out = m.result()
+    torch.cuda.synchronize()
+    eo, el = oparts[0]
+    for o, l in oparts[1:]:
+        eo, el = O.merge(eo, el, o, l)
+    assert lse_err(m.lse, el) <= TOL_LSE
+    assert max_err(out, eo) <= TOL_BF16_OUT
+
+
 @pytest.mark.parametrize("mode", ["incremental", "batched"])
 def test_merger_single_partial(mode):
     """One partial: the incremental merger returns a copy (later changes to the caller's
@@ -479,12 +502,85 @@ def test_attention_e4m3(case, use_vt):
     assert lse_err(lse.cpu()[sel], el[sel]) <= TOL_LSE
 
 
+PAD_CASES = [
+    # tq, tk, h, hkv, d, causal, q_sel, k_sel, cu: head dims without a kernel of their own
+    (200, 200, 8, 2, 32, True, SEL_ALL, SEL_ALL, None),
+    (256, 256, 4, 1, 80, False, SEL_ALL, SEL_FRONT_HALF, None),
+    (256, 256, 8, 2, 96, False, SEL_BACK_HALF, SEL_ALL, None),
+    (None, None, 4, 2, 96, True, SEL_ALL, SEL_ALL, [0, 64, 200, 202, 460]),
+    (130, 130, 4, 2, 192, True, SEL_ALL, SEL_ALL, None),
+    (64, 96, 4, 4, 160, True, SEL_ALL, SEL_ALL, None),  # bottom-right causal
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", PAD_CASES)
+def test_attention_padded_head_dims(dtype, case):
+    """Head dims without a kernel run at the next supported one on zero-padded copies, with
+    the selection semantics intact: rows outside a q selection keep what out held."""
+    tq, tk, h, hkv, d, causal, q_sel, k_sel, cu = case
+    if cu is not None:
+        tq = tk = cu[-1]
+    say(f"attn padded head dim {dtype} tq={tq} tk={tk} h={h}/{hkv} d={d} causal={causal} sel={q_sel},{k_sel} cu={cu}")
+    q, k, v = _qkv(tq, tk, h, hkv, d, 13, dtype)
+    scale = scale_for(d)
+    cud = None if cu is None else torch.tensor(cu, dtype=torch.int32, device=DEV)
+    mx = None if cu is None else max(b - a for a, b in zip(cu[:-1], cu[1:]))
+    out = torch.full((tq, h, d), float("nan"), dtype=dtype, device=DEV)
+    lse = torch.full((tq, h), float("nan"), device=DEV)
+    got, glse = fa4_attn(q.to(dtype).to(DEV), k.to(dtype).to(DEV), v.to(dtype).to(DEV), causal=causal,
+                         cu_seqlens_q=cud, cu_seqlens_k=cud, max_seqlen_q=mx, max_seqlen_k=mx,
+                         q_sel=q_sel, k_sel=k_sel, out=out, lse=lse)
+    assert got is out and glse is lse
+    eo, el = oracle_attn(q, k, v, causal, scale, cu, cu, q_sel, k_sel)  # default scale: 1/sqrt(d)
+    sel = ~torch.isnan(el)
+    assert torch.isnan(out.cpu().float()[~sel]).all() and torch.isnan(lse.cpu()[~sel]).all()
+    assert max_err(out, eo, sel.unsqueeze(-1).expand_as(eo)) <= TOL_BF16_OUT
+    assert lse_err(lse.cpu()[sel], el[sel]) <= TOL_LSE
+    if q_sel == SEL_ALL:  # fresh outputs
+        o2, l2 = fa4_attn(q.to(dtype).to(DEV), k.to(dtype).to(DEV), v.to(dtype).to(DEV), causal=causal,
+                          cu_seqlens_q=cud, cu_seqlens_k=cud, max_seqlen_q=mx, max_seqlen_k=mx, k_sel=k_sel)
+        assert o2.shape == (tq, h, d) and o2.is_contiguous()
+        assert torch.equal(o2, out) and torch.equal(l2, lse)
+
+
+@pytest.mark.parametrize("d", [64, 96, 200])
+def test_attention_e4m3_padded_head_dims(d):
+    say(f"attn e4m3 padded head dim d={d}")
+    tq, h, hkv = 384, 8, 2
+    g = torch.Generator().manual_seed(31)
+    qf, kf, vf = (torch.randn(tq, hh, d, generator=g) for hh in (h, hkv, hkv))
+    sq, sk, sv = O.amax_scale(qf), O.amax_scale(kf), O.amax_scale(vf)
+    q8, k8, v8 = O.quantize_e4m3(qf, sq), O.quantize_e4m3(kf, sk), O.quantize_e4m3(vf, sv)
+    out, lse = fa4_attn(q8.to(DEV), k8.to(DEV), v8.to(DEV), causal=True, q_descale=torch.tensor(sq, device=DEV),
+                        k_descale=torch.tensor(sk, device=DEV), v_descale=torch.tensor(sv, device=DEV))
+    assert out.dtype == torch.bfloat16 and out.shape == (tq, h, d)
+    eo, el = O.cpu_attn(O.dequantize_e4m3(q8, sq), O.dequantize_e4m3(k8, sk), O.dequantize_e4m3(v8, sv), True,
+                        scale_for(d))
+    assert max_err(out, eo) <= TOL_FP8_OUT and lse_err(lse, el) <= TOL_LSE
+
+
+def test_attention_inputs_not_contiguous_in_d():
+    """q, k and v whose head dim is strided are copied to contiguous rows first (as the
+    reference's .contiguous() before FA4): same result as contiguous inputs."""
+    say("attn inputs strided in D")
+    q, k, v = _qkv(256, 256, 8, 2, 128, 17, torch.bfloat16)
+    qb, kb, vb = (t.to(torch.bfloat16).to(DEV) for t in (q, k, v))
+    qs, ks, vs = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (qb, kb, vb))  # stride(2) != 1
+    assert qs.stride(2) != 1 and torch.equal(qs, qb)
+    o1, l1 = fa4_attn(qs, ks, vs, causal=True)
+    o2, l2 = fa4_attn(qb, kb, vb, causal=True)
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    eo, el = O.cpu_attn(q, k, v, True, scale_for(128))
+    assert max_err(o1, eo) <= TOL_BF16_OUT and lse_err(l1, el) <= TOL_LSE
+
+
 def test_attention_rejects_unsupported():
     say("attn rejects")
-    x = torch.zeros(64, 2, 96, dtype=torch.bfloat16, device=DEV)
+    x = torch.zeros(64, 2, 320, dtype=torch.bfloat16, device=DEV)
     with pytest.raises(AssertionError, match="head dim"):
         fa4_attn(x, x, x, causal=True)
-    y = torch.zeros(64, 2, 64, dtype=torch.float8_e4m3fn, device=DEV)
+    y = torch.zeros(64, 2, 288, dtype=torch.float8_e4m3fn, device=DEV)
     with pytest.raises(AssertionError, match="head dim"):
         fa4_attn(y, y, y, causal=True)
     z = torch.zeros(64, 3, 128, dtype=torch.bfloat16, device=DEV)

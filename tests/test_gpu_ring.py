@@ -294,6 +294,57 @@ def test_ring_fp8_all_ranks(n, h, hkv, d, cp, mode):
 
 
 @pytest.mark.parametrize("mode", PATHS)
+@pytest.mark.parametrize("dtype_name,d", [("bf16", 96), ("fp16", 48), ("bf16", 192), ("e4m3", 64)])
+def test_ring_padded_head_dim_all_ranks(dtype_name, d, mode):
+    """Head dims without a kernel: ring_flash_attn pads Q and every shard once and runs the
+    sweep at the next supported head dim; every rank against the oracle's ring."""
+    n, h, hkv, cp = 1024, 8, 2, 4
+    say(f"ring padded head dim {dtype_name} d={d} n={n} cp={cp} path={mode}")
+    q, k, v = O.random_qkv(n, h, hkv, d, seed=6)
+    scale = scale_for(d)
+    for rank in range(cp):
+        cfg, fused = _cfg_path(mode, cp, rank)
+        if dtype_name == "e4m3":
+            (q8, k8, v8, sq, sk, sv), (lq, ks, vs) = _fp8_ring_inputs(q, k, v, cp, rank)
+            ring = LocalKVRing([x.to(DEV) for x in k8], [x.to(DEV) for x in v8])
+            desc = Descales(q=torch.tensor(sq, device=DEV), k=[torch.tensor(s, device=DEV) for s in sk],
+                            v=[torch.tensor(s, device=DEV) for s in sv])
+            out, lse = ring_flash_attn(q8.to(DEV), ring.k[rank], ring.v[rank], cfg, group=ring, descales=desc,
+                                       fused=fused, return_lse=True)
+            tol = TOL_FP8_OUT
+        else:
+            dt = torch.bfloat16 if dtype_name == "bf16" else torch.float16
+            qr, kr, vr = (rounded(t, dt) for t in (q, k, v))
+            qd, ring = _device_ring(qr, kr, vr, cp, dt)
+            lq = O.zigzag_shard(qr, rank, cp)
+            ks = [O.zigzag_shard(kr, r, cp) for r in range(cp)]
+            vs = [O.zigzag_shard(vr, r, cp) for r in range(cp)]
+            out, lse = ring_flash_attn(zigzag_shard(qd, rank, cp), ring.k[rank], ring.v[rank], cfg, group=ring,
+                                       fused=fused, return_lse=True)
+            tol = TOL_BF16_OUT
+        assert out.shape == (n // cp, h, d) and out.is_contiguous()
+        ref, ref_lse = O.ring_rank(lq, ks, vs, rank, cp, scale, merge_mode=cfg.merge_mode)
+        assert max_err(out, ref) <= tol, f"rank {rank}"
+        assert lse_err(lse, ref_lse) <= TOL_LSE, f"rank {rank} lse"
+
+
+def test_ring_inputs_not_contiguous_in_d():
+    """local q and every K / V shard with a strided head dim: copied to contiguous rows, the
+    sweep's result equals the one on contiguous inputs bit for bit."""
+    n, h, hkv, d, cp, rank = 1024, 8, 2, 128, 4, 2
+    say(f"ring inputs strided in D n={n} cp={cp} rank={rank}")
+    q, k, v = O.random_qkv(n, h, hkv, d, seed=8)
+    qd, ring = _device_ring(q, k, v, cp, torch.bfloat16)
+    strided = lambda t: t.transpose(1, 2).contiguous().transpose(1, 2)  # noqa: E731
+    ring_s = LocalKVRing([strided(x) for x in ring.k], [strided(x) for x in ring.v])
+    lq = zigzag_shard(qd, rank, cp)
+    cfg = RingConfig(cp_size=cp, cp_rank=rank)
+    want = ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring)
+    got = ring_flash_attn(strided(lq), strided(ring.k[rank]), strided(ring.v[rank]), cfg, group=ring_s)
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("mode", PATHS)
 def test_ring_fp8_varlen_all_ranks(mode):
     lens = [608, 1216, 1072, 608, 232, 1928, 344, 200]
     cp, h, hkv, d = 4, 8, 2, 128

@@ -362,17 +362,20 @@ def test_ring_without_local_kv_source_raises():
 
 def test_fused_sweep_rejects_what_it_does_not_cover():
     """fused=True is refused (AssertionError, before any device work) outside the fused
-    kernel's cases: fp32, a head dim other than 64/128/256 (bf16) or 128/256 (e4m3), cp_size 1
-    or above 16, bf16 with descales."""
+    kernel's cases: fp32, cp_size 1 or above 16, bf16 with descales.  Head dims above 256
+    are refused for every form."""
     cfg = RingConfig(cp_size=2, cp_rank=0)
 
     def ring_of(x):
         return LocalKVRing([x, x], [x, x])
 
-    for dt, d in [(torch.float32, 128), (torch.bfloat16, 96), (torch.float8_e4m3fn, 64)]:
-        x = torch.zeros(16, 2, d, dtype=dt)
-        with pytest.raises(AssertionError, match="fused ring sweep"):
-            ring_flash_attn(x, x, x, cfg, group=ring_of(x), fused=True)
+    x = torch.zeros(16, 2, 128, dtype=torch.float32)
+    with pytest.raises(AssertionError, match="fused ring sweep"):
+        ring_flash_attn(x, x, x, cfg, group=ring_of(x), fused=True)
+    for dt in (torch.bfloat16, torch.float8_e4m3fn):
+        x = torch.zeros(16, 2, 320, dtype=dt)
+        with pytest.raises(AssertionError, match="head dim 320"):
+            ring_flash_attn(x, x, x, cfg, group=ring_of(x))
     x = torch.zeros(16, 2, 128, dtype=torch.bfloat16)
     with pytest.raises(AssertionError, match="fused ring sweep"):
         ring_flash_attn(x, x, x, cfg, group=ring_of(x), fused=True, descales=Descales(q=torch.tensor(1.0)))
@@ -381,6 +384,41 @@ def test_fused_sweep_rejects_what_it_does_not_cover():
     big = RingConfig(cp_size=17, cp_rank=0)
     with pytest.raises(AssertionError, match="fused ring sweep"):
         ring_flash_attn(x, x, x, big, group=LocalKVRing([x] * 17, [x] * 17), fused=True)
+
+
+def test_kernel_head_dim_and_padding():
+    """Head dims without a kernel run at the next supported one on zero-padded copies."""
+    from fa4_ring.fa4_backend import kernel_head_dim, pad_head_dim
+    bf, e8 = torch.bfloat16, torch.float8_e4m3fn
+    assert [kernel_head_dim(bf, d) for d in (1, 32, 64, 65, 96, 128, 129, 192, 256)] == \
+        [64, 64, 64, 128, 128, 128, 256, 256, 256]
+    assert [kernel_head_dim(e8, d) for d in (16, 64, 128, 160, 256)] == [128, 128, 128, 256, 256]
+    for dt, d in ((bf, 257), (e8, 300), (bf, 0)):
+        with pytest.raises(AssertionError, match="head dim"):
+            kernel_head_dim(dt, d)
+    with pytest.raises(AssertionError, match="dtype"):
+        kernel_head_dim(torch.float32, 128)
+    x = torch.randn(5, 3, 80).to(bf)
+    y = pad_head_dim(x, 128)
+    assert y.shape == (5, 3, 128) and y.is_contiguous() and torch.equal(y[..., :80], x)
+    assert torch.all(y[..., 80:] == 0)
+    assert pad_head_dim(x, 80) is x
+    z = torch.randn(5, 80, 3).to(bf).transpose(1, 2)  # not contiguous in D
+    assert pad_head_dim(z, 80).is_contiguous() and torch.equal(pad_head_dim(z, 80), z)
+    q8 = torch.randn(4, 2, 64).to(e8)
+    p8 = pad_head_dim(q8, 128)
+    assert p8.dtype == e8 and torch.equal(p8[..., :64].view(torch.uint8), q8.view(torch.uint8))
+    assert torch.all(p8[..., 64:].view(torch.uint8) == 0)
+
+
+def test_max_seqlen_below_the_longest_sequence_is_refused():
+    """max_seqlen sizes the kernels' grids: a bound below the longest local sequence would
+    leave rows unwritten, so it is refused before any device work."""
+    cfg = RingConfig(cp_size=1, cp_rank=0)
+    q = torch.zeros(16, 2, 128, dtype=torch.bfloat16)
+    cu = torch.tensor([0, 6, 16], dtype=torch.int32)
+    with pytest.raises(AssertionError, match="max_seqlen 8 is below the longest local sequence"):
+        ring_flash_attn(q, q, q, cfg, cu_seqlens=cu, max_seqlen=8)
 
 
 def test_odd_local_lengths_are_refused():
@@ -398,15 +436,16 @@ def test_odd_local_lengths_are_refused():
         get_half_index(torch.tensor([0, 6, 11], dtype=torch.int32), front=True)
 
 
-def test_kv_shards_must_be_contiguous_in_d():
-    """The sweep's arguments carry K's row and head strides only, so a K or V view whose head
-    dim is strided is refused (it would otherwise be read as contiguous)."""
-    x = torch.zeros(16, 128, 2, dtype=torch.bfloat16).transpose(1, 2)  # [16, 2, 128], stride(2) = 2
+def test_kv_shards_not_contiguous_in_d_are_copied():
+    """The sweep's arguments carry K's row and head strides only, so LocalKVRing keeps a
+    contiguous copy of a K or V view whose head dim is strided (as the reference copies with
+    .contiguous() before FA4); shards already contiguous in D are kept as given."""
+    x = torch.randn(16, 128, 2).to(torch.bfloat16).transpose(1, 2)  # [16, 2, 128], stride(2) = 2
     ok = torch.zeros(16, 2, 128, dtype=torch.bfloat16)
-    with pytest.raises(AssertionError, match="contiguous in D"):
-        LocalKVRing([ok, x], [ok, ok])
-    with pytest.raises(AssertionError, match="contiguous in D"):
-        LocalKVRing([ok, ok], [x, ok])
+    ring = LocalKVRing([ok, x], [ok, x])
+    assert ring.k[0] is ok and ring.v[0] is ok
+    for t in (ring.k[1], ring.v[1]):
+        assert t.stride(2) == 1 and t.stride() == ok.stride() and torch.equal(t, x)
 
 
 def test_merge_entry_points_validate_without_gpu():

@@ -92,17 +92,23 @@ def test_c4_lengths_fixture():
 # ---------------------------------------------------------------- attention + lse
 
 
-def _brute_attn(q, k, v, causal, scale):
-    """float64 triple loop: the textbook definition."""
+def _brute_attn(q, k, v, causal, scale, align=None):
+    """float64 triple loop: the textbook definition.  Causal: query i sees the keys
+    j <= i + align, align = Tk - Tq (bottom-right) unless given; a query that sees no key
+    gets out 0 and lse -inf."""
     tq, h, d = q.shape
     tk, hkv, _ = k.shape
     g = h // hkv
+    align = tk - tq if align is None else align
     out = np.zeros((tq, h, v.shape[2]))
     lse = np.zeros((tq, h))
     qn, kn, vn = q.double().numpy(), k.double().numpy(), v.double().numpy()
     for i in range(tq):
         for hh in range(h):
-            keys = range(tk) if not causal else range(i + 1)
+            keys = range(tk) if not causal else range(min(tk, max(0, i + align + 1)))
+            if len(keys) == 0:
+                lse[i, hh] = -math.inf
+                continue
             sc = np.array([scale * float(np.dot(qn[i, hh], kn[j, hh // g])) for j in keys])
             m = sc.max()
             w = np.exp(sc - m)
@@ -122,6 +128,32 @@ def test_cpu_attn_vs_brute_force(causal, h, hkv):
     bo, bl = _brute_attn(q, k, v, causal, scale)
     assert (out.double() - bo).abs().max() < 1e-5
     assert (lse.double() - bl).abs().max() < 1e-5
+
+
+@pytest.mark.parametrize("tq,tk", [(5, 11), (11, 5), (1, 7), (7, 1), (8, 8)])
+def test_cpu_attn_bottom_right_causal(tq, tk):
+    """Causal with Tq != Tk is bottom-right aligned (query i sees key j <= i + Tk - Tq), the
+    mask the kernel-level tests use for packed query / key lengths that differ.  Rows that
+    see no key give (0, -inf).  A mask aligned top-left instead (a planted mistake) must
+    fail the same comparison."""
+    g = torch.Generator().manual_seed(11)
+    h, hkv, d = 4, 2, 8
+    q = torch.randn(tq, h, d, generator=g)
+    k = torch.randn(tk, hkv, d, generator=g)
+    v = torch.randn(tk, hkv, d, generator=g)
+    scale = 0.41
+    out, lse = O.cpu_attn(q, k, v, True, scale)
+    bo, bl = _brute_attn(q, k, v, True, scale)
+    assert (out.double() - bo).abs().max() < 1e-5
+    fin = torch.isfinite(bl)
+    assert torch.equal(torch.isfinite(lse), fin)
+    assert (lse.double()[fin] - bl[fin]).abs().max() < 1e-5
+    if tq > tk:  # the first Tq - Tk queries see no key
+        assert torch.all(out[: tq - tk] == 0) and torch.all(lse[: tq - tk] == -math.inf)
+    if tq != tk:
+        po, pl = _brute_attn(q, k, v, True, scale, align=0)  # planted: top-left alignment
+        bad = (out.double() - po).abs().max() > 1e-3 or not torch.equal(torch.isfinite(lse), torch.isfinite(pl))
+        assert bad, "a top-left aligned mask went unnoticed"
 
 
 def test_cpu_attn_vs_sdpa_and_chunking():
