@@ -534,7 +534,7 @@ def bwd_block(rank: int, steps: int, warmup: int) -> dict:
                         "source shards, fp32 gradients",
             "ms_per_step": round(ms, 3), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2),
             "frac_of_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-            "flop_per_step": flops, "kernels": "bwd_pack_kernel + bwd_dq_kernel<bf16,128,4> + bwd_dkdv_kernel<bf16,128>"}
+            "flop_per_step": flops, "kernels": "bwd_pack_kernel + bwd_pack_kv_kernel + bwd_dq_pp_kernel<bf16,128,4> + bwd_dkdv_kernel<bf16,128>"}
 
 
 def bench_bwd(args) -> int:

@@ -1,5 +1,5 @@
-// Backward of one rank's causal zig-zag ring sweep (gfx950, bf16 / fp16 inputs, head dim 64
-// or 128), every source rank's K / V resident on this GPU.
+// Backward of one rank's causal zig-zag ring sweep (gfx950, bf16 / fp16 inputs, head dim 64,
+// 128 or 256), every source rank's K / V resident on this GPU.
 //
 // The reference has no backward (its README lists the forward only); this is the training
 // counterpart of fa4cp_ring_sweep_fwd.  With the sweep's final natural-log LSE (one value per
@@ -17,16 +17,18 @@
 // of src's keys.  dK / dV go to one buffer per source rank: this rank's contribution to that
 // source's gradient (a multi-GPU ring sends them back to their owners).
 //
-// Three launches:
+// Four launches:
 // * bwd_pack_kernel (HBM-bound): delta, and every 32-row block of Q and dO copied into the
 //   operand order of the dK / dV products, in rows and transposed;
-// * bwd_dq_kernel: one workgroup per 32 query rows x HP heads of one kv head, walking the same
-//   key segments as the forward sweep;
+// * bwd_pack_kv_kernel (HBM-bound): every 32-key block of each source's K and V copied into
+//   the operand order of the dQ products (K rows, V rows, K transposed);
+// * bwd_dq_pp_kernel (head dims 64 / 128): one workgroup per 64 query rows x 4 heads of one kv
+//   head, two groups of four wavefronts in a ping-pong (one in its MFMA phase while the other
+//   is in its VALU phase on every SIMD), walking the same key blocks as the forward sweep;
+//   at head dim 256, bwd_dq_pair_kernel, whose wavefronts pair as dK / dV's do;
 // * bwd_dkdv_kernel: one workgroup per 128 keys of one source and kv head, eight wavefronts
 //   in pairs, walking the packed blocks of the query rows that attend them, for every query
 //   head of the group.
-// At head dim 256 dq runs as two launches instead: bwd_pack_kv_kernel packs every source's K
-// and V blocks, and bwd_dq_pair_kernel runs its wavefronts in pairs as dK / dV does.
 //
 // Products run on v_mfma_f32_32x32x16_{bf16,f16}.  Operand layouts (lane l, h = l / 32):
 // A lane l holds row l % 32, k = 8h + 0..7; B lane l holds column l % 32, the same k; the
@@ -34,7 +36,8 @@
 // its rows in the order sig(m) (bits 2 and 3 of m swapped) makes accumulator register r of
 // lane l the entry 16 (r / 8) + 8h + r % 8 along the A side, which is exactly the k slot
 // layout of an A or B operand of the next product: the scores of one product feed the next
-// without leaving the registers.  Transposed operands come from ds_read_b64_tr_b16.
+// without leaving the registers.  Every operand an LDS read supplies is a linear 16-byte
+// fragment of a packed block: no transposing LDS read is left.
 #include <type_traits>
 
 #include "common.h"
@@ -61,8 +64,6 @@ constexpr int pack_block_bytes() { return 4 * pack_region_bytes<D>() + 256; }
 template <int D>
 constexpr int kv_block_bytes() { return 3 * pack_region_bytes<D>(); }
 
-typedef short bs16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) bs16x4 lds_bs16x4;
 
 template <typename T>
 struct BwdMfma;
@@ -93,7 +94,7 @@ struct BwdParams {
   float* delta;        // [total][h_q], written by bwd_pack_kernel
   const void* out;
   char* pk;            // packed Q / dO blocks [h_q][n_pb][pack_block_bytes]
-  char* pkv;           // packed K / V blocks [S][h_kv][n_pb][kv_block_bytes] (head dim 256)
+  char* pkv;           // packed K / V blocks [S][h_kv][n_pb][kv_block_bytes]
   int64_t n_pb;
   float* dq;           // [total][h_q][d]
   const void* k[FA4CP_MAX_CP];
@@ -123,37 +124,6 @@ __device__ __forceinline__ StepPairs step_pairs(int rank, int S, int src, int L)
   sp.key_lim = (s != 0 && s <= rank) ? (L >> 1) : L;
   sp.row_min = s > rank ? (L >> 1) : 0;
   return sp;
-}
-
-// 8 elements (16 bytes) of LDS row `row`, starting at element 8 * chunk.
-template <typename T, int RS>
-__device__ __forceinline__ typename BwdMfma<T>::frag lds_frag(const T* lds, int row, int chunk) {
-  return *reinterpret_cast<const typename BwdMfma<T>::frag*>(lds + row * RS + 8 * chunk);
-}
-
-// Transposed operand from a row-major LDS tile: lane l receives column col0 + l % 32 of rows
-// row0 + 8h + 0..7 (two ds_read_b64_tr_b16, each handing every lane of a 16-lane group four
-// rows of its column).
-template <typename T, int RS>
-__device__ __forceinline__ typename BwdMfma<T>::frag lds_frag_tr(const T* lds, int row0, int col0) {
-  const int l = threadIdx.x & 63;
-  const int g = l >> 4, j = l & 15;
-  const int row = row0 + 8 * (g >> 1) + (j >> 2);
-  const int col = col0 + 16 * (g & 1) + 4 * (j & 3);
-  const T* p = lds + row * RS + col;
-  const bs16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_bs16x4*)p);
-  const bs16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_bs16x4*)(p + 4 * RS));
-  const bs16x4 ab[2] = {a, b};
-  return __builtin_bit_cast(typename BwdMfma<T>::frag, ab);
-}
-
-// Workgroup barrier after this wavefront's LDS writes have completed, leaving its global
-// loads in flight: __syncthreads() would also wait for those (its fence waits for every
-// outstanding memory operation), which would serialise the prefetch of the next tile with
-// the barrier.
-__device__ __forceinline__ void lds_written_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt unconstrained
-  wg_barrier();
 }
 
 template <typename T>
@@ -491,72 +461,71 @@ __global__ __launch_bounds__(128 * HP) void bwd_dq_pair_kernel(BwdParams p) {
   }
 }
 
-// A 32-row x D tile in flight to LDS: thread t loads 16-byte chunks t + NT i (row-major over
-// the tile) into registers, so the next tile's loads overlap the current tile's products;
-// rows at or past `lim` read as zeros (a product must never see stale or non-finite data).
-template <typename T, int D, int NT>
-struct TileFetch {
-  static constexpr int CPR = D / 8;
-  static constexpr int N = kBwdRows * CPR / NT;
-  static_assert(N * NT == kBwdRows * CPR, "threads must split the tile evenly");
-  u32x4 x[N];
-  __device__ __forceinline__ void fetch(const T* src, int64_t rs, int row0, int lim) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const int c = (int)threadIdx.x + NT * i, r = c / CPR, ch = c % CPR;
-      x[i] = u32x4{0u, 0u, 0u, 0u};
-      if (row0 + r < lim) x[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)(row0 + r) * rs + 8 * ch);
-    }
-  }
-  template <int RS>
-  __device__ __forceinline__ void store(T* lds) const {
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const int c = (int)threadIdx.x + NT * i, r = c / CPR, ch = c % CPR;
-      *reinterpret_cast<u32x4*>(lds + r * RS + 8 * ch) = x[i];
-    }
-  }
-};
-
-// dQ: one workgroup per 32 query rows x HP query heads of one kv head (one wavefront per
-// head), walking every ring step's keys in tiles of 32 (the forward sweep's schedule).  The
-// tiles go through LDS; the next tile's loads are in flight while the current one is used.
+// dQ up to head dim 128, ping-pong form: one workgroup of eight wavefronts in two groups of
+// four per 64 x RB query rows x HP query heads of one kv head (HP x RB = 4).  Wavefront w of
+// group g = w / 4 takes head (w % 4) % HP and row block RB g + (w % 4) / HP.  Both groups walk
+// the same packed key blocks (bwd_pack_kv_kernel: K rows, V rows, K transposed), group 1 one
+// phase behind group 0, so on every SIMD one wavefront is in its MFMA phase (dQ += dS K of
+// block i - 1, S^T = K Q^T and dP^T = V dO^T of block i: 24 MFMAs at head dim 128, fragment
+// reads four ahead) while the other is in its VALU phase (dS^T = P^T (dP^T - delta) of its
+// block).  A workgroup barrier ends every phase.  Block b sits in stage b % 3: group 1 loads it
+// by LDS-DMA in its VALU phase two phases before group 0's MFMA phase reads it, and waits for
+// it at the end of its next MFMA phase; the stage it overwrites was last read (K^T) in the
+// phase before the load.
 template <typename T, int D, int HP>
-__global__ __launch_bounds__(64 * HP) void bwd_dq_kernel(BwdParams p) {
+__global__ __launch_bounds__(512) void bwd_dq_pp_kernel(BwdParams p) {
   using M = BwdMfma<T>;
-  constexpr int RS = D + 8;     // LDS row stride (elements): rows shift by 16 bytes
-  constexpr int NKS = D / 16;   // k-steps over the head dim
-  constexpr int NDT = D / 32;   // output tiles over the head dim
-  constexpr int NT = 64 * HP;
-  __shared__ __align__(16) T ks[kBwdRows * RS];
-  __shared__ __align__(16) T vs[kBwdRows * RS];
+  typedef typename M::frag frag;
+  constexpr int NKS = D / 16;
+  constexpr int NDT = D / 32;
+  constexpr int R = pack_region_bytes<D>();
+  constexpr int KB = kv_block_bytes<D>();
+  constexpr int RB = 4 / HP;   // 32-row blocks per group
+  constexpr int NF = 3 * NKS;  // 1 KB fragments per key block
+  constexpr int kWaitAll = 7 << 4;  // vmcnt(0), lgkmcnt(0)
+  static_assert(D <= 128 && HP * RB == 4, "two groups of four wavefronts, head dim up to 128");
+  static_assert(NF % 4 == 0, "a block's fragments split over one group");
+  // Three stages in separate arrays: the LDS-DMA destination is chosen at run time, so the
+  // compiler does not make the first LDS read of a phase wait for every load in flight.
+  __shared__ __align__(16) char stage0[KB];
+  __shared__ __align__(16) char stage1[KB];
+  __shared__ __align__(16) char stage2[KB];
+  auto stage_of = [&](int bi) {
+    const int m = bi % 3;
+    return m == 0 ? stage0 : m == 1 ? stage1 : stage2;
+  };
 
+  // longest first: the back-half row tiles attend the later sources and come out first
   const int n_hg = p.h_q / HP;
   int b = blockIdx.x;
   const int hg = b % n_hg;
   b /= n_hg;
-  const int rt = b % p.n_tiles;
+  const int rt = p.n_tiles - 1 - b % p.n_tiles;
   const int seq = b / p.n_tiles;
+  const int64_t pstart = vt_seq_start(p.cu, seq, p.total, FA4CP_SEL_ALL) / kBwdRows;
   int qs, L;
   seq_range(p.cu, seq, p.total, FA4CP_SEL_ALL, qs, L);
-  const int r0 = rt * kBwdRows;
+  const int r0 = rt * kBwdRows * 2 * RB;  // the workgroup's first row
   if (r0 >= L) return;
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, h = l >> 5, lq = l & 31;
-  const int head = hg * HP + w;
-  const int kvh = head / p.group;
-  const int qpos = r0 + lq;  // this lane's query row in the sequence
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int grp = w >> 2, wj = w & 3;
+  const int l = threadIdx.x & 63, h = l >> 5, lq = l & 31;
+  const int head = hg * HP + wj % HP;
+  const int kvh = head / p.group;   // the same for the workgroup's HP heads (group % HP == 0)
+  const int wr0 = r0 + kBwdRows * (RB * grp + wj / HP);  // the wavefront's first row
+  const int qpos = wr0 + lq;                               // this lane's query row in the sequence
   const bool row_ok = qpos < L;
+  const int r_end = r0 + kBwdRows * 2 * RB;                // past the workgroup's last row
 
-  // Q and dO of the lane's row: B operands of S^T = K Q^T and dP^T = V dO^T
-  typename M::frag qf[NKS], df[NKS];
+  frag qf[NKS], df[NKS];
   {
     const T* qr = reinterpret_cast<const T*>(p.q) + (int64_t)(qs + qpos) * p.q_rs + (int64_t)head * p.q_hs;
     const T* dr = reinterpret_cast<const T*>(p.dout) + (int64_t)(qs + qpos) * p.do_rs + (int64_t)head * p.do_hs;
 #pragma unroll
     for (int t = 0; t < NKS; ++t) {
-      typename M::frag z = {};
-      qf[t] = row_ok ? *reinterpret_cast<const typename M::frag*>(qr + 8 * h + 16 * t) : z;
-      df[t] = row_ok ? *reinterpret_cast<const typename M::frag*>(dr + 8 * h + 16 * t) : z;
+      frag z = {};
+      qf[t] = row_ok ? *reinterpret_cast<const frag*>(qr + 8 * h + 16 * t) : z;
+      df[t] = row_ok ? *reinterpret_cast<const frag*>(dr + 8 * h + 16 * t) : z;
     }
   }
   const float c = p.scale * kLog2e;
@@ -566,84 +535,157 @@ __global__ __launch_bounds__(64 * HP) void bwd_dq_kernel(BwdParams p) {
 #pragma unroll
   for (int i = 0; i < NDT; ++i) acc[i] = f32x16{};
 
-  // the key tiles of every step the row tile attends, in order: (step, first key)
+  // the key blocks of every step the workgroup's rows attend, in order: (step, first key)
   auto src_of = [&](int s) { return p.rank - s < 0 ? p.rank - s + p.S : p.rank - s; };
-  auto key_end_of = [&](int s) {  // keys of step s the tile sees (0: no row attends it)
+  auto key_end_of = [&](int s) {  // keys of step s the rows see (0: no row attends it)
     const StepPairs sp = step_pairs(p.rank, p.S, src_of(s), L);
-    if (r0 + kBwdRows <= sp.row_min) return 0;
-    return sp.causal ? min(sp.key_lim, r0 + kBwdRows) : sp.key_lim;
+    if (r_end <= sp.row_min) return 0;
+    return sp.causal ? min(sp.key_lim, r_end) : sp.key_lim;
   };
-  auto next_tile = [&](int& s, int& k0, int& kend) {
-    k0 += kBwdRows;
-    while (s < p.S && k0 >= kend) {
-      ++s;
-      k0 = 0;
-      if (s < p.S) kend = key_end_of(s);
+  int n_blk = 0;
+  for (int s = 0; s < p.S; ++s) n_blk += (key_end_of(s) + kBwdRows - 1) / kBwdRows;
+  struct Cursor {
+    int s, k0, kend;
+  };
+  auto settle = [&](Cursor& cu) {
+    while (cu.s < p.S && cu.k0 >= cu.kend) {
+      ++cu.s;
+      cu.k0 = 0;
+      if (cu.s < p.S) cu.kend = key_end_of(cu.s);
     }
   };
-  auto kv_base = [&](int s, bool isk) {
-    const int src = src_of(s);
-    return isk ? reinterpret_cast<const T*>(p.k[src]) + (int64_t)qs * p.k_rs + (int64_t)kvh * p.k_hs
-               : reinterpret_cast<const T*>(p.v[src]) + (int64_t)qs * p.v_rs + (int64_t)kvh * p.v_hs;
+  Cursor lc{0, 0, key_end_of(0)};  // the next block to load
+  settle(lc);
+  // the block at cursor lc into stage bi % 3, its fragments split over `nw` wavefronts (this
+  // one is number `wi` of them)
+  auto load = [&](int bi, int wi, int nw) {
+    const char* g = p.pkv + (((int64_t)src_of(lc.s) * p.h_kv + kvh) * p.n_pb + pstart + lc.k0 / kBwdRows) * KB;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc32(uniform_ptr(g), KB);
+    char* st = stage_of(bi);
+    for (int f = wi; f < NF; f += nw) dma16(rs, st + 1024 * f, 1024 * f + 16 * l);
+    lc.k0 += kBwdRows;
+    settle(lc);
   };
-  int cs = 0, ck0 = -kBwdRows, ckend = key_end_of(0);
-  next_tile(cs, ck0, ckend);  // the first tile (step 0 always has one: r0 < L)
-  TileFetch<T, D, NT> fk, fv;
-  if (cs < p.S) {
-    const int lim = step_pairs(p.rank, p.S, src_of(cs), L).key_lim;
-    fk.fetch(kv_base(cs, true), p.k_rs, ck0, lim);
-    fv.fetch(kv_base(cs, false), p.v_rs, ck0, lim);
-  }
-  while (cs < p.S) {
-    const StepPairs sp = step_pairs(p.rank, p.S, src_of(cs), L);
-    __syncthreads();  // the previous tile's readers are done
-    fk.template store<RS>(ks);
-    fv.template store<RS>(vs);
-    int ns = cs, nk0 = ck0, nkend = ckend;
-    next_tile(ns, nk0, nkend);
-    if (ns < p.S) {
-      const int lim = step_pairs(p.rank, p.S, src_of(ns), L).key_lim;
-      fk.fetch(kv_base(ns, true), p.k_rs, nk0, lim);
-      fv.fetch(kv_base(ns, false), p.v_rs, nk0, lim);
-    }
-    lds_written_barrier();
-    f32x16 st = {}, dpt = {};
-    // the two chains interleaved: each one's operand reads run under the other's MFMA
+  auto frag_at = [&](const char* st, int off) { return *reinterpret_cast<const frag*>(st + off + 16 * l); };
+
+  Cursor cc{0, 0, key_end_of(0)};  // the block of the wavefront's MFMA phase
+  settle(cc);
+  frag ds0 = {}, ds1 = {};  // dS of the block before (A operands of dQ)
+  f32x16 st = {}, dpt = {};
+  // Every block the workgroup loads meets some row of the workgroup, not necessarily one of
+  // each wavefront (with RB > 1 the causal step's last blocks are past the first row blocks'
+  // rows); such a block's pairs are all masked, so its dS is zero and its products add
+  // nothing.  Every iteration can therefore run the same products.
+  auto sdp_plain = [&](const char* cur) __attribute__((always_inline)) {
+    st = f32x16{};
+    dpt = f32x16{};
 #pragma unroll
     for (int t = 0; t < NKS; ++t) {
-      st = M::mma(lds_frag<T, RS>(ks, sig(lq), 2 * t + h), qf[t], st);
-      dpt = M::mma(lds_frag<T, RS>(vs, sig(lq), 2 * t + h), df[t], dpt);
+      st = M::mma(frag_at(cur, 1024 * t), qf[t], st);
+      dpt = M::mma(frag_at(cur, R + 1024 * t), df[t], dpt);
     }
+  };
+  auto dq_plain = [&](const char* prev) __attribute__((always_inline)) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      acc[dt] = M::mma(ds0, frag_at(prev, 2 * R + 1024 * (2 * dt)), acc[dt]);
+      acc[dt] = M::mma(ds1, frag_at(prev, 2 * R + 1024 * (2 * dt + 1)), acc[dt]);
+    }
+  };
+  // dQ of the block before and S / dP of the current one as straight-line code, every LDS
+  // fragment read four MFMAs ahead of its use into a register of its own (fenced MFMA by
+  // MFMA: left alone, the compiler reads each fragment into one register just before its
+  // MFMA and waits for it, and the matrix core idles through every read)
+  auto dq_sdp = [&](const char* cur, const char* prev) __attribute__((always_inline)) {
+    constexpr int NQ = 2 * NDT, N = 2 * NDT + 2 * NKS, RA = 4;
+    frag fr[N];
+    auto read = [&](int k) __attribute__((always_inline)) {
+      if (k < NQ) fr[k] = frag_at(prev, 2 * R + 1024 * k);
+      else if (k < N) fr[k] = frag_at(cur, ((k - NQ) & 1) * R + 1024 * ((k - NQ) >> 1));
+    };
+    st = f32x16{};
+    dpt = f32x16{};
+#pragma unroll
+    for (int k = 0; k < RA; ++k) read(k);
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      __builtin_amdgcn_sched_barrier(0);
+      read(k + RA);
+      if (k < NQ) {
+        acc[k >> 1] = M::mma(k & 1 ? ds1 : ds0, fr[k], acc[k >> 1]);
+      } else {
+        const int j = k - NQ;
+        if (j & 1) dpt = M::mma(fr[k], df[j >> 1], dpt);
+        else st = M::mma(fr[k], qf[j >> 1], st);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // dS^T = P^T (dP^T - delta) of the block at cursor cc
+  auto make_ds = [&]() __attribute__((always_inline)) {
+    const StepPairs sp = step_pairs(p.rank, p.S, src_of(cc.s), L);
+    const bool full = wr0 + kBwdRows <= L && wr0 >= sp.row_min && cc.k0 + kBwdRows <= sp.key_lim &&
+                      (!sp.causal || cc.k0 + kBwdRows - 1 <= wr0);
     float dsv[16];
-    // no pair of the tile masked (the usual case): no per-element test
-    const bool full = r0 + kBwdRows <= L && r0 >= sp.row_min && ck0 + kBwdRows <= sp.key_lim &&
-                      (!sp.causal || ck0 + kBwdRows - 1 <= r0);
-    if (__builtin_expect(full, 1)) {
+    if (__builtin_expect(full, 1)) {  // no pair of the block masked: no per-element test
 #pragma unroll
       for (int r = 0; r < 16; ++r) dsv[r] = __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2)) * (dpt[r] - dl);
     } else {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int kp = ck0 + acc_pos(r, h);
+        const int kp = cc.k0 + acc_pos(r, h);
         const bool ok = row_ok & (qpos >= sp.row_min) & (kp < sp.key_lim) & (!sp.causal | (kp <= qpos));
         const float pr = __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2));
         dsv[r] = (ok ? pr : 0.f) * (dpt[r] - dl);
       }
     }
-    const typename M::frag ds0 = to_frag<T>(dsv), ds1 = to_frag<T>(dsv + 8);
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      acc[dt] = M::mma(ds0, lds_frag_tr<T, RS>(ks, 0, 32 * dt), acc[dt]);
-      acc[dt] = M::mma(ds1, lds_frag_tr<T, RS>(ks, 16, 32 * dt), acc[dt]);
-    }
-    cs = ns;
-    ck0 = nk0;
-    ckend = nkend;
+    ds0 = to_frag<T>(dsv);
+    ds1 = to_frag<T>(dsv + 8);
+    cc.k0 += kBwdRows;
+    settle(cc);
+  };
+  // the end of an MFMA phase: group 1 waits for the block it loaded in its last VALU phase
+  auto end_mfma_phase = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_s_setprio(0);
+    if (grp == 1) __builtin_amdgcn_s_waitcnt(kWaitAll);
+    wg_barrier();
+  };
+  // the VALU phase of iteration i: group 1 loads block i + 2, every wavefront forms dS of block i
+  auto valu_phase = [&](int i) __attribute__((always_inline)) {
+    if (grp == 1 && i + 2 < n_blk) load(i + 2, wj, 4);
+    make_ds();
+    pin(ds0);
+    pin(ds1);
+    wg_barrier();
+  };
+
+  if (n_blk > 0) {  // blocks 0 and 1, loaded by every wavefront
+    load(0, w, 8);
+    if (n_blk > 1) load(1, w, 8);
   }
+  __builtin_amdgcn_s_waitcnt(kWaitAll);
+  wg_barrier();
+  if (grp == 1) wg_barrier();  // group 1 runs one phase behind group 0
+  __builtin_amdgcn_s_setprio(1);
+  sdp_plain(stage_of(0));
+  end_mfma_phase();
+  valu_phase(0);
+  for (int i = 1; i < n_blk; ++i) {
+    __builtin_amdgcn_s_setprio(1);
+    dq_sdp(stage_of(i), stage_of(i + 2));
+    end_mfma_phase();
+    valu_phase(i);
+  }
+  __builtin_amdgcn_s_setprio(1);
+  dq_plain(stage_of(n_blk + 2));
+  end_mfma_phase();
+  wg_barrier();
+  if (grp == 0) wg_barrier();  // both groups pass the same number of barriers
+  __builtin_amdgcn_s_waitcnt(kWaitAll);
   // accumulator register r of lane l: query row 8 (r / 4) + 4h + r % 4, column 32 dt + lq
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const int row = r0 + 8 * (r >> 2) + 4 * h + (r & 3);
+    const int row = wr0 + 8 * (r >> 2) + 4 * h + (r & 3);
     if (row >= L) continue;
     float* o = p.dq + ((int64_t)(qs + row) * p.h_q + head) * D + lq;
 #pragma unroll
@@ -807,6 +849,7 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
           prev = stage_of(i + 2);
         }
         if constexpr (PW) {
+          __builtin_amdgcn_s_setprio(1);
           if (i > 0) {
             // head dim 256: the two 16-row halves in turn over the d tiles, so that consecutive
             // MFMAs update different accumulators (each still sums its terms in the same
@@ -829,6 +872,7 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
             f32x16 st = {};
 #pragma unroll
             for (int t = 0; t < NKS; ++t) st = M::mma(frag_at(cur, OQ + 1024 * t), kv[t], st);
+            __builtin_amdgcn_s_setprio(0);
             float lse[16], pv[16];
             row_vals(cur, 0, lse);
 #pragma unroll
@@ -863,6 +907,7 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
               dsv[8 + r] = (float)e1[r] * (dpt[8 + r] - dl[8 + r]);
             }
             const frag s0 = to_frag<T>(dsv), s1 = to_frag<T>(dsv + 8);
+            __builtin_amdgcn_s_setprio(1);
             if constexpr (HALVES) {  // as for dV above
 #pragma unroll
               for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt)), s0, acc[dt]);
@@ -882,6 +927,7 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
             for (int t = 0; t < NKS; ++t) dpt = M::mma(frag_at(cur, ODO + 1024 * t), kv[t], dpt);
           }
         }
+        __builtin_amdgcn_s_setprio(0);
         if (i < n_blk) {  // the loads landed (each wavefront's own), P of block i written
           __builtin_amdgcn_s_waitcnt(kWaitAll);
           wg_barrier();
@@ -934,11 +980,17 @@ int launch_bwd(const BwdParams& base, const fa4cp_sweep_bwd_args& a, hipStream_t
       case 2: hipLaunchKernelGGL((bwd_dq_pair_kernel<T, D, 2>), dim3((unsigned)dq_blocks), dim3(256), 0, st, p); break;
       default: hipLaunchKernelGGL((bwd_dq_pair_kernel<T, D, 1>), dim3((unsigned)dq_blocks), dim3(128), 0, st, p); break;
     }
-  } else {
+  } else {  // the packed K / V blocks, then four wavefronts over 4 / hp row blocks
+    const int64_t kv_pack_blocks = (int64_t)p.S * p.h_kv * p.nseq * p.n_tiles;
+    if (kv_pack_blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "ring_sweep_bwd: too many key blocks");
+    hipLaunchKernelGGL((bwd_pack_kv_kernel<T, D>), dim3((unsigned)kv_pack_blocks), dim3(256), 0, st, p);
+    const int rows = kBwdRows * 2 * (4 / hp);  // rows per workgroup
+    p.n_tiles = (p.max_seqlen + rows - 1) / rows;
+    const int64_t blocks = (int64_t)p.nseq * p.n_tiles * (p.h_q / hp);
     switch (hp) {
-      case 4: hipLaunchKernelGGL((bwd_dq_kernel<T, D, 4>), dim3((unsigned)dq_blocks), dim3(256), 0, st, p); break;
-      case 2: hipLaunchKernelGGL((bwd_dq_kernel<T, D, 2>), dim3((unsigned)dq_blocks), dim3(128), 0, st, p); break;
-      default: hipLaunchKernelGGL((bwd_dq_kernel<T, D, 1>), dim3((unsigned)dq_blocks), dim3(64), 0, st, p); break;
+      case 4: hipLaunchKernelGGL((bwd_dq_pp_kernel<T, D, 4>), dim3((unsigned)blocks), dim3(512), 0, st, p); break;
+      case 2: hipLaunchKernelGGL((bwd_dq_pp_kernel<T, D, 2>), dim3((unsigned)blocks), dim3(512), 0, st, p); break;
+      default: hipLaunchKernelGGL((bwd_dq_pp_kernel<T, D, 1>), dim3((unsigned)blocks), dim3(512), 0, st, p); break;
     }
   }
   // dk / dv
@@ -969,11 +1021,12 @@ extern "C" int64_t fa4cp_ring_sweep_bwd_workspace_bytes(const fa4cp_sweep_bwd_ar
   if (a->total < 0 || a->h_q <= 0 || (a->d != 64 && a->d != 128 && a->d != 256) || (a->cu != nullptr && a->nseq <= 0))
     return set_error(FA4CP_EINVAL, "ring_sweep_bwd_workspace_bytes: bad shape total=%d h_q=%d d=%d nseq=%d", a->total,
                      a->h_q, a->d, a->nseq);
-  if (a->d == 256 && (a->h_kv <= 0 || a->cp_size < 1 || a->cp_size > FA4CP_MAX_CP))
+  if (a->h_kv <= 0 || a->cp_size < 1 || a->cp_size > FA4CP_MAX_CP)
     return set_error(FA4CP_EINVAL, "ring_sweep_bwd_workspace_bytes: bad shape h_kv=%d cp_size=%d", a->h_kv,
                      a->cp_size);
   const int64_t n_pb = packed_blocks(a->total, a->cu ? a->nseq : 1);
-  const int64_t kv = a->d == 256 ? (int64_t)a->cp_size * a->h_kv * n_pb * kv_block_bytes<256>() : 0;
+  const int64_t kvb = a->d == 256 ? kv_block_bytes<256>() : a->d == 128 ? kv_block_bytes<128>() : kv_block_bytes<64>();
+  const int64_t kv = (int64_t)a->cp_size * a->h_kv * n_pb * kvb;
   return delta_bytes(a->total, a->h_q) + (int64_t)a->h_q * n_pb * block_bytes(a->d) + kv;
 }
 
@@ -1019,7 +1072,7 @@ extern "C" int fa4cp_ring_sweep_bwd(const fa4cp_sweep_bwd_args* a, void* stream)
   p.delta = reinterpret_cast<float*>(a->workspace);
   p.pk = reinterpret_cast<char*>(a->workspace) + delta_bytes(a->total, a->h_q);
   p.n_pb = packed_blocks(a->total, a->cu ? a->nseq : 1);
-  p.pkv = p.pk + (int64_t)a->h_q * p.n_pb * block_bytes(a->d);  // read at head dim 256 only
+  p.pkv = p.pk + (int64_t)a->h_q * p.n_pb * block_bytes(a->d);
   p.dq = a->dq;
   for (int i = 0; i < a->cp_size; ++i) {
     p.k[i] = a->k[i];

@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libfa4cp.so"
 # FA4CP_LIB selects another build of the library (the in-tree one by default)
 LIB_PATH = os.environ.get("FA4CP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # element types (FA4CP_*)
 BF16, FP16, E4M3, FP32 = 0, 1, 2, 3

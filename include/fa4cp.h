@@ -54,7 +54,7 @@
 extern "C" {
 #endif
 
-#define FA4CP_ABI_VERSION 7
+#define FA4CP_ABI_VERSION 8
 
 /* status codes */
 #define FA4CP_OK 0
@@ -269,13 +269,13 @@ int fa4cp_ring_sweep_fwd_paged(const fa4cp_sweep_args* args, const fa4cp_sweep_k
  * Every (query row, key) pair of the forward's three step patterns contributes, with the
  * probability exp(scale q.k - lse) taken against the final lse.  workspace is caller-owned
  * device memory of at least fa4cp_ring_sweep_bwd_workspace_bytes(args) bytes, 256-byte
- * aligned: the first launch writes rowsum(dout * out) and a copy of q and dout in the operand
- * order of the dk / dv products there (about 4 x the bytes of q), at d = 256 also a copy of
- * every source's k and v (3 x the bytes of one source's k, per source); it holds nothing
- * across calls.  With accumulate != 0 the results are added to dq / dk / dv instead of stored
- * (summing the contributions of several ranks, as a ring's backward does).  q, dout and out
- * may have any row and head stride; k / v shards share strides and the cu layout of
- * fa4cp_ring_sweep_fwd.  Three launches on `stream` (four at d = 256).
+ * aligned: the first two launches write rowsum(dout * out), a copy of q and dout in the
+ * operand order of the dk / dv products (about 4 x the bytes of q) and a copy of every
+ * source's k and v in the operand order of the dq products (3 x the bytes of one source's k,
+ * per source) there; it holds nothing across calls.  With accumulate != 0 the results are
+ * added to dq / dk / dv instead of stored (summing the contributions of several ranks, as a
+ * ring's backward does).  q, dout and out may have any row and head stride; k / v shards
+ * share strides and the cu layout of fa4cp_ring_sweep_fwd.  Four launches on `stream`.
  */
 typedef struct fa4cp_sweep_bwd_args {
   const void* q;    /* [total] x h_q x d */
@@ -301,9 +301,8 @@ typedef struct fa4cp_sweep_bwd_args {
 } fa4cp_sweep_bwd_args;
 
 int fa4cp_ring_sweep_bwd(const fa4cp_sweep_bwd_args* args, void* stream);
-/* Workspace bytes fa4cp_ring_sweep_bwd needs for args' total, nseq (with cu), h_q and d, and
- * at d = 256 h_kv and cp_size (the other fields are not read); a negative FA4CP_E* code for a
- * bad shape. */
+/* Workspace bytes fa4cp_ring_sweep_bwd needs for args' total, nseq (with cu), h_q, h_kv, d and
+ * cp_size (the other fields are not read); a negative FA4CP_E* code for a bad shape. */
 int64_t fa4cp_ring_sweep_bwd_workspace_bytes(const fa4cp_sweep_bwd_args* args);
 
 /*

@@ -208,8 +208,8 @@ def test_sweep_entry_point_validates_before_launching():
 
 def test_backward_workspace_size_and_checks():
     """fa4cp_ring_sweep_bwd_workspace_bytes: delta (total x h_q float32, rounded up to 256
-    bytes) plus h_q x (padded rows / 32) packed blocks of 4 x 64 x d + 256 bytes each, and at
-    head dim 256 cp_size x h_kv x (padded rows / 32) K / V blocks of 3 x 64 x d bytes; the
+    bytes) plus h_q x (padded rows / 32) packed blocks of 4 x 64 x d + 256 bytes each, and
+    cp_size x h_kv x (padded rows / 32) K / V blocks of 3 x 64 x d bytes; the
     backward refuses a workspace that is small or not 256-byte aligned before any HIP call.
     The pointers are fake, so this never runs where a device is visible."""
     if torch.cuda.device_count() > 0:
@@ -241,11 +241,12 @@ def test_backward_workspace_size_and_checks():
         # total + 128 nseq, rounded up to 128 (fa4cp_vt_min_d_stride)
         rows = -(-(total + 128 * nseq) // 128) * 128
         assert rows == lib.fa4cp_vt_min_d_stride(total, nseq)
-        kv = 2 * 2 * (rows // 32) * 3 * 64 * d if d == 256 else 0  # head dim 256: K / V blocks (cp 2, h_kv 2)
+        kv = 2 * 2 * (rows // 32) * 3 * 64 * d  # K / V blocks (cp 2, h_kv 2)
         return delta + h_q * (rows // 32) * (4 * 64 * d + 256) + kv
 
-    # one sequence of 256 rows: 384 padded rows, so 8 heads x 12 blocks of 33024 bytes + 8 KB
-    assert lib.fa4cp_ring_sweep_bwd_workspace_bytes(ctypes.byref(args())) == 8192 + 8 * 12 * 33024
+    # one sequence of 256 rows: 384 padded rows, so 8 heads x 12 blocks of 33024 bytes + 8 KB, and
+    # 2 sources x 2 kv heads x 12 key blocks of 24576 bytes
+    assert lib.fa4cp_ring_sweep_bwd_workspace_bytes(ctypes.byref(args())) == 8192 + 8 * 12 * 33024 + 4 * 12 * 24576
     for total, nseq, h_q, d in [(256, 1, 8, 128), (100, 1, 3, 64), (16384, 1, 32, 128), (1000, 7, 4, 64),
                                 (512, 1, 4, 256)]:
         a = args(total=total, h_q=h_q, d=d, nseq=nseq, cu=fake if nseq > 1 else None)
