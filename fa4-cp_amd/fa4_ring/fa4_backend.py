@@ -62,11 +62,10 @@ def pad_head_dim(x: torch.Tensor, dp: int) -> torch.Tensor:
     return y
 
 
-def _norm_descale(d: Optional[torch.Tensor], h_kv: int, device) -> Optional[torch.Tensor]:
-    """Descale -> float32 contiguous [h_kv] on `device` (a scalar broadcasts to every kv
-    head, [h_kv] and (1, h_kv) are taken as is; fa4_backend.py:45-55)."""
-    if d is None:
-        return None
+def _descale_view(d, h_kv: int, device) -> torch.Tensor:
+    """Descale -> a float32 [h_kv] view on `device` (a scalar broadcasts to every kv head,
+    [h_kv] and (1, h_kv) are taken as is; fa4_backend.py:45-55), copied only if its dtype or
+    device differ."""
     if not torch.is_tensor(d):
         d = torch.tensor(float(d))
     d = d.to(device=device, dtype=torch.float32)
@@ -77,7 +76,21 @@ def _norm_descale(d: Optional[torch.Tensor], h_kv: int, device) -> Optional[torc
         d = d[0]
     _require(d.dim() == 1 and d.shape[0] == h_kv,
              f"descale must be a scalar, [H_kv] or (1, H_kv) with H_kv={h_kv}, got {tuple(d.shape)}")
-    return d.contiguous()
+    return d
+
+
+def _norm_descale(d: Optional[torch.Tensor], h_kv: int, device) -> Optional[torch.Tensor]:
+    """Descale -> float32 contiguous [h_kv] on `device` (see _descale_view)."""
+    if d is None:
+        return None
+    return _descale_view(d, h_kv, device).contiguous()
+
+
+def descale_table(ds, h_kv: int, device) -> torch.Tensor:
+    """Per-source descales -> one float32 contiguous [len(ds), h_kv] table, built by a single
+    stack over views (one small device copy, where normalising each entry on its own and
+    stacking takes one launch per source)."""
+    return torch.stack([_descale_view(d, h_kv, device) for d in ds])
 
 
 def _cu_ok(cu: torch.Tensor, device, name: str) -> None:

@@ -36,8 +36,9 @@ import torch
 
 from . import _lib
 from .config import RingConfig
-from .fa4_backend import (SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, SUPPORTED_HEAD_DIMS, _norm_descale, fa4_attn,
-                          kernel_head_dim, out_dtype_for, pad_head_dim, transpose_v, transpose_v_many, uses_vt)
+from .fa4_backend import (SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, SUPPORTED_HEAD_DIMS, _norm_descale, descale_table,
+                          fa4_attn, kernel_head_dim, out_dtype_for, pad_head_dim, transpose_v, transpose_v_many,
+                          uses_vt)
 from .merge import merge_state_in_place, merge_states
 from .paged import PagedKVRing, gather_kv_pages, transpose_v_paged_many
 from .zigzag import zigzag_shard, zigzag_shard_varlen
@@ -381,9 +382,9 @@ def _sweep_launch(local_q: torch.Tensor, k_ptrs: List[int], k_strides: Tuple[int
     if e4m3 and descales is not None:
         qd = _norm_descale(descales.q, h_kv, dev)
         if descales.k is not None:
-            kd = torch.stack([_norm_descale(descales.k[i], h_kv, dev) for i in range(S)]).contiguous()
+            kd = descale_table(descales.k[:S], h_kv, dev)
         if descales.v is not None:
-            vd = torch.stack([_norm_descale(descales.v[i], h_kv, dev) for i in range(S)]).contiguous()
+            vd = descale_table(descales.v[:S], h_kv, dev)
     if lse is None:
         lse = torch.empty((total, h_q), dtype=torch.float32, device=dev)
     odt = torch.bfloat16 if e4m3 else local_q.dtype

@@ -412,6 +412,18 @@ def test_kernel_head_dim_and_padding():
     assert torch.all(p8[..., 64:].view(torch.uint8) == 0)
 
 
+def test_descale_table_forms():
+    """Per-source descales in every accepted form (Python float, scalar, [H_kv], (1, H_kv))
+    become one contiguous float32 [S, H_kv] table; a wrong shape is refused."""
+    from fa4_ring.fa4_backend import descale_table
+    ds = [0.25, torch.tensor(0.5), torch.tensor([1.0, 2.0], dtype=torch.float64), torch.tensor([[3.0, 4.0]])]
+    t = descale_table(ds, 2, torch.device("cpu"))
+    assert t.dtype == torch.float32 and t.is_contiguous() and t.shape == (4, 2)
+    assert t.tolist() == [[0.25, 0.25], [0.5, 0.5], [1.0, 2.0], [3.0, 4.0]]
+    with pytest.raises(AssertionError, match="descale"):
+        descale_table([torch.tensor([1.0, 2.0, 3.0])], 2, torch.device("cpu"))
+
+
 def test_max_seqlen_below_the_longest_sequence_is_refused():
     """max_seqlen sizes the kernels' grids: a bound below the longest local sequence would
     leave rows unwritten, so it is refused before any device work."""
