@@ -852,7 +852,7 @@ def main():
                      "algorithmic_per_launch": f"{flops / 1e12:.4f} TFLOP (the whole sweep: "
                                                "4*Tq*Tk*D*H_q per step, halved for the causal step)",
                      "avg_launch_ms": round(sw_ms, 4), "launches": clock.count("sweep_kernel")},
-        "transpose_v": {"kernel": "transpose_v_kernel<u16,128> (8 shards per launch)", "avg_launch_ms": round(tr_ms, 4),
+        "transpose_v": {"kernel": "transpose_reg_kernel<u16,128> (8 shards per launch)", "avg_launch_ms": round(tr_ms, 4),
                         "algorithmic_bytes_per_launch": round(tr_bytes),
                         "achieved_GBs": round(tr_bytes / (tr_ms * 1e-3) / 1e9, 1),
                         "frac": round(tr_bytes / (tr_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
@@ -949,7 +949,7 @@ def main():
             "sweep_kernel": {"kernel": "attn_fwd_16bit_sweep<bf16,128,4,paged K>", "avg_launch_ms": round(pk_ms, 4),
                              "TFLOP/s": round(flops / (pk_ms * 1e-3) / 1e12, 2),
                              "frac": round(flops / (pk_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
-            "transpose_v_paged": {"kernel": "transpose_v_kernel<u16,128>, paged (8 caches per launch)",
+            "transpose_v_paged": {"kernel": "transpose_reg_kernel<u16,128>, paged (8 caches per launch)",
                                   "avg_launch_ms": round(pt_ms, 4), "bytes": round(pbytes),
                                   "achieved_GBs": round(pbytes / (pt_ms * 1e-3) / 1e9, 1),
                                   "frac": round(pbytes / (pt_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}}
