@@ -708,11 +708,16 @@ __global__ __launch_bounds__(512) void bwd_dq_pp_kernel(BwdParams p) {
 // pair never wait on each other within an iteration.  One barrier per iteration: the loads
 // have landed, P of block i is in LDS, and what the iteration read is free.
 //
-// Staging.  Up to head dim 128 a whole block arrives by LDS-DMA into stage i % 3 one
-// iteration ahead (3 x 33 KB at 128).  At 256 three whole blocks do not fit the LDS, so a
-// block's row regions and transposed regions go to different half-stages, each kind
-// double-buffered by block parity: iteration i reads rows(i) and transposed(i - 1) and
-// loads rows(i + 1) and transposed(i) over those of blocks i - 1 and i - 2 (4 x 64.25 KB).
+// Staging.  Up to head dim 128 a whole block arrives by LDS-DMA into stage i % 4 two
+// iterations ahead (4 x 33 KB at 128).  Each wavefront loads its share of block i + 2 in its
+// VALU section (the first wavefront after writing P, the second after forming dS), while the
+// partner's MFMAs keep the matrix core busy; issued at the start of an iteration the loads
+// had held every wavefront for about 330 cycles (the CU's vector-memory path moves about
+// 64 bytes per cycle, so a 33 KB block takes some 530 cycles of it).  Every MFMA chain reads
+// its LDS fragments four MFMAs ahead, fenced MFMA by MFMA.  At 256 three whole blocks do not
+// fit the LDS, so a block's row regions and transposed regions go to different half-stages,
+// each kind double-buffered by block parity: iteration i reads rows(i) and transposed(i - 1)
+// and loads rows(i + 1) and transposed(i) over those of blocks i - 1 and i - 2 (4 x 64.25 KB).
 // (The halves measured 7 % slower at 128, where whole stages fit.)
 template <typename T, int D>
 __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
@@ -735,12 +740,12 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
   __shared__ __align__(16) char stage0[HALVES ? HB : BB];
   __shared__ __align__(16) char stage1[HALVES ? HB : BB];
   __shared__ __align__(16) char stage2[HALVES ? HB : BB];
-  __shared__ __align__(16) char stage3[HALVES ? HB : 16];
+  __shared__ __align__(16) char stage3[HALVES ? HB : BB];
   __shared__ __align__(16) char xch[2 * 4 * 2048];  // P of a block per pair, two blocks
-  // whole stages
+  // whole stages: block b in stage b % 4
   auto stage_of = [&](int bi) {
-    const int m = bi % 3;
-    return m == 0 ? stage0 : m == 1 ? stage1 : stage2;
+    const int m = bi & 3;
+    return m == 0 ? stage0 : m == 1 ? stage1 : m == 2 ? stage2 : stage3;
   };
   // half-stages
   auto rows_of = [&](int bi) { return (bi & 1) ? stage1 : stage0; };
@@ -796,16 +801,15 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
       int lh, lr;
     };
     Cursor rc{0, 0}, tc{0, 0};
-    // the block at cursor cu into stage st: whole (r0 < 0), or its half of regions r0 and
-    // r0 + 2; then the per-row values
+    // head dim 256: the half of the block at cursor cu made of regions r0 and r0 + 2 into
+    // half-stage st, then the per-row values
     auto load = [&](Cursor& cu, char* st, int r0) {
       const char* g = p.pk + ((int64_t)(kvh * p.group + cu.lh) * p.n_pb + blk0 + cu.lr) * BB;
       const __amdgpu_buffer_rsrc_t rs = make_rsrc32(uniform_ptr(g), BB);
 #pragma unroll
       for (int j = 0; j < CPW; ++j) {
-        const int f = w + 8 * j;  // of a half: region r0 + 2 (f / NKS), fragment f % NKS
-        const int src = r0 < 0 ? 1024 * f : (r0 + 2 * (f / NKS)) * R + 1024 * (f % NKS);
-        dma16(rs, st + 1024 * f, src + 16 * l);
+        const int f = w + 8 * j;  // region r0 + 2 (f / NKS), fragment f % NKS
+        dma16(rs, st + 1024 * f, (r0 + 2 * (f / NKS)) * R + 1024 * (f % NKS) + 16 * l);
       }
       dma4(rs, st + OVAL, 4 * R + 4 * l);  // every wavefront writes the same per-row values
       if (++cu.lr == n_rb) {
@@ -826,47 +830,30 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
       }
     };
     auto frag_at = [&](const char* st, int off) { return *reinterpret_cast<const frag*>(st + off + 16 * l); };
-    auto run = [&](auto role) {
+    // head dim 256: half-stages, loaded one iteration ahead
+    auto run_halves = [&](auto role) {
       constexpr bool PW = decltype(role)::value;
       frag pb0, pb1;  // first wavefront: P of the previous block (operands of dV)
       f32x16 dpt;     // second wavefront: dP of the previous block
       int cr = 0;     // row block (within the head) of block i
-      if constexpr (HALVES) load(rc, rows_of(0), 0);
-      else load(rc, stage_of(0), -1);
+      load(rc, rows_of(0), 0);
       __builtin_amdgcn_s_waitcnt(kWaitAll);
       wg_barrier();
       for (int i = 0; i <= n_blk; ++i) {
-        const char* cur;   // block i: its row regions
-        const char* prev;  // block i - 1: its transposed regions and the values
-        if constexpr (HALVES) {
-          if (i + 1 < n_blk) load(rc, rows_of(i + 1), 0);
-          if (i < n_blk) load(tc, trans_of(i), 1);
-          cur = rows_of(i);
-          prev = trans_of(i + 1);
-        } else {
-          if (i + 1 < n_blk) load(rc, stage_of(i + 1), -1);
-          cur = stage_of(i);
-          prev = stage_of(i + 2);
-        }
+        if (i + 1 < n_blk) load(rc, rows_of(i + 1), 0);
+        if (i < n_blk) load(tc, trans_of(i), 1);
+        const char* cur = rows_of(i);       // block i: its row regions
+        const char* prev = trans_of(i + 1);  // block i - 1: its transposed regions and the values
         if constexpr (PW) {
           __builtin_amdgcn_s_setprio(1);
           if (i > 0) {
-            // head dim 256: the two 16-row halves in turn over the d tiles, so that consecutive
-            // MFMAs update different accumulators (each still sums its terms in the same
-            // order): 1.5-2 % off this kernel there, where the same order made the head-dim-128
-            // backward 1.2 % slower
-            if constexpr (HALVES) {
+            // the two 16-row halves in turn over the d tiles, so that consecutive MFMAs update
+            // different accumulators (each still sums its terms in the same order): 1.5-2 % off
+            // this kernel, where the same order made the head-dim-128 backward 1.2 % slower
 #pragma unroll
-              for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(frag_at(prev, ODOT + 1024 * (2 * dt)), pb0, acc[dt]);
+            for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(frag_at(prev, ODOT + 1024 * (2 * dt)), pb0, acc[dt]);
 #pragma unroll
-              for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(frag_at(prev, ODOT + 1024 * (2 * dt + 1)), pb1, acc[dt]);
-            } else {
-#pragma unroll
-              for (int dt = 0; dt < NDT; ++dt) {
-                acc[dt] = M::mma(frag_at(prev, ODOT + 1024 * (2 * dt)), pb0, acc[dt]);
-                acc[dt] = M::mma(frag_at(prev, ODOT + 1024 * (2 * dt + 1)), pb1, acc[dt]);
-              }
-            }
+            for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(frag_at(prev, ODOT + 1024 * (2 * dt + 1)), pb1, acc[dt]);
           }
           if (i < n_blk) {
             f32x16 st = {};
@@ -908,18 +895,11 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
             }
             const frag s0 = to_frag<T>(dsv), s1 = to_frag<T>(dsv + 8);
             __builtin_amdgcn_s_setprio(1);
-            if constexpr (HALVES) {  // as for dV above
+            // as for dV above
 #pragma unroll
-              for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt)), s0, acc[dt]);
+            for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt)), s0, acc[dt]);
 #pragma unroll
-              for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt + 1)), s1, acc[dt]);
-            } else {
-#pragma unroll
-              for (int dt = 0; dt < NDT; ++dt) {
-                acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt)), s0, acc[dt]);
-                acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt + 1)), s1, acc[dt]);
-              }
-            }
+            for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt + 1)), s1, acc[dt]);
           }
           if (i < n_blk) {
             dpt = f32x16{};
@@ -935,9 +915,141 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
         if (++cr == n_rb) cr = 0;
       }
     };
+    // n MFMAs in program order, the LDS fragment of MFMA k read four MFMAs ahead into a
+    // register of its own (fenced MFMA by MFMA: left alone, the compiler reads each fragment
+    // just before its MFMA and waits for it)
+    auto chain = [&](auto n_c, auto rd, auto mm) __attribute__((always_inline)) {
+      constexpr int N = decltype(n_c)::value, RA = 4;
+      frag fr[N];
+#pragma unroll
+      for (int k = 0; k < RA && k < N; ++k) fr[k] = rd(k);
+#pragma unroll
+      for (int k = 0; k < N; ++k) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (k + RA < N) fr[k + RA] = rd(k + RA);
+        mm(k, fr[k]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    // up to head dim 128: whole stages, loaded two iterations ahead
+    auto run_whole = [&](auto role) {
+      constexpr bool PW = decltype(role)::value;
+      constexpr int NL = CPW + 1;  // load instructions per wavefront per block
+      constexpr int kWaitNext = NL | (7 << 4);  // the newest block's loads may stay in flight
+      frag pb0, pb1;  // first wavefront: P of the previous block (operands of dV)
+      f32x16 dpt;     // second wavefront: dP of the previous block
+      int cr = 0;     // row block (within the head) of block i
+      // the next block to load (wave-uniform, advanced block by block: the blocks of one query
+      // head are consecutive, the next head's start n_pb blocks after the previous one's)
+      const char* gnext = reinterpret_cast<const char*>(
+          uniform_ptr(p.pk + ((int64_t)(kvh * p.group) * p.n_pb + blk0) * BB));
+      const int64_t head_jump = (int64_t)(p.n_pb - n_rb) * BB;
+      int lr = 0;
+      auto next_rs = [&]() __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc32(gnext, BB);
+        gnext += BB;
+        if (++lr == n_rb) {
+          lr = 0;
+          gnext += head_jump;
+        }
+        return rs;
+      };
+      // this wavefront's share of the next block into stage st: fragments w + 8 j, then the
+      // per-row values (every wavefront writes the same ones)
+      auto load_share = [&](char* st) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t rs = next_rs();
+#pragma unroll
+        for (int j = 0; j < CPW; ++j) {
+          const int f = w + 8 * j;
+          dma16(rs, st + 1024 * f, 1024 * f + 16 * l);
+        }
+        dma4(rs, st + OVAL, 4 * R + 4 * l);
+      };
+      load_share(stage_of(0));
+      if (n_blk > 1) load_share(stage_of(1));
+      __builtin_amdgcn_s_waitcnt(kWaitAll);
+      wg_barrier();
+      for (int i = 0; i <= n_blk; ++i) {
+        // block i + 2 goes into the stage of block i - 2, last read before the previous barrier
+        const bool ld = i + 2 < n_blk;
+        const char* cur = stage_of(i);       // block i: its row regions
+        const char* prev = stage_of(i + 3);  // block i - 1: its transposed regions and the values
+        if constexpr (PW) {
+          __builtin_amdgcn_s_setprio(1);
+          if (i > 0) {
+            chain(std::integral_constant<int, 2 * NDT>{}, [&](int k) { return frag_at(prev, ODOT + 1024 * k); },
+                  [&](int k, frag f) { acc[k >> 1] = M::mma(f, (k & 1) ? pb1 : pb0, acc[k >> 1]); });
+          }
+          if (i < n_blk) {
+            f32x16 st = {};
+            chain(std::integral_constant<int, NKS>{}, [&](int k) { return frag_at(cur, OQ + 1024 * k); },
+                  [&](int k, frag f) { st = M::mma(f, kv[k], st); });
+            __builtin_amdgcn_s_setprio(0);
+            float lse[16], pv[16];
+            row_vals(cur, 0, lse);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse[r]));
+            const int row0 = row_begin + cr * kBwdRows;
+            const bool full = row0 >= sp.row_min && kg0 + kBwdRows <= sp.key_lim &&
+                              (!sp.causal || row0 >= kg0 + kBwdRows - 1);
+            if (!full) {
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const int row = row0 + acc_pos(r, h);
+                const bool ok = row >= sp.row_min && key < sp.key_lim && (!sp.causal || key <= row);
+                pv[r] = ok ? pv[r] : 0.f;
+              }
+            }
+            pb0 = to_frag<T>(pv);
+            pb1 = to_frag<T>(pv + 8);
+            char* xb = xch + ((i & 1) * 4 + (w & 3)) * 2048;
+            *reinterpret_cast<f16x8*>(xb + 16 * l) = to_frag<_Float16>(pv);
+            *reinterpret_cast<f16x8*>(xb + 1024 + 16 * l) = to_frag<_Float16>(pv + 8);
+          }
+          if (ld) load_share(stage_of(i + 2));
+        } else {
+          if (i > 0) {
+            const char* xb = xch + (((i - 1) & 1) * 4 + (w & 3)) * 2048;
+            const f16x8 e0 = *reinterpret_cast<const f16x8*>(xb + 16 * l);
+            const f16x8 e1 = *reinterpret_cast<const f16x8*>(xb + 1024 + 16 * l);
+            float dl[16], dsv[16];
+            row_vals(prev, 128, dl);
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+              dsv[r] = (float)e0[r] * (dpt[r] - dl[r]);
+              dsv[8 + r] = (float)e1[r] * (dpt[8 + r] - dl[8 + r]);
+            }
+            const frag s0 = to_frag<T>(dsv), s1 = to_frag<T>(dsv + 8);
+            if (ld) load_share(stage_of(i + 2));
+            __builtin_amdgcn_s_setprio(1);
+            chain(std::integral_constant<int, 2 * NDT>{}, [&](int k) { return frag_at(prev, OQT + 1024 * k); },
+                  [&](int k, frag f) { acc[k >> 1] = M::mma(f, (k & 1) ? s1 : s0, acc[k >> 1]); });
+          } else if (ld) {
+            load_share(stage_of(i + 2));
+          }
+          if (i < n_blk) {
+            dpt = f32x16{};
+            chain(std::integral_constant<int, NKS>{}, [&](int k) { return frag_at(cur, ODO + 1024 * k); },
+                  [&](int k, frag f) { dpt = M::mma(f, kv[k], dpt); });
+          }
+        }
+        __builtin_amdgcn_s_setprio(0);
+        if (i < n_blk) {  // block i + 1 landed (each wavefront's own loads), P of block i written
+          if (ld) __builtin_amdgcn_s_waitcnt(kWaitNext);
+          else __builtin_amdgcn_s_waitcnt(kWaitAll);
+          wg_barrier();
+        }
+        if (++cr == n_rb) cr = 0;
+      }
+    };
     if (n_blk > 0) {
-      if (pwave) run(std::true_type{});
-      else run(std::false_type{});
+      if constexpr (HALVES) {
+        if (pwave) run_halves(std::true_type{});
+        else run_halves(std::false_type{});
+      } else {
+        if (pwave) run_whole(std::true_type{});
+        else run_whole(std::false_type{});
+      }
     }
   }
   // accumulator register r of lane l: head-dim element 32 dt + 8 (r / 4) + 4h + r % 4 of key
