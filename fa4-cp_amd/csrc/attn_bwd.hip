@@ -468,10 +468,13 @@ __global__ __launch_bounds__(128 * HP) void bwd_dq_pair_kernel(BwdParams p) {
 // phase behind group 0, so on every SIMD one wavefront is in its MFMA phase (dQ += dS K of
 // block i - 1, S^T = K Q^T and dP^T = V dO^T of block i: 24 MFMAs at head dim 128, fragment
 // reads four ahead) while the other is in its VALU phase (dS^T = P^T (dP^T - delta) of its
-// block).  A workgroup barrier ends every phase.  Block b sits in stage b % 3: group 1 loads it
-// by LDS-DMA in its VALU phase two phases before group 0's MFMA phase reads it, and waits for
-// it at the end of its next MFMA phase; the stage it overwrites was last read (K^T) in the
-// phase before the load.
+// block).  A workgroup barrier ends every phase.  Block b sits in stage b % 4.  Every wavefront
+// loads its share of it by LDS-DMA in its VALU phase of iteration b - 2 (group 0 three phases,
+// group 1 two phases before group 0's MFMA phase reads it) and waits for it at the end of its
+// next MFMA phase; the stage was last read (K^T of block b - 4) by group 1 in the phase before
+// group 0's load.  With the loads split over both groups neither VALU phase outlasts the other
+// group's MFMA phase (group 1 alone had spent about 800 cycles issuing a whole block).
+// dP^T accumulates onto -delta, so dS^T = P^T dP^T.
 template <typename T, int D, int HP>
 __global__ __launch_bounds__(512) void bwd_dq_pp_kernel(BwdParams p) {
   using M = BwdMfma<T>;
@@ -490,9 +493,10 @@ __global__ __launch_bounds__(512) void bwd_dq_pp_kernel(BwdParams p) {
   __shared__ __align__(16) char stage0[KB];
   __shared__ __align__(16) char stage1[KB];
   __shared__ __align__(16) char stage2[KB];
+  __shared__ __align__(16) char stage3[KB];
   auto stage_of = [&](int bi) {
-    const int m = bi % 3;
-    return m == 0 ? stage0 : m == 1 ? stage1 : stage2;
+    const int m = bi & 3;
+    return m == 0 ? stage0 : m == 1 ? stage1 : m == 2 ? stage2 : stage3;
   };
 
   // longest first: the back-half row tiles attend the later sources and come out first
@@ -556,13 +560,16 @@ __global__ __launch_bounds__(512) void bwd_dq_pp_kernel(BwdParams p) {
   };
   Cursor lc{0, 0, key_end_of(0)};  // the next block to load
   settle(lc);
-  // the block at cursor lc into stage bi % 3, its fragments split over `nw` wavefronts (this
-  // one is number `wi` of them)
-  auto load = [&](int bi, int wi, int nw) {
+  // this wavefront's share of the block at cursor lc into stage bi % 4: fragments w + 8 j
+  auto load = [&](int bi) {
     const char* g = p.pkv + (((int64_t)src_of(lc.s) * p.h_kv + kvh) * p.n_pb + pstart + lc.k0 / kBwdRows) * KB;
     const __amdgpu_buffer_rsrc_t rs = make_rsrc32(uniform_ptr(g), KB);
     char* st = stage_of(bi);
-    for (int f = wi; f < NF; f += nw) dma16(rs, st + 1024 * f, 1024 * f + 16 * l);
+#pragma unroll
+    for (int j = 0; j < (NF + 7) / 8; ++j) {
+      const int f = w + 8 * j;
+      if (f < NF) dma16(rs, st + 1024 * f, 1024 * f + 16 * l);
+    }
     lc.k0 += kBwdRows;
     settle(lc);
   };
@@ -578,7 +585,7 @@ __global__ __launch_bounds__(512) void bwd_dq_pp_kernel(BwdParams p) {
   // nothing.  Every iteration can therefore run the same products.
   auto sdp_plain = [&](const char* cur) __attribute__((always_inline)) {
     st = f32x16{};
-    dpt = f32x16{};
+    dpt = f32x16{-dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl};  // dP^T - delta
 #pragma unroll
     for (int t = 0; t < NKS; ++t) {
       st = M::mma(frag_at(cur, 1024 * t), qf[t], st);
@@ -604,7 +611,7 @@ __global__ __launch_bounds__(512) void bwd_dq_pp_kernel(BwdParams p) {
       else if (k < N) fr[k] = frag_at(cur, ((k - NQ) & 1) * R + 1024 * ((k - NQ) >> 1));
     };
     st = f32x16{};
-    dpt = f32x16{};
+    dpt = f32x16{-dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl, -dl};
 #pragma unroll
     for (int k = 0; k < RA; ++k) read(k);
 #pragma unroll
@@ -621,7 +628,7 @@ __global__ __launch_bounds__(512) void bwd_dq_pp_kernel(BwdParams p) {
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  // dS^T = P^T (dP^T - delta) of the block at cursor cc
+  // dS^T = P^T (dP^T - delta) of the block at cursor cc (dpt holds dP^T - delta)
   auto make_ds = [&]() __attribute__((always_inline)) {
     const StepPairs sp = step_pairs(p.rank, p.S, src_of(cc.s), L);
     const bool full = wr0 + kBwdRows <= L && wr0 >= sp.row_min && cc.k0 + kBwdRows <= sp.key_lim &&
@@ -629,14 +636,14 @@ __global__ __launch_bounds__(512) void bwd_dq_pp_kernel(BwdParams p) {
     float dsv[16];
     if (__builtin_expect(full, 1)) {  // no pair of the block masked: no per-element test
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dsv[r] = __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2)) * (dpt[r] - dl);
+      for (int r = 0; r < 16; ++r) dsv[r] = __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2)) * dpt[r];
     } else {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int kp = cc.k0 + acc_pos(r, h);
         const bool ok = row_ok & (qpos >= sp.row_min) & (kp < sp.key_lim) & (!sp.causal | (kp <= qpos));
         const float pr = __builtin_amdgcn_exp2f(fmaf(st[r], c, -lse2));
-        dsv[r] = (ok ? pr : 0.f) * (dpt[r] - dl);
+        dsv[r] = (ok ? pr : 0.f) * dpt[r];
       }
     }
     ds0 = to_frag<T>(dsv);
@@ -644,24 +651,26 @@ __global__ __launch_bounds__(512) void bwd_dq_pp_kernel(BwdParams p) {
     cc.k0 += kBwdRows;
     settle(cc);
   };
-  // the end of an MFMA phase: group 1 waits for the block it loaded in its last VALU phase
+  // the end of an MFMA phase: each wavefront waits for its share of the block it loaded in its
+  // last VALU phase
   auto end_mfma_phase = [&]() __attribute__((always_inline)) {
     __builtin_amdgcn_s_setprio(0);
-    if (grp == 1) __builtin_amdgcn_s_waitcnt(kWaitAll);
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
     wg_barrier();
   };
-  // the VALU phase of iteration i: group 1 loads block i + 2, every wavefront forms dS of block i
+  // the VALU phase of iteration i: each wavefront loads its share of block i + 2 and forms dS of
+  // block i
   auto valu_phase = [&](int i) __attribute__((always_inline)) {
-    if (grp == 1 && i + 2 < n_blk) load(i + 2, wj, 4);
+    if (i + 2 < n_blk) load(i + 2);
     make_ds();
     pin(ds0);
     pin(ds1);
     wg_barrier();
   };
 
-  if (n_blk > 0) {  // blocks 0 and 1, loaded by every wavefront
-    load(0, w, 8);
-    if (n_blk > 1) load(1, w, 8);
+  if (n_blk > 0) {  // blocks 0 and 1
+    load(0);
+    if (n_blk > 1) load(1);
   }
   __builtin_amdgcn_s_waitcnt(kWaitAll);
   wg_barrier();
@@ -672,12 +681,12 @@ __global__ __launch_bounds__(512) void bwd_dq_pp_kernel(BwdParams p) {
   valu_phase(0);
   for (int i = 1; i < n_blk; ++i) {
     __builtin_amdgcn_s_setprio(1);
-    dq_sdp(stage_of(i), stage_of(i + 2));
+    dq_sdp(stage_of(i), stage_of(i + 3));
     end_mfma_phase();
     valu_phase(i);
   }
   __builtin_amdgcn_s_setprio(1);
-  dq_plain(stage_of(n_blk + 2));
+  dq_plain(stage_of(n_blk + 3));
   end_mfma_phase();
   wg_barrier();
   if (grp == 0) wg_barrier();  // both groups pass the same number of barriers
