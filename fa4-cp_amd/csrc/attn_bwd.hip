@@ -27,8 +27,8 @@
 //   is in its VALU phase on every SIMD), walking the same key blocks as the forward sweep;
 //   at head dim 256, bwd_dq_pair_kernel, whose wavefronts pair as dK / dV's do;
 // * bwd_dkdv_kernel: one workgroup per 128 keys of one source and kv head, eight wavefronts
-//   in pairs, walking the packed blocks of the query rows that attend them, for every query
-//   head of the group.
+//   in pairs (up to head dim 128 a ninth that only loads), walking the packed blocks of the
+//   query rows that attend them, for every query head of the group.
 //
 // Products run on v_mfma_f32_32x32x16_{bf16,f16}.  Operand layouts (lane l, h = l / 32):
 // A lane l holds row l % 32, k = 8h + 0..7; B lane l holds column l % 32, the same k; the
@@ -718,18 +718,20 @@ __global__ __launch_bounds__(512) void bwd_dq_pp_kernel(BwdParams p) {
 // have landed, P of block i is in LDS, and what the iteration read is free.
 //
 // Staging.  Up to head dim 128 a whole block arrives by LDS-DMA into stage i % 4 two
-// iterations ahead (4 x 33 KB at 128).  Each wavefront loads its share of block i + 2 in its
-// VALU section (the first wavefront after writing P, the second after forming dS), while the
-// partner's MFMAs keep the matrix core busy; issued at the start of an iteration the loads
-// had held every wavefront for about 330 cycles (the CU's vector-memory path moves about
-// 64 bytes per cycle, so a 33 KB block takes some 530 cycles of it).  Every MFMA chain reads
-// its LDS fragments four MFMAs ahead, fenced MFMA by MFMA.  At 256 three whole blocks do not
+// iterations ahead (4 x 33 KB at 128), loaded by a ninth wavefront that does nothing else:
+// it waits for block i + 1, issues block i + 2 and joins the iteration's barrier.  The CU's
+// vector-memory path moves about 64 bytes per cycle, so a 33 KB block takes some 530 cycles
+// of it, and a wavefront that issues loads waits for them to be accepted; issued by the
+// compute wavefronts (at the start of an iteration, or in their VALU sections) the loads had
+// held each for 180-330 cycles.  The ninth wavefront shares a SIMD with one pair (three
+// wavefronts of at most 168 registers).  Every MFMA chain reads its LDS fragments four MFMAs
+// ahead, fenced MFMA by MFMA.  At 256 three whole blocks do not
 // fit the LDS, so a block's row regions and transposed regions go to different half-stages,
 // each kind double-buffered by block parity: iteration i reads rows(i) and transposed(i - 1)
 // and loads rows(i + 1) and transposed(i) over those of blocks i - 1 and i - 2 (4 x 64.25 KB).
 // (The halves measured 7 % slower at 128, where whole stages fit.)
 template <typename T, int D>
-__global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
+__global__ __launch_bounds__(D > 128 ? 512 : 576) void bwd_dkdv_kernel(BwdParams p) {
   using M = BwdMfma<T>;
   typedef typename M::frag frag;
   constexpr int NKS = D / 16;
@@ -778,6 +780,7 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int l = threadIdx.x & 63, h = l >> 5, lk = l & 31;
   const bool pwave = w < 4;
+  const bool producer = !HALVES && w == 8;   // up to head dim 128: the ninth wavefront loads the blocks
   const int kg0 = kb0 + kBwdRows * (w & 3);  // first key of the pair's group
   const int key = kg0 + lk;                  // this lane's key in the sequence
   const StepPairs sp = step_pairs(p.rank, p.S, src, L);
@@ -789,7 +792,7 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
   if (kb0 < sp.key_lim) {
     // K (first wavefront) or V (second) of the lane's key: B operands of S and dP
     frag kv[NKS];
-    {
+    if (!producer) {
       const bool ok = key < sp.key_lim;
       const T* r = pwave ? reinterpret_cast<const T*>(p.k[src]) + (int64_t)(qs + key) * p.k_rs + (int64_t)kvh * p.k_hs
                          : reinterpret_cast<const T*>(p.v[src]) + (int64_t)(qs + key) * p.v_rs + (int64_t)kvh * p.v_hs;
@@ -940,47 +943,44 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
       }
       __builtin_amdgcn_sched_barrier(0);
     };
-    // up to head dim 128: whole stages, loaded two iterations ahead
-    auto run_whole = [&](auto role) {
-      constexpr bool PW = decltype(role)::value;
-      constexpr int NL = CPW + 1;  // load instructions per wavefront per block
-      constexpr int kWaitNext = NL | (7 << 4);  // the newest block's loads may stay in flight
-      frag pb0, pb1;  // first wavefront: P of the previous block (operands of dV)
-      f32x16 dpt;     // second wavefront: dP of the previous block
-      int cr = 0;     // row block (within the head) of block i
+    // up to head dim 128: whole stages, loaded two iterations ahead by the ninth wavefront
+    auto run_producer = [&]() __attribute__((always_inline)) {
       // the next block to load (wave-uniform, advanced block by block: the blocks of one query
       // head are consecutive, the next head's start n_pb blocks after the previous one's)
       const char* gnext = reinterpret_cast<const char*>(
           uniform_ptr(p.pk + ((int64_t)(kvh * p.group) * p.n_pb + blk0) * BB));
       const int64_t head_jump = (int64_t)(p.n_pb - n_rb) * BB;
       int lr = 0;
-      auto next_rs = [&]() __attribute__((always_inline)) {
+      auto load_block = [&](char* st) __attribute__((always_inline)) {
         const __amdgpu_buffer_rsrc_t rs = make_rsrc32(gnext, BB);
         gnext += BB;
         if (++lr == n_rb) {
           lr = 0;
           gnext += head_jump;
         }
-        return rs;
-      };
-      // this wavefront's share of the next block into stage st: fragments w + 8 j, then the
-      // per-row values (every wavefront writes the same ones)
-      auto load_share = [&](char* st) __attribute__((always_inline)) {
-        const __amdgpu_buffer_rsrc_t rs = next_rs();
 #pragma unroll
-        for (int j = 0; j < CPW; ++j) {
-          const int f = w + 8 * j;
-          dma16(rs, st + 1024 * f, 1024 * f + 16 * l);
-        }
+        for (int f = 0; f < 4 * NKS; ++f) dma16(rs, st + 1024 * f, 1024 * f + 16 * l);
         dma4(rs, st + OVAL, 4 * R + 4 * l);
       };
-      load_share(stage_of(0));
-      if (n_blk > 1) load_share(stage_of(1));
+      load_block(stage_of(0));
+      if (n_blk > 1) load_block(stage_of(1));
       __builtin_amdgcn_s_waitcnt(kWaitAll);
       wg_barrier();
-      for (int i = 0; i <= n_blk; ++i) {
+      for (int i = 0; i < n_blk; ++i) {
+        // block i + 1 (loaded an iteration ago) has landed before this iteration's barrier;
         // block i + 2 goes into the stage of block i - 2, last read before the previous barrier
-        const bool ld = i + 2 < n_blk;
+        __builtin_amdgcn_s_waitcnt(kWaitAll);
+        if (i + 2 < n_blk) load_block(stage_of(i + 2));
+        wg_barrier();
+      }
+    };
+    auto run_whole = [&](auto role) {
+      constexpr bool PW = decltype(role)::value;
+      frag pb0, pb1;  // first wavefront: P of the previous block (operands of dV)
+      f32x16 dpt;     // second wavefront: dP of the previous block
+      int cr = 0;     // row block (within the head) of block i
+      wg_barrier();
+      for (int i = 0; i <= n_blk; ++i) {
         const char* cur = stage_of(i);       // block i: its row regions
         const char* prev = stage_of(i + 3);  // block i - 1: its transposed regions and the values
         if constexpr (PW) {
@@ -1015,7 +1015,6 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
             *reinterpret_cast<f16x8*>(xb + 16 * l) = to_frag<_Float16>(pv);
             *reinterpret_cast<f16x8*>(xb + 1024 + 16 * l) = to_frag<_Float16>(pv + 8);
           }
-          if (ld) load_share(stage_of(i + 2));
         } else {
           if (i > 0) {
             const char* xb = xch + (((i - 1) & 1) * 4 + (w & 3)) * 2048;
@@ -1029,12 +1028,9 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
               dsv[8 + r] = (float)e1[r] * (dpt[8 + r] - dl[8 + r]);
             }
             const frag s0 = to_frag<T>(dsv), s1 = to_frag<T>(dsv + 8);
-            if (ld) load_share(stage_of(i + 2));
             __builtin_amdgcn_s_setprio(1);
             chain(std::integral_constant<int, 2 * NDT>{}, [&](int k) { return frag_at(prev, OQT + 1024 * k); },
                   [&](int k, frag f) { acc[k >> 1] = M::mma(f, (k & 1) ? s1 : s0, acc[k >> 1]); });
-          } else if (ld) {
-            load_share(stage_of(i + 2));
           }
           if (i < n_blk) {
             dpt = f32x16{};
@@ -1043,9 +1039,8 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
           }
         }
         __builtin_amdgcn_s_setprio(0);
-        if (i < n_blk) {  // block i + 1 landed (each wavefront's own loads), P of block i written
-          if (ld) __builtin_amdgcn_s_waitcnt(kWaitNext);
-          else __builtin_amdgcn_s_waitcnt(kWaitAll);
+        if (i < n_blk) {  // P of block i written (the producer has waited for block i + 1)
+          __builtin_amdgcn_s_waitcnt(kWaitAll);
           wg_barrier();
         }
         if (++cr == n_rb) cr = 0;
@@ -1056,14 +1051,15 @@ __global__ __launch_bounds__(512) void bwd_dkdv_kernel(BwdParams p) {
         if (pwave) run_halves(std::true_type{});
         else run_halves(std::false_type{});
       } else {
-        if (pwave) run_whole(std::true_type{});
+        if (producer) run_producer();
+        else if (pwave) run_whole(std::true_type{});
         else run_whole(std::false_type{});
       }
     }
   }
   // accumulator register r of lane l: head-dim element 32 dt + 8 (r / 4) + 4h + r % 4 of key
   // `key`; keys no query of this rank attends (past key_lim) get zeros
-  if (key >= L) return;
+  if (producer || key >= L) return;
   float* o = pwave ? p.dv[src] + ((int64_t)(qs + key) * p.h_kv + kvh) * D
                    : p.dk[src] + ((int64_t)(qs + key) * p.h_kv + kvh) * D;
   const float sc = pwave ? 1.f : p.scale;
@@ -1118,7 +1114,7 @@ int launch_bwd(const BwdParams& base, const fa4cp_sweep_bwd_args& a, hipStream_t
   p.n_tiles = (p.max_seqlen + kDkdvKeys - 1) / kDkdvKeys;
   const int64_t kv_blocks = (int64_t)p.S * p.h_kv * p.nseq * p.n_tiles;
   if (kv_blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "ring_sweep_bwd: too many key tiles");
-  hipLaunchKernelGGL((bwd_dkdv_kernel<T, D>), dim3((unsigned)kv_blocks), dim3(512), 0, st, p);
+  hipLaunchKernelGGL((bwd_dkdv_kernel<T, D>), dim3((unsigned)kv_blocks), dim3(D > 128 ? 512 : 576), 0, st, p);
   return check_launch("ring_sweep_bwd");
 }
 
