@@ -383,7 +383,12 @@ __global__ __launch_bounds__(128 * HP) void bwd_dq_pair_kernel(BwdParams p) {
     __builtin_amdgcn_s_waitcnt(kWaitAll);
     wg_barrier();
     for (int i = 0; i <= n_blk; ++i) {
-      if (i + 1 < n_blk) load(i + 1);
+      // block i + 1: the first wavefront loads its share after writing P^T (its MFMAs done),
+      // the second at the start of the iteration (2.5 % faster than both at the start; the
+      // second's loads any later spill its registers or leave them no time to land)
+      auto loads = [&]() __attribute__((always_inline)) {
+        if (i + 1 < n_blk) load(i + 1);
+      };
       const char* cur = stage_of(i);
       const char* prev = stage_of(i + 2);
       if constexpr (SW) {
@@ -412,7 +417,9 @@ __global__ __launch_bounds__(128 * HP) void bwd_dq_pair_kernel(BwdParams p) {
           cc.k0 += kBwdRows;
           settle(cc);
         }
+        loads();
       } else {
+        loads();
         if (i > 0) {
           const char* xb = xch + (((i - 1) & 1) * HP + w % HP) * 2048;
           const f16x8 e0 = *reinterpret_cast<const f16x8*>(xb + 16 * l);
@@ -852,8 +859,12 @@ __global__ __launch_bounds__(D > 128 ? 512 : 576) void bwd_dkdv_kernel(BwdParams
       __builtin_amdgcn_s_waitcnt(kWaitAll);
       wg_barrier();
       for (int i = 0; i <= n_blk; ++i) {
-        if (i + 1 < n_blk) load(rc, rows_of(i + 1), 0);
-        if (i < n_blk) load(tc, trans_of(i), 1);
+        // this iteration's loads, issued in the VALU section of each wavefront (the first after
+        // writing P, the second after forming dS): 1.3 % faster than at the iteration start
+        auto loads = [&]() __attribute__((always_inline)) {
+          if (i + 1 < n_blk) load(rc, rows_of(i + 1), 0);
+          if (i < n_blk) load(tc, trans_of(i), 1);
+        };
         const char* cur = rows_of(i);       // block i: its row regions
         const char* prev = trans_of(i + 1);  // block i - 1: its transposed regions and the values
         if constexpr (PW) {
@@ -893,6 +904,7 @@ __global__ __launch_bounds__(D > 128 ? 512 : 576) void bwd_dkdv_kernel(BwdParams
             *reinterpret_cast<f16x8*>(xb + 16 * l) = to_frag<_Float16>(pv);
             *reinterpret_cast<f16x8*>(xb + 1024 + 16 * l) = to_frag<_Float16>(pv + 8);
           }
+          loads();
         } else {
           if (i > 0) {
             const char* xb = xch + (((i - 1) & 1) * 4 + (w & 3)) * 2048;
@@ -906,12 +918,15 @@ __global__ __launch_bounds__(D > 128 ? 512 : 576) void bwd_dkdv_kernel(BwdParams
               dsv[8 + r] = (float)e1[r] * (dpt[8 + r] - dl[8 + r]);
             }
             const frag s0 = to_frag<T>(dsv), s1 = to_frag<T>(dsv + 8);
+            loads();
             __builtin_amdgcn_s_setprio(1);
             // as for dV above
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt)), s0, acc[dt]);
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) acc[dt] = M::mma(frag_at(prev, OQT + 1024 * (2 * dt + 1)), s1, acc[dt]);
+          } else {
+            loads();
           }
           if (i < n_blk) {
             dpt = f32x16{};
