@@ -48,6 +48,7 @@ CASES = [  # (lens, H, H_kv, D, cp, dtype)
     ([320, 640, 192], 4, 2, 128, 4, torch.bfloat16),  # packed: sequences of 80, 160 and 48 local rows
     ([400, 208], 8, 4, 64, 2, torch.float16),  # local lengths not multiples of 32
     ([1024], 16, 2, 128, 4, torch.bfloat16),  # 8 query heads per kv head
+    ([320, 144], 4, 4, 128, 2, torch.bfloat16),  # one query head per kv head: dk/dv workgroups of one block
     ([1024], 8, 2, 256, 4, torch.bfloat16),  # head dim 256
     ([512, 384], 4, 2, 256, 2, torch.float16),  # head dim 256, packed, two query heads per kv head
     ([512], 2, 2, 256, 2, torch.bfloat16),  # head dim 256, one query head per kv head
