@@ -103,21 +103,22 @@ __global__ __launch_bounds__(kBlock) void merge_inplace_kernel(
 
 constexpr int kStateChunk = 4;  // states whose loads are in flight together
 
-// S-way merge of one (row, head): 16 lanes, 8 elements of v per lane per pass.  States go
+// S-way merge of one (row, head): G lanes (16, or 32 from head dim 256), 8 elements of v per
+// lane per pass, passes 8 G columns apart.  States go
 // in chunks: the chunk's LSEs are loaded together, and unless all are -inf its v slices are
 // loaded together through a buffer resource over the row's states; a state with LSE -inf
 // (whose v may never have been written) and a state past num_states read past the end,
 // which returns zeros without touching memory.  Each chunk is folded into a running
 // (max, weight sum, accumulator) with an online rescale.  Weights use the hardware exp2
 // (relative error a few ulp; the sum and the final log are in fp32).
-template <typename T>
+template <typename T, int G = kGroup>
 __global__ __launch_bounds__(kBlock) void merge_states_kernel(
     const T* __restrict__ v, const float* __restrict__ s, T* __restrict__ vout,
     float* __restrict__ sout, int64_t n_groups, int num_states, int h, int d) {
   constexpr int NQ = sizeof(T) == 4 ? 2 : 1;  // 16-byte loads per 8 elements
   constexpr float kLog2e = 1.4426950408889634f;
-  const int64_t g = (int64_t)blockIdx.x * (kBlock / kGroup) + (threadIdx.x / kGroup);
-  const int lane = threadIdx.x % kGroup;
+  const int64_t g = (int64_t)blockIdx.x * (kBlock / G) + (threadIdx.x / G);
+  const int lane = threadIdx.x % G;
   if (g >= n_groups) return;
   const int64_t row = g / h;
   const int head = (int)(g - row * h);
@@ -127,7 +128,7 @@ __global__ __launch_bounds__(kBlock) void merge_states_kernel(
   const int past_end = (int)row_bytes;  // < 2^31, checked by the host
   T* vo = vout + (row * h + head) * (int64_t)d;
   float m = -INFINITY, wsum = 0.f;
-  for (int c = lane * 8; c < d; c += kGroup * 8) {
+  for (int c = lane * 8; c < d; c += G * 8) {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     m = -INFINITY;
     wsum = 0.f;
@@ -360,6 +361,18 @@ extern "C" int fa4cp_merge_states(const void* v, const float* s, void* v_out, fl
   const int64_t blocks = (n_groups + (kBlock / kGroup) - 1) / (kBlock / kGroup);
   if (blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "merge_states: too many rows");
   hipStream_t st = (hipStream_t)stream;
+  // head dim 256 and more (16-bit): 32 lanes per (row, head), so a lane of a 256-wide row takes
+  // one 8-column chunk instead of two in turn (2.8 % faster at 8 states x 16 heads x 256)
+  const int64_t blocks32 = (n_groups + (kBlock / 32) - 1) / (kBlock / 32);
+  if (d >= 256 && dtype != FA4CP_FP32 && blocks32 <= 0x7fffffffLL) {
+    if (dtype == FA4CP_BF16)
+      hipLaunchKernelGGL((merge_states_kernel<__bf16, 32>), dim3((unsigned)blocks32), dim3(kBlock), 0, st,
+                         (const __bf16*)v, s, (__bf16*)v_out, s_out, n_groups, num_states, h, d);
+    else
+      hipLaunchKernelGGL((merge_states_kernel<_Float16, 32>), dim3((unsigned)blocks32), dim3(kBlock), 0, st,
+                         (const _Float16*)v, s, (_Float16*)v_out, s_out, n_groups, num_states, h, d);
+    return check_launch("merge_states");
+  }
   switch (dtype) {
     case FA4CP_BF16:
       hipLaunchKernelGGL(merge_states_kernel<__bf16>, dim3((unsigned)blocks), dim3(kBlock), 0, st,
