@@ -747,9 +747,11 @@ __global__ __launch_bounds__(D > 128 ? 512 : 576) void bwd_dkdv_kernel(BwdParams
   constexpr int BB = pack_block_bytes<D>();
   constexpr bool HALVES = D > 128;
   constexpr int HB = 2 * R + 256;   // a half-stage: two regions and the per-row values
-  constexpr int CPW = (HALVES ? 2 : 4) * NKS / 8;  // 1 KB fragments each wavefront loads per (half-)stage
+  // head dim 256: 1 KB fragments each wavefront loads per half-stage (below it the ninth
+  // wavefront loads every fragment of a stage)
+  constexpr int CPW = 2 * NKS / 8;
   constexpr int kWaitAll = 7 << 4;  // vmcnt(0), lgkmcnt(0)
-  static_assert(CPW * 8 == (HALVES ? 2 : 4) * NKS, "fragments must split evenly over the wavefronts");
+  static_assert(CPW * 8 == 2 * NKS, "fragments must split evenly over the wavefronts");
   // Stages in separate arrays: the LDS-DMA destination is chosen at run time, so the
   // compiler does not make the first LDS read of an iteration wait for every load in flight.
   // A whole stage holds regions 0-3 then the per-row values.  Row halves: region 0 (Q rows)
