@@ -152,7 +152,7 @@ __global__ __launch_bounds__(kBlock) void merge_states_kernel(
                             ? past_end
                             : (int)((((int64_t)(st0 + i) * h + head) * d + c) * (int64_t)sizeof(T));
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) raw[i][q] = bload128(rv, off + 16 * q);
+        for (int q = 0; q < NQ; ++q) raw[i][q] = bload128_nt(rv, off + 16 * q);
       }
       const float nm = fmaxf(m, cm);
       const float r = __builtin_amdgcn_exp2f((m - nm) * kLog2e);  // 0 while m is -inf
@@ -237,7 +237,7 @@ __global__ __launch_bounds__(kBlock) void merge_states_list_kernel(
         if (w[st] != 0.f) {
           const T* p = static_cast<const T*>(L.v[st]) + g * (int64_t)d + c;
 #pragma unroll
-          for (int q = 0; q < NQ; ++q) raw[i][q] = reinterpret_cast<const u32x4*>(p)[q];
+          for (int q = 0; q < NQ; ++q) raw[i][q] = load16_nt(p + (16 / sizeof(T)) * q);
         }
       }
 #pragma unroll
