@@ -52,7 +52,7 @@ SWEEP_TRAFFIC_BYTES_RANK3 = 2395694 * 1024
 C4_SWEEP_TRAFFIC_BYTES = (2 * 144522 + 102470) * 1024
 C5_SWEEP_TRAFFIC_BYTES = (2 * 2793692 + 266244) * 1024
 C4_MERGE_STATES_TRAFFIC_BYTES = (2 * 204965 + 100913) * 1024
-C5_MERGE_STATES_TRAFFIC_BYTES = (2 * 799004 + 264223) * 1024
+C5_MERGE_STATES_TRAFFIC_BYTES = (2 * 802850 + 264192) * 1024
 
 
 def sweep_flops(t_local: int, cp: int, hq: int, d: int) -> float:
@@ -162,6 +162,15 @@ def merge_bytes_inplace(rows: int, h: int, d: int, bv: int) -> float:
 
 def merge_bytes_batched(rows: int, s: int, h: int, d: int, bv: int) -> float:
     return rows * h * (s * (d * bv + 4) + d * bv + 4)
+
+
+def merge_counter_rate(traffic, ms: float) -> dict:
+    """merge_states GB/s and fraction of HBM peak on counter bytes (None off the profiled rank):
+    the algorithmic figure counts -inf states the kernel does not read."""
+    if traffic is None:
+        return {"merge_states_counter_GBs": None, "merge_states_counter_frac": None}
+    gbs = traffic / (ms * 1e-3) / 1e9
+    return {"merge_states_counter_GBs": round(gbs, 1), "merge_states_counter_frac": round(gbs / PEAK_HBM_GBS, 4)}
 
 
 def cpu_baseline(rank: int, rows: int) -> dict:
@@ -301,7 +310,8 @@ def c4_block(rank: int, steps: int, warmup: int, with_cpu: bool) -> dict:
                              "merge_states_ms": round(ms_ms, 4), "merge_states_bytes": round(bb),
                              "merge_states_GBs": round(bb / (ms_ms * 1e-3) / 1e9, 1),
                              "merge_states_frac": round(bb / (ms_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                             "merge_states_traffic": C4_MERGE_STATES_TRAFFIC_BYTES if rank == 3 else None},
+                             "merge_states_traffic": C4_MERGE_STATES_TRAFFIC_BYTES if rank == 3 else None,
+                             **merge_counter_rate(C4_MERGE_STATES_TRAFFIC_BYTES if rank == 3 else None, ms_ms)},
         "zigzag_varlen": {"kernel": "shard_kernel<u32x4> (packed sequences, full q)", "avg_launch_ms": round(zms, 4),
                           "bytes": round(zbytes), "achieved_GBs": round(zbytes / (zms * 1e-3) / 1e9, 1),
                           "frac": round(zbytes / (zms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
@@ -382,7 +392,8 @@ def c5_block(rank: int, steps: int, warmup: int, with_cpu: bool, cpu_rows: int =
                              "merge_states_ms": round(ms_ms, 4), "merge_states_bytes": round(bb),
                              "merge_states_GBs": round(bb / (ms_ms * 1e-3) / 1e9, 1),
                              "merge_states_frac": round(bb / (ms_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                             "merge_states_traffic": C5_MERGE_STATES_TRAFFIC_BYTES if rank == 3 else None},
+                             "merge_states_traffic": C5_MERGE_STATES_TRAFFIC_BYTES if rank == 3 else None,
+                             **merge_counter_rate(C5_MERGE_STATES_TRAFFIC_BYTES if rank == 3 else None, ms_ms)},
         "per_step_incremental": {"ms_per_step": round(seci * 1e3, 3), "TFLOP/s": round(flops / seci / 1e12, 2)},
     }
     if with_cpu:
