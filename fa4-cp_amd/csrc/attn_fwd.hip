@@ -294,6 +294,60 @@ __device__ __forceinline__ void decode_block(const Params& p, int& hg, int& seq,
   rt = p.n_rt - 1 - (r - seq * p.n_rt);
 }
 
+// decode_block for the sweep kernels over packed sequences: the grid counts n_rt row tiles for
+// every sequence (the longest one's), so most of a short sequence's workgroups have no rows.
+// Here the row tiles of a head group are numbered across the sequences without those gaps
+// (sequence j has ceil(L_j / rows) of them, still longest first within a sequence), and the
+// workgroups past the last real tile, all empty, come last in each XCD's dispatch order
+// instead of ahead of every sequence's tiles.  Returns false for those.  The sequences'
+// tile counts are summed 64 at a time across the wavefront's lanes.  The sweep kernels take
+// it as a template variant (PACK) used for more than one sequence only: with one sequence
+// there are no gaps, and the headline kernel built with the plain decode ran 0.2 % faster
+// (code placement), while C4 (8 sequences) gains 0.8 % from the packed order.
+template <typename Params>
+__device__ __forceinline__ bool decode_sweep_block(const Params& p, int rows, int& hg, int& seq, int& rt) {
+  const int per_hg = p.nseq * p.n_rt;
+  const int k = p.n_hg < 8 ? 8 / p.n_hg : 1;
+  int r;
+  if (k > 1 && p.n_hg * k == 8 && p.n_blocks % 8 == 0 && per_hg % k == 0) {
+    const int x = (int)blockIdx.x & 7;
+    hg = x / k;
+    r = x % k + k * (int)(blockIdx.x >> 3);
+  } else {
+    const int b = xcd_remap((int)blockIdx.x, p.n_blocks);
+    hg = b / per_hg;
+    r = b - hg * per_hg;
+  }
+  const int lane = (int)(threadIdx.x & 63);
+  int base = 0;  // real row tiles of the sequences before j0
+  for (int j0 = 0; j0 < p.nseq; j0 += 64) {
+    const int j = j0 + lane;
+    int nt = 0;
+    if (j < p.nseq) {
+      int s0, L;
+      seq_range(p.cu, j, p.total, FA4CP_SEL_ALL, s0, L);
+      nt = (L + rows - 1) / rows;
+    }
+    int incl = nt;  // inclusive prefix sum over the lanes
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += v;
+    }
+    const int tot = __builtin_amdgcn_readlane(incl, 63);
+    if (r < base + tot) {
+      const int jl = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)__ballot(incl > r - base)) - 1);
+      const int ntj = __builtin_amdgcn_readlane(nt, jl);
+      const int before = __builtin_amdgcn_readlane(incl, jl) - ntj;
+      seq = j0 + jl;
+      rt = ntj - 1 - (r - base - before);
+      return true;
+    }
+    base += tot;
+  }
+  return false;
+}
+
 // Number of leading key tiles of BN keys that need no mask for any row of the workgroup.
 template <int BN = kBN>
 __device__ __forceinline__ int mask_free_tiles(int n_tiles, int Lk, bool causal, int row_tile0,
@@ -1456,11 +1510,15 @@ struct RingSegments {
   __device__ __forceinline__ int num_pages() const { return p->num_pages; }
 };
 
-template <typename T, int D, int HP, bool PAGED>
+template <typename T, int D, int HP, bool PAGED, bool PACK>
 __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_sweep(SweepParams p) {
   constexpr int RB = kPPWaves / HP;
   int hg, seq, rt;
-  decode_block(p, hg, seq, rt);
+  if constexpr (PACK) {
+    if (!decode_sweep_block(p, RB * 32, hg, seq, rt)) return;
+  } else {
+    decode_block(p, hg, seq, rt);
+  }
   int qs, L;
   seq_range(p.cu, seq, p.total, FA4CP_SEL_ALL, qs, L);
   const int row_tile0 = rt * RB * 32;
@@ -2637,11 +2695,15 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_vt(AttnParams p) 
 // source with its own k / v descales.  Row tiles whose keys are all their own (rank 0, front
 // half) take the precision rules of a causal attention call; every other row tile sees at
 // least half a shard of other sources' keys and uses one e4m3 term for P.
-template <int D, int HP, bool PAGED>
+template <int D, int HP, bool PAGED, bool PACK>
 __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_sweep(SweepParams p) {
   constexpr int RB = kPPWaves / HP;
   int hg, seq, rt;
-  decode_block(p, hg, seq, rt);
+  if constexpr (PACK) {
+    if (!decode_sweep_block(p, RB * 32, hg, seq, rt)) return;
+  } else {
+    decode_block(p, hg, seq, rt);
+  }
   int qs, L;
   seq_range(p.cu, seq, p.total, FA4CP_SEL_ALL, qs, L);
   const int row_tile0 = rt * RB * 32;
@@ -2956,11 +3018,17 @@ static int ring_sweep_launch(const fa4cp_sweep_args* a, const fa4cp_sweep_kpages
   if (blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "ring_sweep_fwd: grid too large");
   p.n_blocks = (int)blocks;
   void (*fn)(SweepParams) = nullptr;
-#define FA4CP_PICK_HP(KERNEL, ...)                                           \
-  {                                                                          \
-    if (hp == 4) fn = paged ? KERNEL<__VA_ARGS__, 4, true> : KERNEL<__VA_ARGS__, 4, false>; \
-    else if (hp == 2) fn = paged ? KERNEL<__VA_ARGS__, 2, true> : KERNEL<__VA_ARGS__, 2, false>; \
-    else fn = paged ? KERNEL<__VA_ARGS__, 1, true> : KERNEL<__VA_ARGS__, 1, false>; \
+  const bool pack = nseq > 1;  // several sequences: the gap-free row tile order
+#define FA4CP_PICK_PK(KERNEL, H, ...)                                                       \
+  {                                                                                         \
+    if (paged) fn = pack ? KERNEL<__VA_ARGS__, H, true, true> : KERNEL<__VA_ARGS__, H, true, false>; \
+    else fn = pack ? KERNEL<__VA_ARGS__, H, false, true> : KERNEL<__VA_ARGS__, H, false, false>;   \
+  }
+#define FA4CP_PICK_HP(KERNEL, ...)                      \
+  {                                                     \
+    if (hp == 4) FA4CP_PICK_PK(KERNEL, 4, __VA_ARGS__)  \
+    else if (hp == 2) FA4CP_PICK_PK(KERNEL, 2, __VA_ARGS__) \
+    else FA4CP_PICK_PK(KERNEL, 1, __VA_ARGS__)          \
   }
   if (fp8) {
     if (d == 128) FA4CP_PICK_HP(attn_fwd_e4m3_sweep, 128)
@@ -2975,6 +3043,7 @@ static int ring_sweep_launch(const fa4cp_sweep_args* a, const fa4cp_sweep_kpages
     else FA4CP_PICK_HP(attn_fwd_16bit_sweep, _Float16, 256)
   }
 #undef FA4CP_PICK_HP
+#undef FA4CP_PICK_PK
   hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kPPThreads), 0, (hipStream_t)stream, p);
   return check_launch(paged ? "ring_sweep_fwd_paged" : "ring_sweep_fwd");
 }
