@@ -38,7 +38,9 @@
 // into one FMA per score, and rescales the output only when the running max grows by
 // more than 2^8; the LSE written is natural-log, as fa4_ring/merge.py expects.
 #include <algorithm>
+#include <atomic>
 #include <cfloat>
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -276,22 +278,28 @@ struct MfmaOps<_Float16> {
 // With fewer head groups than XCDs, each head group spans k = 8 / n_hg XCDs; a contiguous
 // split would hand one XCD the heavy back-half row tiles and another the light front half,
 // so the k XCDs take every k-th row tile instead (still longest first on each).
+//
+// `bid` is the workgroup id of this order (blockIdx.x, or the id a sweep workgroup claimed).
 template <typename Params>
-__device__ __forceinline__ void decode_block(const Params& p, int& hg, int& seq, int& rt) {
+__device__ __forceinline__ void decode_block_at(const Params& p, int bid, int& hg, int& seq, int& rt) {
   const int per_hg = p.nseq * p.n_rt;
   const int k = p.n_hg < 8 ? 8 / p.n_hg : 1;
   int r;
   if (k > 1 && p.n_hg * k == 8 && p.n_blocks % 8 == 0 && per_hg % k == 0) {
-    const int x = (int)blockIdx.x & 7;  // the XCD the hardware sends this workgroup to
+    const int x = bid & 7;  // the XCD the hardware sends workgroup bid to
     hg = x / k;
-    r = x % k + k * (int)(blockIdx.x >> 3);
+    r = x % k + k * (bid >> 3);
   } else {
-    const int b = xcd_remap((int)blockIdx.x, p.n_blocks);
+    const int b = xcd_remap(bid, p.n_blocks);
     hg = b / per_hg;
     r = b - hg * per_hg;
   }
   seq = r / p.n_rt;
   rt = p.n_rt - 1 - (r - seq * p.n_rt);
+}
+template <typename Params>
+__device__ __forceinline__ void decode_block(const Params& p, int& hg, int& seq, int& rt) {
+  decode_block_at(p, (int)blockIdx.x, hg, seq, rt);
 }
 
 // decode_block for the sweep kernels over packed sequences: the grid counts n_rt row tiles for
@@ -346,6 +354,44 @@ __device__ __forceinline__ bool decode_sweep_block(const Params& p, int rows, in
     base += tot;
   }
   return false;
+}
+
+// Dynamic hand-out of the sweep's row tiles.  The hardware sends workgroup i to XCD i % 8,
+// so a fixed order gives every XCD the same share, and the slowest XCD (their speeds differ
+// by several per cent on one GPU) sets the end of the launch.  Here the grid has some spare
+// workgroups, and each workgroup claims the next entry of its XCD's list (the entries
+// y + 8 i, i = 0, 1, ..., of the fixed order for XCD y: the same head groups and longest-first
+// order) from that XCD's counter; when the list is used up it claims from the other XCDs'
+// lists in turn, and when all are, it exits.  Every entry is claimed once (a counter hands out
+// each value once, and a workgroup only exits after it found every list used up, so with at
+// least as many workgroups as entries none is left).  `claim` points at nine counters 128
+// bytes apart, zero at the start (eight lists, then the workgroups that finished claiming);
+// the last workgroup to finish claiming sets them back to zero for the launch that reuses
+// them.  Returns the claimed id of the fixed order, or -1.  (Packed sequences keep the fixed
+// order: there a workgroup averages a few dozen tiles, and the claim at its start cost more
+// than the balance gained, 0.8825-0.8877 against 0.8711-0.8786 ms for C4.)
+constexpr int kClaimStride = 32;  // words between counters
+template <typename Params>
+__device__ __forceinline__ int claim_block(const Params& p) {
+  __shared__ int claimed;
+  if (threadIdx.x == 0) {
+    const int lim = p.n_blocks >> 3;  // entries per list
+    const int x = (int)blockIdx.x & 7;
+    int b = -1;
+    for (int d = 0; d < 8; ++d) {
+      const int y = (x + d) & 7;
+      const int i = (int)atomicAdd(p.claim + kClaimStride * y, 1u);
+      if (i < lim) {
+        b = y + 8 * i;
+        break;
+      }
+    }
+    if (atomicAdd(p.claim + kClaimStride * 8, 1u) == gridDim.x - 1)
+      for (int y = 0; y <= 8; ++y) atomicExch(p.claim + kClaimStride * y, 0u);
+    claimed = b;
+  }
+  __syncthreads();
+  return __builtin_amdgcn_readfirstlane(claimed);
 }
 
 // Number of leading key tiles of BN keys that need no mask for any row of the workgroup.
@@ -1462,6 +1508,8 @@ struct SweepParams {
   // [n * page_size, (n + 1) * page_size) of local sequence seq
   const int32_t* kpt[FA4CP_MAX_CP];
   int kpt_stride, page_size, num_pages;
+  // dynamic row tile hand-out (claim_block): the launch's counters, or NULL for the fixed order
+  unsigned* claim;
 };
 
 // The ring steps of one row tile (rows [row_tile0, row_tile0 + rows) of a sequence of L),
@@ -1516,6 +1564,10 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_sweep(SweepParam
   int hg, seq, rt;
   if constexpr (PACK) {
     if (!decode_sweep_block(p, RB * 32, hg, seq, rt)) return;
+  } else if (p.claim != nullptr) {
+    const int b = claim_block(p);
+    if (b < 0) return;
+    decode_block_at(p, b, hg, seq, rt);
   } else {
     decode_block(p, hg, seq, rt);
   }
@@ -2701,6 +2753,10 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_sweep(SweepParams
   int hg, seq, rt;
   if constexpr (PACK) {
     if (!decode_sweep_block(p, RB * 32, hg, seq, rt)) return;
+  } else if (p.claim != nullptr) {
+    const int b = claim_block(p);
+    if (b < 0) return;
+    decode_block_at(p, b, hg, seq, rt);
   } else {
     decode_block(p, hg, seq, rt);
   }
@@ -2932,6 +2988,48 @@ extern "C" int fa4cp_attn_fwd(const fa4cp_attn_args* a, void* stream) {
   return check_launch("attn_fwd");
 }
 
+// Counters of the sweeps' dynamic row tile hand-out (claim_block): kClaimSlots slots of nine
+// counters kClaimStride words apart, zero at module load.  Each launch takes the next slot of
+// its GPU and its last workgroup to claim clears it, so up to kClaimSlots sweep launches may
+// be in flight on one GPU at a time (a launch captured in a graph keeps its slot: replays of
+// it must not overlap).  In host code the array's name is a host-side stand-in: its device
+// address is looked up once per device (hipGetSymbolAddress, with the device current).
+constexpr int kClaimSlots = 64;
+static __device__ __align__(256) unsigned sweep_claims[kClaimSlots * 9 * kClaimStride];
+
+namespace {
+constexpr int kClaimDevices = 64;
+std::mutex g_claims_mu;
+unsigned* g_claims_addr[kClaimDevices] = {};
+std::atomic<unsigned> g_claims_next[kClaimDevices];
+
+// The next claim slot of the stream's GPU, or NULL (the fixed order then) when the stream
+// belongs to another GPU than the current one or the lookup fails.
+unsigned* claim_slot(hipStream_t st) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kClaimDevices) return nullptr;
+  if (st != nullptr) {
+    int sdev = -1;
+    if (hipStreamGetDevice(st, &sdev) != hipSuccess || sdev != dev) return nullptr;
+  }
+  unsigned* base;
+  {
+    std::lock_guard<std::mutex> lock(g_claims_mu);
+    if (g_claims_addr[dev] == nullptr) {
+      void* ptr = nullptr;
+      if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(sweep_claims)) != hipSuccess || ptr == nullptr) {
+        (void)hipGetLastError();
+        return nullptr;
+      }
+      g_claims_addr[dev] = static_cast<unsigned*>(ptr);
+    }
+    base = g_claims_addr[dev];
+  }
+  const unsigned slot = g_claims_next[dev].fetch_add(1u, std::memory_order_relaxed) % kClaimSlots;
+  return base + (size_t)slot * 9 * kClaimStride;
+}
+}  // namespace
+
 // fa4cp_ring_sweep_fwd (kp == NULL) and fa4cp_ring_sweep_fwd_paged.
 static int ring_sweep_launch(const fa4cp_sweep_args* a, const fa4cp_sweep_kpages* kp, void* stream) {
   clear_error();
@@ -3044,7 +3142,17 @@ static int ring_sweep_launch(const fa4cp_sweep_args* a, const fa4cp_sweep_kpages
   }
 #undef FA4CP_PICK_HP
 #undef FA4CP_PICK_PK
-  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kPPThreads), 0, (hipStream_t)stream, p);
+  // one sequence: dynamic hand-out with a tenth more workgroups than row tiles (the spares
+  // exit once every XCD's list is used up)
+  unsigned grid = (unsigned)blocks;
+  p.claim = nullptr;
+  const int64_t per_xcd = blocks / 8;
+  const int64_t spare = (per_xcd + 9) / 10;
+  if (!pack && blocks % 8 == 0 && blocks + 8 * spare <= 0x7fffffffLL) {
+    p.claim = claim_slot((hipStream_t)stream);
+    if (p.claim != nullptr) grid = (unsigned)(blocks + 8 * spare);
+  }
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(kPPThreads), 0, (hipStream_t)stream, p);
   return check_launch(paged ? "ring_sweep_fwd_paged" : "ring_sweep_fwd");
 }
 

@@ -615,6 +615,70 @@ def test_ring_c4_varlen_full_size(rank):
                  scale_for(d), TOL_BF16_OUT)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("packed", [False, True])
+def test_sweep_handout_counters_reused(packed, dtype):
+    """The fused sweep over one sequence hands its row tiles out from counters that each
+    launch takes from a set of 64 per GPU and that the launch's last workgroup clears
+    (packed sequences keep the fixed order and are checked the same way).  The first launch
+    matches the oracle, and 70 more in a row (every counter set reused) and 6 alternating
+    between two streams give bit-identical out and LSE."""
+    lens = [608, 1216, 1072, 608, 232, 1928, 344, 200] if packed else [2048]
+    cp, h, hkv, d, rank = 4, 32, 8, 128, 3
+    fp8 = dtype == torch.float8_e4m3fn
+    say(f"sweep hand-out reuse packed={packed} {dtype}")
+    full_cu = [0]
+    for n in lens:
+        full_cu.append(full_cu[-1] + n)
+    q, k, v = O.random_qkv(full_cu[-1], h, hkv, d, seed=6)
+    q, k, v = (rounded(t, torch.bfloat16) for t in (q, k, v))
+    qd, kd, vd = (t.to(torch.bfloat16).to(DEV) for t in (q, k, v))
+    cfg = RingConfig(cp_size=cp, cp_rank=rank)
+    if packed:
+        ring = LocalKVRing.from_full(kd, vd, cp, full_cu)
+        lq, local_cu = zigzag_shard_varlen(qd, full_cu, rank, cp)
+        kw = dict(cu_seqlens=local_cu, max_seqlen=int((local_cu[1:] - local_cu[:-1]).max()))
+    else:
+        ring = LocalKVRing.from_full(kd, vd, cp)
+        lq = zigzag_shard(qd, rank, cp)
+        kw = {}
+    if fp8:
+        from fa4_ring import quantize_ring
+        lq, k8, v8, desc = quantize_ring(lq, list(ring.k), list(ring.v))
+        ring = LocalKVRing(k8, v8)
+        kw["descales"] = desc
+
+    def sweep():
+        return ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, return_lse=True, **kw)
+
+    out0, lse0 = sweep()
+    if fp8:
+        # the oracle on the dequantised e4m3 inputs
+        qo = lq.float().cpu() * float(desc.q)
+        ks = [ring.k[r].float().cpu() * float(desc.k[r]) for r in range(cp)]
+        vs = [ring.v[r].float().cpu() * float(desc.v[r]) for r in range(cp)]
+    else:
+        qo = lq.float().cpu()
+        ks = [ring.k[r].float().cpu() for r in range(cp)]
+        vs = [ring.v[r].float().cpu() for r in range(cp)]
+    ocu = kw["cu_seqlens"].cpu().tolist() if packed else None
+    ref, ref_lse = O.ring_rank(qo, ks, vs, rank, cp, scale_for(d), cu=ocu)
+    assert max_err(out0, ref) <= (TOL_FP8_OUT if fp8 else TOL_BF16_OUT)
+    assert lse_err(lse0, ref_lse) <= TOL_LSE
+    for i in range(70):
+        out, lse = sweep()
+        assert torch.equal(out, out0) and torch.equal(lse, lse0), f"launch {i + 1}"
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    res = []
+    for i in range(6):
+        with torch.cuda.stream(streams[i % 2]):
+            res.append(sweep())
+    torch.cuda.synchronize()
+    for i, (out, lse) in enumerate(res):
+        assert torch.equal(out, out0) and torch.equal(lse, lse0), f"stream launch {i}"
+
+
 EMPTY_CASES = [(torch.bfloat16, p) for p in PATHS] + [(torch.float8_e4m3fn, "fused"),
                                                        (torch.float8_e4m3fn, "incremental")]
 
