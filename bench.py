@@ -45,7 +45,7 @@ N, CP, HQ, HKV, D = 131072, 8, 32, 8, 128
 # The summary with both commands is under profiles/.
 ATTN_TRAFFIC_BYTES_RANK3 = 466593 * 1024
 # The same for the fused sweep kernel (one launch per sweep).
-SWEEP_TRAFFIC_BYTES_RANK3 = 2395694 * 1024
+SWEEP_TRAFFIC_BYTES_RANK3 = 2436944 * 1024
 # ... for the packed-sequence sweep (cp_size 4, rank 3) and the e4m3 head-dim-256 sweep
 # (N = 262144, rank 3), and for merge_states in their batched per-step forms (same factors,
 # counter passes over `bench.py --workload c4` / `--workload c5`).
