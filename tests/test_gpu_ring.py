@@ -679,6 +679,41 @@ def test_sweep_handout_counters_reused(packed, dtype):
         assert torch.equal(out, out0) and torch.equal(lse, lse0), f"stream launch {i}"
 
 
+def test_sweep_graph_replays():
+    """A captured fused sweep (one sequence: the V transposes and the sweep launch, which keeps
+    the set of hand-out counters it took at capture) replayed five times, with eager sweeps
+    and synchronisations between the replays, gives the eager result every time."""
+    cp, h, hkv, d, rank, n = 4, 32, 8, 128, 2, 2048
+    say("sweep graph replays")
+    q, k, v = O.random_qkv(n, h, hkv, d, seed=9)
+    qd, ring = _device_ring(q, k, v, cp, torch.bfloat16)
+    lq = zigzag_shard(qd, rank, cp)
+    cfg = RingConfig(cp_size=cp, cp_rank=rank)
+
+    def sweep():
+        return ring_flash_attn(lq, ring.k[rank], ring.v[rank], cfg, group=ring, return_lse=True)
+
+    out0, lse0 = sweep()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm the allocator off the default stream, as capture requires
+        sweep()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gout, glse = sweep()
+    for i in range(5):
+        gout.zero_()
+        glse.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout, out0) and torch.equal(glse, lse0), f"replay {i}"
+        out, lse = sweep()  # eager work between the replays
+        torch.cuda.synchronize()
+        assert torch.equal(out, out0) and torch.equal(lse, lse0), f"eager after replay {i}"
+
+
 EMPTY_CASES = [(torch.bfloat16, p) for p in PATHS] + [(torch.float8_e4m3fn, "fused"),
                                                        (torch.float8_e4m3fn, "incremental")]
 
