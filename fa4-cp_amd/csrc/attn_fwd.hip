@@ -77,6 +77,8 @@ struct AttnParams {
   int n_rt;  // row tiles per sequence (of 32 * RB rows)
   int n_hg;  // head groups: h_kv * group / HP
   int n_blocks;
+  // dynamic row tile hand-out (claim_block): the launch's counters, or NULL for the fixed order
+  unsigned* claim;
 };
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -394,6 +396,20 @@ __device__ __forceinline__ int claim_block(const Params& p) {
   return __builtin_amdgcn_readfirstlane(claimed);
 }
 
+// The row tile of a per-step attention workgroup: the fixed order, or a claimed id of it
+// (false: none left, the workgroup exits).
+template <typename Params>
+__device__ __forceinline__ bool pick_block(const Params& p, int& hg, int& seq, int& rt) {
+  if (p.claim == nullptr) {
+    decode_block(p, hg, seq, rt);
+    return true;
+  }
+  const int b = claim_block(p);
+  if (b < 0) return false;
+  decode_block_at(p, b, hg, seq, rt);
+  return true;
+}
+
 // Number of leading key tiles of BN keys that need no mask for any row of the workgroup.
 template <int BN = kBN>
 __device__ __forceinline__ int mask_free_tiles(int n_tiles, int Lk, bool causal, int row_tile0,
@@ -432,7 +448,7 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_16bit(A
   __shared__ __attribute__((aligned(1024))) T vl[2][BN * D];
 
   int hg, seq, rt;
-  decode_block(p, hg, seq, rt);
+  if (!pick_block(p, hg, seq, rt)) return;
   int qs, Lq, ks, Lk;
   seq_range(p.cu_q, seq, p.total_q, p.q_sel, qs, Lq);
   seq_range(p.cu_k, seq, p.total_k, p.k_sel, ks, Lk);
@@ -689,7 +705,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_pp(AttnParams p)
   __shared__ __attribute__((aligned(1024))) T vt[2][D * VTS];
 
   int hg, seq, rt;
-  decode_block(p, hg, seq, rt);
+  if (!pick_block(p, hg, seq, rt)) return;
   int qs, Lq, ks, Lk;
   seq_range(p.cu_q, seq, p.total_q, p.q_sel, qs, Lq);
   seq_range(p.cu_k, seq, p.total_k, p.k_sel, ks, Lk);
@@ -1439,7 +1455,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_vt(AttnParams p)
   constexpr int BN = vt_bn<D>();
   constexpr int RB = kPPWaves / HP;  // 32-row blocks per workgroup
   int hg, seq, rt;
-  decode_block(p, hg, seq, rt);
+  if (!pick_block(p, hg, seq, rt)) return;
   int qs, Lq, ks, Lk;
   seq_range(p.cu_q, seq, p.total_q, p.q_sel, qs, Lq);
   seq_range(p.cu_k, seq, p.total_k, p.k_sel, ks, Lk);
@@ -1658,7 +1674,7 @@ __global__ __launch_bounds__(kThreads, (D >= 256 ? 1 : 2)) void attn_fwd_e4m3(At
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * BUF];
 
   int hg, seq, rt;
-  decode_block(p, hg, seq, rt);
+  if (!pick_block(p, hg, seq, rt)) return;
   int qs, Lq, ks, Lk;
   seq_range(p.cu_q, seq, p.total_q, p.q_sel, qs, Lq);
   seq_range(p.cu_k, seq, p.total_k, p.k_sel, ks, Lk);
@@ -1939,7 +1955,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_pp(AttnParams p) 
   __shared__ __attribute__((aligned(1024))) uint8_t qsm[kPPWaves][NKS][64 * 32];
 
   int hg, seq, rt;
-  decode_block(p, hg, seq, rt);
+  if (!pick_block(p, hg, seq, rt)) return;
   int qs, Lq, ks, Lk;
   seq_range(p.cu_q, seq, p.total_q, p.q_sel, qs, Lq);
   seq_range(p.cu_k, seq, p.total_k, p.k_sel, ks, Lk);
@@ -2690,7 +2706,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_vt(AttnParams p) 
   constexpr int BN = e8_bn<D>();
   constexpr int RB = kPPWaves / HP;  // 32-row blocks per workgroup
   int hg, seq, rt;
-  decode_block(p, hg, seq, rt);
+  if (!pick_block(p, hg, seq, rt)) return;
   int qs, Lq, ks, Lk;
   seq_range(p.cu_q, seq, p.total_q, p.q_sel, qs, Lq);
   seq_range(p.cu_k, seq, p.total_k, p.k_sel, ks, Lk);
@@ -2901,6 +2917,48 @@ static bool tile_offsets_fit(int64_t row_stride, int esz, int d, int64_t vt_d_st
   return 256 * row_stride * esz < kMax && (int64_t)d * vt_d_stride * esz + 256 < kMax;
 }
 
+// Counters of the dynamic row tile hand-out (claim_block) of the sweeps and the per-step
+// attention kernels: kClaimSlots slots of nine counters kClaimStride words apart, zero at
+// module load.  Each launch takes the next slot of its GPU and its last workgroup to claim
+// clears it, so up to kClaimSlots such launches may be in flight on one GPU at a time (a
+// launch captured in a graph keeps its slot: replays of it must not overlap).  In host code the array's name is a host-side stand-in: its device
+// address is looked up once per device (hipGetSymbolAddress, with the device current).
+constexpr int kClaimSlots = 64;
+static __device__ __align__(256) unsigned sweep_claims[kClaimSlots * 9 * kClaimStride];
+
+namespace {
+constexpr int kClaimDevices = 64;
+std::mutex g_claims_mu;
+unsigned* g_claims_addr[kClaimDevices] = {};
+std::atomic<unsigned> g_claims_next[kClaimDevices];
+
+// The next claim slot of the stream's GPU, or NULL (the fixed order then) when the stream
+// belongs to another GPU than the current one or the lookup fails.
+unsigned* claim_slot(hipStream_t st) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kClaimDevices) return nullptr;
+  if (st != nullptr) {
+    int sdev = -1;
+    if (hipStreamGetDevice(st, &sdev) != hipSuccess || sdev != dev) return nullptr;
+  }
+  unsigned* base;
+  {
+    std::lock_guard<std::mutex> lock(g_claims_mu);
+    if (g_claims_addr[dev] == nullptr) {
+      void* ptr = nullptr;
+      if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(sweep_claims)) != hipSuccess || ptr == nullptr) {
+        (void)hipGetLastError();
+        return nullptr;
+      }
+      g_claims_addr[dev] = static_cast<unsigned*>(ptr);
+    }
+    base = g_claims_addr[dev];
+  }
+  const unsigned slot = g_claims_next[dev].fetch_add(1u, std::memory_order_relaxed) % kClaimSlots;
+  return base + (size_t)slot * 9 * kClaimStride;
+}
+}  // namespace
+
 extern "C" int fa4cp_attn_fwd(const fa4cp_attn_args* a, void* stream) {
   clear_error();
   if (a == nullptr) return set_error(FA4CP_EINVAL, "attn_fwd: null args");
@@ -2984,51 +3042,18 @@ extern "C" int fa4cp_attn_fwd(const fa4cp_attn_args* a, void* stream) {
   if (blocks == 0 || a->total_q == 0) return FA4CP_OK;
   if (blocks > 0x7fffffffLL) return set_error(FA4CP_EINVAL, "attn_fwd: grid too large");
   p.n_blocks = (int)blocks;
-  hipLaunchKernelGGL(kc.fn, dim3((unsigned)blocks), dim3(kc.threads), 0, (hipStream_t)stream, p);
+  // one sequence: the dynamic hand-out of the row tiles, with a tenth more workgroups
+  unsigned grid = (unsigned)blocks;
+  p.claim = nullptr;
+  const int64_t spare = (blocks / 8 + 9) / 10;
+  if (nseq == 1 && blocks % 8 == 0 && blocks + 8 * spare <= 0x7fffffffLL) {
+    p.claim = claim_slot((hipStream_t)stream);
+    if (p.claim != nullptr) grid = (unsigned)(blocks + 8 * spare);
+  }
+  hipLaunchKernelGGL(kc.fn, dim3(grid), dim3(kc.threads), 0, (hipStream_t)stream, p);
   return check_launch("attn_fwd");
 }
 
-// Counters of the sweeps' dynamic row tile hand-out (claim_block): kClaimSlots slots of nine
-// counters kClaimStride words apart, zero at module load.  Each launch takes the next slot of
-// its GPU and its last workgroup to claim clears it, so up to kClaimSlots sweep launches may
-// be in flight on one GPU at a time (a launch captured in a graph keeps its slot: replays of
-// it must not overlap).  In host code the array's name is a host-side stand-in: its device
-// address is looked up once per device (hipGetSymbolAddress, with the device current).
-constexpr int kClaimSlots = 64;
-static __device__ __align__(256) unsigned sweep_claims[kClaimSlots * 9 * kClaimStride];
-
-namespace {
-constexpr int kClaimDevices = 64;
-std::mutex g_claims_mu;
-unsigned* g_claims_addr[kClaimDevices] = {};
-std::atomic<unsigned> g_claims_next[kClaimDevices];
-
-// The next claim slot of the stream's GPU, or NULL (the fixed order then) when the stream
-// belongs to another GPU than the current one or the lookup fails.
-unsigned* claim_slot(hipStream_t st) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kClaimDevices) return nullptr;
-  if (st != nullptr) {
-    int sdev = -1;
-    if (hipStreamGetDevice(st, &sdev) != hipSuccess || sdev != dev) return nullptr;
-  }
-  unsigned* base;
-  {
-    std::lock_guard<std::mutex> lock(g_claims_mu);
-    if (g_claims_addr[dev] == nullptr) {
-      void* ptr = nullptr;
-      if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(sweep_claims)) != hipSuccess || ptr == nullptr) {
-        (void)hipGetLastError();
-        return nullptr;
-      }
-      g_claims_addr[dev] = static_cast<unsigned*>(ptr);
-    }
-    base = g_claims_addr[dev];
-  }
-  const unsigned slot = g_claims_next[dev].fetch_add(1u, std::memory_order_relaxed) % kClaimSlots;
-  return base + (size_t)slot * 9 * kClaimStride;
-}
-}  // namespace
 
 // fa4cp_ring_sweep_fwd (kp == NULL) and fa4cp_ring_sweep_fwd_paged.
 static int ring_sweep_launch(const fa4cp_sweep_args* a, const fa4cp_sweep_kpages* kp, void* stream) {

@@ -19,14 +19,15 @@
  *     the kernels size their grids by them, and with a too-small bound some rows are not
  *     written;
  *   - the library's state is that thread-local message; for fa4cp_quantize_e4m3_noalloc, a
- *     static 4 KiB device array per GPU (its amax words); and for fa4cp_ring_sweep_fwd and
- *     fa4cp_ring_sweep_fwd_paged over one sequence, a static 72 KiB device array per GPU of
- *     64 sets of row tile counters (a launch takes the next set, its last workgroup clears
- *     it).  Each array has a per-device cache of its address (filled once per device under
- *     a mutex) and the sweeps a per-device set counter.  Two calls that write the same memory
- *     on different streams race, and so do two fa4cp_quantize_e4m3_noalloc calls that
- *     overlap on one GPU; at most 64 one-sequence sweep launches may be in flight on one GPU
- *     at a time, and replays of one captured sweep launch must not overlap each other.
+ *     static 4 KiB device array per GPU (its amax words); and for fa4cp_ring_sweep_fwd,
+ *     fa4cp_ring_sweep_fwd_paged and fa4cp_attn_fwd over one sequence, a static 72 KiB device
+ *     array per GPU of 64 sets of row tile counters (a launch takes the next set, its last
+ *     workgroup clears it).  Each array has a per-device cache of its address (filled once
+ *     per device under a mutex) and the counters a per-device set index.  Two calls that
+ *     write the same memory on different streams race, and so do two
+ *     fa4cp_quantize_e4m3_noalloc calls that overlap on one GPU; at most 64 one-sequence
+ *     attention or sweep launches may be in flight on one GPU at a time, and replays of one
+ *     captured launch must not overlap each other.
  *
  * Reference interfaces replaced (paths are in hxy0118/fa4-cp):
  *   fa4cp_attn_fwd              <- fa4_ring/fa4_backend.py:58-123 (fa4_attn -> FA4 _flash_attn_fwd)
