@@ -43,14 +43,14 @@ N, CP, HQ, HKV, D = 131072, 8, 32, 8, 128
 # rocprofv3 counter passes over this script: FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the
 # factors being what those counters read for the zig-zag gather (a plain copy of known size).
 # The summary with both commands is under profiles/.
-ATTN_TRAFFIC_BYTES_RANK3 = 466593 * 1024
+ATTN_TRAFFIC_BYTES_RANK3 = 467355 * 1024
 # The same for the fused sweep kernel (one launch per sweep).
 SWEEP_TRAFFIC_BYTES_RANK3 = 2436944 * 1024
 # ... for the packed-sequence sweep (cp_size 4, rank 3) and the e4m3 head-dim-256 sweep
 # (N = 262144, rank 3), and for merge_states in their batched per-step forms (same factors,
 # counter passes over `bench.py --workload c4` / `--workload c5`).
 C4_SWEEP_TRAFFIC_BYTES = (2 * 144522 + 102470) * 1024
-C5_SWEEP_TRAFFIC_BYTES = (2 * 2793692 + 266244) * 1024
+C5_SWEEP_TRAFFIC_BYTES = (2 * 2384638 + 266445) * 1024
 C4_MERGE_STATES_TRAFFIC_BYTES = (2 * 204965 + 100913) * 1024
 C5_MERGE_STATES_TRAFFIC_BYTES = (2 * 802850 + 264192) * 1024
 
