@@ -2920,10 +2920,9 @@ static bool tile_offsets_fit(int64_t row_stride, int esz, int d, int64_t vt_d_st
 // Counters of the dynamic row tile hand-out (claim_block) of the sweeps and the per-step
 // attention kernels: kClaimSlots slots of nine counters kClaimStride words apart, zero at
 // module load.  Each launch takes the next slot of its GPU and its last workgroup to claim
-// clears it, so up to kClaimSlots such launches may run at the same time on one GPU (on
-// different streams; launches on one stream run in order, so a slot is free again when the
-// launch 64 later on that stream starts).  A launch captured in a graph keeps its slot:
-// replays of it must not overlap.  In host code the array's name is a host-side stand-in: its device
+// clears it, so a launch must have finished before the kClaimSlots-th launch after it on
+// the same GPU (over all streams) starts; on one stream that always holds.  A launch captured
+// in a graph keeps its slot: replays of it must not overlap.  In host code the array's name is a host-side stand-in: its device
 // address is looked up once per device (hipGetSymbolAddress, with the device current).
 constexpr int kClaimSlots = 64;
 static __device__ __align__(256) unsigned sweep_claims[kClaimSlots * 9 * kClaimStride];

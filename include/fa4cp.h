@@ -25,10 +25,11 @@
  *     workgroup clears it).  Each array has a per-device cache of its address (filled once
  *     per device under a mutex) and the counters a per-device set index.  Two calls that
  *     write the same memory on different streams race, and so do two
- *     fa4cp_quantize_e4m3_noalloc calls that overlap on one GPU; of the one-sequence attention
- *     and sweep launches, at most 64 may run at the same time on one GPU (on different streams;
- *     launches on one stream run in order and reuse the counter sets safely), and replays of
- *     one captured launch must not overlap each other.
+ *     fa4cp_quantize_e4m3_noalloc calls that overlap on one GPU; the one-sequence attention
+ *     and sweep calls on one GPU take the 64 counter sets in turn, so a call must have
+ *     finished on the GPU before the 64th such call after it (counted over all streams)
+ *     starts there (always true on one stream), and replays of one captured launch must not
+ *     overlap each other.
  *
  * Reference interfaces replaced (paths are in hxy0118/fa4-cp):
  *   fa4cp_attn_fwd              <- fa4_ring/fa4_backend.py:58-123 (fa4_attn -> FA4 _flash_attn_fwd)
