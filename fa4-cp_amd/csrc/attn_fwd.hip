@@ -315,7 +315,8 @@ __device__ __forceinline__ void decode_block(const Params& p, int& hg, int& seq,
 // there are no gaps, and the headline kernel built with the plain decode ran 0.2 % faster
 // (code placement), while C4 (8 sequences) gains 0.8 % from the packed order.
 template <typename Params>
-__device__ __forceinline__ bool decode_sweep_block(const Params& p, int rows, int& hg, int& seq, int& rt) {
+__device__ __forceinline__ bool decode_sweep_block(const Params& p, int rows, int& hg, int& seq, int& rt,
+                                                   int& qs, int& len, int64_t& vt_pos) {
   const int per_hg = p.nseq * p.n_rt;
   const int k = p.n_hg < 8 ? 8 / p.n_hg : 1;
   int r;
@@ -329,20 +330,25 @@ __device__ __forceinline__ bool decode_sweep_block(const Params& p, int rows, in
     r = b - hg * per_hg;
   }
   const int lane = (int)(threadIdx.x & 63);
-  int base = 0;  // real row tiles of the sequences before j0
+  int base = 0;       // real row tiles of the sequences before j0
+  int64_t vbase = 0;  // their V^T columns (lengths padded to kVtPad, as vt_seq_start sums them)
   for (int j0 = 0; j0 < p.nseq; j0 += 64) {
     const int j = j0 + lane;
-    int nt = 0;
+    int nt = 0, s0 = 0, L = 0, pl = 0;
     if (j < p.nseq) {
-      int s0, L;
       seq_range(p.cu, j, p.total, FA4CP_SEL_ALL, s0, L);
       nt = (L + rows - 1) / rows;
+      pl = (L + kVtPad - 1) / kVtPad * kVtPad;
     }
-    int incl = nt;  // inclusive prefix sum over the lanes
+    int incl = nt, vincl = pl;  // inclusive prefix sums over the lanes
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       const int v = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += v;
+      const int w = __shfl_up(vincl, o, 64);
+      if (lane >= o) {
+        incl += v;
+        vincl += w;
+      }
     }
     const int tot = __builtin_amdgcn_readlane(incl, 63);
     if (r < base + tot) {
@@ -351,9 +357,14 @@ __device__ __forceinline__ bool decode_sweep_block(const Params& p, int rows, in
       const int before = __builtin_amdgcn_readlane(incl, jl) - ntj;
       seq = j0 + jl;
       rt = ntj - 1 - (r - base - before);
+      // the sequence's rows and V^T start from the same loads (no second round trip)
+      qs = __builtin_amdgcn_readlane(s0, jl);
+      len = __builtin_amdgcn_readlane(L, jl);
+      vt_pos = vbase + (__builtin_amdgcn_readlane(vincl, jl) - __builtin_amdgcn_readlane(pl, jl));
       return true;
     }
     base += tot;
+    vbase += __builtin_amdgcn_readlane(vincl, 63);
   }
   return false;
 }
@@ -1578,8 +1589,10 @@ template <typename T, int D, int HP, bool PAGED, bool PACK>
 __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_sweep(SweepParams p) {
   constexpr int RB = kPPWaves / HP;
   int hg, seq, rt;
+  int qs, L;
+  int64_t vt_pos_pk = 0;
   if constexpr (PACK) {
-    if (!decode_sweep_block(p, RB * 32, hg, seq, rt)) return;
+    if (!decode_sweep_block(p, RB * 32, hg, seq, rt, qs, L, vt_pos_pk)) return;
   } else if (p.claim != nullptr) {
     const int b = claim_block(p);
     if (b < 0) return;
@@ -1587,8 +1600,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_sweep(SweepParam
   } else {
     decode_block(p, hg, seq, rt);
   }
-  int qs, L;
-  seq_range(p.cu, seq, p.total, FA4CP_SEL_ALL, qs, L);
+  if constexpr (!PACK) seq_range(p.cu, seq, p.total, FA4CP_SEL_ALL, qs, L);
   const int row_tile0 = rt * RB * 32;
   if (row_tile0 >= L) return;
 
@@ -1605,7 +1617,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_sweep(SweepParam
   geo.rows = RB * 32;
   geo.kvh = kvh;
   geo.seq = seq;
-  const int64_t vt_pos = p.cu ? vt_seq_start(p.cu, seq, p.total, FA4CP_SEL_ALL) : 0;
+  const int64_t vt_pos = PACK ? vt_pos_pk : p.cu ? vt_seq_start(p.cu, seq, p.total, FA4CP_SEL_ALL) : 0;
   if (vt_pos + (L + kVtPad - 1) / kVtPad * kVtPad > p.vt_ds) return;  // malformed cu: outside V^T
   geo.k_off = ((PAGED ? 0 : (int64_t)qs * p.k_rs) + (int64_t)kvh * p.k_hs) * (int64_t)sizeof(T);
   geo.v_off = ((int64_t)kvh * D * p.vt_ds + vt_pos) * (int64_t)sizeof(T);
@@ -2767,8 +2779,10 @@ template <int D, int HP, bool PAGED, bool PACK>
 __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_sweep(SweepParams p) {
   constexpr int RB = kPPWaves / HP;
   int hg, seq, rt;
+  int qs, L;
+  int64_t vt_pos_pk = 0;
   if constexpr (PACK) {
-    if (!decode_sweep_block(p, RB * 32, hg, seq, rt)) return;
+    if (!decode_sweep_block(p, RB * 32, hg, seq, rt, qs, L, vt_pos_pk)) return;
   } else if (p.claim != nullptr) {
     const int b = claim_block(p);
     if (b < 0) return;
@@ -2776,8 +2790,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_sweep(SweepParams
   } else {
     decode_block(p, hg, seq, rt);
   }
-  int qs, L;
-  seq_range(p.cu, seq, p.total, FA4CP_SEL_ALL, qs, L);
+  if constexpr (!PACK) seq_range(p.cu, seq, p.total, FA4CP_SEL_ALL, qs, L);
   const int row_tile0 = rt * RB * 32;
   if (row_tile0 >= L) return;
 
@@ -2794,7 +2807,7 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_sweep(SweepParams
   geo.rows = RB * 32;
   geo.kvh = kvh;
   geo.seq = seq;
-  const int64_t vt_pos = p.cu ? vt_seq_start(p.cu, seq, p.total, FA4CP_SEL_ALL) : 0;
+  const int64_t vt_pos = PACK ? vt_pos_pk : p.cu ? vt_seq_start(p.cu, seq, p.total, FA4CP_SEL_ALL) : 0;
   if (vt_pos + (L + kVtPad - 1) / kVtPad * kVtPad > p.vt_ds) return;  // malformed cu: outside V^T
   geo.k_off = (PAGED ? 0 : (int64_t)qs * p.k_rs) + (int64_t)kvh * p.k_hs;
   geo.v_off = (int64_t)kvh * D * p.vt_ds + vt_pos;
