@@ -52,6 +52,8 @@ SWEEP_TRAFFIC_BYTES_RANK3 = 2436944 * 1024
 C4_SWEEP_TRAFFIC_BYTES = (2 * 144522 + 102470) * 1024
 C5_SWEEP_TRAFFIC_BYTES = (2 * 2384638 + 266445) * 1024
 C4_MERGE_STATES_TRAFFIC_BYTES = (2 * 204965 + 100913) * 1024
+# ... for the e4m3 sweep at the headline shape (rank 3), counter passes over `--workload c3`
+C3_SWEEP_TRAFFIC_BYTES_RANK3 = (2 * 567996 + 135355) * 1024
 C5_MERGE_STATES_TRAFFIC_BYTES = (2 * 802850 + 264192) * 1024
 
 
@@ -508,7 +510,8 @@ def bench_c3(args) -> int:
     line = _single_line(args, block, "e4m3", PEAK_FP8_TFLOPS, config)
     line["roofline"] = {"bound": "mfma", "kernel": block["sweep_kernel"]["kernel"],
                         "achieved": block["sweep_kernel"]["TFLOP/s"], "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
-                        "frac": block["sweep_kernel"]["frac"], "traffic": None,
+                        "frac": block["sweep_kernel"]["frac"],
+                        "traffic": C3_SWEEP_TRAFFIC_BYTES_RANK3 if args.rank == 3 else None,
                         "avg_launch_ms": block["sweep_kernel"]["avg_launch_ms"]}
     print(json.dumps(line), flush=True)
     return 0
