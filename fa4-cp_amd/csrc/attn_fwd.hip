@@ -2944,8 +2944,9 @@ static bool tile_offsets_fit(int64_t row_stride, int esz, int d, int64_t vt_d_st
 // module load.  Each launch takes the next slot of its GPU and its last workgroup to claim
 // clears it, so a launch must have finished before the kClaimSlots-th launch after it on
 // the same GPU (over all streams) starts; on one stream that always holds.  A launch captured
-// in a graph keeps its slot: replays of it must not overlap.  In host code the array's name is a host-side stand-in: its device
-// address is looked up once per device (hipGetSymbolAddress, with the device current).
+// in a graph keeps its slot: replays of it must not overlap.  In host code the array's name
+// is a host-side stand-in: its device address is looked up once per device
+// (hipGetSymbolAddress, with the device current).
 constexpr int kClaimSlots = 64;
 static __device__ __align__(256) unsigned sweep_claims[kClaimSlots * 9 * kClaimStride];
 
