@@ -390,30 +390,87 @@ constexpr int kClaimStride = 32;  // words between counters
 // last quarter (at least a tenth of the list's work, since the lightest tiles come last) and
 // the spare workgroups take part in the claims.  That keeps the claims' cost to a quarter of
 // the workgroups while leaving enough work at the end to even out XCDs up to about 10 % apart.
-template <typename Params>
-__device__ __forceinline__ int claim_block(const Params& p) {
-  const int lim = p.n_blocks >> 3;        // entries per list
-  const int fixed = lim - (lim + 3) / 4;  // entries of a list in the fixed order
-  if ((int)(blockIdx.x >> 3) < fixed) return (int)blockIdx.x;
+//
+// claim_tail: entries fixed .. lim - 1 of the lists, among `parts` claiming workgroups (those
+// past the fixed part of the grid); every thread of the workgroup calls it.
+__device__ __forceinline__ int claim_tail(unsigned* claim, int fixed, int lim, unsigned parts) {
   __shared__ int claimed;
   if (threadIdx.x == 0) {
     const int x = (int)blockIdx.x & 7;
     int b = -1;
     for (int d = 0; d < 8; ++d) {
       const int y = (x + d) & 7;
-      const int i = fixed + (int)atomicAdd(p.claim + kClaimStride * y, 1u);
+      const int i = fixed + (int)atomicAdd(claim + kClaimStride * y, 1u);
       if (i < lim) {
         b = y + 8 * i;
         break;
       }
     }
-    // the workgroups that claim: every one past the fixed part (gridDim.x is a multiple of 8)
-    if (atomicAdd(p.claim + kClaimStride * 8, 1u) == gridDim.x - 8u * (unsigned)fixed - 1u)
-      for (int y = 0; y <= 8; ++y) atomicExch(p.claim + kClaimStride * y, 0u);
+    if (atomicAdd(claim + kClaimStride * 8, 1u) == parts - 1u)
+      for (int y = 0; y <= 8; ++y) atomicExch(claim + kClaimStride * y, 0u);
     claimed = b;
   }
   __syncthreads();
   return __builtin_amdgcn_readfirstlane(claimed);
+}
+template <typename Params>
+__device__ __forceinline__ int claim_block(const Params& p) {
+  const int lim = p.n_blocks >> 3;        // entries per list
+  const int fixed = lim - (lim + 3) / 4;  // entries of a list in the fixed order
+  if ((int)(blockIdx.x >> 3) < fixed) return (int)blockIdx.x;
+  // the workgroups that claim: every one past the fixed part (gridDim.x is a multiple of 8)
+  return claim_tail(p.claim, fixed, lim, gridDim.x - 8u * (unsigned)fixed);
+}
+
+// decode_sweep_block for packed sequences with the hand-out of the lists' tails, where each
+// XCD owns one head group (n_hg = 8) and there are at most 64 sequences: one pass over the
+// sequences (a lane each) gives the head group's real row tiles `tot`, so that the first
+// three quarters of them keep the fixed order and the rest go to the claims of the
+// workgroups tot - tot / 4 .. tot + tot / 10 of each XCD (the others, empty in the fixed
+// order too, exit at once).  Returns false when the workgroup has no tile.
+template <typename Params>
+__device__ __forceinline__ bool decode_sweep_claimed(const Params& p, int rows, int& hg, int& seq, int& rt,
+                                                     int& qs, int& len, int64_t& vt_pos) {
+  const int lane = (int)(threadIdx.x & 63);
+  int nt = 0, s0 = 0, L = 0, pl = 0;
+  if (lane < p.nseq) {
+    seq_range(p.cu, lane, p.total, FA4CP_SEL_ALL, s0, L);
+    nt = (L + rows - 1) / rows;
+    pl = (L + kVtPad - 1) / kVtPad * kVtPad;
+  }
+  int incl = nt, vincl = pl;  // inclusive prefix sums over the lanes
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o, 64);
+    const int w = __shfl_up(vincl, o, 64);
+    if (lane >= o) {
+      incl += v;
+      vincl += w;
+    }
+  }
+  const int tot = __builtin_amdgcn_readlane(incl, 63);  // entries of each XCD's list
+  const int fixed = tot - (tot + 3) / 4;
+  const int parts_per_xcd = tot + (tot + 9) / 10 - fixed;
+  const int i = (int)(blockIdx.x >> 3);
+  int b = (int)blockIdx.x;
+  if (i >= fixed) {
+    if (i >= fixed + parts_per_xcd) return false;
+    b = claim_tail(p.claim, fixed, tot, 8u * (unsigned)parts_per_xcd);
+    if (b < 0) return false;
+  }
+  // one head group per XCD: entry b is row tile b >> 3 (in the order decode_sweep_block
+  // numbers them) of head group b & 7
+  hg = b & 7;
+  const int r = b >> 3;
+  const int jl = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)__ballot(incl > r)) - 1);
+  const int ntj = __builtin_amdgcn_readlane(nt, jl);
+  const int before = __builtin_amdgcn_readlane(incl, jl) - ntj;
+  seq = jl;
+  rt = ntj - 1 - (r - before);
+  qs = __builtin_amdgcn_readlane(s0, jl);
+  len = __builtin_amdgcn_readlane(L, jl);
+  vt_pos = __builtin_amdgcn_readlane(vincl, jl) - __builtin_amdgcn_readlane(pl, jl);
+  return true;
 }
 
 // The row tile of a per-step attention workgroup: the fixed order, or a claimed id of it
@@ -1601,7 +1658,11 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_16bit_sweep(SweepParam
   int qs, L;
   int64_t vt_pos_pk = 0;
   if constexpr (PACK) {
-    if (!decode_sweep_block(p, RB * 32, hg, seq, rt, qs, L, vt_pos_pk)) return;
+    if (p.claim != nullptr) {
+      if (!decode_sweep_claimed(p, RB * 32, hg, seq, rt, qs, L, vt_pos_pk)) return;
+    } else if (!decode_sweep_block(p, RB * 32, hg, seq, rt, qs, L, vt_pos_pk)) {
+      return;
+    }
   } else if (p.claim != nullptr) {
     const int b = claim_block(p);
     if (b < 0) return;
@@ -2791,7 +2852,11 @@ __global__ __launch_bounds__(kPPThreads, 2) void attn_fwd_e4m3_sweep(SweepParams
   int qs, L;
   int64_t vt_pos_pk = 0;
   if constexpr (PACK) {
-    if (!decode_sweep_block(p, RB * 32, hg, seq, rt, qs, L, vt_pos_pk)) return;
+    if (p.claim != nullptr) {
+      if (!decode_sweep_claimed(p, RB * 32, hg, seq, rt, qs, L, vt_pos_pk)) return;
+    } else if (!decode_sweep_block(p, RB * 32, hg, seq, rt, qs, L, vt_pos_pk)) {
+      return;
+    }
   } else if (p.claim != nullptr) {
     const int b = claim_block(p);
     if (b < 0) return;
@@ -3191,13 +3256,14 @@ static int ring_sweep_launch(const fa4cp_sweep_args* a, const fa4cp_sweep_kpages
   }
 #undef FA4CP_PICK_HP
 #undef FA4CP_PICK_PK
-  // one sequence: dynamic hand-out with a tenth more workgroups than row tiles (the spares
-  // exit once every XCD's list is used up)
+  // dynamic hand-out of the lists' tails with a tenth more workgroups than row tiles (the
+  // spares exit once every XCD's list is used up): one sequence, or up to 64 packed ones
+  // where each XCD owns one head group
   unsigned grid = (unsigned)blocks;
   p.claim = nullptr;
   const int64_t per_xcd = blocks / 8;
   const int64_t spare = (per_xcd + 9) / 10;
-  if (!pack && blocks % 8 == 0 && blocks + 8 * spare <= 0x7fffffffLL) {
+  if ((!pack || (p.n_hg == 8 && nseq <= 64)) && blocks % 8 == 0 && blocks + 8 * spare <= 0x7fffffffLL) {
     p.claim = claim_slot((hipStream_t)stream);
     if (p.claim != nullptr) grid = (unsigned)(blocks + 8 * spare);
   }

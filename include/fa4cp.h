@@ -19,14 +19,15 @@
  *     the kernels size their grids by them, and with a too-small bound some rows are not
  *     written;
  *   - the library's state is that thread-local message; for fa4cp_quantize_e4m3_noalloc, a
- *     static 4 KiB device array per GPU (its amax words); and for fa4cp_ring_sweep_fwd,
- *     fa4cp_ring_sweep_fwd_paged and fa4cp_attn_fwd over one sequence, a static 72 KiB device
- *     array per GPU of 64 sets of row tile counters (a launch takes the next set, its last
+ *     static 4 KiB device array per GPU (its amax words); and for fa4cp_attn_fwd over one
+ *     sequence and fa4cp_ring_sweep_fwd / fa4cp_ring_sweep_fwd_paged over one sequence or up
+ *     to 64 packed ones (with h_kv * group / 4 = 8 head groups), a static 72 KiB device array
+ *     per GPU of 64 sets of row tile counters (a launch takes the next set, its last
  *     workgroup clears it).  Each array has a per-device cache of its address (filled once
  *     per device under a mutex) and the counters a per-device set index.  Two calls that
  *     write the same memory on different streams race, and so do two
- *     fa4cp_quantize_e4m3_noalloc calls that overlap on one GPU; the one-sequence attention
- *     and sweep calls on one GPU take the 64 counter sets in turn, so a call must have
+ *     fa4cp_quantize_e4m3_noalloc calls that overlap on one GPU; those attention and sweep
+ *     calls on one GPU take the 64 counter sets in turn, so a call must have
  *     finished on the GPU before the 64th such call after it (counted over all streams)
  *     starts there (always true on one stream), and replays of one captured launch must not
  *     overlap each other.
