@@ -21,9 +21,9 @@
  *   - the library's state is that thread-local message; for fa4cp_quantize_e4m3_noalloc, a
  *     static 4 KiB device array per GPU (its amax words); and for fa4cp_attn_fwd over one
  *     sequence and fa4cp_ring_sweep_fwd / fa4cp_ring_sweep_fwd_paged over one sequence or up
- *     to 64 packed ones (whose query heads form eight workgroup head groups, as H_q 32 / H_kv 8), a static 72 KiB device array
- *     per GPU of 64 sets of row tile counters (a launch takes the next set, its last
- *     workgroup clears it).  Each array has a per-device cache of its address (filled once
+ *     to 64 packed ones (whose query heads form eight workgroup head groups, as H_q 32 /
+ *     H_kv 8), a static 72 KiB device array per GPU of 64 sets of row tile counters (a
+ *     launch takes the next set, its last workgroup clears it).  Each array has a per-device cache of its address (filled once
  *     per device under a mutex) and the counters a per-device set index.  Two calls that
  *     write the same memory on different streams race, and so do two
  *     fa4cp_quantize_e4m3_noalloc calls that overlap on one GPU; those attention and sweep
