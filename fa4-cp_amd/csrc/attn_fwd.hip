@@ -369,30 +369,25 @@ __device__ __forceinline__ bool decode_sweep_block(const Params& p, int rows, in
   return false;
 }
 
-// Dynamic hand-out of the sweep's row tiles.  The hardware sends workgroup i to XCD i % 8,
-// so a fixed order gives every XCD the same share, and the slowest XCD (their speeds differ
-// by several per cent on one GPU) sets the end of the launch.  Here the grid has some spare
-// workgroups, and each workgroup claims the next entry of its XCD's list (the entries
-// y + 8 i, i = 0, 1, ..., of the fixed order for XCD y: the same head groups and longest-first
-// order) from that XCD's counter; when the list is used up it claims from the other XCDs'
-// lists in turn, and when all are, it exits.  Every entry is claimed once (a counter hands out
-// each value once, and a workgroup only exits after it found every list used up, so with at
-// least as many workgroups as entries none is left).  `claim` points at nine counters 128
-// bytes apart, zero at the start (eight lists, then the workgroups that finished claiming);
-// the last workgroup to finish claiming sets them back to zero for the launch that reuses
-// them.  Returns the claimed id of the fixed order, or -1.  (Packed sequences keep the fixed
-// order: there a workgroup averages a few dozen tiles, and the claim at its start cost more
-// than the balance gained, 0.8825-0.8877 against 0.8711-0.8786 ms for C4.)
+// Dynamic hand-out of the row tiles.  The hardware sends workgroup i to XCD i % 8, so a fixed
+// order gives every XCD the same share, and the slowest XCD (their speeds differ by several
+// per cent on one GPU) sets the end of the launch.  XCD y's list is the entries y + 8 i,
+// i = 0 .. lim - 1, of the fixed order (its head groups, longest first).  The first three
+// quarters of each list go to the workgroups the fixed order sends there, with no atomics;
+// the last quarter (the lightest tiles: at least a tenth of the list's work, enough to even
+// out XCDs up to about 10 % apart) is claimed by the workgroups past that point, with a tenth
+// of spare workgroups in the grid.  A claiming workgroup takes the next entry of its own
+// XCD's list from that XCD's counter, then of the other XCDs' lists in turn, and exits when
+// all are used up.  Every entry is claimed once: a counter hands out each value once, and a
+// workgroup only exits after it found every list used up, so with at least as many claiming
+// workgroups as claimed entries none is left.  `claim` points at nine counters kClaimStride
+// words apart, zero at the start (the eight lists, then the workgroups that finished
+// claiming); the last of the `parts` claiming workgroups sets them back to zero for the
+// launch that reuses them.
 constexpr int kClaimStride = 32;  // words between counters
-//
-// Only the tail of each list is claimed: the first three quarters of its entries (the heavy
-// row tiles first) go to the workgroups the fixed order sends there, with no atomics, and the
-// last quarter (at least a tenth of the list's work, since the lightest tiles come last) and
-// the spare workgroups take part in the claims.  That keeps the claims' cost to a quarter of
-// the workgroups while leaving enough work at the end to even out XCDs up to about 10 % apart.
-//
-// claim_tail: entries fixed .. lim - 1 of the lists, among `parts` claiming workgroups (those
-// past the fixed part of the grid); every thread of the workgroup calls it.
+
+// The claims of entries fixed .. lim - 1 of every list; returns the entry's id in the fixed
+// order, or -1.  Every thread of the workgroup calls it.
 __device__ __forceinline__ int claim_tail(unsigned* claim, int fixed, int lim, unsigned parts) {
   __shared__ int claimed;
   if (threadIdx.x == 0) {
