@@ -422,7 +422,10 @@ __device__ __forceinline__ int claim_block(const Params& p) {
 // sequences (a lane each) gives the head group's real row tiles `tot`, so that the first
 // three quarters of them keep the fixed order and the rest go to the claims of the
 // workgroups tot - tot / 4 .. tot + tot / 10 of each XCD (the others, empty in the fixed
-// order too, exit at once).  Returns false when the workgroup has no tile.
+// order too, exit at once).  The list takes the sequences longest first (ties by index),
+// each sequence's row tiles last first: a row tile's keys grow with its sequence's length
+// and its position in it, so the claimed tail holds the lightest tiles.  Returns false when
+// the workgroup has no tile.
 template <typename Params>
 __device__ __forceinline__ bool decode_sweep_claimed(const Params& p, int rows, int& hg, int& seq, int& rt,
                                                      int& qs, int& len, int64_t& vt_pos) {
@@ -453,13 +456,20 @@ __device__ __forceinline__ bool decode_sweep_claimed(const Params& p, int rows, 
     b = claim_tail(p.claim, fixed, tot, 8u * (unsigned)parts_per_xcd);
     if (b < 0) return false;
   }
-  // one head group per XCD: entry b is row tile b >> 3 (in the order decode_sweep_block
-  // numbers them) of head group b & 7
+  // one head group per XCD: entry b is row tile b >> 3 of head group b & 7
   hg = b & 7;
   const int r = b >> 3;
-  const int jl = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)__ballot(incl > r)) - 1);
+  int ahead = 0;  // row tiles of the sequences ahead of this lane's, longest first
+  for (int k = 0; k < p.nseq; ++k) {
+    const int Lk = __builtin_amdgcn_readlane(L, k);
+    if (Lk > L || (Lk == L && k < lane)) ahead += __builtin_amdgcn_readlane(nt, k);
+  }
+  // the intervals [ahead, ahead + nt) of the lanes partition [0, tot), and r < tot
+  const unsigned long long hit = __ballot(ahead <= r && r < ahead + nt);
+  if (hit == 0ull) return false;
+  const int jl = __builtin_amdgcn_readfirstlane(__ffsll(hit) - 1);
   const int ntj = __builtin_amdgcn_readlane(nt, jl);
-  const int before = __builtin_amdgcn_readlane(incl, jl) - ntj;
+  const int before = __builtin_amdgcn_readlane(ahead, jl);
   seq = jl;
   rt = ntj - 1 - (r - before);
   qs = __builtin_amdgcn_readlane(s0, jl);
