@@ -2430,6 +2430,10 @@ __device__ __forceinline__ void e8_pipeline(E8Lds<D>& lds, const Geo& geo,
   static_assert(NG < 16, "vmcnt field");
   // MFMAs whose fragments are read ahead (D = 256 keeps 128 registers of O and 32 of Q^T)
   constexpr int RA = D == 256 ? (KPAD ? 2 : 1) : kPPReadAhead;
+  // LATE_MAX (D = 256): mask, row max and rescale open the softmax phase instead of closing the
+  // MFMA phase.  A 64-key tile's softmax (32 scores per lane) issues in well under its 16
+  // products, so there the MFMA phase is the longer one.  Same operations: bit-identical.
+  constexpr bool LATE_MAX = D == 256;
   auto& kl = lds.kl;
   auto& vt = lds.vt;
 
@@ -2702,8 +2706,10 @@ __device__ __forceinline__ void e8_pipeline(E8Lds<D>& lds, const Geo& geo,
     const auto r = walk.rsrc(lc, isk);
     const float c = c_q * mc.g.kd * kLog2e;
     __builtin_amdgcn_s_setprio(0);
-    if (__builtin_expect(mc.t >= mc.g.first_mask, 0)) mask();
-    max_rescale(c);
+    if constexpr (!LATE_MAX) {
+      if (__builtin_expect(mc.t >= mc.g.first_mask, 0)) mask();
+      max_rescale(c);
+    }
     // K_{j+1} / V^T_j, loaded two VALU phases ago, are read in the next phase; with two
     // V^T slots V^T_j is group 1's latest load, with three K slots K_{j+1} group 0's
     if ((VS == 2 && !isk) || (KS == 3 && isk)) __builtin_amdgcn_s_waitcnt(0);
@@ -2719,6 +2725,10 @@ __device__ __forceinline__ void e8_pipeline(E8Lds<D>& lds, const Geo& geo,
       if (n < NG || isk) dma16(r, dst + 1024 * (wi + 4 * n), ld_voff[n]);
     ld_slot = ld_slot + 1 == ld_slots ? 0 : ld_slot + 1;
     if constexpr (KPAD) kr = kr + 1 == KS ? 0 : kr + 1;
+    if constexpr (LATE_MAX) {
+      if (__builtin_expect(mc.t >= mc.g.first_mask, 0)) mask();
+      max_rescale(c);
+    }
     exp_tile(c);
     pack_e4m3<NPS, NMT>(s, pf);
     if constexpr (decltype(split)::value) pack_e4m3_residual<NPS, NMT>(s, pf, pl);
