@@ -50,7 +50,7 @@ SWEEP_TRAFFIC_BYTES_RANK3 = 2436944 * 1024
 # (N = 262144, rank 3), and for merge_states in their batched per-step forms (same factors,
 # counter passes over `bench.py --workload c4` / `--workload c5`).
 C4_SWEEP_TRAFFIC_BYTES = (2 * 162099 + 102521) * 1024
-C5_SWEEP_TRAFFIC_BYTES = (2 * 2384638 + 266445) * 1024
+C5_SWEEP_TRAFFIC_BYTES = (2 * 2595454 + 266600) * 1024
 C4_MERGE_STATES_TRAFFIC_BYTES = (2 * 204965 + 100913) * 1024
 # ... for the e4m3 sweep at the headline shape (rank 3), counter passes over `--workload c3`
 C3_SWEEP_TRAFFIC_BYTES_RANK3 = (2 * 567996 + 135355) * 1024
