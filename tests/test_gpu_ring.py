@@ -371,16 +371,18 @@ def test_ring_fp8_varlen_all_ranks(mode):
         assert lse_err(lse, ref_lse) <= TOL_LSE, f"rank {rank} lse"
 
 
+@pytest.mark.parametrize("d", [128, 256])
 @pytest.mark.parametrize("mode", PATHS)
 @pytest.mark.parametrize("growth", [5.0, 8.8, 150.0])
-def test_ring_fp8_row_max_grows_inside_a_later_source(growth, mode):
-    """The row max jumps by `growth` (log2 units) on the third key tile of the second source
-    (rank 1 of 2: local causal keys, then the front half of source 0), whose v descale is
-    ten times the first source's: 5 stays under the lazy-rescale bound, 8.8 moves the
-    reference max mid-segment (O must change units once, at the segment start, not again
-    here), 150 overflows the exponentials taken against the old max."""
-    n, h, hkv, d, cp, rank = 2048, 2, 1, 128, 2, 1
-    say(f"ring e4m3 late max growth={growth} path={mode}")
+def test_ring_fp8_row_max_grows_inside_a_later_source(growth, mode, d):
+    """The row max jumps by `growth` (log2 units) on key 300 of the second source (rank 1 of
+    2: local causal keys, then the front half of source 0; the third 128-key tile at head dim
+    128, the fifth 64-key tile at 256, where the mask, row max and rescale run in the softmax
+    phase), whose v descale is ten times the first source's: 5 stays under the lazy-rescale
+    bound, 8.8 moves the reference max mid-segment (O must change units once, at the segment
+    start, not again here), 150 overflows the exponentials taken against the old max."""
+    n, h, hkv, cp, rank = 2048, 2, 1, 2, 1
+    say(f"ring e4m3 late max growth={growth} d={d} path={mode}")
     g = torch.Generator().manual_seed(8)
     u = torch.randn(d, generator=g)
     u = u / u.norm()
