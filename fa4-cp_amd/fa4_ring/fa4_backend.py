@@ -93,6 +93,22 @@ def descale_table(ds, h_kv: int, device) -> torch.Tensor:
     return torch.stack([_descale_view(d, h_kv, device) for d in ds])
 
 
+def sweep_descales(q, ks, vs, h_kv: int, device):
+    """The fused sweep's descales -> (q [h_kv], k [len(ks), h_kv], v [len(vs), h_kv]), float32
+    rows of one contiguous table built by a single stack (one device copy per call instead of
+    three); a part given as None comes back None."""
+    parts = [[] if q is None else [q], list(ks or []), list(vs or [])]
+    views = [_descale_view(d, h_kv, device) for part in parts for d in part]
+    if not views:
+        return None, None, None
+    table = torch.stack(views)
+    out, row = [], 0
+    for part, given in zip(parts, (q is not None, ks is not None, vs is not None)):
+        out.append(table[row:row + len(part)] if given else None)
+        row += len(part)
+    return out[0][0] if q is not None else None, out[1], out[2]
+
+
 def _cu_ok(cu: torch.Tensor, device, name: str) -> None:
     _require(cu.dtype == torch.int32, f"{name} must be int32, got {cu.dtype}")
     _require(cu.device == device, f"{name} must live on {device}, got {cu.device}")

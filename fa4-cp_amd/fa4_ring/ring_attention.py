@@ -36,9 +36,8 @@ import torch
 
 from . import _lib
 from .config import RingConfig
-from .fa4_backend import (SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, SUPPORTED_HEAD_DIMS, _norm_descale, descale_table,
-                          fa4_attn, kernel_head_dim, out_dtype_for, pad_head_dim, transpose_v, transpose_v_many,
-                          uses_vt)
+from .fa4_backend import (SEL_ALL, SEL_BACK_HALF, SEL_FRONT_HALF, SUPPORTED_HEAD_DIMS, fa4_attn, kernel_head_dim,
+                          out_dtype_for, pad_head_dim, sweep_descales, transpose_v, transpose_v_many, uses_vt)
 from .merge import merge_state_in_place, merge_states
 from .paged import PagedKVRing, gather_kv_pages, transpose_v_paged_many
 from .zigzag import zigzag_shard, zigzag_shard_varlen
@@ -380,11 +379,8 @@ def _sweep_launch(local_q: torch.Tensor, k_ptrs: List[int], k_strides: Tuple[int
         out = torch.empty(local_q.shape, dtype=torch.bfloat16 if e4m3 else local_q.dtype, device=dev)
     qd = kd = vd = None
     if e4m3 and descales is not None:
-        qd = _norm_descale(descales.q, h_kv, dev)
-        if descales.k is not None:
-            kd = descale_table(descales.k[:S], h_kv, dev)
-        if descales.v is not None:
-            vd = descale_table(descales.v[:S], h_kv, dev)
+        qd, kd, vd = sweep_descales(descales.q, None if descales.k is None else descales.k[:S],
+                                    None if descales.v is None else descales.v[:S], h_kv, dev)
     if lse is None:
         lse = torch.empty((total, h_q), dtype=torch.float32, device=dev)
     odt = torch.bfloat16 if e4m3 else local_q.dtype

@@ -14,7 +14,7 @@ import torch
 import fa4_ring
 from fa4_ring import _lib
 from fa4_ring.config import RingConfig
-from fa4_ring.fa4_backend import _norm_descale, fa4_attn
+from fa4_ring.fa4_backend import _norm_descale, fa4_attn, sweep_descales
 from fa4_ring.merge import BatchedMerger, IncrementalMerger, make_merger
 from fa4_ring.ring_attention import Descales, LocalKVRing, ring_flash_attn
 from fa4_ring.zigzag import get_half_index, half_indices, local_seqlen
@@ -318,6 +318,25 @@ def test_make_merger():
     t = torch.zeros(2, 1, 8)
     b.add(t, torch.zeros(2, 1))
     assert b.result() is t
+
+
+def test_sweep_descales_one_table():
+    """The fused sweep's q / k / v descales come back as rows of one stack, each equal to the
+    per-part normalisation, contiguous, float32; a part given as None comes back None."""
+    ks = [torch.tensor(0.5), torch.arange(4.0) + 1, torch.full((1, 4), 3.0)]
+    vs = [torch.tensor(2.0, dtype=torch.float64), torch.tensor(4.0), torch.arange(4.0).reshape(1, 4)]
+    q = torch.tensor(0.25)
+    qd, kd, vd = sweep_descales(q, ks, vs, 4, "cpu")
+    assert qd.tolist() == [0.25] * 4 and qd.is_contiguous() and qd.dtype == torch.float32
+    assert kd.shape == (3, 4) and kd.is_contiguous() and vd.shape == (3, 4) and vd.is_contiguous()
+    assert kd.tolist() == [_norm_descale(k, 4, "cpu").tolist() for k in ks]
+    assert vd.tolist() == [_norm_descale(v, 4, "cpu").tolist() for v in vs]
+    assert kd.dtype == vd.dtype == torch.float32
+    qd, kd, vd = sweep_descales(None, ks, None, 4, "cpu")
+    assert qd is None and vd is None and kd.tolist() == [_norm_descale(k, 4, "cpu").tolist() for k in ks]
+    assert sweep_descales(None, None, None, 4, "cpu") == (None, None, None)
+    qd, kd, vd = sweep_descales(q, None, vs[:1], 4, "cpu")
+    assert kd is None and qd.tolist() == [0.25] * 4 and vd.tolist() == [[2.0] * 4]
 
 
 def test_norm_descale_shapes():
